@@ -1,0 +1,183 @@
+/*
+ * omhip.h — C ABI of libomhip.so, the gfx950 (MI355X) compute backend for the
+ * OmniMatch HAL matmul / conv2d hot path.
+ *
+ * Conventions (identical to the reference omCuda* ABI, src/cuda/cuda_kernels.cuh:10-535):
+ *   - every entry returns int: 0 on success, -1 on a HIP error or invalid
+ *     argument (omHipGetLastError() names the cause);
+ *   - every data pointer is a DEVICE pointer to row-major contiguous data;
+ *   - kernels are asynchronous on one library-owned stream; results become
+ *     host-visible after omHipCopyD2H / omHipSynchronize;
+ *   - omHipInit(dev) must precede use; it is idempotent and thread-safe.
+ *   - GEMM entries with M<=0, N<=0 or K<=0 (or a null input) zero C when C and
+ *     its extent are valid and return 0, as CPUBackend::matmul does
+ *     (src/hal/om.hal.cpu_backend.ixx:246-251).
+ *
+ * Each declaration cites the reference interface it replaces (file:line).
+ * Entries marked NEW have no omCuda* counterpart; their comment states the
+ * reference composition they are equivalent to.
+ */
+#ifndef OMHIP_H
+#define OMHIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ===== device management (src/cuda/cuda_kernels.cuh:18-34, :63-69, :184) ===== */
+
+/* replaces omCudaInit (cuda_kernels.cuh:18): select device, create the library stream */
+int omHipInit(int nDeviceId);
+/* replaces omCudaGetDeviceCount (cuda_kernels.cuh:21); returns the count (0 without GPU) */
+int omHipGetDeviceCount(void);
+/* replaces omCudaGetDeviceName (cuda_kernels.cuh:24) */
+int omHipGetDeviceName(int nDeviceId, char* pNameBuf, int nBufSize);
+/* replaces omCudaGetMemInfo (cuda_kernels.cuh:27) */
+int omHipGetMemInfo(int nDeviceId, size_t* pFreeMem, size_t* pTotalMem);
+/* replaces omCudaGetComputeCapability (cuda_kernels.cuh:34): gfx950 reports 9 / 5 */
+int omHipGetComputeCapability(int nDeviceId, int* pMajor, int* pMinor);
+/* replaces omCudaSynchronize (cuda_kernels.cuh:184): waits for the library stream */
+int omHipSynchronize(void);
+/* replaces omCudaSyncComputeStream (cuda_kernels.cuh:66) */
+int omHipSyncComputeStream(void);
+/* replaces omCudaCleanup (cuda_kernels.cuh:69): frees the pool, destroys the stream */
+int omHipCleanup(void);
+/* NEW: the library stream as a hipStream_t (for event timing / interop) */
+int omHipGetStream(void** ppStream);
+/* NEW: route subsequent work to a caller-owned hipStream_t (NULL restores the
+ * library stream). The caller keeps ownership of the stream. */
+int omHipSetStream(void* pStream);
+/* NEW: message of the last failing call on this thread ("" if none) */
+const char* omHipGetLastError(void);
+
+/* ===== memory (src/cuda/cuda_kernels.cuh:39-60) ===== */
+
+/* replaces omCudaMalloc (cuda_kernels.cuh:39): caching pool, flush-and-retry on OOM */
+int omHipMalloc(void** ppDevPtr, size_t nBytes);
+/* replaces omCudaFree (cuda_kernels.cuh:42): returns the block to the pool */
+int omHipFree(void* pDevPtr);
+/* replaces omCudaCopyH2D (cuda_kernels.cuh:45): synchronous */
+int omHipCopyH2D(void* pDst, const void* pSrc, size_t nBytes);
+/* replaces omCudaCopyD2H (cuda_kernels.cuh:48): synchronous */
+int omHipCopyD2H(void* pDst, const void* pSrc, size_t nBytes);
+/* replaces omCudaCopyD2D (cuda_kernels.cuh:51): stream-ordered */
+int omHipCopyD2D(void* pDst, const void* pSrc, size_t nBytes);
+/* replaces omCudaMemset (cuda_kernels.cuh:54): stream-ordered */
+int omHipMemset(void* pDev, int nValue, size_t nBytes);
+/* NEW: pool statistics: bytes held by the pool, bytes currently handed out */
+int omHipPoolStats(size_t* pHeldBytes, size_t* pUsedBytes);
+/* NEW: release every cached (free) block back to the driver */
+int omHipPoolTrim(void);
+
+/* ===== fills / copy (src/cuda/cuda_kernels.cuh:257-266; CPUBackend cpu_backend.ixx:65-77, :444-446) ===== */
+
+int omHipFillZeros(float* pData, int nCount);                 /* omCudaFillZeros  cuh:257 */
+int omHipFillOnes(float* pData, int nCount);                  /* omCudaFillOnes   cuh:260 */
+int omHipFillValue(float* pData, int nCount, float fValue);   /* omCudaFillValue  cuh:263 */
+int omHipCopy(const float* pSrc, float* pDst, int nCount);    /* omCudaCopy       cuh:266 */
+
+/* ===== activations / bias (cuda_kernels.cuh:91-94, :249) ===== */
+
+/* replaces omCudaReLU (cuh:91): out = x > 0 ? x : 0 (NaN -> 0, -0 -> +0), as cpu_backend.ixx:317-332 */
+int omHipReLU(const float* pIn, float* pOut, int nCount);
+/* replaces omCudaReLUBackward (cuh:94): gradIn = x > 0 ? gradOut : 0, as cpu_backend.ixx:337-346 */
+int omHipReLUBackward(const float* pIn, const float* pGradOut, float* pGradIn, int nCount);
+/* replaces omCudaAddBias (cuh:249): out[n,c,hw] = data[n,c,hw] + bias[c].
+ * CPUBackend::addBias(A, bias, out, batch, cols) (cpu_backend.ixx:433-440) is
+ * the case nN=batch, nC=cols, nHW=1. */
+int omHipAddBias(const float* pData, const float* pBias, float* pOut, int nN, int nC, int nHW);
+
+/* ===== fp32 GEMM (cuda_kernels.cuh:109-117) ===== */
+
+/* replaces omCudaMatmul (cuh:109): C[M,N] = A[M,K] * B[K,N] (CPUBackend::matmul cpu_backend.ixx:239-286) */
+int omHipMatmul(const float* pA, const float* pB, float* pC, int nM, int nK, int nN);
+/* NEW: C[M,N] = A[M,K] * B[N,K]^T  (Linear-weight layout). Reference composition:
+ * transpose2d(B, Bt, N, K); matmul(A, Bt, C, M, K, N)  (cpu_backend.ixx:1535-1539, :239-286;
+ * used by MatMulBackward autograd.ixx:261-273) */
+int omHipMatmulTransB(const float* pA, const float* pB, float* pC, int nM, int nK, int nN);
+/* NEW: C[M,N] = A[K,M]^T * B[K,N]. Reference composition: transpose2d(A, At, K, M);
+ * matmul(At, B, C, M, K, N)  (the dB half of MatMulBackward autograd.ixx:276-286) */
+int omHipMatmulTransA(const float* pA, const float* pB, float* pC, int nM, int nK, int nN);
+/* replaces omCudaBatchedMatmul (cuh:112): C[b] = A[b] * B[b], strides M*K, K*N, M*N
+ * (CPUBackend::batchedMatmul cpu_backend.ixx:1520-1532) */
+int omHipBatchedMatmul(const float* pA, const float* pB, float* pC, int nBatch, int nM, int nK, int nN);
+/* NEW: C[b] = A[b] * B[b]^T with B[b] stored [N,K]; reference composition:
+ * tensorTranspose2dBatched + batchedMatmul (tensor_ops.ixx:1588-1625, :1561-1582; vit.ixx:175-176) */
+int omHipBatchedMatmulTransB(const float* pA, const float* pB, float* pC, int nBatch, int nM, int nK, int nN);
+/* NEW: general strided-batched fp32 GEMM. transA/transB select A[K,M] / B[N,K]
+ * storage; lda/ldb/ldc are row strides in elements; strides are per-batch element
+ * offsets (0 shares an operand across the batch). */
+int omHipGemmStridedBatched(int bTransA, int bTransB, int nBatch, int nM, int nN, int nK,
+                            const float* pA, long long nLda, long long nStrideA,
+                            const float* pB, long long nLdb, long long nStrideB,
+                            float* pC, long long nLdc, long long nStrideC);
+/* replaces omCudaTranspose (cuh:117): out[c,r] = in[r,c]; CPUBackend::transpose2d cpu_backend.ixx:1535-1539 */
+int omHipTranspose(const float* pIn, float* pOut, int nRows, int nCols);
+
+/* ===== conv2d / batchnorm (cuda_kernels.cuh:136-146, :165-170) ===== */
+
+/* replaces omCudaConv2d (cuh:136): NCHW conv, symmetric stride/pad, dilation 1,
+ * groups 1; pBias may be NULL. CPUBackend::conv2d cpu_backend.ixx:619-658 */
+int omHipConv2d(const float* pInput, const float* pWeight, const float* pBias, float* pOutput,
+                int nBatch, int nCin, int nH, int nW,
+                int nCout, int nKH, int nKW, int nStride, int nPad);
+/* replaces omCudaConv2dIm2col (cuh:142): same result as omHipConv2d via an explicit
+ * im2col buffer followed by a shared-weight batched GEMM */
+int omHipConv2dIm2col(const float* pInput, const float* pWeight, const float* pBias, float* pOutput,
+                      int nBatch, int nCin, int nH, int nW,
+                      int nCout, int nKH, int nKW, int nStride, int nPad);
+/* NEW: conv2d + bias + BatchNorm(inference) + activation in one kernel.
+ * Reference composition: conv2d (cpu_backend.ixx:619-658) -> batchNorm2d(bTraining=false)
+ * (cpu_backend.ixx:781-842, eval branch 823-840) -> relu (cpu_backend.ixx:317-332).
+ * pBias may be NULL; pGamma/pBeta/pMean/pVar may all be NULL (no BN);
+ * nAct: 0 = identity, 1 = ReLU. */
+int omHipConv2dBiasBnAct(const float* pInput, const float* pWeight, const float* pBias,
+                         const float* pGamma, const float* pBeta,
+                         const float* pMean, const float* pVar, float fEps, int nAct,
+                         float* pOutput,
+                         int nBatch, int nCin, int nH, int nW,
+                         int nCout, int nKH, int nKW, int nStride, int nPad);
+/* NEW: im2col of one image, col[(c*KH+kh)*KW+kw, oh*Wout+ow]; CPUBackend::im2col cpu_backend.ixx:544-575 */
+int omHipIm2col(const float* pInput, int nCin, int nH, int nW, int nKH, int nKW,
+                int nPadH, int nPadW, int nStrideH, int nStrideW, float* pCol);
+/* replaces omCudaBatchNorm2d (cuh:165). Inference mode only (bTraining == 0):
+ * y = gamma*((x-runMean)*invStd)+beta, invStd = 1/sqrt(runVar+eps), savedMean/
+ * savedInvStd written as cpu_backend.ixx:823-840. bTraining != 0 returns -1. */
+int omHipBatchNorm2d(const float* pInput, float* pOutput,
+                     const float* pGamma, const float* pBeta,
+                     float* pRunMean, float* pRunVar,
+                     float* pSavedMean, float* pSavedInvStd,
+                     int nBatch, int nChannels, int nH, int nW,
+                     float fEps, float fMomentum, int bTraining);
+
+/* ===== fp16 / bf16 GEMM, fp32 accumulate (NEW; the reference has only the software
+ * converter om.engine.fp16.ixx:36-164) ===== */
+
+/* NEW: fp32 -> IEEE binary16 / bfloat16, round-to-nearest-even; and back */
+int omHipConvertF32ToF16(const float* pIn, uint16_t* pOut, int nCount);
+int omHipConvertF32ToBF16(const float* pIn, uint16_t* pOut, int nCount);
+int omHipConvertF16ToF32(const uint16_t* pIn, float* pOut, int nCount);
+int omHipConvertBF16ToF32(const uint16_t* pIn, float* pOut, int nCount);
+/* NEW: C[M,N] (fp32) = A[M,K] * B[K,N], A/B binary16. Reference composition:
+ * halfToFloat(A), halfToFloat(B), matmul (fp16.ixx:103-164, cpu_backend.ixx:239-286) */
+int omHipMatmulF16(const uint16_t* pA, const uint16_t* pB, float* pC, int nM, int nK, int nN);
+/* NEW: as omHipMatmulF16 with bfloat16 inputs */
+int omHipMatmulBF16(const uint16_t* pA, const uint16_t* pB, float* pC, int nM, int nK, int nN);
+/* NEW: C = A * B^T with B stored [N,K] (Linear weight layout), fp16 / bf16 inputs */
+int omHipMatmulTransBF16(const uint16_t* pA, const uint16_t* pB, float* pC, int nM, int nK, int nN);
+int omHipMatmulTransBBF16(const uint16_t* pA, const uint16_t* pB, float* pC, int nM, int nK, int nN);
+/* NEW: general strided-batched half-precision GEMM with fp32 output.
+ * nDtype: 0 = binary16, 1 = bfloat16. Layout arguments as omHipGemmStridedBatched. */
+int omHipGemmStridedBatchedHalf(int nDtype, int bTransA, int bTransB, int nBatch, int nM, int nN, int nK,
+                                const uint16_t* pA, long long nLda, long long nStrideA,
+                                const uint16_t* pB, long long nLdb, long long nStrideB,
+                                float* pC, long long nLdc, long long nStrideC);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* OMHIP_H */

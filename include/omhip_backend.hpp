@@ -1,0 +1,125 @@
+// omhip_backend.hpp — om::HIPBackend, the C++23 HAL class for MI355X.
+//
+// Drop-in for the GPU slot of the reference HAL: same static-method shape as
+// om::CPUBackend (src/hal/om.hal.cpu_backend.ixx:61-1631) and the slot that
+// om::CUDABackend occupies today (src/hal/om.hal.cuda_backend.ixx:283-983),
+// selected by the existing `if (isCudaTensor(t))` dispatch
+// (src/engine/om.engine.tensor_ops.ixx:35-37). Signatures and argument order are
+// CPUBackend's (CUDABackend's conv2d / batchNorm2d orders differ:
+// cuda_backend.ixx:438-448, :571-586). Pointers are device pointers.
+//
+// Error behaviour: every call checks the omHip* status and throws
+// std::runtime_error carrying omHipGetLastError(); the reference CUDABackend
+// ignores the int it gets back.
+#pragma once
+
+#include <cstddef>
+#include <cstdint>
+#include <stdexcept>
+#include <string>
+
+#include "omhip.h"
+
+namespace om {
+
+class HIPBackend {
+public:
+    // ---- device ----
+    static void init(int nDevice = 0) { check(omHipInit(nDevice), "omHipInit"); }
+    static void synchronize() { check(omHipSynchronize(), "omHipSynchronize"); }
+    static void* malloc(size_t nBytes) {
+        void* p = nullptr;
+        check(omHipMalloc(&p, nBytes), "omHipMalloc");
+        return p;
+    }
+    static void free(void* p) { check(omHipFree(p), "omHipFree"); }
+    static void copyH2D(void* pDst, const void* pSrc, size_t nBytes) { check(omHipCopyH2D(pDst, pSrc, nBytes), "omHipCopyH2D"); }
+    static void copyD2H(void* pDst, const void* pSrc, size_t nBytes) { check(omHipCopyD2H(pDst, pSrc, nBytes), "omHipCopyD2H"); }
+
+    // ---- fills / copy (cpu_backend.ixx:65-77, :444-446) ----
+    static void fillZeros(float* pData, size_t nCount) { check(omHipFillZeros(pData, toInt(nCount)), "fillZeros"); }
+    static void fillOnes(float* pData, size_t nCount) { check(omHipFillOnes(pData, toInt(nCount)), "fillOnes"); }
+    static void fillValue(float* pData, size_t nCount, float fValue) {
+        check(omHipFillValue(pData, toInt(nCount), fValue), "fillValue");
+    }
+    static void copy(const float* pSrc, float* pDst, size_t nCount) { check(omHipCopy(pSrc, pDst, toInt(nCount)), "copy"); }
+
+    // ---- GEMM (cpu_backend.ixx:239-286, :1520-1539) ----
+    static void matmul(const float* pA, const float* pB, float* pC, int nM, int nK, int nN) {
+        check(omHipMatmul(pA, pB, pC, nM, nK, nN), "matmul");
+    }
+    static void batchedMatmul(const float* pA, const float* pB, float* pC, int nBatch, int nM, int nK, int nN) {
+        check(omHipBatchedMatmul(pA, pB, pC, nBatch, nM, nK, nN), "batchedMatmul");
+    }
+    static void transpose2d(const float* pA, float* pB, int nRows, int nCols) {
+        check(omHipTranspose(pA, pB, nRows, nCols), "transpose2d");
+    }
+
+    // ---- activations / bias (cpu_backend.ixx:317-346, :433-440) ----
+    static void relu(const float* pIn, float* pOut, size_t nCount) { check(omHipReLU(pIn, pOut, toInt(nCount)), "relu"); }
+    static void reluBackward(const float* pIn, const float* pGradOut, float* pGradIn, size_t nCount) {
+        check(omHipReLUBackward(pIn, pGradOut, pGradIn, toInt(nCount)), "reluBackward");
+    }
+    static void addBias(const float* pA, const float* pBias, float* pOut, int nBatch, int nCols) {
+        check(omHipAddBias(pA, pBias, pOut, nBatch, nCols, 1), "addBias");
+    }
+
+    // ---- conv / BN (cpu_backend.ixx:544-575, :619-658, :781-842) ----
+    static void im2col(const float* pInput, int nCin, int nH, int nW, int nKH, int nKW, int nPadH, int nPadW,
+                       int nStrideH, int nStrideW, float* pCol) {
+        check(omHipIm2col(pInput, nCin, nH, nW, nKH, nKW, nPadH, nPadW, nStrideH, nStrideW, pCol), "im2col");
+    }
+    static void conv2d(const float* pInput, const float* pWeight, const float* pBias, float* pOutput, int nBatch,
+                       int nCin, int nH, int nW, int nCout, int nKH, int nKW, int nStride, int nPad) {
+        check(omHipConv2d(pInput, pWeight, pBias, pOutput, nBatch, nCin, nH, nW, nCout, nKH, nKW, nStride, nPad),
+              "conv2d");
+    }
+    // Inference mode only: bTraining == true throws (batch statistics are not provided).
+    static void batchNorm2d(const float* pInput, float* pOutput, const float* pGamma, const float* pBeta,
+                            float* pRunMean, float* pRunVar, float* pSavedMean, float* pSavedInvStd, int nBatch,
+                            int nChannels, int nH, int nW, float fEps, float fMomentum, bool bTraining) {
+        check(omHipBatchNorm2d(pInput, pOutput, pGamma, pBeta, pRunMean, pRunVar, pSavedMean, pSavedInvStd, nBatch,
+                               nChannels, nH, nW, fEps, fMomentum, bTraining ? 1 : 0),
+              "batchNorm2d");
+    }
+
+    // ---- entries the reference builds by composition ----
+    // transpose2d(B) + matmul (autograd.ixx:261-273)
+    static void matmulTransB(const float* pA, const float* pB, float* pC, int nM, int nK, int nN) {
+        check(omHipMatmulTransB(pA, pB, pC, nM, nK, nN), "matmulTransB");
+    }
+    // transpose2d(A) + matmul (autograd.ixx:276-286)
+    static void matmulTransA(const float* pA, const float* pB, float* pC, int nM, int nK, int nN) {
+        check(omHipMatmulTransA(pA, pB, pC, nM, nK, nN), "matmulTransA");
+    }
+    static void batchedMatmulTransB(const float* pA, const float* pB, float* pC, int nBatch, int nM, int nK, int nN) {
+        check(omHipBatchedMatmulTransB(pA, pB, pC, nBatch, nM, nK, nN), "batchedMatmulTransB");
+    }
+    // conv2d -> batchNorm2d(eval) -> relu (tensor_ops.ixx:672-833, :511-536)
+    static void conv2dBiasBnAct(const float* pInput, const float* pWeight, const float* pBias, const float* pGamma,
+                                const float* pBeta, const float* pMean, const float* pVar, float fEps, int nAct,
+                                float* pOutput, int nBatch, int nCin, int nH, int nW, int nCout, int nKH, int nKW,
+                                int nStride, int nPad) {
+        check(omHipConv2dBiasBnAct(pInput, pWeight, pBias, pGamma, pBeta, pMean, pVar, fEps, nAct, pOutput, nBatch,
+                                   nCin, nH, nW, nCout, nKH, nKW, nStride, nPad),
+              "conv2dBiasBnAct");
+    }
+    // halfToFloat(A), halfToFloat(B), matmul (fp16.ixx:103-164) with fp32 accumulate
+    static void matmulF16(const uint16_t* pA, const uint16_t* pB, float* pC, int nM, int nK, int nN) {
+        check(omHipMatmulF16(pA, pB, pC, nM, nK, nN), "matmulF16");
+    }
+    static void matmulBF16(const uint16_t* pA, const uint16_t* pB, float* pC, int nM, int nK, int nN) {
+        check(omHipMatmulBF16(pA, pB, pC, nM, nK, nN), "matmulBF16");
+    }
+
+private:
+    static int toInt(size_t n) {
+        if (n > static_cast<size_t>(0x7fffffff)) throw std::runtime_error("HIPBackend: element count exceeds INT_MAX");
+        return static_cast<int>(n);
+    }
+    static void check(int rc, const char* what) {
+        if (rc != 0) throw std::runtime_error(std::string("HIPBackend::") + what + ": " + omHipGetLastError());
+    }
+};
+
+}  // namespace om

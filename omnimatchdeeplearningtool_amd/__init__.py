@@ -1,0 +1,328 @@
+"""omnimatchdeeplearningtool_amd — MI355X (gfx950) compute backend for the
+OmniMatch HAL matmul / conv2d hot path.
+
+The product is ``libomhip.so`` (C ABI declared in ``include/omhip.h``) and the
+C++23 ``om::HIPBackend`` in ``include/omhip_backend.hpp``. This Python module
+is the host-side mirror used by tests and the bench:
+
+* :func:`lib` loads ``libomhip.so`` (ctypes, signatures from the header) and
+  raises if it is missing — there is no CPU fallback;
+* :class:`DeviceBuffer` owns device memory from the library's caching pool;
+* :class:`HIPBackend` exposes the HAL with the reference ``CPUBackend`` method
+  names and argument order (src/hal/om.hal.cpu_backend.ixx), taking device
+  pointers; a failing call raises ``RuntimeError`` with the library's message
+  instead of being swallowed as ``CUDABackend`` does (om.hal.cuda_backend.ixx:283-983).
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from typing import Optional
+
+import numpy as np
+
+__all__ = ["lib", "lib_path", "DeviceBuffer", "HIPBackend", "OmHipError", "init", "synchronize"]
+
+_PKG = os.path.dirname(os.path.abspath(__file__))
+_LIB: Optional[ctypes.CDLL] = None
+
+
+class OmHipError(RuntimeError):
+    pass
+
+
+def lib_path() -> str:
+    return os.path.join(_PKG, "libomhip.so")
+
+
+_vp = ctypes.c_void_p
+_i = ctypes.c_int
+_ll = ctypes.c_longlong
+_sz = ctypes.c_size_t
+_fl = ctypes.c_float
+
+# name -> argtypes (all return int)
+_SIGS = {
+    "omHipInit": [_i],
+    "omHipGetDeviceCount": [],
+    "omHipGetDeviceName": [_i, ctypes.c_char_p, _i],
+    "omHipGetMemInfo": [_i, ctypes.POINTER(_sz), ctypes.POINTER(_sz)],
+    "omHipGetComputeCapability": [_i, ctypes.POINTER(_i), ctypes.POINTER(_i)],
+    "omHipSynchronize": [],
+    "omHipSyncComputeStream": [],
+    "omHipCleanup": [],
+    "omHipGetStream": [ctypes.POINTER(_vp)],
+    "omHipSetStream": [_vp],
+    "omHipMalloc": [ctypes.POINTER(_vp), _sz],
+    "omHipFree": [_vp],
+    "omHipCopyH2D": [_vp, _vp, _sz],
+    "omHipCopyD2H": [_vp, _vp, _sz],
+    "omHipCopyD2D": [_vp, _vp, _sz],
+    "omHipMemset": [_vp, _i, _sz],
+    "omHipPoolStats": [ctypes.POINTER(_sz), ctypes.POINTER(_sz)],
+    "omHipPoolTrim": [],
+    "omHipFillZeros": [_vp, _i],
+    "omHipFillOnes": [_vp, _i],
+    "omHipFillValue": [_vp, _i, _fl],
+    "omHipCopy": [_vp, _vp, _i],
+    "omHipReLU": [_vp, _vp, _i],
+    "omHipReLUBackward": [_vp, _vp, _vp, _i],
+    "omHipAddBias": [_vp, _vp, _vp, _i, _i, _i],
+    "omHipMatmul": [_vp, _vp, _vp, _i, _i, _i],
+    "omHipMatmulTransB": [_vp, _vp, _vp, _i, _i, _i],
+    "omHipMatmulTransA": [_vp, _vp, _vp, _i, _i, _i],
+    "omHipBatchedMatmul": [_vp, _vp, _vp, _i, _i, _i, _i],
+    "omHipBatchedMatmulTransB": [_vp, _vp, _vp, _i, _i, _i, _i],
+    "omHipGemmStridedBatched": [_i, _i, _i, _i, _i, _i, _vp, _ll, _ll, _vp, _ll, _ll, _vp, _ll, _ll],
+    "omHipTranspose": [_vp, _vp, _i, _i],
+    "omHipConv2d": [_vp, _vp, _vp, _vp] + [_i] * 9,
+    "omHipConv2dIm2col": [_vp, _vp, _vp, _vp] + [_i] * 9,
+    "omHipConv2dBiasBnAct": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _fl, _i, _vp] + [_i] * 9,
+    "omHipIm2col": [_vp] + [_i] * 9 + [_vp],
+    "omHipBatchNorm2d": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _fl, _fl, _i],
+    "omHipConvertF32ToF16": [_vp, _vp, _i],
+    "omHipConvertF32ToBF16": [_vp, _vp, _i],
+    "omHipConvertF16ToF32": [_vp, _vp, _i],
+    "omHipConvertBF16ToF32": [_vp, _vp, _i],
+    "omHipMatmulF16": [_vp, _vp, _vp, _i, _i, _i],
+    "omHipMatmulBF16": [_vp, _vp, _vp, _i, _i, _i],
+    "omHipMatmulTransBF16": [_vp, _vp, _vp, _i, _i, _i],
+    "omHipMatmulTransBBF16": [_vp, _vp, _vp, _i, _i, _i],
+    "omHipGemmStridedBatchedHalf": [_i, _i, _i, _i, _i, _i, _i, _vp, _ll, _ll, _vp, _ll, _ll, _vp, _ll, _ll],
+}
+
+
+def lib() -> ctypes.CDLL:
+    """Loads libomhip.so; raises OmHipError when it has not been built."""
+    global _LIB
+    if _LIB is None:
+        p = lib_path()
+        if not os.path.exists(p):
+            raise OmHipError(f"libomhip.so not built at {p}: run `python -m omnimatchdeeplearningtool_amd.build`")
+        L = ctypes.CDLL(p)
+        for name, args in _SIGS.items():
+            fn = getattr(L, name)
+            fn.argtypes = args
+            fn.restype = ctypes.c_int
+        L.omHipGetLastError.argtypes = []
+        L.omHipGetLastError.restype = ctypes.c_char_p
+        _LIB = L
+    return _LIB
+
+
+def _check(rc: int, what: str) -> None:
+    if rc != 0:
+        msg = lib().omHipGetLastError().decode(errors="replace")
+        raise OmHipError(f"{what} failed: {msg}")
+
+
+def call(name: str, *args) -> None:
+    """Calls a C ABI entry and raises OmHipError on a nonzero status."""
+    _check(getattr(lib(), name)(*args), name)
+
+
+def init(device: int = 0) -> None:
+    call("omHipInit", device)
+
+
+def synchronize() -> None:
+    call("omHipSynchronize")
+
+
+def device_count() -> int:
+    return int(lib().omHipGetDeviceCount())
+
+
+def device_name(device: int = 0) -> str:
+    buf = ctypes.create_string_buffer(256)
+    call("omHipGetDeviceName", device, buf, 256)
+    return buf.value.decode()
+
+
+def stream_handle() -> int:
+    s = _vp()
+    call("omHipGetStream", ctypes.byref(s))
+    return s.value or 0
+
+
+class DeviceBuffer:
+    """Device allocation from the library pool (omHipMalloc / omHipFree)."""
+
+    def __init__(self, nbytes: int, dtype=np.float32, shape=None):
+        self.nbytes = int(nbytes)
+        self.dtype = np.dtype(dtype)
+        self.shape = tuple(shape) if shape is not None else (self.nbytes // self.dtype.itemsize,)
+        p = _vp()
+        call("omHipMalloc", ctypes.byref(p), max(self.nbytes, 1))
+        self.ptr = int(p.value)
+
+    @classmethod
+    def empty(cls, shape, dtype=np.float32) -> "DeviceBuffer":
+        shape = tuple(int(s) for s in np.atleast_1d(shape)) if not isinstance(shape, tuple) else shape
+        n = int(np.prod(shape)) if len(shape) else 1
+        return cls(n * np.dtype(dtype).itemsize, dtype, shape)
+
+    @classmethod
+    def from_numpy(cls, a: np.ndarray) -> "DeviceBuffer":
+        a = np.ascontiguousarray(a)
+        b = cls(a.nbytes, a.dtype, a.shape)
+        if a.nbytes:
+            call("omHipCopyH2D", b.ptr, a.ctypes.data, a.nbytes)
+        return b
+
+    def upload(self, a: np.ndarray) -> None:
+        a = np.ascontiguousarray(a, dtype=self.dtype)
+        assert a.nbytes <= self.nbytes
+        if a.nbytes:
+            call("omHipCopyH2D", self.ptr, a.ctypes.data, a.nbytes)
+
+    def numpy(self, shape=None, dtype=None) -> np.ndarray:
+        dt = np.dtype(dtype) if dtype is not None else self.dtype
+        shp = tuple(shape) if shape is not None else self.shape
+        out = np.empty(shp, dt)
+        if out.nbytes:
+            call("omHipCopyD2H", out.ctypes.data, self.ptr, out.nbytes)
+        return out
+
+    def free(self) -> None:
+        if getattr(self, "ptr", 0) and _LIB is not None:
+            _LIB.omHipFree(self.ptr)
+        self.ptr = 0
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+    def __int__(self) -> int:
+        return self.ptr
+
+
+def _ptr(x) -> Optional[int]:
+    if x is None:
+        return None
+    return int(x)
+
+
+class HIPBackend:
+    """The HAL with CPUBackend names and argument order, on device pointers.
+
+    Method signatures follow src/hal/om.hal.cpu_backend.ixx (line numbers in
+    each docstring); entries the reference builds by composition (A x B^T,
+    fused conv+BN+ReLU, half-precision GEMM) are the extra methods at the end.
+    Every pointer argument is a device pointer (int or DeviceBuffer).
+    """
+
+    # ---- fills / copy (cpu_backend.ixx:65-77, :444-446) ----
+    @staticmethod
+    def fillZeros(pData, nCount: int) -> None:
+        call("omHipFillZeros", _ptr(pData), nCount)
+
+    @staticmethod
+    def fillOnes(pData, nCount: int) -> None:
+        call("omHipFillOnes", _ptr(pData), nCount)
+
+    @staticmethod
+    def fillValue(pData, nCount: int, fValue: float) -> None:
+        call("omHipFillValue", _ptr(pData), nCount, fValue)
+
+    @staticmethod
+    def copy(pSrc, pDst, nCount: int) -> None:
+        call("omHipCopy", _ptr(pSrc), _ptr(pDst), nCount)
+
+    # ---- GEMM (cpu_backend.ixx:239-286, :1520-1539) ----
+    @staticmethod
+    def matmul(pA, pB, pC, nM: int, nK: int, nN: int) -> None:
+        call("omHipMatmul", _ptr(pA), _ptr(pB), _ptr(pC), nM, nK, nN)
+
+    @staticmethod
+    def batchedMatmul(pA, pB, pC, nBatch: int, nM: int, nK: int, nN: int) -> None:
+        call("omHipBatchedMatmul", _ptr(pA), _ptr(pB), _ptr(pC), nBatch, nM, nK, nN)
+
+    @staticmethod
+    def transpose2d(pA, pB, nRows: int, nCols: int) -> None:
+        call("omHipTranspose", _ptr(pA), _ptr(pB), nRows, nCols)
+
+    # ---- activations / bias (cpu_backend.ixx:317-346, :433-440) ----
+    @staticmethod
+    def relu(pIn, pOut, nCount: int) -> None:
+        call("omHipReLU", _ptr(pIn), _ptr(pOut), nCount)
+
+    @staticmethod
+    def reluBackward(pIn, pGradOut, pGradIn, nCount: int) -> None:
+        call("omHipReLUBackward", _ptr(pIn), _ptr(pGradOut), _ptr(pGradIn), nCount)
+
+    @staticmethod
+    def addBias(pA, pBias, pOut, nBatch: int, nCols: int) -> None:
+        call("omHipAddBias", _ptr(pA), _ptr(pBias), _ptr(pOut), nBatch, nCols, 1)
+
+    # ---- conv / BN (cpu_backend.ixx:544-575, :619-658, :781-842) ----
+    @staticmethod
+    def im2col(pInput, nCin, nH, nW, nKH, nKW, nPadH, nPadW, nStrideH, nStrideW, pCol) -> None:
+        call("omHipIm2col", _ptr(pInput), nCin, nH, nW, nKH, nKW, nPadH, nPadW, nStrideH, nStrideW, _ptr(pCol))
+
+    @staticmethod
+    def conv2d(pInput, pWeight, pBias, pOutput, nBatch, nCin, nH, nW, nCout, nKH, nKW, nStride, nPad) -> None:
+        call("omHipConv2d", _ptr(pInput), _ptr(pWeight), _ptr(pBias), _ptr(pOutput),
+             nBatch, nCin, nH, nW, nCout, nKH, nKW, nStride, nPad)
+
+    @staticmethod
+    def batchNorm2d(pInput, pOutput, pGamma, pBeta, pRunMean, pRunVar, pSavedMean, pSavedInvStd,
+                    nBatch, nChannels, nH, nW, fEps, fMomentum, bTraining) -> None:
+        call("omHipBatchNorm2d", _ptr(pInput), _ptr(pOutput), _ptr(pGamma), _ptr(pBeta), _ptr(pRunMean),
+             _ptr(pRunVar), _ptr(pSavedMean), _ptr(pSavedInvStd), nBatch, nChannels, nH, nW, fEps, fMomentum,
+             1 if bTraining else 0)
+
+    # ---- entries the reference builds by composition ----
+    @staticmethod
+    def matmulTransB(pA, pB, pC, nM: int, nK: int, nN: int) -> None:
+        """C = A[M,K] x B[N,K]^T (reference: transpose2d + matmul, autograd.ixx:261-273)."""
+        call("omHipMatmulTransB", _ptr(pA), _ptr(pB), _ptr(pC), nM, nK, nN)
+
+    @staticmethod
+    def matmulTransA(pA, pB, pC, nM: int, nK: int, nN: int) -> None:
+        """C = A[K,M]^T x B[K,N] (reference: transpose2d + matmul, autograd.ixx:276-286)."""
+        call("omHipMatmulTransA", _ptr(pA), _ptr(pB), _ptr(pC), nM, nK, nN)
+
+    @staticmethod
+    def batchedMatmulTransB(pA, pB, pC, nBatch: int, nM: int, nK: int, nN: int) -> None:
+        call("omHipBatchedMatmulTransB", _ptr(pA), _ptr(pB), _ptr(pC), nBatch, nM, nK, nN)
+
+    @staticmethod
+    def conv2dIm2col(pInput, pWeight, pBias, pOutput, nBatch, nCin, nH, nW, nCout, nKH, nKW, nStride, nPad) -> None:
+        call("omHipConv2dIm2col", _ptr(pInput), _ptr(pWeight), _ptr(pBias), _ptr(pOutput),
+             nBatch, nCin, nH, nW, nCout, nKH, nKW, nStride, nPad)
+
+    @staticmethod
+    def conv2dBiasBnAct(pInput, pWeight, pBias, pGamma, pBeta, pMean, pVar, fEps, nAct, pOutput,
+                        nBatch, nCin, nH, nW, nCout, nKH, nKW, nStride, nPad) -> None:
+        """conv2d -> batchNorm2d(eval) -> relu in one kernel (tensor_ops.ixx:672-833, :511-536)."""
+        call("omHipConv2dBiasBnAct", _ptr(pInput), _ptr(pWeight), _ptr(pBias), _ptr(pGamma), _ptr(pBeta),
+             _ptr(pMean), _ptr(pVar), fEps, nAct, _ptr(pOutput), nBatch, nCin, nH, nW, nCout, nKH, nKW, nStride, nPad)
+
+    @staticmethod
+    def gemmStridedBatched(bTransA, bTransB, nBatch, nM, nN, nK, pA, nLda, nStrideA, pB, nLdb, nStrideB,
+                           pC, nLdc, nStrideC) -> None:
+        call("omHipGemmStridedBatched", int(bTransA), int(bTransB), nBatch, nM, nN, nK, _ptr(pA), nLda, nStrideA,
+             _ptr(pB), nLdb, nStrideB, _ptr(pC), nLdc, nStrideC)
+
+    @staticmethod
+    def convertToHalf(pIn, pOut, nCount: int, bf16: bool = False) -> None:
+        call("omHipConvertF32ToBF16" if bf16 else "omHipConvertF32ToF16", _ptr(pIn), _ptr(pOut), nCount)
+
+    @staticmethod
+    def convertFromHalf(pIn, pOut, nCount: int, bf16: bool = False) -> None:
+        call("omHipConvertBF16ToF32" if bf16 else "omHipConvertF16ToF32", _ptr(pIn), _ptr(pOut), nCount)
+
+    @staticmethod
+    def matmulHalf(pA, pB, pC, nM: int, nK: int, nN: int, bf16: bool = False, transB: bool = False) -> None:
+        name = {(False, False): "omHipMatmulF16", (True, False): "omHipMatmulBF16",
+                (False, True): "omHipMatmulTransBF16", (True, True): "omHipMatmulTransBBF16"}[(bf16, transB)]
+        call(name, _ptr(pA), _ptr(pB), _ptr(pC), nM, nK, nN)
+
+    @staticmethod
+    def gemmStridedBatchedHalf(nDtype, bTransA, bTransB, nBatch, nM, nN, nK, pA, nLda, nStrideA, pB, nLdb,
+                               nStrideB, pC, nLdc, nStrideC) -> None:
+        call("omHipGemmStridedBatchedHalf", nDtype, int(bTransA), int(bTransB), nBatch, nM, nN, nK, _ptr(pA), nLda,
+             nStrideA, _ptr(pB), nLdb, nStrideB, _ptr(pC), nLdc, nStrideC)

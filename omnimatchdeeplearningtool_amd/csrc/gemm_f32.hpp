@@ -1,0 +1,27 @@
+// gemm_f32.hpp — host-side interface of the fp32 MFMA GEMM shared by the GEMM
+// and conv entry points.
+#pragma once
+
+namespace omhip {
+
+struct GemmF32Params {
+    const float* A;
+    const float* B;
+    float* C;
+    int M, N, K;
+    long long lda, ldb, ldc;
+    long long sA, sB, sC;   // per-batch element offsets (0 shares the operand)
+    int tilesM, tilesN;
+};
+
+// C[b] = op(A[b]) * op(B[b]); ta: A stored [K,M]; tb: B stored [N,K].
+// Enqueues on the library stream; returns 0 or -1 (message via fail()).
+int gemmF32(bool ta, bool tb, int batch, int M, int N, int K,
+            const float* A, long long lda, long long sA,
+            const float* B, long long ldb, long long sB,
+            float* C, long long ldc, long long sC);
+
+// Zeroes C (batch x M x N, row stride ldc, batch stride sC) on the stream.
+int zeroOutput(float* C, int batch, int M, int N, long long ldc, long long sC);
+
+}  // namespace omhip

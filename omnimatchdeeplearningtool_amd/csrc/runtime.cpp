@@ -1,0 +1,281 @@
+// runtime.cpp — device bring-up, library stream, caching pool, copies.
+//
+// Mirrors the reference runtime (src/cuda/cuda_kernels.cu:63-158 streams,
+// :167-281 pool, :287-438 device management) with one library-owned
+// non-blocking stream: host copies are enqueued on that stream and then waited
+// for, so ordering with the kernels is explicit instead of relying on the
+// legacy default stream.
+#include "omhip_internal.hpp"
+#include "caching_pool.hpp"
+#include "../../include/omhip.h"
+
+#include <atomic>
+#include <cstdarg>
+#include <cstring>
+#include <memory>
+#include <mutex>
+
+namespace omhip {
+namespace {
+
+std::mutex g_initMutex;
+std::atomic<bool> g_inited{false};
+int g_device = 0;
+hipStream_t g_ownStream = nullptr;
+std::atomic<hipStream_t> g_userStream{nullptr};
+int g_cuCount = 0;
+int g_maxShared = 65536;
+std::unique_ptr<CachingPool> g_pool;
+std::mutex g_wsMutex;
+void* g_ws = nullptr;
+size_t g_wsBytes = 0;
+
+thread_local char t_err[512] = {0};
+
+int initLocked(int nDev) {
+    hipError_t e = hipSetDevice(nDev);
+    if (e != hipSuccess) return fail("hipSetDevice(%d): %s", nDev, hipGetErrorString(e));
+    (void)hipGetLastError();  // clear a stale error left by an earlier failure
+    e = hipStreamCreateWithFlags(&g_ownStream, hipStreamNonBlocking);
+    if (e != hipSuccess) return fail("hipStreamCreate: %s", hipGetErrorString(e));
+    hipDeviceProp_t prop;
+    e = hipGetDeviceProperties(&prop, nDev);
+    if (e != hipSuccess) return fail("hipGetDeviceProperties: %s", hipGetErrorString(e));
+    g_cuCount = prop.multiProcessorCount;
+    g_maxShared = static_cast<int>(prop.sharedMemPerBlock);
+    g_device = nDev;
+    g_pool = std::make_unique<CachingPool>(
+        [](size_t n) -> void* {
+            void* p = nullptr;
+            return hipMalloc(&p, n) == hipSuccess ? p : ((void)hipGetLastError(), nullptr);
+        },
+        [](void* p) { (void)hipFree(p); });
+    return 0;
+}
+
+int ensureInit(int nDev, bool bExplicit) {
+    if (g_inited.load(std::memory_order_acquire)) {
+        if (bExplicit && nDev != g_device) {
+            hipError_t e = hipSetDevice(nDev);
+            if (e != hipSuccess) return fail("hipSetDevice(%d): %s", nDev, hipGetErrorString(e));
+        }
+        return 0;
+    }
+    std::lock_guard<std::mutex> lock(g_initMutex);
+    if (g_inited.load(std::memory_order_relaxed)) return 0;
+    int rc = initLocked(nDev);
+    if (rc == 0) g_inited.store(true, std::memory_order_release);
+    return rc;
+}
+
+}  // namespace
+
+hipStream_t stream() {
+    hipStream_t s = g_userStream.load(std::memory_order_acquire);
+    if (s) return s;
+    if (!g_inited.load(std::memory_order_acquire)) ensureInit(0, false);
+    return g_ownStream;
+}
+
+int fail(const char* fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    std::vsnprintf(t_err, sizeof(t_err), fmt, ap);
+    va_end(ap);
+    return -1;
+}
+
+void clearError() { t_err[0] = 0; }
+
+int cuCount() {
+    if (!g_inited.load(std::memory_order_acquire)) ensureInit(0, false);
+    return g_cuCount > 0 ? g_cuCount : 256;
+}
+
+int maxSharedPerBlock() { return g_maxShared; }
+
+void* workspace(size_t bytes) {
+    std::lock_guard<std::mutex> lock(g_wsMutex);
+    if (bytes <= g_wsBytes) return g_ws;
+    if (!g_inited.load(std::memory_order_acquire) && ensureInit(0, false)) return nullptr;
+    if (g_ws) {
+        // the old buffer may still be read by enqueued kernels: wait before handing it back
+        (void)hipStreamSynchronize(stream());
+        g_pool->release(g_ws);
+        g_ws = nullptr;
+        g_wsBytes = 0;
+    }
+    void* p = g_pool->allocate(bytes);
+    if (!p) return nullptr;
+    g_ws = p;
+    g_wsBytes = bytes;
+    return g_ws;
+}
+
+}  // namespace omhip
+
+using namespace omhip;
+
+extern "C" {
+
+int omHipInit(int nDeviceId) {
+    clearError();
+    return ensureInit(nDeviceId, true);
+}
+
+int omHipGetDeviceCount(void) {
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess) {
+        (void)hipGetLastError();
+        return 0;
+    }
+    return n;
+}
+
+int omHipGetDeviceName(int nDeviceId, char* pNameBuf, int nBufSize) {
+    clearError();
+    if (!pNameBuf || nBufSize <= 0) return fail("omHipGetDeviceName: bad buffer");
+    hipDeviceProp_t prop;
+    OMHIP_CHECK(hipGetDeviceProperties(&prop, nDeviceId));
+    std::snprintf(pNameBuf, static_cast<size_t>(nBufSize), "%s (%s)", prop.name, prop.gcnArchName);
+    return 0;
+}
+
+int omHipGetMemInfo(int nDeviceId, size_t* pFreeMem, size_t* pTotalMem) {
+    clearError();
+    if (ensureInit(nDeviceId, true)) return -1;
+    size_t f = 0, t = 0;
+    OMHIP_CHECK(hipMemGetInfo(&f, &t));
+    if (pFreeMem) *pFreeMem = f;
+    if (pTotalMem) *pTotalMem = t;
+    return 0;
+}
+
+int omHipGetComputeCapability(int nDeviceId, int* pMajor, int* pMinor) {
+    clearError();
+    hipDeviceProp_t prop;
+    OMHIP_CHECK(hipGetDeviceProperties(&prop, nDeviceId));
+    if (pMajor) *pMajor = prop.major;
+    if (pMinor) *pMinor = prop.minor;
+    return 0;
+}
+
+int omHipSynchronize(void) {
+    clearError();
+    OMHIP_CHECK(hipStreamSynchronize(stream()));
+    return 0;
+}
+
+int omHipSyncComputeStream(void) { return omHipSynchronize(); }
+
+int omHipCleanup(void) {
+    clearError();
+    std::lock_guard<std::mutex> lock(g_initMutex);
+    if (!g_inited.load(std::memory_order_acquire)) return 0;
+    (void)hipStreamSynchronize(g_ownStream);
+    {
+        std::lock_guard<std::mutex> wsLock(g_wsMutex);
+        g_ws = nullptr;
+        g_wsBytes = 0;
+    }
+    if (g_pool) g_pool->clear();
+    g_pool.reset();
+    (void)hipStreamDestroy(g_ownStream);
+    g_ownStream = nullptr;
+    g_userStream.store(nullptr, std::memory_order_release);
+    g_inited.store(false, std::memory_order_release);
+    return 0;
+}
+
+int omHipGetStream(void** ppStream) {
+    clearError();
+    if (!ppStream) return fail("omHipGetStream: null output");
+    *ppStream = static_cast<void*>(stream());
+    return 0;
+}
+
+int omHipSetStream(void* pStream) {
+    clearError();
+    if (ensureInit(0, false)) return -1;
+    g_userStream.store(static_cast<hipStream_t>(pStream), std::memory_order_release);
+    return 0;
+}
+
+const char* omHipGetLastError(void) { return t_err; }
+
+int omHipMalloc(void** ppDevPtr, size_t nBytes) {
+    clearError();
+    if (!ppDevPtr) return fail("omHipMalloc: null output");
+    *ppDevPtr = nullptr;
+    if (ensureInit(0, false)) return -1;
+    void* p = g_pool->allocate(nBytes);
+    if (!p) return fail("omHipMalloc(%zu): out of device memory after flushing the pool", nBytes);
+    *ppDevPtr = p;
+    return 0;
+}
+
+int omHipFree(void* pDevPtr) {
+    clearError();
+    if (!pDevPtr) return 0;
+    if (!g_inited.load(std::memory_order_acquire) || !g_pool) {
+        OMHIP_CHECK(hipFree(pDevPtr));
+        return 0;
+    }
+    // Blocks are recycled by later allocations whose kernels are enqueued on the
+    // same stream, so stream order already protects a block still being read.
+    g_pool->release(pDevPtr);
+    return 0;
+}
+
+int omHipPoolStats(size_t* pHeldBytes, size_t* pUsedBytes) {
+    clearError();
+    if (pHeldBytes) *pHeldBytes = g_pool ? g_pool->heldBytes() : 0;
+    if (pUsedBytes) *pUsedBytes = g_pool ? g_pool->usedBytes() : 0;
+    return 0;
+}
+
+int omHipPoolTrim(void) {
+    clearError();
+    if (!g_pool) return 0;
+    OMHIP_CHECK(hipStreamSynchronize(stream()));
+    g_pool->trim();
+    return 0;
+}
+
+int omHipCopyH2D(void* pDst, const void* pSrc, size_t nBytes) {
+    clearError();
+    if (nBytes == 0) return 0;
+    if (!pDst || !pSrc) return fail("omHipCopyH2D: null pointer");
+    hipStream_t s = stream();
+    OMHIP_CHECK(hipMemcpyAsync(pDst, pSrc, nBytes, hipMemcpyHostToDevice, s));
+    OMHIP_CHECK(hipStreamSynchronize(s));
+    return 0;
+}
+
+int omHipCopyD2H(void* pDst, const void* pSrc, size_t nBytes) {
+    clearError();
+    if (nBytes == 0) return 0;
+    if (!pDst || !pSrc) return fail("omHipCopyD2H: null pointer");
+    hipStream_t s = stream();
+    OMHIP_CHECK(hipMemcpyAsync(pDst, pSrc, nBytes, hipMemcpyDeviceToHost, s));
+    OMHIP_CHECK(hipStreamSynchronize(s));
+    return 0;
+}
+
+int omHipCopyD2D(void* pDst, const void* pSrc, size_t nBytes) {
+    clearError();
+    if (nBytes == 0) return 0;
+    if (!pDst || !pSrc) return fail("omHipCopyD2D: null pointer");
+    OMHIP_CHECK(hipMemcpyAsync(pDst, pSrc, nBytes, hipMemcpyDeviceToDevice, stream()));
+    return 0;
+}
+
+int omHipMemset(void* pDev, int nValue, size_t nBytes) {
+    clearError();
+    if (nBytes == 0) return 0;
+    if (!pDev) return fail("omHipMemset: null pointer");
+    OMHIP_CHECK(hipMemsetAsync(pDev, nValue, nBytes, stream()));
+    return 0;
+}
+
+}  // extern "C"

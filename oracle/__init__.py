@@ -1,0 +1,424 @@
+"""The oracle: CPU restatement of the reference CPUBackend hot path.
+
+TEST INFRASTRUCTURE ONLY. Only ``tests/``, ``__graft_entry__.smoke()`` and the
+``cpu_baseline`` leg of ``bench.py`` import this package, and only as the
+checker (or the timed CPU baseline). The product library ``libomhip.so`` never
+links, loads or calls anything here.
+
+Contents
+--------
+``liboracle.so`` (``omref.cpp``)
+    C++ restatement of ``CPUBackend::matmul / batchedMatmul / transpose2d /
+    im2col / conv2d / batchNorm2d / relu / reluBackward / addBias`` and the
+    ``MatMulBackward`` composition (reference files
+    ``src/hal/om.hal.cpu_backend.ixx``, ``src/hal/om.hal.simd.ixx``,
+    ``src/engine/om.engine.autograd.ixx``; line numbers at each function).
+    Bit-identical to the reference CPUBackend compiled with clang.
+``_ref/libomref_reference.so`` (optional, built by ``oracle/Makefile`` from the
+    reference sources where they lie) — the reference CPUBackend itself.
+float64 checkers (this file)
+    ``gemm_f64`` / ``conv_f64`` return the float64 result together with the
+    error budget ``sum_k |a_ik| |b_kj|`` used by the K-scaled tolerance
+    ``|C - C64| <= tol * sum_k |a_ik||b_kj|`` (tol 1e-4 for fp32 inputs,
+    1e-2 for fp16/bf16 inputs against fp32 CPUBackend).
+
+Pinning (see tests/test_oracle_*.py): the restatement is checked bit-exactly
+against the reference's own known-answer tests
+(test_tensor_ops.cpp:55-82, test_phase5.cpp:206-222, test_nn.cpp:34-48),
+against golden vectors written by the compiled reference (tests/golden/),
+against ``_ref`` on fresh seeded inputs when it is built, and against float64
+brute force plus closed forms (identity, transpose identity, linearity,
+all-ones conv interior = sum of weights, BN closed form).
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from typing import Optional, Tuple
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB: Optional[ctypes.CDLL] = None
+_REF: Optional[ctypes.CDLL] = None
+_REF_TRIED = False
+
+_f = ctypes.POINTER(ctypes.c_float)
+_u16 = ctypes.POINTER(ctypes.c_uint16)
+_i = ctypes.c_int
+_sz = ctypes.c_size_t
+
+
+def lib_path() -> str:
+    return os.path.join(_HERE, "liboracle.so")
+
+
+def ref_path() -> str:
+    return os.path.join(_HERE, "_ref", "libomref_reference.so")
+
+
+def lib() -> ctypes.CDLL:
+    """The restatement (liboracle.so). Raises if it was not built."""
+    global _LIB
+    if _LIB is None:
+        p = lib_path()
+        if not os.path.exists(p):
+            raise RuntimeError(f"oracle library missing: {p} (run `make -C oracle`)")
+        L = ctypes.CDLL(p)
+        sig = {
+            "omrefMatmul": [_f, _f, _f, _i, _i, _i],
+            "omrefMatmulTransB": [_f, _f, _f, _i, _i, _i],
+            "omrefMatmulTransA": [_f, _f, _f, _i, _i, _i],
+            "omrefBatchedMatmul": [_f, _f, _f, _i, _i, _i, _i],
+            "omrefBatchedMatmulTransB": [_f, _f, _f, _i, _i, _i, _i],
+            "omrefTranspose2d": [_f, _f, _i, _i],
+            "omrefMatmulBackward": [_f, _f, _f, _f, _f, _i, _i, _i],
+            "omrefIm2col": [_f, _i, _i, _i, _i, _i, _i, _i, _i, _i, _f],
+            "omrefConv2d": [_f, _f, _f, _f] + [_i] * 9,
+            "omrefBatchNorm2d": [_f, _f, _f, _f, _f, _f, _f, _f, _i, _i, _i, _i,
+                                 ctypes.c_float, ctypes.c_float, _i],
+            "omrefRelu": [_f, _f, _sz],
+            "omrefReluBackward": [_f, _f, _f, _sz],
+            "omrefAddBias": [_f, _f, _f, _i, _i],
+            "omrefConvBnRelu": [_f, _f, _f, _f, _f, _f, _f, ctypes.c_float, _i, _f] + [_i] * 9,
+            "omrefFloatToHalfTruncN": [_f, _u16, _sz],
+            "omrefFillValue": [_f, _sz, ctypes.c_float],
+        }
+        for name, args in sig.items():
+            fn = getattr(L, name)
+            fn.argtypes = args
+            fn.restype = None
+        L.omrefHasAvx2.restype = ctypes.c_int
+        L.omrefMaxThreads.restype = ctypes.c_int
+        _LIB = L
+    return _LIB
+
+
+def ref_lib() -> Optional[ctypes.CDLL]:
+    """The compiled reference CPUBackend, or None when it was not built."""
+    global _REF, _REF_TRIED
+    if not _REF_TRIED:
+        _REF_TRIED = True
+        p = ref_path()
+        if os.path.exists(p):
+            R = ctypes.CDLL(p)
+            sig = {
+                "refMatmul": [_f, _f, _f, _i, _i, _i],
+                "refBatchedMatmul": [_f, _f, _f, _i, _i, _i, _i],
+                "refTranspose2d": [_f, _f, _i, _i],
+                "refIm2col": [_f, _i, _i, _i, _i, _i, _i, _i, _i, _i, _f],
+                "refConv2d": [_f, _f, _f, _f] + [_i] * 9,
+                "refBatchNorm2d": [_f, _f, _f, _f, _f, _f, _f, _f, _i, _i, _i, _i,
+                                   ctypes.c_float, ctypes.c_float, _i],
+                "refRelu": [_f, _f, _sz],
+                "refReluBackward": [_f, _f, _f, _sz],
+                "refAddBias": [_f, _f, _f, _i, _i],
+            }
+            for name, args in sig.items():
+                fn = getattr(R, name)
+                fn.argtypes = args
+                fn.restype = None
+            _REF = R
+    return _REF
+
+
+def _p(a: Optional[np.ndarray]):
+    if a is None:
+        return None
+    assert a.dtype == np.float32 and a.flags["C_CONTIGUOUS"], "oracle takes C-contiguous float32"
+    return a.ctypes.data_as(_f)
+
+
+def _f32(a) -> np.ndarray:
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+# ---------------------------------------------------------------------------
+# restatement wrappers (numpy in, numpy out)
+# ---------------------------------------------------------------------------
+
+def matmul(A, B, backend: str = "oracle") -> np.ndarray:
+    """CPUBackend::matmul (cpu_backend.ixx:239-286): C[M,N] = A[M,K] B[K,N]."""
+    A, B = _f32(A), _f32(B)
+    M, K = A.shape
+    K2, N = B.shape
+    assert K == K2
+    C = np.empty((M, N), np.float32)
+    if backend == "reference":
+        ref_lib().refMatmul(_p(A), _p(B), _p(C), M, K, N)
+    else:
+        lib().omrefMatmul(_p(A), _p(B), _p(C), M, K, N)
+    return C
+
+
+def matmul_transB(A, Bnk) -> np.ndarray:
+    """transpose2d(B) + matmul: A[M,K] x B[N,K]^T (autograd.ixx:261-273)."""
+    A, Bnk = _f32(A), _f32(Bnk)
+    M, K = A.shape
+    N = Bnk.shape[0]
+    C = np.empty((M, N), np.float32)
+    lib().omrefMatmulTransB(_p(A), _p(Bnk), _p(C), M, K, N)
+    return C
+
+
+def matmul_transA(Akm, B) -> np.ndarray:
+    """transpose2d(A) + matmul: A[K,M]^T x B[K,N] (autograd.ixx:276-286)."""
+    Akm, B = _f32(Akm), _f32(B)
+    K, M = Akm.shape
+    N = B.shape[1]
+    C = np.empty((M, N), np.float32)
+    lib().omrefMatmulTransA(_p(Akm), _p(B), _p(C), M, K, N)
+    return C
+
+
+def batched_matmul(A, B, backend: str = "oracle") -> np.ndarray:
+    """CPUBackend::batchedMatmul (cpu_backend.ixx:1520-1532)."""
+    A, B = _f32(A), _f32(B)
+    b, M, K = A.shape
+    N = B.shape[2]
+    C = np.empty((b, M, N), np.float32)
+    if backend == "reference":
+        ref_lib().refBatchedMatmul(_p(A), _p(B), _p(C), b, M, K, N)
+    else:
+        lib().omrefBatchedMatmul(_p(A), _p(B), _p(C), b, M, K, N)
+    return C
+
+
+def batched_matmul_transB(A, Bnk) -> np.ndarray:
+    A, Bnk = _f32(A), _f32(Bnk)
+    b, M, K = A.shape
+    N = Bnk.shape[1]
+    C = np.empty((b, M, N), np.float32)
+    lib().omrefBatchedMatmulTransB(_p(A), _p(Bnk), _p(C), b, M, K, N)
+    return C
+
+
+def transpose2d(A, backend: str = "oracle") -> np.ndarray:
+    A = _f32(A)
+    r, c = A.shape
+    out = np.empty((c, r), np.float32)
+    (ref_lib().refTranspose2d if backend == "reference" else lib().omrefTranspose2d)(_p(A), _p(out), r, c)
+    return out
+
+
+def matmul_backward(G, A, B) -> Tuple[np.ndarray, np.ndarray]:
+    """MatMulBackward::backward (autograd.ixx:226-290): (dA, dB)."""
+    G, A, B = _f32(G), _f32(A), _f32(B)
+    M, K = A.shape
+    N = B.shape[1]
+    dA = np.empty((M, K), np.float32)
+    dB = np.empty((K, N), np.float32)
+    lib().omrefMatmulBackward(_p(G), _p(A), _p(B), _p(dA), _p(dB), M, K, N)
+    return dA, dB
+
+
+def out_hw(H, W, KH, KW, stride, pad):
+    return (H + 2 * pad - KH) // stride + 1, (W + 2 * pad - KW) // stride + 1
+
+
+def im2col(x, KH, KW, pad, stride, backend: str = "oracle") -> np.ndarray:
+    """CPUBackend::im2col (cpu_backend.ixx:544-575) of one image x[Cin,H,W]."""
+    x = _f32(x)
+    Cin, H, W = x.shape
+    Ho, Wo = out_hw(H, W, KH, KW, stride, pad)
+    col = np.empty((Cin * KH * KW, Ho * Wo), np.float32)
+    fn = ref_lib().refIm2col if backend == "reference" else lib().omrefIm2col
+    fn(_p(x), Cin, H, W, KH, KW, pad, pad, stride, stride, _p(col))
+    return col
+
+
+def conv2d(x, w, bias=None, stride=1, pad=0, backend: str = "oracle") -> np.ndarray:
+    """CPUBackend::conv2d (cpu_backend.ixx:619-658), NCHW."""
+    x, w = _f32(x), _f32(w)
+    N, Cin, H, W = x.shape
+    Cout, Cin2, KH, KW = w.shape
+    assert Cin == Cin2
+    Ho, Wo = out_hw(H, W, KH, KW, stride, pad)
+    out = np.empty((N, Cout, Ho, Wo), np.float32)
+    b = _f32(bias) if bias is not None else None
+    fn = ref_lib().refConv2d if backend == "reference" else lib().omrefConv2d
+    fn(_p(x), _p(w), _p(b), _p(out), N, Cin, H, W, Cout, KH, KW, stride, pad)
+    return out
+
+
+def batchnorm2d_eval(x, gamma, beta, mean, var, eps=1e-5, backend: str = "oracle"):
+    """CPUBackend::batchNorm2d with bTraining=false (cpu_backend.ixx:781-842).
+
+    Returns (y, savedMean, savedInvStd)."""
+    x = _f32(x)
+    N, C, H, W = x.shape
+    y = np.empty_like(x)
+    rm, rv = _f32(mean).copy(), _f32(var).copy()
+    sm = np.empty(C, np.float32)
+    si = np.empty(C, np.float32)
+    fn = ref_lib().refBatchNorm2d if backend == "reference" else lib().omrefBatchNorm2d
+    fn(_p(x), _p(y), _p(_f32(gamma)), _p(_f32(beta)), _p(rm), _p(rv), _p(sm), _p(si), N, C, H, W,
+       ctypes.c_float(eps), ctypes.c_float(0.1), 0)
+    return y, sm, si
+
+
+def batchnorm2d_train(x, gamma, beta, run_mean, run_var, eps=1e-5, momentum=0.1, backend: str = "oracle"):
+    """Training branch (cpu_backend.ixx:796-822): returns (y, runMean', runVar', savedMean, savedInvStd)."""
+    x = _f32(x)
+    N, C, H, W = x.shape
+    y = np.empty_like(x)
+    rm, rv = _f32(run_mean).copy(), _f32(run_var).copy()
+    sm = np.empty(C, np.float32)
+    si = np.empty(C, np.float32)
+    fn = ref_lib().refBatchNorm2d if backend == "reference" else lib().omrefBatchNorm2d
+    fn(_p(x), _p(y), _p(_f32(gamma)), _p(_f32(beta)), _p(rm), _p(rv), _p(sm), _p(si), N, C, H, W,
+       ctypes.c_float(eps), ctypes.c_float(momentum), 1)
+    return y, rm, rv, sm, si
+
+
+def relu(x, backend: str = "oracle") -> np.ndarray:
+    x = _f32(x)
+    y = np.empty_like(x)
+    (ref_lib().refRelu if backend == "reference" else lib().omrefRelu)(_p(x), _p(y), x.size)
+    return y
+
+
+def relu_backward(x, g, backend: str = "oracle") -> np.ndarray:
+    x, g = _f32(x), _f32(g)
+    gi = np.empty_like(x)
+    (ref_lib().refReluBackward if backend == "reference" else lib().omrefReluBackward)(_p(x), _p(g), _p(gi), x.size)
+    return gi
+
+
+def add_bias(A, bias, backend: str = "oracle") -> np.ndarray:
+    """CPUBackend::addBias (cpu_backend.ixx:433-440): out[b,j] = A[b,j] + bias[j]."""
+    A, bias = _f32(A), _f32(bias)
+    b, c = A.shape
+    out = np.empty_like(A)
+    (ref_lib().refAddBias if backend == "reference" else lib().omrefAddBias)(_p(A), _p(bias), _p(out), b, c)
+    return out
+
+
+def conv_bn_act(x, w, bias, gamma, beta, mean, var, eps=1e-5, act=1, stride=1, pad=0) -> np.ndarray:
+    """conv2d -> batchNorm2d(eval) -> relu: the unfused reference chain."""
+    x, w = _f32(x), _f32(w)
+    N, Cin, H, W = x.shape
+    Cout, _, KH, KW = w.shape
+    Ho, Wo = out_hw(H, W, KH, KW, stride, pad)
+    out = np.empty((N, Cout, Ho, Wo), np.float32)
+    b = _f32(bias) if bias is not None else None
+    g = _f32(gamma) if gamma is not None else None
+    bt = _f32(beta) if beta is not None else None
+    m = _f32(mean) if mean is not None else None
+    v = _f32(var) if var is not None else None
+    lib().omrefConvBnRelu(_p(x), _p(w), _p(b), _p(g), _p(bt), _p(m), _p(v), ctypes.c_float(eps), act, _p(out),
+                          N, Cin, H, W, Cout, KH, KW, stride, pad)
+    return out
+
+
+def float_to_half_trunc(x) -> np.ndarray:
+    """FP16Converter::floatToHalf (fp16.ixx:36-100): truncating fp32 -> fp16 bits."""
+    x = _f32(x)
+    out = np.empty(x.shape, np.uint16)
+    lib().omrefFloatToHalfTruncN(_p(x), out.ctypes.data_as(_u16), x.size)
+    return out
+
+
+# ---------------------------------------------------------------------------
+# float64 checkers and the K-scaled tolerance
+# ---------------------------------------------------------------------------
+
+def gemm_f64(A, B, transA=False, transB=False) -> Tuple[np.ndarray, np.ndarray]:
+    """float64 C = op(A) op(B) and the error budget |op(A)| |op(B)|."""
+    A64 = np.asarray(A, np.float64)
+    B64 = np.asarray(B, np.float64)
+    if transA:
+        A64 = np.swapaxes(A64, -1, -2)
+    if transB:
+        B64 = np.swapaxes(B64, -1, -2)
+    return A64 @ B64, np.abs(A64) @ np.abs(B64)
+
+
+def _im2col64(x64, KH, KW, stride, pad):
+    N, C, H, W = x64.shape
+    Ho, Wo = out_hw(H, W, KH, KW, stride, pad)
+    xp = np.zeros((N, C, H + 2 * pad, W + 2 * pad), np.float64)
+    xp[:, :, pad:pad + H, pad:pad + W] = x64
+    cols = np.empty((N, C, KH, KW, Ho, Wo), np.float64)
+    for kh in range(KH):
+        for kw in range(KW):
+            cols[:, :, kh, kw] = xp[:, :, kh:kh + stride * (Ho - 1) + 1:stride, kw:kw + stride * (Wo - 1) + 1:stride]
+    return cols.reshape(N, C * KH * KW, Ho * Wo), Ho, Wo
+
+
+def conv_f64(x, w, bias=None, stride=1, pad=0, gamma=None, beta=None, mean=None, var=None, eps=1e-5, act=0):
+    """float64 direct convolution (+ bias, BN eval, ReLU) and its error budget.
+
+    The budget is conv(|x|,|w|) scaled by |gamma|*invStd when BN is applied;
+    ReLU does not enlarge it (|relu(a)-relu(b)| <= |a-b|)."""
+    x64 = np.asarray(x, np.float64)
+    w64 = np.asarray(w, np.float64)
+    N = x64.shape[0]
+    Cout, Cin, KH, KW = w64.shape
+    cols, Ho, Wo = _im2col64(x64, KH, KW, stride, pad)
+    wm = w64.reshape(Cout, -1)
+    out = np.matmul(wm[None], cols).reshape(N, Cout, Ho, Wo)
+    bound = np.matmul(np.abs(wm)[None], np.abs(cols)).reshape(N, Cout, Ho, Wo)
+    if bias is not None:
+        b = np.asarray(bias, np.float64)[None, :, None, None]
+        out = out + b
+        bound = bound + np.abs(b)
+    if gamma is not None:
+        g = np.asarray(gamma, np.float64)[None, :, None, None]
+        bt = np.asarray(beta, np.float64)[None, :, None, None]
+        m = np.asarray(mean, np.float64)[None, :, None, None]
+        inv = 1.0 / np.sqrt(np.asarray(var, np.float64) + eps)[None, :, None, None]
+        out = g * (out - m) * inv + bt
+        bound = (bound + np.abs(m)) * np.abs(g) * inv + np.abs(bt)
+    if act == 1:
+        out = np.maximum(out, 0.0)
+    return out, bound
+
+
+def normalized_error(C, C64, bound) -> float:
+    """max |C - C64| / max(bound, tiny): the K-scaled error measure."""
+    C = np.asarray(C, np.float64)
+    d = np.abs(C - C64)
+    den = np.maximum(bound, np.finfo(np.float64).tiny)
+    return float(np.max(d / den)) if d.size else 0.0
+
+
+def frobenius_rel(C, Cref) -> float:
+    C = np.asarray(C, np.float64)
+    R = np.asarray(Cref, np.float64)
+    n = np.linalg.norm(R)
+    return float(np.linalg.norm(C - R) / n) if n > 0 else float(np.linalg.norm(C))
+
+
+# Tolerances (north star): fp32 inputs 1e-4; fp16/bf16 inputs with fp32 accumulate 1e-2.
+TOL_FP32 = 1e-4
+TOL_HALF = 1e-2
+
+
+# ---------------------------------------------------------------------------
+# seeded data
+# ---------------------------------------------------------------------------
+
+def rng(seed: int) -> np.random.Generator:
+    return np.random.Generator(np.random.PCG64(seed))
+
+
+def randn(shape, seed: int, scale: float = 1.0) -> np.ndarray:
+    return (rng(seed).standard_normal(shape, dtype=np.float32) * np.float32(scale)).astype(np.float32)
+
+
+def uniform(shape, seed: int, lo: float = 0.0, hi: float = 1.0) -> np.ndarray:
+    return rng(seed).uniform(lo, hi, size=shape).astype(np.float32)
+
+
+def bf16_round(x) -> np.ndarray:
+    """fp32 -> bf16 -> fp32 with round-to-nearest-even (NaN kept quiet)."""
+    u = np.ascontiguousarray(x, np.float32).view(np.uint32).astype(np.uint64)
+    r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint32)
+    nan = (u & 0x7FFFFFFF) > 0x7F800000
+    r = np.where(nan, ((u >> 16) | 0x40).astype(np.uint32), r)
+    return (r.astype(np.uint32) << 16).view(np.float32)
+
+
+def bf16_bits(x) -> np.ndarray:
+    return (bf16_round(x).view(np.uint32) >> 16).astype(np.uint16)

@@ -1,0 +1,295 @@
+// omref.cpp — the ORACLE: a CPU restatement of the reference CPUBackend hot
+// path (rhine311014/OmniMatchDeeplearningTool, src/hal/om.hal.cpu_backend.ixx
+// and src/hal/om.hal.simd.ixx). Test infrastructure only: the parity tests,
+// the smoke check and the bench's CPU baseline leg load it as the checker;
+// libomhip never links or calls it.
+//
+// Every function follows the cited reference lines, including evaluation
+// order, so its results are bit-identical to the reference CPUBackend built
+// with clang (-O3 -mavx2 -mfma, which contracts a*b+c into one fma):
+//   - matmul: each C[i][j] is the fma chain acc = fma(A[i][k], B[k][j], acc)
+//     over k = 0..K-1 from acc = 0 — the 4x8 AVX2 tile (simd.ixx:102-124), the
+//     1x8 row remainder (:135-144) and the contracted scalar column remainder
+//     (:149-157) all evaluate that chain; the AVX2 restatement below keeps the
+//     4x8 register tile and the OpenMP 4-row blocking (cpu_backend.ixx:256-265)
+//     so it is also a fair timing of the reference path;
+//   - conv2d: per image im2col -> matmul -> separate bias add (:619-658);
+//   - batchNorm2d: invStd = 1/sqrt(var+eps) in fp32, y = fma(gamma, (x-mean)*invStd, beta)
+//     (:781-842);
+//   - relu: x > 0 ? x : 0 (:317-332, simd.ixx:248-274).
+// Each extern "C" entry below names its reference lines.
+#include <cmath>
+#include <cstddef>
+#include <cstdint>
+#include <cstring>
+#include <vector>
+#include <algorithm>
+#include <omp.h>
+#if defined(__AVX2__) && defined(__FMA__)
+#include <immintrin.h>
+#define OMREF_AVX2 1
+#endif
+
+namespace {
+
+// simd.ixx:72-170 — C[M,N] = A[M,K] B[K,N]; C zeroed first (simd.ixx:81).
+void matmulTile(const float* A, const float* B, float* C, int M, int K, int N) {
+    std::memset(C, 0, sizeof(float) * (size_t)M * N);
+#ifdef OMREF_AVX2
+    const int N8 = N & ~7, M4 = M & ~3;
+    for (int j = 0; j < N8; j += 8) {
+        for (int i = 0; i < M4; i += 4) {
+            __m256 s0 = _mm256_setzero_ps(), s1 = _mm256_setzero_ps();
+            __m256 s2 = _mm256_setzero_ps(), s3 = _mm256_setzero_ps();
+            for (int k = 0; k < K; ++k) {
+                const __m256 b = _mm256_loadu_ps(B + (size_t)k * N + j);
+                s0 = _mm256_fmadd_ps(_mm256_set1_ps(A[(size_t)(i + 0) * K + k]), b, s0);
+                s1 = _mm256_fmadd_ps(_mm256_set1_ps(A[(size_t)(i + 1) * K + k]), b, s1);
+                s2 = _mm256_fmadd_ps(_mm256_set1_ps(A[(size_t)(i + 2) * K + k]), b, s2);
+                s3 = _mm256_fmadd_ps(_mm256_set1_ps(A[(size_t)(i + 3) * K + k]), b, s3);
+            }
+            _mm256_storeu_ps(C + (size_t)(i + 0) * N + j, s0);
+            _mm256_storeu_ps(C + (size_t)(i + 1) * N + j, s1);
+            _mm256_storeu_ps(C + (size_t)(i + 2) * N + j, s2);
+            _mm256_storeu_ps(C + (size_t)(i + 3) * N + j, s3);
+        }
+        for (int i = M4; i < M; ++i) {
+            __m256 s = _mm256_setzero_ps();
+            for (int k = 0; k < K; ++k)
+                s = _mm256_fmadd_ps(_mm256_set1_ps(A[(size_t)i * K + k]), _mm256_loadu_ps(B + (size_t)k * N + j), s);
+            _mm256_storeu_ps(C + (size_t)i * N + j, s);
+        }
+    }
+    for (int i = 0; i < M; ++i)
+        for (int j = N8; j < N; ++j) {
+            float v = 0.f;
+            for (int k = 0; k < K; ++k) v = std::fma(A[(size_t)i * K + k], B[(size_t)k * N + j], v);
+            C[(size_t)i * N + j] = v;
+        }
+#else
+    // Same per-element fma chain without vector registers.
+    for (int i = 0; i < M; ++i)
+        for (int j = 0; j < N; ++j) {
+            float v = 0.f;
+            for (int k = 0; k < K; ++k) v = std::fma(A[(size_t)i * K + k], B[(size_t)k * N + j], v);
+            C[(size_t)i * N + j] = v;
+        }
+#endif
+}
+
+}  // namespace
+
+extern "C" {
+
+// cpu_backend.ixx:65-77
+void omrefFillValue(float* p, size_t n, float v) { for (size_t i = 0; i < n; ++i) p[i] = v; }
+
+// cpu_backend.ixx:239-286: null pointers or non-positive dims zero C (246-251);
+// M >= 4 -> OpenMP over 4-row blocks, each a 4-row matmulAVX2 (256-265); M < 4 -> one call (269).
+void omrefMatmul(const float* A, const float* B, float* C, int M, int K, int N) {
+    if (!A || !B || !C || M <= 0 || K <= 0 || N <= 0) {
+        if (C && M > 0 && N > 0) std::memset(C, 0, sizeof(float) * (size_t)M * N);
+        return;
+    }
+    if (M >= 4) {
+#pragma omp parallel for schedule(dynamic, 1)
+        for (int b = 0; b < M; b += 4) {
+            const int rows = std::min(4, M - b);
+            matmulTile(A + (size_t)b * K, B, C + (size_t)b * N, rows, K, N);
+        }
+        return;
+    }
+    matmulTile(A, B, C, M, K, N);
+}
+
+// cpu_backend.ixx:1535-1539
+void omrefTranspose2d(const float* A, float* B, int rows, int cols) {
+    for (int r = 0; r < rows; ++r)
+        for (int c = 0; c < cols; ++c) B[(size_t)c * rows + r] = A[(size_t)r * cols + c];
+}
+
+// cpu_backend.ixx:1520-1532 (the batch loop; the per-batch results do not
+// depend on the OpenMP clause, which only changes which thread runs a batch)
+void omrefBatchedMatmul(const float* A, const float* B, float* C, int batch, int M, int K, int N) {
+    for (int b = 0; b < batch; ++b)
+        omrefMatmul(A + (size_t)b * M * K, B + (size_t)b * K * N, C + (size_t)b * M * N, M, K, N);
+}
+
+// transpose2d + matmul: the composition the reference uses for A x B^T
+// (autograd.ixx:261-273; vit.ixx:175-176 via tensorTranspose2dBatched).
+void omrefMatmulTransB(const float* A, const float* Bnk, float* C, int M, int K, int N) {
+    std::vector<float> bt((size_t)K * N);
+    omrefTranspose2d(Bnk, bt.data(), N, K);
+    omrefMatmul(A, bt.data(), C, M, K, N);
+}
+
+// transpose2d + matmul for A^T x B (autograd.ixx:276-286).
+void omrefMatmulTransA(const float* Akm, const float* B, float* C, int M, int K, int N) {
+    std::vector<float> at((size_t)M * K);
+    omrefTranspose2d(Akm, at.data(), K, M);
+    omrefMatmul(at.data(), B, C, M, K, N);
+}
+
+void omrefBatchedMatmulTransB(const float* A, const float* B, float* C, int batch, int M, int K, int N) {
+    for (int b = 0; b < batch; ++b)
+        omrefMatmulTransB(A + (size_t)b * M * K, B + (size_t)b * N * K, C + (size_t)b * M * N, M, K, N);
+}
+
+// MatMulBackward::backward (autograd.ixx:226-290): dA = G[M,N] x B^T, dB = A^T x G,
+// each an explicit transpose followed by matmul (both always computed).
+void omrefMatmulBackward(const float* G, const float* A, const float* B, float* dA, float* dB, int M, int K, int N) {
+    std::vector<float> bt((size_t)N * K), at((size_t)K * M);
+    for (int i = 0; i < K; ++i)
+        for (int j = 0; j < N; ++j) bt[(size_t)j * K + i] = B[(size_t)i * N + j];
+    omrefMatmul(G, bt.data(), dA, M, N, K);
+    for (int i = 0; i < M; ++i)
+        for (int j = 0; j < K; ++j) at[(size_t)j * M + i] = A[(size_t)i * K + j];
+    omrefMatmul(at.data(), G, dB, K, M, N);
+}
+
+// cpu_backend.ixx:544-575
+void omrefIm2col(const float* x, int Cin, int H, int W, int KH, int KW, int ph, int pw, int sh, int sw, float* col) {
+    const int Ho = (H + 2 * ph - KH) / sh + 1, Wo = (W + 2 * pw - KW) / sw + 1;
+    const int cols = Ho * Wo;
+    for (int c = 0; c < Cin; ++c)
+        for (int kh = 0; kh < KH; ++kh)
+            for (int kw = 0; kw < KW; ++kw) {
+                const int row = (c * KH + kh) * KW + kw;
+                for (int oh = 0; oh < Ho; ++oh)
+                    for (int ow = 0; ow < Wo; ++ow) {
+                        const int ih = oh * sh - ph + kh, iw = ow * sw - pw + kw;
+                        col[(size_t)row * cols + oh * Wo + ow] =
+                            (ih >= 0 && ih < H && iw >= 0 && iw < W) ? x[((size_t)c * H + ih) * W + iw] : 0.f;
+                    }
+            }
+}
+
+// cpu_backend.ixx:619-658: per image im2col -> matmul(W[Cout,K], col) -> bias add.
+void omrefConv2d(const float* x, const float* w, const float* bias, float* out, int N, int Cin, int H, int W,
+                 int Cout, int KH, int KW, int stride, int pad) {
+    const int Ho = (H + 2 * pad - KH) / stride + 1, Wo = (W + 2 * pad - KW) / stride + 1;
+    const int rows = Cin * KH * KW, cols = Ho * Wo;
+    std::vector<float> col((size_t)rows * cols);
+    for (int n = 0; n < N; ++n) {
+        omrefIm2col(x + (size_t)n * Cin * H * W, Cin, H, W, KH, KW, pad, pad, stride, stride, col.data());
+        float* o = out + (size_t)n * Cout * cols;
+        omrefMatmul(w, col.data(), o, Cout, rows, cols);
+        if (bias)
+            for (int c = 0; c < Cout; ++c)
+                for (int i = 0; i < cols; ++i) o[(size_t)c * cols + i] += bias[c];
+    }
+}
+
+// cpu_backend.ixx:781-842 (training 796-822, eval 823-830, normalize 832-840).
+void omrefBatchNorm2d(const float* x, float* y, const float* gamma, const float* beta, float* runMean, float* runVar,
+                      float* savedMean, float* savedInvStd, int N, int C, int H, int W, float eps, float momentum,
+                      int training) {
+    const int S = H * W;
+    const int cnt = N * S;
+#pragma omp parallel for schedule(static)
+    for (int c = 0; c < C; ++c) {
+        float mean = 0.f, var = 0.f;
+        if (training) {
+            for (int n = 0; n < N; ++n)
+                for (int s = 0; s < S; ++s) mean += x[((size_t)n * C + c) * S + s];
+            mean /= (float)cnt;
+            for (int n = 0; n < N; ++n)
+                for (int s = 0; s < S; ++s) {
+                    const float d = x[((size_t)n * C + c) * S + s] - mean;
+                    var = std::fma(d, d, var);
+                }
+            var /= (float)cnt;
+            if (savedMean) savedMean[c] = mean;
+            if (savedInvStd) savedInvStd[c] = 1.0f / std::sqrt(var + eps);
+            runMean[c] = std::fma(1.0f - momentum, runMean[c], momentum * mean);
+            runVar[c] = std::fma(1.0f - momentum, runVar[c], momentum * var);
+        } else {
+            mean = runMean[c];
+            var = runVar[c];
+            if (savedMean) savedMean[c] = mean;
+            if (savedInvStd) savedInvStd[c] = 1.0f / std::sqrt(var + eps);
+        }
+        const float inv = 1.0f / std::sqrt(var + eps);
+        for (int n = 0; n < N; ++n)
+            for (int s = 0; s < S; ++s) {
+                const size_t i = ((size_t)n * C + c) * S + s;
+                y[i] = std::fma(gamma[c], (x[i] - mean) * inv, beta[c]);
+            }
+    }
+}
+
+// cpu_backend.ixx:317-332 / simd.ixx:248-274
+void omrefRelu(const float* x, float* y, size_t n) {
+    for (size_t i = 0; i < n; ++i) y[i] = x[i] > 0.f ? x[i] : 0.f;
+}
+
+// cpu_backend.ixx:337-346
+void omrefReluBackward(const float* x, const float* g, float* gi, size_t n) {
+    for (size_t i = 0; i < n; ++i) gi[i] = x[i] > 0.f ? g[i] : 0.f;
+}
+
+// cpu_backend.ixx:433-440 (row broadcast)
+void omrefAddBias(const float* A, const float* bias, float* out, int batch, int cols) {
+    for (int b = 0; b < batch; ++b)
+        for (int j = 0; j < cols; ++j) out[(size_t)b * cols + j] = A[(size_t)b * cols + j] + bias[j];
+}
+
+// conv2d -> batchNorm2d(eval) -> relu: the reference 3-call chain that the
+// fused entry replaces (tensor_ops.ixx:672-833, :511-536).
+void omrefConvBnRelu(const float* x, const float* w, const float* bias, const float* gamma, const float* beta,
+                     const float* mean, const float* var, float eps, int act, float* out, int N, int Cin, int H,
+                     int W, int Cout, int KH, int KW, int stride, int pad) {
+    const int Ho = (H + 2 * pad - KH) / stride + 1, Wo = (W + 2 * pad - KW) / stride + 1;
+    const size_t n = (size_t)N * Cout * Ho * Wo;
+    std::vector<float> t(n);
+    omrefConv2d(x, w, bias, t.data(), N, Cin, H, W, Cout, KH, KW, stride, pad);
+    if (gamma) {
+        std::vector<float> m(mean, mean + Cout), v(var, var + Cout);
+        omrefBatchNorm2d(t.data(), t.data(), gamma, beta, m.data(), v.data(), nullptr, nullptr, N, Cout, Ho, Wo, eps,
+                         0.1f, 0);
+    }
+    if (act == 1) omrefRelu(t.data(), out, n);
+    else std::memcpy(out, t.data(), n * sizeof(float));
+}
+
+// FP16Converter::floatToHalf (src/engine/om.engine.fp16.ixx:36-100): the
+// reference's software converter TRUNCATES the mantissa (>>13) and flushes
+// fp32 subnormals to signed zero. Restated for documentation of the rounding
+// difference; the GPU path converts with round-to-nearest-even instead.
+uint16_t omrefFloatToHalfTrunc(float f) {
+    uint32_t b;
+    std::memcpy(&b, &f, 4);
+    const uint32_t sign = (b >> 31) & 1u, ex = (b >> 23) & 0xffu, man = b & 0x7fffffu;
+    uint16_t he = 0, hm = 0;
+    const int ne = (int)ex - 127 + 15;
+    if (ex == 0xff) {
+        he = 0x1f;
+        if (man) { hm = (uint16_t)(man >> 13); if (!hm) hm = 1; }
+    } else if (ex == 0) {
+        he = 0; hm = 0;
+    } else if (ne >= 0x1f) {
+        he = 0x1f; hm = 0;
+    } else if (ne <= 0) {
+        if (ne >= -10) hm = (uint16_t)((man | 0x800000u) >> (14 - ne));
+    } else {
+        he = (uint16_t)ne;
+        hm = (uint16_t)(man >> 13);
+    }
+    return (uint16_t)((sign << 15) | (he << 10) | hm);
+}
+
+void omrefFloatToHalfTruncN(const float* in, uint16_t* out, size_t n) {
+    for (size_t i = 0; i < n; ++i) out[i] = omrefFloatToHalfTrunc(in[i]);
+}
+
+int omrefHasAvx2(void) {
+#ifdef OMREF_AVX2
+    return __builtin_cpu_supports("avx2") && __builtin_cpu_supports("fma");
+#else
+    return 0;
+#endif
+}
+
+int omrefMaxThreads(void) { return omp_get_max_threads(); }
+
+}  // extern "C"

@@ -1,0 +1,139 @@
+// test_hip_backend.cpp — C++23 caller of om::HIPBackend (the drop-in HAL
+// class), written like the reference's own GTest cases. Needs a GPU; run by
+// tests/test_gpu_cpp_backend.py. Exit status 0 = every check passed.
+//
+// Known answers are the reference's: Matmul2D / MatmulNonSquare
+// (tests/test_tensor_ops.cpp:55-82), BatchedMatmulForward
+// (tests/test_phase5.cpp:206-222), LinearWithBias zero input
+// (tests/test_nn.cpp:34-48), Conv2dForward shapes on all-ones input
+// (tests/test_conv.cpp:21-49; interior value = sum of weights).
+#include <cmath>
+#include <cstdio>
+#include <stdexcept>
+#include <vector>
+
+#include "omhip_backend.hpp"
+
+using om::HIPBackend;
+
+static int g_fail = 0;
+#define EXPECT_NEAR(a, b, tol)                                                                            \
+    do {                                                                                                  \
+        const double a_ = (a), b_ = (b);                                                                  \
+        if (!(std::fabs(a_ - b_) <= (tol))) {                                                             \
+            std::printf("FAIL %s:%d: %s = %.9g, expected %.9g\n", __FILE__, __LINE__, #a, a_, b_);        \
+            ++g_fail;                                                                                     \
+        }                                                                                                 \
+    } while (0)
+
+struct Dev {
+    float* p = nullptr;
+    size_t n = 0;
+    explicit Dev(size_t count) : n(count) { p = static_cast<float*>(HIPBackend::malloc(count * sizeof(float))); }
+    Dev(const std::vector<float>& h) : Dev(h.size()) { HIPBackend::copyH2D(p, h.data(), h.size() * sizeof(float)); }
+    ~Dev() { HIPBackend::free(p); }
+    std::vector<float> host() const {
+        std::vector<float> h(n);
+        HIPBackend::copyD2H(h.data(), p, n * sizeof(float));
+        return h;
+    }
+};
+
+static void testMatmul2D() {
+    Dev a(std::vector<float>{1, 2, 3, 4}), b(std::vector<float>{5, 6, 7, 8}), c(4);
+    HIPBackend::matmul(a.p, b.p, c.p, 2, 2, 2);
+    auto h = c.host();
+    EXPECT_NEAR(h[0], 19, 0); EXPECT_NEAR(h[1], 22, 0); EXPECT_NEAR(h[2], 43, 0); EXPECT_NEAR(h[3], 50, 0);
+    std::printf("Matmul2D done\n");
+}
+
+static void testMatmulNonSquare() {
+    Dev a(std::vector<float>{1, 2, 3, 4, 5, 6}), b(std::vector<float>{7, 8, 9, 10, 11, 12}), c(4);
+    HIPBackend::matmul(a.p, b.p, c.p, 2, 3, 2);
+    auto h = c.host();
+    EXPECT_NEAR(h[0], 58, 0); EXPECT_NEAR(h[1], 64, 0); EXPECT_NEAR(h[2], 139, 0); EXPECT_NEAR(h[3], 154, 0);
+    // the same product with B given as [N,K] (Linear weight layout)
+    Dev bt(std::vector<float>{7, 9, 11, 8, 10, 12}), c2(4);
+    HIPBackend::matmulTransB(a.p, bt.p, c2.p, 2, 3, 2);
+    auto h2 = c2.host();
+    EXPECT_NEAR(h2[0], 58, 0); EXPECT_NEAR(h2[1], 64, 0); EXPECT_NEAR(h2[2], 139, 0); EXPECT_NEAR(h2[3], 154, 0);
+    std::printf("MatmulNonSquare done\n");
+}
+
+static void testBatchedMatmulForward() {
+    const int B = 2, M = 3, K = 4, N = 5;
+    Dev a(std::vector<float>(B * M * K, 1.f)), b(std::vector<float>(B * K * N, 1.f)), c(B * M * N);
+    HIPBackend::batchedMatmul(a.p, b.p, c.p, B, M, K, N);
+    for (float v : c.host()) EXPECT_NEAR(v, 4.0, 1e-5);
+    std::printf("BatchedMatmulForward done\n");
+}
+
+static void testLinearZeroInput() {
+    // y = x @ W + b with x = 0, b = 0 -> y = 0 (Linear stores W[in,out], linear.ixx:31,52)
+    const int batch = 2, in = 4, out = 3;
+    Dev x(std::vector<float>(batch * in, 0.f)), w(std::vector<float>{.1f, .2f, .3f, .4f, .5f, .6f, .7f, .8f, .9f, 1.f, 1.1f, 1.2f});
+    Dev bias(std::vector<float>(out, 0.f)), y(batch * out);
+    HIPBackend::matmul(x.p, w.p, y.p, batch, in, out);
+    HIPBackend::addBias(y.p, bias.p, y.p, batch, out);
+    for (float v : y.host()) EXPECT_NEAR(v, 0.0, 0);
+    std::printf("LinearZeroInput done\n");
+}
+
+static void testConvAllOnes() {
+    // Conv2d(1,4,3,stride=1,pad=1) on [1,1,8,8] ones: shape [1,4,8,8]; interior = sum of weights
+    std::vector<float> wh(4 * 9);
+    for (size_t i = 0; i < wh.size(); ++i) wh[i] = 0.125f * (float)(i % 7) - 0.25f;
+    Dev x(std::vector<float>(64, 1.f)), w(wh), y(4 * 64), y2(4 * 36);
+    HIPBackend::conv2d(x.p, w.p, nullptr, y.p, 1, 1, 8, 8, 4, 3, 3, 1, 1);
+    auto h = y.host();
+    for (int co = 0; co < 4; ++co) {
+        double s = 0;
+        for (int t = 0; t < 9; ++t) s += wh[co * 9 + t];
+        for (int r = 1; r < 7; ++r)
+            for (int c = 1; c < 7; ++c) EXPECT_NEAR(h[co * 64 + r * 8 + c], s, 1e-6);
+    }
+    // no padding: (8-3)/1+1 = 6 -> every output is interior
+    HIPBackend::conv2d(x.p, w.p, nullptr, y2.p, 1, 1, 8, 8, 4, 3, 3, 1, 0);
+    auto h2 = y2.host();
+    for (int co = 0; co < 4; ++co) {
+        double s = 0;
+        for (int t = 0; t < 9; ++t) s += wh[co * 9 + t];
+        for (int i = 0; i < 36; ++i) EXPECT_NEAR(h2[co * 36 + i], s, 1e-6);
+    }
+    std::printf("ConvAllOnes done\n");
+}
+
+static void testReluAndErrors() {
+    Dev x(std::vector<float>{-1.f, 0.f, 2.f, NAN, -0.f}), y(5);
+    HIPBackend::relu(x.p, y.p, 5);
+    auto h = y.host();
+    EXPECT_NEAR(h[0], 0, 0); EXPECT_NEAR(h[2], 2, 0); EXPECT_NEAR(h[3], 0, 0);
+    EXPECT_NEAR(std::signbit(h[4]) ? 1 : 0, 0, 0);
+    bool threw = false;
+    try {
+        HIPBackend::batchNorm2d(x.p, y.p, x.p, x.p, x.p, x.p, nullptr, nullptr, 1, 1, 1, 1, 1e-5f, 0.1f, true);
+    } catch (const std::runtime_error& e) {
+        threw = true;
+        std::printf("expected error: %s\n", e.what());
+    }
+    if (!threw) { std::printf("FAIL: training-mode batchNorm2d did not throw\n"); ++g_fail; }
+    std::printf("ReluAndErrors done\n");
+}
+
+int main() {
+    try {
+        HIPBackend::init(0);
+        testMatmul2D();
+        testMatmulNonSquare();
+        testBatchedMatmulForward();
+        testLinearZeroInput();
+        testConvAllOnes();
+        testReluAndErrors();
+        HIPBackend::synchronize();
+    } catch (const std::exception& e) {
+        std::printf("FAIL: exception %s\n", e.what());
+        return 2;
+    }
+    std::printf(g_fail ? "FAILED %d checks\n" : "ALL PASSED\n", g_fail);
+    return g_fail ? 1 : 0;
+}
