@@ -1,0 +1,169 @@
+"""conv2d parity: implicit-GEMM MFMA conv (+ fused bias/BN/ReLU) against the
+oracle's reference chain conv2d -> batchNorm2d(eval) -> relu.
+
+Tolerance (K-scaled): |out_hip - out_ref| <= 1e-4 * budget, where budget is
+the float64 conv of |x| and |w| (plus |bias|), scaled by |gamma| * invStd after
+BN — the conv analogue of sum_k |a_ik||b_kj|. Every ResNet-18 conv shape (the
+benchmark's 20 layers) runs at batch 2 against the oracle and at batch 32 on
+images {0, 1, 30, 31} (tiles straddle image boundaries differently there);
+ResNet-50 shapes, odd geometries and the explicit im2col path follow.
+"""
+import zlib
+
+import numpy as np
+import pytest
+
+import oracle as O
+from conftest import empty_dev, to_dev
+from resnet_shapes import out_hw, resnet18_convs, resnet50_convs
+
+pytestmark = pytest.mark.gpu
+TOL = O.TOL_FP32
+
+
+def _params(cout, seed):
+    gamma = O.uniform((cout,), seed + 1, 0.5, 1.5)
+    beta = O.randn((cout,), seed + 2, 0.1)
+    mean = O.randn((cout,), seed + 3, 0.1)
+    var = O.uniform((cout,), seed + 4, 0.5, 1.5)
+    return gamma, beta, mean, var
+
+
+def _kaiming_uniform(shape, seed):
+    fan_in = int(np.prod(shape[1:]))
+    bound = np.sqrt(6.0 / fan_in)
+    return O.uniform(shape, seed, -bound, bound)
+
+
+def _run_conv(hip, x, w, bias, bn, act, stride, pad, entry="omHipConv2dBiasBnAct"):
+    N, Cin, H, W = x.shape
+    Cout, _, KH, KW = w.shape
+    Ho, Wo = out_hw(H, KH, stride, pad), out_hw(W, KW, stride, pad)
+    dx, dw = to_dev(hip, x), to_dev(hip, w)
+    db = to_dev(hip, bias) if bias is not None else None
+    dout = empty_dev(hip, (N, Cout, Ho, Wo))
+    if entry == "omHipConv2dBiasBnAct":
+        dbn = [to_dev(hip, a) for a in bn] if bn is not None else [None] * 4
+        hip.call(entry, dx.ptr, dw.ptr, db.ptr if db else None, *[d.ptr if d else None for d in dbn],
+                 1e-5, act, dout.ptr, N, Cin, H, W, Cout, KH, KW, stride, pad)
+    else:
+        hip.call(entry, dx.ptr, dw.ptr, db.ptr if db else None, dout.ptr, N, Cin, H, W, Cout, KH, KW, stride, pad)
+    return dout.numpy()
+
+
+def _check(out, x, w, bias, bn, act, stride, pad):
+    ref = O.conv_bn_act(x, w, bias, *(bn if bn is not None else (None,) * 4), eps=1e-5, act=act,
+                        stride=stride, pad=pad)
+    kw = dict(zip(("gamma", "beta", "mean", "var"), bn)) if bn is not None else {}
+    o64, bound = O.conv_f64(x, w, bias, stride, pad, act=act, **kw)
+    e_ref = O.normalized_error(out, ref, bound)
+    e_64 = O.normalized_error(out, o64, bound)
+    assert e_ref <= TOL, f"vs oracle {e_ref:.3e}"
+    assert e_64 <= TOL, f"vs float64 {e_64:.3e}"
+    return e_ref
+
+
+R18 = resnet18_convs()
+
+
+@pytest.mark.parametrize("shape", R18, ids=[s[0] for s in R18])
+def test_resnet18_layer_fused_b2(hip, shape):
+    name, cin, h, w, cout, k, s, p = shape
+    seed = zlib.crc32(name.encode()) % 10000
+    x = O.randn((2, cin, h, w), seed)
+    wt = _kaiming_uniform((cout, cin, k, k), seed + 10)
+    bn = _params(cout, seed + 20)
+    print(f"case r18 {name} b2", flush=True)
+    out = _run_conv(hip, x, wt, None, bn, 1, s, p)
+    _check(out, x, wt, None, bn, 1, s, p)
+
+
+@pytest.mark.parametrize("shape", R18, ids=[s[0] for s in R18])
+def test_resnet18_layer_fused_b32_sampled(hip, shape):
+    name, cin, h, w, cout, k, s, p = shape
+    seed = zlib.crc32(name.encode()) % 10000 + 7
+    x = O.randn((32, cin, h, w), seed)
+    wt = _kaiming_uniform((cout, cin, k, k), seed + 10)
+    bn = _params(cout, seed + 20)
+    print(f"case r18 {name} b32", flush=True)
+    out = _run_conv(hip, x, wt, None, bn, 1, s, p)
+    idx = [0, 1, 30, 31]
+    _check(out[idx], np.ascontiguousarray(x[idx]), wt, None, bn, 1, s, p)
+
+
+R50 = [c for c in resnet50_convs() if c[0].endswith((".0.conv1", ".0.conv2", ".0.conv3", ".0.ds", "stem"))]
+
+
+@pytest.mark.parametrize("shape", R50, ids=[s[0] for s in R50])
+def test_resnet50_layer_fused_b2(hip, shape):
+    name, cin, h, w, cout, k, s, p = shape
+    seed = zlib.crc32(("r50" + name).encode()) % 10000
+    x = O.randn((2, cin, h, w), seed)
+    wt = _kaiming_uniform((cout, cin, k, k), seed + 10)
+    bn = _params(cout, seed + 20)
+    out = _run_conv(hip, x, wt, None, bn, 1, s, p)
+    _check(out, x, wt, None, bn, 1, s, p)
+
+
+ODD = [
+    # N, Cin, H, W, Cout, K, stride, pad
+    (1, 1, 8, 8, 4, 3, 1, 1), (1, 1, 8, 8, 4, 3, 1, 0), (2, 3, 9, 9, 4, 3, 2, 1),
+    (3, 5, 13, 11, 7, 3, 1, 1), (2, 7, 17, 19, 100, 5, 2, 2), (1, 16, 7, 7, 300, 1, 1, 0),
+    (4, 3, 31, 29, 33, 7, 3, 3), (2, 64, 10, 10, 65, 3, 1, 1), (1, 2, 5, 5, 3, 5, 1, 0),
+]
+
+
+@pytest.mark.parametrize("geom", ODD)
+@pytest.mark.parametrize("variant", ["plain", "bias", "bias_bn", "bn_relu", "bias_bn_relu"])
+def test_odd_geometry(hip, geom, variant):
+    N, cin, h, w, cout, k, s, p = geom
+    seed = 100 + sum(geom)
+    x = O.randn((N, cin, h, w), seed)
+    wt = O.randn((cout, cin, k, k), seed + 1, 0.3)
+    bias = O.randn((cout,), seed + 2) if "bias" in variant else None
+    bn = _params(cout, seed + 3) if "bn" in variant else None
+    act = 1 if "relu" in variant else 0
+    if variant in ("plain", "bias"):
+        out = _run_conv(hip, x, wt, bias, None, 0, s, p, entry="omHipConv2d")
+    else:
+        out = _run_conv(hip, x, wt, bias, bn, act, s, p)
+    _check(out, x, wt, bias, bn, act, s, p)
+
+
+@pytest.mark.parametrize("geom", [(2, 3, 9, 9, 4, 3, 2, 1), (2, 64, 56, 56, 64, 3, 1, 1), (2, 3, 224, 224, 64, 7, 2, 3),
+                                  (2, 256, 14, 14, 512, 1, 2, 0)])
+def test_im2col_path(hip, geom):
+    """omHipConv2dIm2col: explicit im2col + shared-weight batched GEMM + bias."""
+    N, cin, h, w, cout, k, s, p = geom
+    x = O.randn((N, cin, h, w), 500)
+    wt = _kaiming_uniform((cout, cin, k, k), 501)
+    bias = O.randn((cout,), 502)
+    out = _run_conv(hip, x, wt, bias, None, 0, s, p, entry="omHipConv2dIm2col")
+    _check(out, x, wt, bias, None, 0, s, p)
+
+
+def test_conv_all_ones_interior(hip):
+    """tests/test_conv.cpp:21-49 shapes; all-ones input -> interior = sum of weights."""
+    x = np.ones((1, 1, 8, 8), np.float32)
+    wt = O.randn((4, 1, 3, 3), 9)
+    out = _run_conv(hip, x, wt, None, None, 0, 1, 1, entry="omHipConv2d")
+    assert out.shape == (1, 4, 8, 8)
+    s = wt.astype(np.float64).reshape(4, -1).sum(axis=1)
+    for c in range(4):
+        np.testing.assert_allclose(out[0, c, 1:7, 1:7], s[c], rtol=0, atol=1e-6)
+    out0 = _run_conv(hip, x, wt, None, None, 0, 1, 0, entry="omHipConv2d")
+    assert out0.shape == (1, 4, 6, 6)
+
+
+def test_conv_invalid_arguments(hip):
+    x = to_dev(hip, np.ones((1, 1, 4, 4), np.float32))
+    w = to_dev(hip, np.ones((1, 1, 5, 5), np.float32))
+    y = empty_dev(hip, (16,))
+    with pytest.raises(hip.OmHipError):
+        hip.call("omHipConv2d", x.ptr, w.ptr, None, y.ptr, 1, 1, 4, 4, 1, 5, 5, 1, 0)   # kernel > input
+    with pytest.raises(hip.OmHipError):
+        hip.call("omHipConv2d", x.ptr, w.ptr, None, y.ptr, 1, 1, 4, 4, 1, 3, 3, 0, 0)   # stride 0
+    g = to_dev(hip, np.ones(1, np.float32))
+    with pytest.raises(hip.OmHipError):   # partial BN parameters
+        hip.call("omHipConv2dBiasBnAct", x.ptr, w.ptr, None, g.ptr, None, None, None, 1e-5, 1, y.ptr,
+                 1, 1, 4, 4, 1, 3, 3, 1, 1)

@@ -1,0 +1,77 @@
+"""fp16 / bf16 GEMM (fp32 accumulate) parity.
+
+Two bars, both K-scaled (|C - C_ref| <= tol * sum_k |a_ik||b_kj|):
+  * against the oracle CPUBackend matmul on the SAME rounded inputs
+    (halfToFloat(A), halfToFloat(B), matmul): tol 1e-4 (only accumulation
+    order differs: every fp16/bf16 product is exact in fp32);
+  * against CPUBackend on the ORIGINAL fp32 inputs: tol 1e-2 (north star).
+Inputs are rounded to nearest-even (the reference's own FP16Converter
+truncates, fp16.ixx:92; the rounding rule is stated, not reproduced).
+Shapes: the ViT-B/16 projections (tokens 12608 = 64 x 197) on a token subset,
+and batched attention Q.K^T / P.V at the ragged 197.
+"""
+import numpy as np
+import pytest
+
+import oracle as O
+from conftest import empty_dev, to_dev
+
+pytestmark = pytest.mark.gpu
+
+
+def _round(x, bf16):
+    return O.bf16_round(x) if bf16 else x.astype(np.float16).astype(np.float32)
+
+
+def _bits(x, bf16):
+    return O.bf16_bits(x) if bf16 else x.astype(np.float16).view(np.uint16)
+
+
+@pytest.mark.parametrize("bf16", [False, True], ids=["f16", "bf16"])
+@pytest.mark.parametrize("transB", [False, True], ids=["NN", "NT"])
+@pytest.mark.parametrize("M,K,N", [(2, 3, 4), (197, 768, 2304), (394, 768, 768), (256, 768, 3072), (256, 3072, 768),
+                                   (33, 40, 17), (512, 512, 512), (1024, 1024, 1024)])
+def test_matmul_half(hip, bf16, transB, M, K, N):
+    A = O.randn((M, K), M + K)
+    B = O.randn((N, K) if transB else (K, N), N + 1, 0.02 if K >= 768 else 1.0)
+    dA, dB = to_dev(hip, _bits(A, bf16)), to_dev(hip, _bits(B, bf16))
+    dC = empty_dev(hip, (M, N))
+    hip.HIPBackend.matmulHalf(dA, dB, dC, M, K, N, bf16=bf16, transB=transB)
+    C = dC.numpy()
+    Ar, Br = _round(A, bf16), _round(B, bf16)
+    ref_rounded = O.matmul_transB(Ar, Br) if transB else O.matmul(Ar, Br)
+    _, bound_r = O.gemm_f64(Ar, Br, transB=transB)
+    assert O.normalized_error(C, ref_rounded, bound_r) <= 1e-4
+    ref_fp32 = O.matmul_transB(A, B) if transB else O.matmul(A, B)
+    _, bound = O.gemm_f64(A, B, transB=transB)
+    assert O.normalized_error(C, ref_fp32, bound) <= O.TOL_HALF
+
+
+@pytest.mark.parametrize("bf16", [False, True], ids=["f16", "bf16"])
+def test_attention_batched(hip, bf16):
+    """Q.K^T (NT, 12 heads x 197 x 64 x 197) and P.V (NN, 197 x 197 x 64), 2 images."""
+    BH, S, D = 24, 197, 64
+    Q, Kt, V = O.randn((BH, S, D), 1), O.randn((BH, S, D), 2), O.randn((BH, S, D), 3)
+    P = O.uniform((BH, S, S), 4, 0, 2.0 / S)
+    dQ, dK, dV, dP = (to_dev(hip, _bits(a, bf16)) for a in (Q, Kt, V, P))
+    dS, dO = empty_dev(hip, (BH, S, S)), empty_dev(hip, (BH, S, D))
+    dt = 1 if bf16 else 0
+    hip.HIPBackend.gemmStridedBatchedHalf(dt, 0, 1, BH, S, S, D, dQ, D, S * D, dK, D, S * D, dS, S, S * S)
+    hip.HIPBackend.gemmStridedBatchedHalf(dt, 0, 0, BH, S, D, S, dP, S, S * S, dV, D, S * D, dO, D, S * D)
+    Qr, Kr, Vr, Pr = (_round(a, bf16) for a in (Q, Kt, V, P))
+    S_ref = O.batched_matmul_transB(Qr, Kr)
+    _, bS = O.gemm_f64(Qr, Kr, transB=True)
+    assert O.normalized_error(dS.numpy(), S_ref, bS) <= 1e-4
+    O_ref = O.batched_matmul(Pr, Vr)
+    _, bO = O.gemm_f64(Pr, Vr)
+    assert O.normalized_error(dO.numpy(), O_ref, bO) <= 1e-4
+    _, bS32 = O.gemm_f64(Q, Kt, transB=True)
+    assert O.normalized_error(dS.numpy(), O.batched_matmul_transB(Q, Kt), bS32) <= O.TOL_HALF
+
+
+def test_half_known_answer(hip):
+    A = np.array([[1, 2], [3, 4]], np.float16).view(np.uint16)
+    B = np.array([[5, 6], [7, 8]], np.float16).view(np.uint16)
+    dA, dB, dC = to_dev(hip, A), to_dev(hip, B), empty_dev(hip, (2, 2))
+    hip.HIPBackend.matmulHalf(dA, dB, dC, 2, 2, 2)
+    assert dC.numpy().tolist() == [[19, 22], [43, 50]]

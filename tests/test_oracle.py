@@ -1,0 +1,214 @@
+"""Pins the oracle (CPU restatement of the reference CPUBackend) — CPU only.
+
+Checks, in order of strength:
+  1. golden vectors written by the compiled reference CPUBackend
+     (tests/golden/reference_cpubackend.npz): bit-exact;
+  2. the reference's own known-answer tests (test_tensor_ops.cpp:55-82,
+     test_phase5.cpp:206-222, test_nn.cpp:34-48, test_conv.cpp:21-49);
+  3. the compiled reference on fresh seeded inputs, when oracle/_ref is built;
+  4. float64 brute force within the K-scaled bound, plus closed forms
+     (identity, transpose identity, linearity, all-ones conv interior = sum of
+     weights, BN closed form) chosen so a dropped term, a wrong index or a
+     transposed operand fails.
+"""
+import os
+
+import numpy as np
+import pytest
+
+import oracle as O
+
+GOLD = os.path.join(os.path.dirname(__file__), "golden", "reference_cpubackend.npz")
+
+
+def bits(a):
+    return np.ascontiguousarray(a, np.float32).view(np.uint32)
+
+
+@pytest.fixture(scope="module")
+def gold():
+    with np.load(GOLD, allow_pickle=False) as z:
+        return {k: z[k] for k in z.files}
+
+
+# ---------------------------------------------------------------- 1. golden
+def test_golden_matmul(gold):
+    names = sorted({k.split(".")[0] for k in gold if k.startswith("matmul_") and k.endswith(".C")})
+    assert len(names) >= 6
+    for n in names:
+        C = O.matmul(gold[f"{n}.A"], gold[f"{n}.B"])
+        assert np.array_equal(bits(C), bits(gold[f"{n}.C"])), n
+
+
+def test_golden_batched_transpose_backward(gold):
+    assert np.array_equal(bits(O.batched_matmul(gold["batched_3x5x7x9.A"], gold["batched_3x5x7x9.B"])),
+                          bits(gold["batched_3x5x7x9.C"]))
+    assert np.array_equal(O.transpose2d(gold["transpose_13x7.A"]), gold["transpose_13x7.B"])
+    dA, dB = O.matmul_backward(gold["matmul_backward_6x4x5.G"], gold["matmul_backward_6x4x5.A"],
+                               gold["matmul_backward_6x4x5.B"])
+    assert np.array_equal(bits(dA), bits(gold["matmul_backward_6x4x5.dA"]))
+    assert np.array_equal(bits(dB), bits(gold["matmul_backward_6x4x5.dB"]))
+
+
+def test_golden_conv(gold):
+    assert np.array_equal(O.im2col(gold["im2col_3x9x9_k3s2p1.x"], 3, 3, 1, 2), gold["im2col_3x9x9_k3s2p1.col"])
+    g = "conv_2x3x9x9_4_k3s2p1"
+    y = O.conv2d(gold[f"{g}.x"], gold[f"{g}.w"], gold[f"{g}.bias"], 2, 1)
+    assert np.array_equal(bits(y), bits(gold[f"{g}.y"]))
+    g = "conv_2x3x9x9_5_k5s1p0"
+    assert np.array_equal(bits(O.conv2d(gold[f"{g}.x"], gold[f"{g}.w"], None, 1, 0)), bits(gold[f"{g}.y"]))
+
+
+def test_golden_bn(gold):
+    p = [gold[f"bn_eval.{k}"] for k in ("x", "gamma", "beta", "mean", "var")]
+    y, sm, si = O.batchnorm2d_eval(*p)
+    for a, k in zip((y, sm, si), ("y", "savedMean", "savedInvStd")):
+        assert np.array_equal(bits(a), bits(gold[f"bn_eval.{k}"])), k
+    p = [gold[f"bn_train.{k}"] for k in ("x", "gamma", "beta", "mean", "var")]
+    res = O.batchnorm2d_train(*p)
+    for a, k in zip(res, ("y", "runMean", "runVar", "savedMean", "savedInvStd")):
+        assert np.array_equal(bits(a), bits(gold[f"bn_train.{k}"])), k
+
+
+def test_golden_relu_bias(gold):
+    assert np.array_equal(bits(O.relu(gold["relu.x"])), bits(gold["relu.y"]))
+    assert np.array_equal(bits(O.relu_backward(gold["relu.x"], gold["relu.g"])), bits(gold["relu.gi"]))
+    assert np.array_equal(bits(O.add_bias(gold["add_bias.A"], gold["add_bias.bias"])), bits(gold["add_bias.out"]))
+
+
+# ---------------------------------------------------------- 2. known answers
+def test_known_answers():
+    assert O.matmul(np.array([[1, 2], [3, 4]]), np.array([[5, 6], [7, 8]])).tolist() == [[19, 22], [43, 50]]
+    assert O.matmul(np.arange(1, 7).reshape(2, 3), np.arange(7, 13).reshape(3, 2)).tolist() == [[58, 64], [139, 154]]
+    assert np.all(O.batched_matmul(np.ones((2, 3, 4)), np.ones((2, 4, 5))) == 4.0)
+    # Linear with zero input and zero bias -> 0 (test_nn.cpp:34-48)
+    y = O.add_bias(O.matmul(np.zeros((2, 4)), O.randn((4, 3), 1)), np.zeros(3))
+    assert np.all(y == 0)
+    # Conv2d(1,4,3,s1,p1) on ones(1,1,8,8): shape (1,4,8,8), interior = sum(w); p0 -> (1,4,6,6)
+    w = O.randn((4, 1, 3, 3), 2)
+    y = O.conv2d(np.ones((1, 1, 8, 8), np.float32), w, None, 1, 1)
+    assert y.shape == (1, 4, 8, 8)
+    s = w.reshape(4, -1).astype(np.float64).sum(1)
+    assert np.allclose(y[0, :, 1:7, 1:7], s[:, None, None], atol=1e-6)
+    assert O.conv2d(np.ones((1, 1, 8, 8), np.float32), w, None, 1, 0).shape == (1, 4, 6, 6)
+
+
+def test_degenerate_dims_zero_output():
+    C = np.full((3, 4), 7, np.float32)
+    O.lib().omrefMatmul(O._p(O.randn((3, 2), 1)), O._p(O.randn((2, 4), 2)), O._p(C), 3, 0, 4)
+    assert np.all(C == 0)
+
+
+# ------------------------------------------------ 3. compiled reference, fresh
+ref_built = pytest.mark.skipif(O.ref_lib() is None, reason="oracle/_ref not built (needs the reference tree)")
+
+
+@ref_built
+@pytest.mark.parametrize("M,K,N", [(5, 9, 17), (64, 147, 100), (130, 257, 31), (4, 1, 8), (9, 300, 1)])
+def test_vs_reference_matmul(M, K, N):
+    A, B = O.randn((M, K), M), O.randn((K, N), N)
+    assert np.array_equal(bits(O.matmul(A, B)), bits(O.matmul(A, B, backend="reference")))
+
+
+@ref_built
+@pytest.mark.parametrize("geom", [(2, 3, 11, 13, 5, 3, 2, 1), (1, 8, 7, 7, 16, 1, 1, 0), (2, 4, 12, 12, 6, 7, 2, 3)])
+def test_vs_reference_conv_bn_relu(geom):
+    N, cin, h, w, cout, k, s, p = geom
+    x, wt, b = O.randn((N, cin, h, w), 1), O.randn((cout, cin, k, k), 2), O.randn((cout,), 3)
+    y1 = O.conv2d(x, wt, b, s, p)
+    y2 = O.conv2d(x, wt, b, s, p, backend="reference")
+    assert np.array_equal(bits(y1), bits(y2))
+    g, be, m, v = O.uniform((cout,), 4, .5, 1.5), O.randn((cout,), 5), O.randn((cout,), 6), O.uniform((cout,), 7, .5, 2)
+    a = O.batchnorm2d_eval(y1, g, be, m, v)
+    bb = O.batchnorm2d_eval(y2, g, be, m, v, backend="reference")
+    assert all(np.array_equal(bits(u), bits(t)) for u, t in zip(a, bb))
+    assert np.array_equal(bits(O.relu(a[0])), bits(O.relu(bb[0], backend="reference")))
+
+
+# ----------------------------------------------- 4. float64 and closed forms
+@pytest.mark.parametrize("M,K,N", [(33, 65, 17), (128, 784, 256), (7, 1000, 9)])
+def test_matmul_vs_float64(M, K, N):
+    A, B = O.randn((M, K), 7), O.randn((K, N), 8)
+    C64, bound = O.gemm_f64(A, B)
+    assert O.normalized_error(O.matmul(A, B), C64, bound) <= 1e-6
+    assert O.normalized_error(O.matmul_transB(A, np.ascontiguousarray(B.T)), C64, bound) <= 1e-6
+    assert O.normalized_error(O.matmul_transA(np.ascontiguousarray(A.T), B), C64, bound) <= 1e-6
+
+
+def test_matmul_identity_and_transpose_rule():
+    A = O.randn((9, 12), 1)
+    assert np.array_equal(O.matmul(A, np.eye(12, dtype=np.float32)), A)
+    B = O.randn((12, 5), 2)
+    # (AB)^T = B^T A^T, exactly (same fma chains in the same k order)
+    assert np.array_equal(O.matmul(A, B).T, O.matmul(np.ascontiguousarray(B.T), np.ascontiguousarray(A.T)))
+
+
+def test_conv_vs_float64_and_direct_loop():
+    x, w, b = O.randn((2, 3, 7, 6), 1), O.randn((4, 3, 3, 2), 2), O.randn((4,), 3)
+    for s, p in [(1, 0), (2, 1), (3, 2)]:
+        y = O.conv2d(x, w, b, s, p)
+        y64, bound = O.conv_f64(x, w, b, s, p)
+        assert O.normalized_error(y, y64, bound) <= 1e-6
+    # the textbook 7-loop convolution on a tiny case (independent of im2col)
+    y = O.conv2d(x, w, b, 2, 1)
+    Ho, Wo = y.shape[2:]
+    ref = np.zeros_like(y, dtype=np.float64)
+    for n in range(2):
+        for co in range(4):
+            for oh in range(Ho):
+                for ow in range(Wo):
+                    acc = float(b[co])
+                    for ci in range(3):
+                        for kh in range(3):
+                            for kw in range(2):
+                                ih, iw = oh * 2 - 1 + kh, ow * 2 - 1 + kw
+                                if 0 <= ih < 7 and 0 <= iw < 6:
+                                    acc += float(x[n, ci, ih, iw]) * float(w[co, ci, kh, kw])
+                    ref[n, co, oh, ow] = acc
+    assert np.allclose(y, ref, atol=1e-5)
+
+
+def test_bn_closed_form():
+    x = O.randn((2, 3, 4, 4), 9)
+    g, b, m, v = O.uniform((3,), 1, .5, 1.5), O.randn((3,), 2), O.randn((3,), 3), O.uniform((3,), 4, .5, 1.5)
+    y, sm, si = O.batchnorm2d_eval(x, g, b, m, v)
+    inv = 1.0 / np.sqrt(v.astype(np.float64) + 1e-5)
+    expect = g[None, :, None, None] * (x - m[None, :, None, None]) * inv[None, :, None, None] + b[None, :, None, None]
+    assert np.allclose(y, expect, rtol=1e-6, atol=1e-6)
+    assert np.array_equal(sm, m)
+    assert np.allclose(si, inv, rtol=1e-7)
+
+
+def test_half_truncation_rule():
+    """FP16Converter::floatToHalf truncates (fp16.ixx:92): differs from RNE only
+    where the dropped 13 bits are >= half an ulp."""
+    x = np.array([1.0, 65504.0, 1.0 + 2 ** -11 + 2 ** -12, -2.5, 0.0, 1e-40, 7e4, 2 ** -20], np.float32)
+    t = O.float_to_half_trunc(x)
+    assert t[0] == 0x3C00 and t[1] == 0x7BFF and t[3] == 0xC100 and t[4] == 0
+    assert t[2] == 0x3C00                      # truncated; round-to-nearest gives 0x3C01
+    assert x[2:3].astype(np.float16).view(np.uint16)[0] == 0x3C01
+    assert t[5] == 0                           # fp32 subnormal flushed
+    assert t[6] == 0x7C00                      # overflow -> inf
+    assert t[7] == (x[7:8].astype(np.float16).view(np.uint16)[0])   # exact fp16 subnormal
+
+
+# ---------------------------------------- planted mistakes are caught (CPU)
+def test_tolerance_catches_planted_mistakes():
+    """A dropped k term, a transposed operand or an off-by-one row in a result
+    built from the oracle must fail the K-scaled 1e-4 bar."""
+    A, B = O.randn((64, 256), 1), O.randn((256, 48), 2)
+    C64, bound = O.gemm_f64(A, B)
+    good = O.matmul(A, B)
+    assert O.normalized_error(good, C64, bound) <= O.TOL_FP32
+    dropped = O.matmul(A[:, 1:], B[1:])                       # k = 0 term missing
+    assert O.normalized_error(dropped, C64, bound) > O.TOL_FP32
+    Bsq = O.randn((256, 256), 3)
+    C64s, bounds = O.gemm_f64(A, Bsq)
+    assert O.normalized_error(O.matmul(A, np.ascontiguousarray(Bsq.T)), C64s, bounds) > O.TOL_FP32
+    shifted = np.roll(good, 1, axis=0)
+    assert O.normalized_error(shifted, C64, bound) > O.TOL_FP32
+    # conv: wrong padding offset
+    x, w = O.randn((1, 3, 10, 10), 4), O.randn((5, 3, 3, 3), 5)
+    y64, cb = O.conv_f64(x, w, None, 1, 1)
+    wrong = np.roll(O.conv2d(x, w, None, 1, 1), 1, axis=3)
+    assert O.normalized_error(wrong, y64, cb) > O.TOL_FP32
