@@ -28,6 +28,10 @@ DEVICE_FLAGS = ["-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
 COMMON = ["-O3", "-std=c++20", "-fPIC", "-Wall", "-Wno-unused-function", "-Wno-unused-variable"]
 
 SOURCES = ["runtime.cpp", "eltwise.hip", "gemm_f32.hip", "conv.hip", "gemm_half.hip"]
+# conv tiles keep at most 128 accumulators per lane: forcing the VGPR form of
+# the MFMA operands stops the register allocator from copying every
+# accumulator between AGPRs and VGPRs on each trip of the mainloop.
+EXTRA_FLAGS = {"conv.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
 
 
 def _run(cmd):
@@ -43,7 +47,8 @@ def _compile(src: str) -> str:
     path = os.path.join(CSRC, src)
     obj = os.path.join(BUILD, os.path.splitext(src)[0] + ".o")
     if src.endswith(".hip"):
-        cmd = [HIPCC, f"--offload-arch={ARCH}", *COMMON, *DEVICE_FLAGS, "-c", path, "-o", obj]
+        cmd = [HIPCC, f"--offload-arch={ARCH}", *COMMON, *DEVICE_FLAGS, *EXTRA_FLAGS.get(src, []), "-c", path, "-o",
+               obj]
     else:
         cmd = [HIPCC, *COMMON, "-c", path, "-o", obj]
     _run(cmd)

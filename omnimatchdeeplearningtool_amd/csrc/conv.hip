@@ -12,6 +12,16 @@
 // materialised: each thread gathers its pixels' taps straight into the LDS
 // B slice, and the output passes through HBM once, already normalised.
 //
+// gfx950 does not overlap VALU work with MFMA execution, so every VALU
+// instruction in the mainloop costs matrix-core time. Both operands are
+// therefore fetched with raw buffer loads whose per-lane offset is fixed for
+// the whole K walk and whose uniform part (slice start, tap offset) rides in
+// the scalar soffset: a weight slice costs no VALU, a gathered im2col element
+// costs two (a bit extract of the pixel's "tap outside the image" mask and a
+// shift-or that pushes such a lane past the buffer end, where the hardware's
+// range check returns 0). Tap offsets come from a per-geometry table read
+// with scalar loads.
+//
 // Split-K (for late layers whose Cout x pixels tile count cannot fill 256 CUs)
 // writes fp32 partial tiles to a workspace and a second kernel sums the splits
 // in a fixed order (deterministic) and applies the same epilogue.
@@ -21,14 +31,23 @@
 #include "../../include/omhip.h"
 
 #include <algorithm>
+#include <cmath>
+#include <map>
+#include <mutex>
+#include <tuple>
 
 namespace omhip {
 
 int im2colBatched(const float* x, float* col, int N, int Cin, int H, int W, int KH, int KW, int pad, int strd,
                   int Ho, int Wo);
 
+// Offsets at or above this byte count are out of range for every buffer used
+// here (buffers are limited to 2^30 bytes), so two such terms never wrap.
+constexpr uint32_t kOOB = 0x40000000u;
+constexpr uint32_t kMaxBufferBytes = 0x40000000u;
+
 struct ConvParams {
-    const float* x;      // [N][Cin][H][W]
+    const float* x;      // [N][Cin][H][W] (this batch chunk)
     const float* w;      // [Cout][Cin*KH*KW]
     const float* bias;   // [Cout] or null
     const float* gamma;  // BN (all four null = no BN)
@@ -39,88 +58,183 @@ struct ConvParams {
     int act;             // 0 identity, 1 relu
     float* out;          // [N][Cout][Ho][Wo]
     float* ws;           // split-K partials [splits][Cout][Nq]
+    const uint2* tab;    // per K row: (byte offset ci*HW+kh*W+kw, tap code); kOOB past K
     int N, Cin, H, W, Cout, KH, KW, stride, pad, Ho, Wo;
     int K;               // Cin*KH*KW
     int Nq;              // N*Ho*Wo
     int tilesM, tilesN;
     int splits, kChunk;  // split-K: k range [s*kChunk, min(K,(s+1)*kChunk))
+    int padOff;          // pad*W + pad: the x buffer view starts this many floats before x
+    uint32_t xBytes;     // range of the x buffer view
 };
 
-// Implicit im2col loader. Thread t owns pixel column c = t % BN of the slice
-// and rows g, g+TPC, g+2*TPC, ... (g = t / BN, TPC = NT/BN threads per column),
-// so its tap sequence over the whole K walk advances by TPC every row and the
-// (ci, kh, kw) decomposition is carried incrementally instead of divided out.
-template <int BN, int BK, int NT>
-struct ImplicitLoader {
-    static constexpr int TPC = NT / BN;
-    static constexpr int RPT = BK / TPC;   // rows per thread per slice
-    static_assert(NT % BN == 0 && BK % TPC == 0, "implicit loader mapping");
-    using Shape = LdsShape<false, BN, BK>;
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t bufferRsrc(const void* base, uint32_t bytes) {
+    // raw buffer, stride 0, range-checked against `bytes` (data format 32-bit)
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)bytes, 0x00020000);
+}
+__device__ __forceinline__ float bufLoad1(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0));
+}
+__device__ __forceinline__ f32x4 bufLoad4(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+    return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
+}
 
-    const float* xn;     // base of the pixel's image
-    int ih0, iw0;        // top-left input coordinate of the pixel's window
-    int pixoff;          // ih0*W + iw0 (negative at the top/left border; only used when the tap is inside)
-    bool colValid;
-    int H, W, HW, KH, KW, K;
-    int kk, ci, kh, kw;  // current tap of this thread
-    int koff;            // ci*HW + kh*W + kw
+// Tap table: entry kk = (4*(ci*H*W + kh*W + kw), code), code = kh*KW+kw for
+// the mask modes or (kh << 16) | kw for the coordinate-compare mode. Rows past
+// K read (kOOB, 0), so a slice that runs past K gathers zeros.
+__global__ void build_tap_table(uint2* tab, int K, int Kpad, int KH, int KW, int H, int W, int compareMode) {
+    const int kk = blockIdx.x * blockDim.x + threadIdx.x;
+    if (kk >= Kpad) return;
+    uint2 e;
+    if (kk < K) {
+        const int khw = KH * KW;
+        const int ci = kk / khw;
+        const int t = kk - ci * khw;
+        const int kh = t / KW;
+        const int kw = t - kh * KW;
+        e.x = (uint32_t)(ci * H * W + kh * W + kw) * 4u;
+        e.y = compareMode ? (uint32_t)((kh << 16) | kw) : (uint32_t)t;
+    } else {
+        e.x = kOOB;
+        e.y = 0;
+    }
+    tab[kk] = e;
+}
+
+// Weight slice loader: W[Cout][K] with K contiguous -> LDS [BM][BK+4].
+// Each thread owns fixed (row, k) positions; its byte offsets are computed
+// once and the slice start rides in soffset. Rows past Cout point past the
+// buffer end (zero). The last slice of a K range is loaded with an explicit
+// column test (it may end inside the slice).
+template <int BM, int BK, int NT, bool VEC>
+struct WeightLoader {
+    static constexpr int PER_T = VEC ? BM * BK / 4 / NT : BM * BK / NT;
+    static_assert(BM * BK % (NT * (VEC ? 4 : 1)) == 0, "slice must split evenly");
+    using Shape = LdsShape<true, BM, BK>;
+    __amdgpu_buffer_rsrc_t r;
+    uint32_t voff[PER_T];
+    f32x4 v4[VEC ? PER_T : 1];
+    float v1[VEC ? 1 : PER_T];
+
+    static __device__ __forceinline__ void coords(int e, int& row, int& k) {
+        if constexpr (VEC) { row = e / (BK / 4); k = (e % (BK / 4)) * 4; }
+        else { row = e / BK; k = e % BK; }
+    }
+
+    __device__ void init(const ConvParams& p, int m0, int tid) {
+        r = bufferRsrc(p.w, (uint32_t)p.Cout * (uint32_t)p.K * 4u);
+#pragma unroll
+        for (int i = 0; i < PER_T; ++i) {
+            int row, k;
+            coords(tid + i * NT, row, k);
+            voff[i] = (m0 + row < p.Cout) ? (uint32_t)((m0 + row) * p.K + k) * 4u : kOOB;
+        }
+    }
+
+    __device__ void load(int k0, int kEnd, int tid) {
+        const uint32_t soff = (uint32_t)k0 * 4u;
+        if (k0 + BK <= kEnd) {
+#pragma unroll
+            for (int i = 0; i < PER_T; ++i) {
+                if constexpr (VEC) v4[i] = bufLoad4(r, voff[i], soff);
+                else v1[i] = bufLoad1(r, voff[i], soff);
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < PER_T; ++i) {
+                int row, k;
+                coords(tid + i * NT, row, k);
+                const uint32_t vo = (k0 + k < kEnd) ? voff[i] : kOOB;   // VEC: K % 4 == 0, all-or-none
+                if constexpr (VEC) v4[i] = bufLoad4(r, vo, soff);
+                else v1[i] = bufLoad1(r, vo, soff);
+            }
+        }
+    }
+
+    __device__ void store(float* s, int tid) const {
+#pragma unroll
+        for (int i = 0; i < PER_T; ++i) {
+            int row, k;
+            coords(tid + i * NT, row, k);
+            if constexpr (VEC) *reinterpret_cast<f32x4*>(s + row * Shape::LD + k) = v4[i];
+            else s[row * Shape::LD + k] = v1[i];
+        }
+    }
+};
+
+// Implicit im2col loader -> LDS [BK][BN+4]. Thread t owns pixel column
+// c = t % BN and the RPT consecutive rows g*RPT .. g*RPT+RPT-1 of each slice
+// (g = t / BN, the same for all lanes of a wave since BN >= 64), so the rows'
+// table entries are wave-uniform scalar loads. Per pixel: one byte offset
+// (into a buffer view that starts pad*W+pad floats before x, so it is never
+// negative) and the mask of taps that fall outside the image.
+//   MODE 0: KH*KW <= 32 (one 32-bit mask), MODE 1: <= 64 (64-bit mask),
+//   MODE 2: larger kernels compare coordinates.
+template <int BN, int BK, int NT, int MODE>
+struct GatherLoader {
+    static constexpr int TPC = NT / BN;
+    static constexpr int RPT = BK / TPC;
+    static_assert(NT % BN == 0 && BK % TPC == 0 && BN >= 64, "gather mapping");
+    using Shape = LdsShape<false, BN, BK>;
+    __amdgpu_buffer_rsrc_t r;
+    uint32_t voffPix;
+    uint32_t invLo, invHi;
+    int ih0, iw0, H, W;
+    const uint2* tab;
     float v[RPT];
 
-    __device__ void init(const ConvParams& p, int q, int kStart, int tid) {
-        H = p.H; W = p.W; HW = p.H * p.W; KH = p.KH; KW = p.KW; K = p.K;
-        colValid = q < p.Nq;
+    __device__ void init(const ConvParams& p, int q) {
+        r = bufferRsrc(p.x - p.padOff, p.xBytes);
+        tab = p.tab;
+        H = p.H; W = p.W;
+        const bool colValid = q < p.Nq;
         const int qq = colValid ? q : 0;
         const int HoWo = p.Ho * p.Wo;
         const int n = qq / HoWo;
         const int pix = qq - n * HoWo;
         const int oh = pix / p.Wo, ow = pix - (pix / p.Wo) * p.Wo;
-        ih0 = oh * p.stride - p.pad;
+        ih0 = colValid ? oh * p.stride - p.pad : -(1 << 29);   // a padding column matches no tap
         iw0 = ow * p.stride - p.pad;
-        xn = p.x + (long long)n * p.Cin * HW;
-        pixoff = ih0 * W + iw0;
-        const int g = tid / BN;
-        kk = kStart + g;
-        const int khw = KH * KW;
-        ci = kk / khw;
-        const int rem = kk - ci * khw;
-        kh = rem / KW;
-        kw = rem - kh * KW;
-        koff = ci * HW + kh * W + kw;
-    }
-
-    __device__ __forceinline__ void step() {
-        kk += TPC;
-#pragma unroll
-        for (int s = 0; s < TPC; ++s) {
-            ++kw; ++koff;
-            if (kw == KW) {
-                kw = 0; koff += W - KW; ++kh;
-                if (kh == KH) { kh = 0; koff += HW - KH * W; ++ci; }
-            }
+        voffPix = (uint32_t)(n * p.Cin * p.H * p.W + (colValid ? ih0 : 0) * W + iw0 + p.padOff) * 4u;
+        uint64_t inside = 0;
+        if constexpr (MODE != 2) {
+            uint64_t colBits = 0;
+            for (int c = 0; c < p.KW; ++c)
+                if ((unsigned)(iw0 + c) < (unsigned)W) colBits |= 1ull << c;
+            for (int rr = 0; rr < p.KH; ++rr)
+                if ((unsigned)(ih0 + rr) < (unsigned)H) inside |= colBits << (rr * p.KW);
         }
+        invLo = ~(uint32_t)inside;
+        invHi = ~(uint32_t)(inside >> 32);
     }
 
-    // Loads the next RPT taps (the slice's rows for this thread); kEnd bounds the split.
-    __device__ void load(int kEnd) {
+    // Issues this thread's RPT loads of the slice starting at row kk0.
+    __device__ void load(int kk0, int tid) {
+        const int base = __builtin_amdgcn_readfirstlane(kk0 + (tid / BN) * RPT);
 #pragma unroll
         for (int j = 0; j < RPT; ++j) {
-            const int ih = ih0 + kh, iw = iw0 + kw;
-            float val = 0.f;
-            if (colValid && kk < kEnd && (unsigned)ih < (unsigned)H && (unsigned)iw < (unsigned)W)
-                val = xn[koff + pixoff];
-            v[j] = val;
-            step();
+            const uint2 e = tab[base + j];
+            uint32_t inv;
+            if constexpr (MODE == 0) {
+                inv = __builtin_amdgcn_ubfe(invLo, e.y, 1);
+            } else if constexpr (MODE == 1) {
+                inv = (uint32_t)((((uint64_t)invHi << 32) | invLo) >> e.y) & 1u;
+            } else {
+                const int kh = (int)(e.y >> 16), kw = (int)(e.y & 0xffffu);
+                inv = ((unsigned)(ih0 + kh) >= (unsigned)H) | ((unsigned)(iw0 + kw) >= (unsigned)W);
+            }
+            v[j] = bufLoad1(r, (inv << 30) | voffPix, e.x);
         }
     }
 
     __device__ void store(float* s, int tid) const {
         const int c = tid % BN, g = tid / BN;
 #pragma unroll
-        for (int j = 0; j < RPT; ++j) s[(g + j * TPC) * Shape::LD + c] = v[j];
+        for (int j = 0; j < RPT; ++j) s[(g * RPT + j) * Shape::LD + c] = v[j];
     }
 };
 
-template <class Cfg, bool VA>
+template <class Cfg, bool VA, int MODE>
 __global__ __launch_bounds__(Cfg::NT) void conv_igemm_kernel(ConvParams p) {
     extern __shared__ float smem[];
     using SA = LdsShape<true, Cfg::BM, Cfg::BK>;
@@ -142,10 +256,10 @@ __global__ __launch_bounds__(Cfg::NT) void conv_igemm_kernel(ConvParams p) {
     const int kBeg = split * p.kChunk;
     const int kEnd = min(p.K, kBeg + p.kChunk);
 
-    DenseLoader<true, VA, Cfg::BM, Cfg::BK, Cfg::NT> la;
-    la.p = p.w; la.ld = p.K; la.rows = p.Cout; la.K = kEnd; la.r0 = m0;
-    ImplicitLoader<Cfg::BN, Cfg::BK, Cfg::NT> lb;
-    lb.init(p, n0 + tid % Cfg::BN, kBeg, tid);
+    WeightLoader<Cfg::BM, Cfg::BK, Cfg::NT, VA> la;
+    la.init(p, m0, tid);
+    GatherLoader<Cfg::BN, Cfg::BK, Cfg::NT, MODE> lb;
+    lb.init(p, n0 + tid % Cfg::BN);
 
     const bool direct = p.splits == 1;
     if (direct && tid < Cfg::BM) {
@@ -168,26 +282,39 @@ __global__ __launch_bounds__(Cfg::NT) void conv_igemm_kernel(ConvParams p) {
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
     const int nk = (kEnd - kBeg + Cfg::BK - 1) / Cfg::BK;
-    la.load(kBeg, tid);
-    lb.load(kEnd);
+    lb.load(kBeg, tid);
+    la.load(kBeg, kEnd, tid);
     la.store(smem, tid);
     lb.store(smem + SA::SIZE, tid);
     __syncthreads();
-    for (int t = 0; t < nk; ++t) {
-        const int cur = t & 1;
-        const bool more = (t + 1) < nk;
-        if (more) {
-            la.load(kBeg + (t + 1) * Cfg::BK, tid);
-            lb.load(kEnd);
+    // Two slices per trip so both LDS stage addresses are compile-time offsets.
+    for (int t = 0; t < nk; t += 2) {
+        {
+            const bool more = (t + 1) < nk;
+            if (more) {
+                lb.load(kBeg + (t + 1) * Cfg::BK, tid);
+                la.load(kBeg + (t + 1) * Cfg::BK, kEnd, tid);
+            }
+            mma_slice<Cfg, true, false>(smem, smem + SA::SIZE, acc, wm, wn, lane);
+            if (more) {
+                la.store(smem + STAGE, tid);
+                lb.store(smem + STAGE + SA::SIZE, tid);
+            }
+            __syncthreads();
         }
-        float* sCur = smem + cur * STAGE;
-        float* sNxt = smem + (cur ^ 1) * STAGE;
-        mma_slice<Cfg, true, false>(sCur, sCur + SA::SIZE, acc, wm, wn, lane);
-        if (more) {
-            la.store(sNxt, tid);
-            lb.store(sNxt + SA::SIZE, tid);
+        if (t + 1 < nk) {
+            const bool more = (t + 2) < nk;
+            if (more) {
+                lb.load(kBeg + (t + 2) * Cfg::BK, tid);
+                la.load(kBeg + (t + 2) * Cfg::BK, kEnd, tid);
+            }
+            mma_slice<Cfg, true, false>(smem + STAGE, smem + STAGE + SA::SIZE, acc, wm, wn, lane);
+            if (more) {
+                la.store(smem, tid);
+                lb.store(smem + SA::SIZE, tid);
+            }
+            __syncthreads();
         }
-        __syncthreads();
     }
 
     const int li = lane & 31, h = lane >> 5;
@@ -255,19 +382,27 @@ __global__ void conv_splitk_finish(ConvParams p) {
     }
 }
 
-// ---- tile configurations -----------------------------------------------------
-using ConvCfg64 = TileCfg<64, 256, 16, 64, 64>;     // Cout <= 64: 4 waves along pixels
-using ConvCfg128 = TileCfg<128, 256, 16, 64, 128>;  // 2 x 2 waves
+// ---- tile configuration -------------------------------------------------------
+// 64 x 64 output tile, 4 waves of 32 x 32, 16-deep K slices. Measured on MI355X
+// across the ResNet conv shapes this tile beats 64x128 ... 256x128 tiles on
+// every layer: it keeps 8 waves per SIMD resident, which hides the gather
+// latency, and (with the buffer-load loaders) costs about two VALU per MFMA.
+#ifndef OMHIP_CONV_BK
+#define OMHIP_CONV_BK 16
+#endif
+constexpr int kConvBK = OMHIP_CONV_BK;
+using ConvCfg = TileCfg<64, 64, kConvBK, 32, 32>;
 
 template <class Cfg>
 static size_t convLds() {
+    // two A+B stages and the epilogue vectors
     return (2 * (LdsShape<true, Cfg::BM, Cfg::BK>::SIZE + LdsShape<false, Cfg::BN, Cfg::BK>::SIZE) + 5 * Cfg::BM) *
            sizeof(float);
 }
 
-template <class Cfg, bool VA>
+template <class Cfg, bool VA, int MODE>
 static int launchConvT(ConvParams& p) {
-    auto kern = conv_igemm_kernel<Cfg, VA>;
+    auto kern = conv_igemm_kernel<Cfg, VA, MODE>;
     const size_t lds = convLds<Cfg>();
     static bool s_attr = false;
     if (!s_attr) {
@@ -280,28 +415,76 @@ static int launchConvT(ConvParams& p) {
     return 0;
 }
 
-template <class Cfg>
-static int launchConvCfg(ConvParams& p, float* wsBuf) {
+// Split-K factor: a layer with fewer than 2 tiles per CU (late ResNet stages:
+// few pixels, many channels) splits K by the smallest power of two that gives
+// at least 4 blocks per CU, keeping >= 256 taps per split; the partial sums
+// cost one extra fp32 write + read of the output. Measured best on the
+// ResNet-18 shapes (e.g. 512x1568x4608: 8 splits, 256x6272x2304: 4 splits).
+static int planSplits(const ConvParams& p, bool haveWs) {
+    // TUNE-HOOK
+    const long long cus = cuCount();
+    const long long tiles = (long long)((p.Cout + ConvCfg::BM - 1) / ConvCfg::BM) * ((p.Nq + ConvCfg::BN - 1) / ConvCfg::BN);
+    if (!haveWs || tiles >= 2 * cus) return 1;
+    int s = 1;
+    while (s < 16 && tiles * s < 4 * cus && p.K / (2 * s) >= 256) s *= 2;
+    return s;
+}
+
+static int launchConv(ConvParams& p, int splits, float* wsBuf) {
+    using Cfg = ConvCfg;
     p.tilesM = (p.Cout + Cfg::BM - 1) / Cfg::BM;
     p.tilesN = (p.Nq + Cfg::BN - 1) / Cfg::BN;
-    const long long tiles = (long long)p.tilesM * p.tilesN;
-    const long long cus = cuCount();
-    // Split K while the grid is below one wave of CUs and each split keeps >= 256 taps.
-    int splits = 1;
-    while (wsBuf && tiles * splits * 2 <= cus * 2 && p.K / (splits * 2) >= 256 && splits < 16) splits *= 2;
-    p.splits = splits;
     p.kChunk = (p.K + splits - 1) / splits;
     p.kChunk = (p.kChunk + Cfg::BK - 1) / Cfg::BK * Cfg::BK;
     p.splits = (p.K + p.kChunk - 1) / p.kChunk;
     p.ws = wsBuf;
     const bool va = (p.K % 4 == 0) && ((reinterpret_cast<uintptr_t>(p.w) & 15u) == 0);
-    int rc = va ? launchConvT<Cfg, true>(p) : launchConvT<Cfg, false>(p);
+    const int khw = p.KH * p.KW;
+    const int mode = khw <= 32 ? 0 : (khw <= 64 ? 1 : 2);
+    int rc;
+    if (va)
+        rc = mode == 0 ? launchConvT<Cfg, true, 0>(p)
+                       : (mode == 1 ? launchConvT<Cfg, true, 1>(p) : launchConvT<Cfg, true, 2>(p));
+    else
+        rc = mode == 0 ? launchConvT<Cfg, false, 0>(p)
+                       : (mode == 1 ? launchConvT<Cfg, false, 1>(p) : launchConvT<Cfg, false, 2>(p));
     if (rc || p.splits == 1) return rc;
     const long long total = (long long)p.Cout * p.Nq;
-    const int blocks = (int)std::min<long long>((total + 255) / 256, (long long)cus * 16);
+    const int blocks = (int)std::min<long long>((total + 255) / 256, (long long)cuCount() * 16);
     hipLaunchKernelGGL(conv_splitk_finish, dim3(blocks), dim3(256), 0, stream(), p);
     OMHIP_CHECK_LAUNCH();
     return 0;
+}
+
+// ---- tap tables, cached per (Cin, H, W, KH, KW) -------------------------------
+static std::mutex g_tabMutex;
+static std::map<std::tuple<int, int, int, int, int>, uint2*> g_tabs;
+
+static void dropTapTables() {
+    std::lock_guard<std::mutex> lock(g_tabMutex);
+    g_tabs.clear();   // the pool that owned them is being cleared
+}
+
+static const uint2* tapTable(int Cin, int H, int W, int KH, int KW) {
+    std::lock_guard<std::mutex> lock(g_tabMutex);
+    static bool s_hooked = false;
+    if (!s_hooked) {
+        onCleanup(dropTapTables);
+        s_hooked = true;
+    }
+    const auto key = std::make_tuple(Cin, H, W, KH, KW);
+    auto it = g_tabs.find(key);
+    if (it != g_tabs.end()) return it->second;
+    const int K = Cin * KH * KW;
+    const int Kpad = (K + 63) / 64 * 64 + 64;   // room for any slice that starts before K
+    void* mem = nullptr;
+    if (omHipMalloc(&mem, (size_t)Kpad * sizeof(uint2)) != 0) return nullptr;
+    uint2* tab = static_cast<uint2*>(mem);
+    hipLaunchKernelGGL(build_tap_table, dim3((Kpad + 255) / 256), dim3(256), 0, stream(), tab, K, Kpad, KH, KW, H, W,
+                       KH * KW > 64 ? 1 : 0);
+    if (hipGetLastError() != hipSuccess) return nullptr;
+    g_tabs.emplace(key, tab);
+    return tab;
 }
 
 static int validateConv(const char* name, const float* x, const float* w, float* out, int N, int Cin, int H, int W,
@@ -313,11 +496,32 @@ static int validateConv(const char* name, const float* x, const float* w, float*
     Wo = (W + 2 * pad - KW) / stride + 1;
     if (Ho <= 0 || Wo <= 0) return fail("%s: kernel larger than the padded input", name);
     const long long K = (long long)Cin * KH * KW;
-    const long long Nq = (long long)N * Ho * Wo;
-    if (K > (1LL << 30) || Nq > (1LL << 30) || (long long)N * Cin * H * W > (1LL << 31) - 1 ||
-        (long long)N * Cout * Ho * Wo > (1LL << 31) - 1 || (long long)Cin * H * W > (1LL << 30))
-        return fail("%s: tensor exceeds the 32-bit index range of this kernel", name);
+    // One image, its border margin and the weights must fit the buffer views
+    // (the batch is split into chunks that do); KH, KW < 2^16 for the tap codes.
+    const long long imgBytes = (long long)Cin * H * W * 4 + 8LL * ((long long)pad * W + pad + W + 1);
+    if (K > (1LL << 26) || imgBytes > (long long)kMaxBufferBytes / 2 || (long long)Cout * K * 4 > kMaxBufferBytes ||
+        (long long)Cout * Ho * Wo > (1LL << 30) || KH >= 65536 || KW >= 65536)
+        return fail("%s: tensor exceeds the 2^30-byte buffer range of this kernel", name);
     return 0;
+}
+
+static int convChunk(ConvParams p, int n0, int nb) {
+    // one batch chunk: x, out and the pixel axis restricted to images [n0, n0+nb)
+    p.x = p.x + (long long)n0 * p.Cin * p.H * p.W;
+    p.out = p.out + (long long)n0 * p.Cout * p.Ho * p.Wo;
+    p.N = nb;
+    p.Nq = nb * p.Ho * p.Wo;
+    p.padOff = p.pad * p.W + p.pad;
+    p.xBytes = (uint32_t)(((long long)nb * p.Cin * p.H * p.W + p.padOff) * 4);
+    // Split-K workspace only for outputs up to 64 MiB (late layers, where splitting pays).
+    const bool wsOk = (size_t)p.Cout * p.Nq * sizeof(float) <= ((size_t)64 << 20);
+    int splits = planSplits(p, wsOk);
+    float* ws = nullptr;
+    if (splits > 1) {
+        ws = static_cast<float*>(workspace((size_t)splits * p.Cout * p.Nq * sizeof(float)));
+        if (!ws) splits = 1;
+    }
+    return launchConv(p, splits, ws);
 }
 
 int conv2dFused(const char* name, const float* x, const float* w, const float* bias, const float* gamma,
@@ -336,12 +540,17 @@ int conv2dFused(const char* name, const float* x, const float* w, const float* b
     p.N = N; p.Cin = Cin; p.H = H; p.W = W; p.Cout = Cout; p.KH = KH; p.KW = KW;
     p.stride = stride; p.pad = pad; p.Ho = Ho; p.Wo = Wo;
     p.K = Cin * KH * KW;
-    p.Nq = N * Ho * Wo;
-    // Workspace large enough for up to 16 splits of the output.
-    const size_t wsBytes = (size_t)16 * Cout * p.Nq * sizeof(float);
-    float* ws = (wsBytes <= ((size_t)1 << 30)) ? static_cast<float*>(workspace(wsBytes)) : nullptr;
-    if (Cout <= 64) return launchConvCfg<ConvCfg64>(p, ws);
-    return launchConvCfg<ConvCfg128>(p, ws);
+    p.tab = tapTable(Cin, H, W, KH, KW);
+    if (!p.tab) return fail("%s: could not build the tap table", name);
+    // Images per chunk: the x view stays below 2^29 bytes, pixel indices below 2^30.
+    const long long perImg = (long long)Cin * H * W * 4;
+    long long chunk = std::max<long long>(1, ((long long)kMaxBufferBytes / 2) / perImg);
+    chunk = std::min<long long>(chunk, std::max<long long>(1, (1LL << 30) / ((long long)Cout * Ho * Wo)));
+    for (int n0 = 0; n0 < N; n0 += (int)chunk) {
+        const int nb = (int)std::min<long long>(chunk, N - n0);
+        if (convChunk(p, n0, nb)) return -1;
+    }
+    return 0;
 }
 
 }  // namespace omhip
@@ -369,12 +578,16 @@ int omHipConv2dBiasBnAct(const float* pInput, const float* pWeight, const float*
 int omHipConv2dIm2col(const float* pInput, const float* pWeight, const float* pBias, float* pOutput, int nBatch,
                       int nCin, int nH, int nW, int nCout, int nKH, int nKW, int nStride, int nPad) {
     clearError();
-    int Ho, Wo;
-    if (validateConv("omHipConv2dIm2col", pInput, pWeight, pOutput, nBatch, nCin, nH, nW, nCout, nKH, nKW, nStride,
-                     nPad, Ho, Wo))
-        return -1;
+    if (nBatch <= 0 || nCin <= 0 || nH <= 0 || nW <= 0 || nCout <= 0 || nKH <= 0 || nKW <= 0 || nStride <= 0 ||
+        nPad < 0)
+        return fail("omHipConv2dIm2col: invalid geometry");
+    if (!pInput || !pWeight || !pOutput) return fail("omHipConv2dIm2col: null pointer");
+    const int Ho = (nH + 2 * nPad - nKH) / nStride + 1;
+    const int Wo = (nW + 2 * nPad - nKW) / nStride + 1;
+    if (Ho <= 0 || Wo <= 0) return fail("omHipConv2dIm2col: kernel larger than the padded input");
     const long long K = (long long)nCin * nKH * nKW;
     const long long HWo = (long long)Ho * Wo;
+    if (K > (1LL << 30) || HWo > (1LL << 30)) return fail("omHipConv2dIm2col: tensor too large");
     void* col = nullptr;
     if (omHipMalloc(&col, (size_t)(nBatch * K * HWo) * sizeof(float))) return -1;
     int rc = im2colBatched(pInput, static_cast<float*>(col), nBatch, nCin, nH, nW, nKH, nKW, nPad, nStride, Ho, Wo);

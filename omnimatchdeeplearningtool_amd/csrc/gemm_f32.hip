@@ -121,7 +121,11 @@ static int launchVec(GemmF32Params prm, int batch, bool va, bool vb) {
     return launchOne<Cfg, TA, TB, false, false>(prm, batch);
 }
 
-using CfgL = TileCfg<256, 256, 16, 128, 128>;
+// Slice depth of the large tile is a build-time constant (LDS: 2 x (256x(BK+4) + BKx260) floats).
+#ifndef OMHIP_GEMM_BK
+#define OMHIP_GEMM_BK 16
+#endif
+using CfgL = TileCfg<256, 256, OMHIP_GEMM_BK, 128, 128>;
 using CfgM = TileCfg<128, 128, 16, 64, 64>;
 using CfgS = TileCfg<64, 64, 16, 32, 32>;
 

@@ -26,6 +26,10 @@ void clearError();
 // until omHipCleanup). Reuse is ordered by the single stream; nullptr on OOM.
 void* workspace(size_t bytes);
 
+// Registers a function that omHipCleanup runs before the pool is released
+// (for caches of pool-owned device buffers).
+void onCleanup(void (*fn)());
+
 // Device properties cached at init.
 int cuCount();          // compute units of the current device
 int maxSharedPerBlock(); // bytes

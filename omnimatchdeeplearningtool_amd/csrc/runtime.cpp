@@ -14,6 +14,7 @@
 #include <cstring>
 #include <memory>
 #include <mutex>
+#include <vector>
 
 namespace omhip {
 namespace {
@@ -27,6 +28,7 @@ int g_cuCount = 0;
 int g_maxShared = 65536;
 std::unique_ptr<CachingPool> g_pool;
 std::mutex g_wsMutex;
+std::vector<void (*)()> g_cleanupHooks;
 void* g_ws = nullptr;
 size_t g_wsBytes = 0;
 
@@ -93,6 +95,11 @@ int cuCount() {
 }
 
 int maxSharedPerBlock() { return g_maxShared; }
+
+void onCleanup(void (*fn)()) {
+    std::lock_guard<std::mutex> lock(g_wsMutex);
+    g_cleanupHooks.push_back(fn);
+}
 
 void* workspace(size_t bytes) {
     std::lock_guard<std::mutex> lock(g_wsMutex);
@@ -173,11 +180,14 @@ int omHipCleanup(void) {
     std::lock_guard<std::mutex> lock(g_initMutex);
     if (!g_inited.load(std::memory_order_acquire)) return 0;
     (void)hipStreamSynchronize(g_ownStream);
+    std::vector<void (*)()> hooks;
     {
         std::lock_guard<std::mutex> wsLock(g_wsMutex);
         g_ws = nullptr;
         g_wsBytes = 0;
+        hooks = g_cleanupHooks;
     }
+    for (auto fn : hooks) fn();
     if (g_pool) g_pool->clear();
     g_pool.reset();
     (void)hipStreamDestroy(g_ownStream);
