@@ -147,36 +147,87 @@ def bench_resnet18(om, steps: int, warmup: int, batch: int = 32):
     return ms, flops, roof_ms, per, max(errs)
 
 
-def cpu_baseline_gemm():
-    """Reference CPUBackend::matmul (oracle/_ref) on 4096^3 after a 1024^3 warm-up."""
+def cpu_baseline_gemm(budget_s: float = 10.0):
+    """Reference CPUBackend::matmul (oracle/_ref) on 4096^3: one warm-up, then
+    repeated for about budget_s seconds; the median run is reported."""
     import oracle as O
     backend = "reference" if O.ref_lib() is not None else "oracle"
-    A1, B1 = O.randn((1024, 1024), 1), O.randn((1024, 1024), 2)
-    O.matmul(A1, B1, backend=backend)
     A, B = O.randn((M, K), 11), O.randn((K, N), 12)
-    t = time.perf_counter()
     O.matmul(A, B, backend=backend)
-    dt = time.perf_counter() - t
-    return backend, 2.0 * M * N * K / dt / 1e12, dt
+    times = []
+    t_start = time.perf_counter()
+    while len(times) < 3 or (time.perf_counter() - t_start < budget_s and len(times) < 50):
+        t = time.perf_counter()
+        O.matmul(A, B, backend=backend)
+        times.append(time.perf_counter() - t)
+    dt = float(np.median(times))
+    return backend, 2.0 * M * N * K / dt / 1e12, dt, len(times)
 
 
-def cpu_baseline_resnet18(n_img: int = 2):
-    """Reference conv2d -> batchNorm2d(eval) -> relu over the 20 convs, n_img images."""
+def cpu_baseline_resnet18(batch: int = 32, budget_s: float = 10.0):
+    """Reference conv2d -> batchNorm2d(eval) -> relu over the 20 ResNet-18 convs
+    at the benchmark batch, repeated for about budget_s seconds (median pass)."""
     import oracle as O
     from resnet_shapes import resnet18_convs
     backend = "reference" if O.ref_lib() is not None else "oracle"
-    t_total = 0.0
+    data = []
     for li, (name, cin, h, w, cout, k, s, p) in enumerate(resnet18_convs()):
-        x = O.randn((n_img, cin, h, w), 100 + li)
-        wt = O.randn((cout, cin, k, k), 200 + li, 0.05)
-        g, b = O.uniform((cout,), 300 + li, 0.5, 1.5), O.randn((cout,), 400 + li, 0.1)
-        m, v = O.randn((cout,), 500 + li, 0.1), O.uniform((cout,), 600 + li, 0.5, 1.5)
-        t = time.perf_counter()
-        y = O.conv2d(x, wt, None, s, p, backend=backend)
-        y, _, _ = O.batchnorm2d_eval(y, g, b, m, v, backend=backend)
-        O.relu(y, backend=backend)
-        t_total += time.perf_counter() - t
-    return backend, n_img / t_total, t_total
+        data.append(((s, p), O.randn((batch, cin, h, w), 100 + li), O.randn((cout, cin, k, k), 200 + li, 0.05),
+                     O.uniform((cout,), 300 + li, 0.5, 1.5), O.randn((cout,), 400 + li, 0.1),
+                     O.randn((cout,), 500 + li, 0.1), O.uniform((cout,), 600 + li, 0.5, 1.5)))
+
+    def one_pass():
+        t0 = time.perf_counter()
+        for (s, p), x, wt, g, b, m, v in data:
+            y = O.conv2d(x, wt, None, s, p, backend=backend)
+            y, _, _ = O.batchnorm2d_eval(y, g, b, m, v, backend=backend)
+            O.relu(y, backend=backend)
+        return time.perf_counter() - t0
+
+    one_pass()
+    times = []
+    t_start = time.perf_counter()
+    while len(times) < 2 or (time.perf_counter() - t_start < budget_s and len(times) < 20):
+        times.append(one_pass())
+    dt = float(np.median(times))
+    return backend, batch / dt, dt, len(times)
+
+
+def traffic_probe():
+    """The dispatch sequence the HBM-traffic counter passes profile: a 256 MiB
+    device copy (calibration), three 4096^3 NN GEMMs, one ResNet-18 conv stack
+    pass at batch 32 (each layer once), one dispatch at a time."""
+    import omnimatchdeeplearningtool_amd as om
+    from resnet_shapes import out_hw, resnet18_convs
+    om.init(0)
+    H = om.HIPBackend
+    n = 64 << 20
+    src, dst = om.DeviceBuffer.empty((n,)), om.DeviceBuffer.empty((n,))
+    H.fillValue(src, n, 1.0)
+    om.synchronize()
+    H.copy(src, dst, n)
+    om.synchronize()
+    A = om.DeviceBuffer.from_numpy(np.random.default_rng(1).standard_normal((M, K), dtype=np.float32))
+    B = om.DeviceBuffer.from_numpy(np.random.default_rng(2).standard_normal((K, N), dtype=np.float32))
+    C = om.DeviceBuffer.empty((M, N))
+    for _ in range(3):
+        H.matmul(A, B, C, M, K, N)
+    om.synchronize()
+    bs = 32
+    for name, cin, h, w, cout, k, s, p in resnet18_convs():
+        ho, wo = out_hw(h, k, s, p), out_hw(w, k, s, p)
+        x = om.DeviceBuffer.empty((bs * cin * h * w,))
+        H.fillValue(x, bs * cin * h * w, 0.1)
+        wt = om.DeviceBuffer.empty((cout * cin * k * k,))
+        H.fillValue(wt, cout * cin * k * k, 0.01)
+        bn = [om.DeviceBuffer.empty((cout,)) for _ in range(4)]
+        for d in bn:
+            H.fillValue(d, cout, 1.0)
+        y = om.DeviceBuffer.empty((bs * cout * ho * wo,))
+        om.synchronize()
+        H.conv2dBiasBnAct(x, wt, None, bn[0], bn[1], bn[2], bn[3], 1e-5, 1, y, bs, cin, h, w, cout, k, k, s, p)
+        om.synchronize()
+    log("traffic probe done")
 
 
 def main():
@@ -185,12 +236,17 @@ def main():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--traffic-probe", action="store_true",
+                    help="run only the dispatch sequence profiled for HBM traffic (no JSON line)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}); the HAL path runs on a single "
               f"MI355X and multi-GPU runs are not part of this build.", file=sys.stderr)
         sys.exit(2)
     rank = int(os.environ.get("RANK", "0"))
+    if args.traffic_probe:
+        traffic_probe()
+        return
 
     import omnimatchdeeplearningtool_amd as om
     om.init(0)
@@ -213,16 +269,16 @@ def main():
     if rank == 0 and not args.no_cpu:
         threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
         log(f"cpu baseline (reference CPUBackend, {threads} threads)")
-        kind, cpu_tf, cpu_dt = cpu_baseline_gemm()
+        kind, cpu_tf, cpu_dt, n1 = cpu_baseline_gemm()
         cpu = {"value": round(cpu_tf, 4), "unit": "TFLOP/s", "cores": threads,
                "kind": "reference" if kind == "reference" else "port",
-               "sample": f"one 4096^3 NN fp32 GEMM ({cpu_dt:.2f} s) after a 1024^3 warm-up, CPUBackend::matmul "
-                         f"(AVX2 4x8 FMA + OpenMP) compiled from the reference sources"}
-        kind2, r18_ips, r18_dt = cpu_baseline_resnet18(2)
+               "sample": f"median of {n1} runs of the 4096^3 NN fp32 GEMM ({cpu_dt:.2f} s each) after one warm-up: "
+                         f"CPUBackend::matmul (AVX2 4x8 FMA + OpenMP) compiled from the reference sources"}
+        kind2, r18_ips, r18_dt, n2 = cpu_baseline_resnet18()
         cpu_r18 = {"value": round(r18_ips, 3), "unit": "img/s", "cores": threads,
                    "kind": "reference" if kind2 == "reference" else "port",
-                   "sample": f"2 images through the 20 ResNet-18 convs, conv2d -> batchNorm2d(eval) -> relu "
-                             f"({r18_dt:.2f} s)"}
+                   "sample": f"median of {n2} passes of batch 32 through the 20 ResNet-18 convs "
+                             f"(conv2d -> batchNorm2d(eval) -> relu, {r18_dt:.2f} s each) after one warm-up"}
         log(f"cpu gemm {cpu_tf * 1e3:.1f} GFLOP/s, cpu resnet18 {r18_ips:.3f} img/s")
 
     gemm_kernel_ms = ms

@@ -1,0 +1,70 @@
+"""Host-side checks that need no GPU: the C ABI library loads and exports every
+function include/omhip.h declares, the headers compile as C and C++23, the
+caching pool behaves (fake device), and bench.py refuses more than one GPU."""
+import ctypes
+import os
+import re
+import subprocess
+import sys
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "omhip.h")
+LIB = os.path.join(ROOT, "omnimatchdeeplearningtool_amd", "libomhip.so")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(omHip\w+)\s*\(", text)))
+
+
+def test_header_declares_the_hot_path():
+    names = declared_functions()
+    for must in ("omHipMatmul", "omHipMatmulTransB", "omHipBatchedMatmul", "omHipConv2d", "omHipConv2dBiasBnAct",
+                 "omHipBatchNorm2d", "omHipReLU", "omHipAddBias", "omHipMatmulF16", "omHipMatmulBF16", "omHipInit",
+                 "omHipMalloc", "omHipFree", "omHipCopyH2D", "omHipCopyD2H"):
+        assert must in names
+    assert len(names) >= 45
+
+
+@pytest.mark.skipif(not os.path.exists(LIB), reason="libomhip.so not built")
+def test_library_exports_every_declared_symbol():
+    lib = ctypes.CDLL(LIB)
+    missing = [n for n in declared_functions() if not hasattr(lib, n)]
+    assert not missing, f"not exported: {missing}"
+
+
+@pytest.mark.skipif(not os.path.exists(LIB), reason="libomhip.so not built")
+def test_python_signatures_cover_header():
+    import omnimatchdeeplearningtool_amd as om
+    sigs = set(om._SIGS) | {"omHipGetLastError"}
+    assert set(declared_functions()) == sigs
+
+
+def test_headers_compile_as_c_and_cpp23(tmp_path):
+    c_src = tmp_path / "c.c"
+    c_src.write_text('#include "omhip.h"\nint main(void){ int (*f)(int) = omHipInit; (void)f; return 0; }\n')
+    subprocess.run(["gcc", "-std=c99", "-Wall", "-Werror", f"-I{ROOT}/include", "-c", str(c_src), "-o",
+                    str(tmp_path / "c.o")], check=True)
+    cpp = tmp_path / "b.cpp"
+    cpp.write_text('#include "omhip_backend.hpp"\nint main(){ auto f = &om::HIPBackend::matmul; (void)f; return 0; }\n')
+    subprocess.run(["g++", "-std=c++23", "-Wall", "-Werror", f"-I{ROOT}/include", "-c", str(cpp), "-o",
+                    str(tmp_path / "b.o")], check=True)
+
+
+def test_caching_pool(tmp_path):
+    exe = tmp_path / "pool"
+    subprocess.run(["g++", "-std=c++17", "-O1", "-g", "-pthread", "-fsanitize=address,undefined",
+                    os.path.join(ROOT, "tests", "cpp", "test_caching_pool.cpp"), "-o", str(exe)], check=True)
+    r = subprocess.run([str(exe)], stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True, timeout=120)
+    print(r.stdout)
+    assert r.returncode == 0 and "ALL PASSED" in r.stdout
+
+
+def test_bench_refuses_multi_gpu():
+    r = subprocess.run([sys.executable, os.path.join(ROOT, "bench.py"), "--gpus", "2"], stdout=subprocess.PIPE,
+                       stderr=subprocess.PIPE, text=True, timeout=120)
+    assert r.returncode == 2
+    assert "one GPU" in r.stderr
