@@ -147,6 +147,137 @@ def bench_resnet18(om, steps: int, warmup: int, batch: int = 32):
     return ms, flops, roof_ms, per, max(errs)
 
 
+def bench_resnet50(om, steps: int, warmup: int, batch: int = 64):
+    """ResNet-50 conv stack forward (53 convs, fused conv+BN+ReLU) at batch 64."""
+    from omnimatchdeeplearningtool_amd.hiptime import StreamTimer
+    from resnet_shapes import conv_bytes, conv_flops, out_hw, resnet50_convs
+    import oracle as O
+    H = om.HIPBackend
+    layers = []
+    for li, (name, cin, h, w, cout, k, s, p) in enumerate(resnet50_convs()):
+        bnd = np.sqrt(6.0 / (cin * k * k))
+        ho, wo = out_hw(h, k, s, p), out_hw(w, k, s, p)
+        x = om.DeviceBuffer.from_numpy(O.randn((batch, cin, h, w), 700 + li))
+        wt = om.DeviceBuffer.from_numpy(O.uniform((cout, cin, k, k), 800 + li, -bnd, bnd))
+        bn = [om.DeviceBuffer.from_numpy(a) for a in (O.uniform((cout,), 900 + li, 0.5, 1.5), O.randn((cout,), 1000 + li, 0.1),
+                                                       O.randn((cout,), 1100 + li, 0.1), O.uniform((cout,), 1200 + li, 0.5, 1.5))]
+        y = om.DeviceBuffer.empty((batch, cout, ho, wo))
+        layers.append(((name, cin, h, w, cout, k, s, p), x, wt, bn, y))
+
+    def forward():
+        for (name, cin, h, w, cout, k, s, p), x, wt, bn, y in layers:
+            H.conv2dBiasBnAct(x, wt, None, bn[0], bn[1], bn[2], bn[3], 1e-5, 1, y, batch, cin, h, w, cout, k, k, s, p)
+
+    for _ in range(warmup):
+        forward()
+    om.synchronize()
+    timer = StreamTimer(om.stream_handle())
+    timer.start()
+    for _ in range(steps):
+        forward()
+    timer.stop()
+    ms = timer.ms() / steps
+    flops = sum(conv_flops(sh, batch) for sh, *_ in layers)
+    roof_ms = sum(max(conv_flops(sh, batch) / PEAK_FP32, conv_bytes(sh, batch) / PEAK_HBM) for sh, *_ in layers) * 1e3
+    return ms, flops, roof_ms
+
+
+def vit_gemm_shapes(batch: int = 64, tokens: int = 197, d: int = 768, heads: int = 12):
+    """(name, batch, M, N, K, transB) of the ViT-B/16 GEMMs: projections in the
+    Linear-weight layout (x[T,in] x W[out,in]^T), attention Q.K^T (transB) and P.V."""
+    T = batch * tokens
+    dh = d // heads
+    return [("qkv", 1, T, 3 * d, d, True), ("out_proj", 1, T, d, d, True), ("fc1", 1, T, 4 * d, d, True),
+            ("fc2", 1, T, d, 4 * d, True), ("qk_t", batch * heads, tokens, tokens, dh, True),
+            ("pv", batch * heads, tokens, dh, tokens, False)]
+
+
+def bench_vit_half(om, steps: int, warmup: int, bf16: bool):
+    """The ViT-B/16 GEMM set (batch 64, 197 tokens) with fp16 / bf16 inputs, fp32 accumulate."""
+    from omnimatchdeeplearningtool_amd.hiptime import StreamTimer
+    H = om.HIPBackend
+    dt = 1 if bf16 else 0
+    bufs = []
+    rng = np.random.default_rng(5)
+    for name, b, m, n, k, tb in vit_gemm_shapes():
+        a = rng.standard_normal(b * m * k, dtype=np.float32)
+        w = (rng.standard_normal(b * n * k, dtype=np.float32) * (0.02 if b == 1 else 1.0)).astype(np.float32)
+        da, dw = om.DeviceBuffer.from_numpy(a), om.DeviceBuffer.from_numpy(w)
+        ha, hw = om.DeviceBuffer.empty((a.size,), np.uint16), om.DeviceBuffer.empty((w.size,), np.uint16)
+        H.convertToHalf(da, ha, a.size, bf16=bf16)
+        H.convertToHalf(dw, hw, w.size, bf16=bf16)
+        c = om.DeviceBuffer.empty((b * m * n,))
+        bufs.append((name, b, m, n, k, tb, ha, hw, c))
+
+    def run(item):
+        name, b, m, n, k, tb, ha, hw, c = item
+        H.gemmStridedBatchedHalf(dt, 0, tb, b, m, n, k, ha, k, m * k, hw, k if tb else n, n * k, c, n, m * n)
+
+    per = []
+    total_ms = 0.0
+    flops_total = 0.0
+    for item in bufs:
+        for _ in range(warmup):
+            run(item)
+        om.synchronize()
+        t = StreamTimer(om.stream_handle())
+        t.start()
+        for _ in range(steps):
+            run(item)
+        t.stop()
+        ms = t.ms() / steps
+        name, b, m, n, k = item[:5]
+        f = 2.0 * b * m * n * k
+        flops_total += f
+        total_ms += ms
+        per.append({"gemm": name, "shape": [b, m, n, k], "ms": round(ms, 4), "tflops": round(f / ms / 1e9, 1)})
+    return total_ms, flops_total, per
+
+
+def bench_mlp(om, steps: int, warmup: int, batch: int = 128):
+    """MLP 784-256-128-10 (ReLU) forward + backward through the HAL entries, fp32, batch 128."""
+    from omnimatchdeeplearningtool_amd.hiptime import StreamTimer
+    import oracle as O
+    H = om.HIPBackend
+    dims = [784, 256, 128, 10]
+    x = om.DeviceBuffer.from_numpy(O.uniform((batch, 784), 1))
+    Ws = [om.DeviceBuffer.from_numpy(O.uniform((i, o), 10 + j, -np.sqrt(6 / i), np.sqrt(6 / i)))
+          for j, (i, o) in enumerate(zip(dims[:-1], dims[1:]))]
+    bs = [om.DeviceBuffer.from_numpy(np.zeros(o, np.float32)) for o in dims[1:]]
+    z = [om.DeviceBuffer.empty((batch, o)) for o in dims[1:]]
+    a = [x] + [om.DeviceBuffer.empty((batch, o)) for o in dims[1:-1]]
+    g = [om.DeviceBuffer.empty((batch, o)) for o in dims[1:]]
+    gA = [om.DeviceBuffer.empty((batch, i)) for i in dims[:-1]]
+    gW = [om.DeviceBuffer.empty((i, o)) for i, o in zip(dims[:-1], dims[1:])]
+    H.fillValue(g[-1], batch * 10, 0.01)
+
+    def step():
+        for j in range(3):
+            i, o = dims[j], dims[j + 1]
+            H.matmul(a[j], Ws[j], z[j], batch, i, o)
+            H.addBias(z[j], bs[j], z[j], batch, o)
+            if j < 2:
+                H.relu(z[j], a[j + 1], batch * o)
+        for j in reversed(range(3)):
+            i, o = dims[j], dims[j + 1]
+            H.matmulTransA(a[j], g[j], gW[j], i, batch, o)        # dW = A^T G
+            H.matmulTransB(g[j], Ws[j], gA[j], batch, o, i)        # dA = G W^T (as the reference, every layer)
+            if j > 0:
+                H.reluBackward(z[j - 1], gA[j], g[j - 1], batch * i)
+
+    for _ in range(warmup):
+        step()
+    om.synchronize()
+    t = StreamTimer(om.stream_handle())
+    t.start()
+    for _ in range(steps):
+        step()
+    t.stop()
+    ms = t.ms() / steps
+    flops = sum(3 * 2.0 * batch * i * o for i, o in zip(dims[:-1], dims[1:]))
+    return ms, flops
+
+
 def cpu_baseline_gemm(budget_s: float = 10.0):
     """Reference CPUBackend::matmul (oracle/_ref) on 4096^3: one warm-up, then
     repeated for about budget_s seconds; the median run is reported."""
@@ -191,6 +322,75 @@ def cpu_baseline_resnet18(batch: int = 32, budget_s: float = 10.0):
         times.append(one_pass())
     dt = float(np.median(times))
     return backend, batch / dt, dt, len(times)
+
+
+def cpu_baseline_resnet50(n_img: int = 2):
+    """Reference conv2d -> batchNorm2d(eval) -> relu over the 53 ResNet-50 convs, n_img images (one pass)."""
+    import oracle as O
+    from resnet_shapes import resnet50_convs
+    backend = "reference" if O.ref_lib() is not None else "oracle"
+    t_total = 0.0
+    for li, (name, cin, h, w, cout, k, s, p) in enumerate(resnet50_convs()):
+        x, wt = O.randn((n_img, cin, h, w), 700 + li), O.randn((cout, cin, k, k), 800 + li, 0.05)
+        g, b = O.uniform((cout,), 900 + li, 0.5, 1.5), O.randn((cout,), 1000 + li, 0.1)
+        m, v = O.randn((cout,), 1100 + li, 0.1), O.uniform((cout,), 1200 + li, 0.5, 1.5)
+        t = time.perf_counter()
+        y = O.conv2d(x, wt, None, s, p, backend=backend)
+        y, _, _ = O.batchnorm2d_eval(y, g, b, m, v, backend=backend)
+        O.relu(y, backend=backend)
+        t_total += time.perf_counter() - t
+    return backend, n_img / t_total, t_total
+
+
+def cpu_baseline_vit():
+    """Reference matmul / batchedMatmul (+ transpose2d for the B^T operands) on one image's
+    share of the ViT GEMM set (197 tokens), fp32 on fp16-rounded inputs."""
+    import oracle as O
+    backend = "reference" if O.ref_lib() is not None else "oracle"
+    flops = 0.0
+    t_total = 0.0
+    for name, b, m, n, k, tb in vit_gemm_shapes(batch=1):
+        a = O.randn((b, m, k), 1).astype(np.float16).astype(np.float32)
+        w = O.randn((b, n, k) if tb else (b, k, n), 2).astype(np.float16).astype(np.float32)
+        t = time.perf_counter()
+        for i in range(b):
+            wi = O.transpose2d(w[i], backend=backend) if tb else w[i]
+            O.matmul(a[i], wi, backend=backend)
+        t_total += time.perf_counter() - t
+        flops += 2.0 * b * m * n * k
+    return backend, flops / t_total / 1e12, t_total
+
+
+def cpu_baseline_mlp(reps: int = 20):
+    """The MLP fwd+bwd step as the reference computes it (matmul, addBias, relu;
+    MatMulBackward's explicit transposes + matmul for dA and dW on every layer)."""
+    import oracle as O
+    backend = "reference" if O.ref_lib() is not None else "oracle"
+    dims = [784, 256, 128, 10]
+    x = O.uniform((128, 784), 1)
+    Ws = [O.uniform((i, o), 10 + j, -0.1, 0.1) for j, (i, o) in enumerate(zip(dims[:-1], dims[1:]))]
+    G = O.randn((128, 10), 3, 0.01)
+
+    def step():
+        acts, pre = [x], []
+        for j, W in enumerate(Ws):
+            z = O.add_bias(O.matmul(acts[-1], W, backend=backend), np.zeros(W.shape[1], np.float32), backend=backend)
+            pre.append(z)
+            if j < 2:
+                acts.append(O.relu(z, backend=backend))
+        g = G
+        for j in reversed(range(3)):
+            O.matmul(O.transpose2d(acts[j], backend=backend), g, backend=backend)
+            gA = O.matmul(g, O.transpose2d(Ws[j], backend=backend), backend=backend)
+            if j > 0:
+                g = O.relu_backward(pre[j - 1], gA, backend=backend)
+
+    step()
+    t = time.perf_counter()
+    for _ in range(reps):
+        step()
+    dt = (time.perf_counter() - t) / reps
+    return backend, dt * 1e3
 
 
 def traffic_probe():
@@ -264,8 +464,21 @@ def main():
     img_s = 32.0 / (r_ms / 1e3)
     log(f"resnet18 {r_ms:.3f} ms/batch  {img_s:.0f} img/s  roof frac {r_roof_ms / r_ms:.3f}  parity {conv_err:.2e}")
 
+    log("resnet50 conv stack b64")
+    r50_ms, r50_flops, r50_roof = bench_resnet50(om, max(3, args.steps // 10), 1)
+    log(f"resnet50 {r50_ms:.3f} ms/batch  {64 / r50_ms * 1e3:.0f} img/s  roof frac {r50_roof / r50_ms:.3f}")
+    vit = {}
+    for bf in (False, True):
+        v_ms, v_flops, v_per = bench_vit_half(om, max(5, args.steps // 5), 2, bf)
+        vit["bf16" if bf else "fp16"] = {"ms_per_set": round(v_ms, 4), "tflops": round(v_flops / v_ms / 1e9, 1),
+                                         "frac_of_2516_tflops": round(v_flops / v_ms / 1e9 / 2516.6, 4), "gemms": v_per}
+        log(f"vit {'bf16' if bf else 'fp16'} {v_ms:.3f} ms  {v_flops / v_ms / 1e9:.1f} TFLOP/s")
+    mlp_ms, mlp_flops = bench_mlp(om, max(20, args.steps), 5)
+    log(f"mlp step {mlp_ms * 1e3:.1f} us")
+
     cpu = None
     cpu_r18 = None
+    cpu_extra = {}
     if rank == 0 and not args.no_cpu:
         threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
         log(f"cpu baseline (reference CPUBackend, {threads} threads)")
@@ -280,6 +493,15 @@ def main():
                    "sample": f"median of {n2} passes of batch 32 through the 20 ResNet-18 convs "
                              f"(conv2d -> batchNorm2d(eval) -> relu, {r18_dt:.2f} s each) after one warm-up"}
         log(f"cpu gemm {cpu_tf * 1e3:.1f} GFLOP/s, cpu resnet18 {r18_ips:.3f} img/s")
+        k50, ips50, dt50 = cpu_baseline_resnet50()
+        cpu_extra["resnet50"] = {"value": round(ips50, 3), "unit": "img/s", "cores": threads, "kind": k50 if k50 == "reference" else "port",
+                                 "sample": f"2 images through the 53 ResNet-50 convs ({dt50:.2f} s, one pass)"}
+        kv, tfv, dtv = cpu_baseline_vit()
+        cpu_extra["vit"] = {"value": round(tfv, 4), "unit": "TFLOP/s", "cores": threads, "kind": kv if kv == "reference" else "port",
+                            "sample": f"one image's share of the ViT GEMM set (197 tokens, fp16-rounded fp32 inputs), {dtv:.2f} s"}
+        km, msm = cpu_baseline_mlp()
+        cpu_extra["mlp"] = {"value": round(msm, 3), "unit": "ms/step", "cores": threads, "kind": km if km == "reference" else "port",
+                            "sample": "mean of 20 MLP fwd+bwd steps after one warm-up"}
 
     gemm_kernel_ms = ms
     traffic = _traffic("gemm_f32_4096_nn")
@@ -309,6 +531,14 @@ def main():
                           "roofline": {"bound": "mfma (per-layer max(flops/157.3T, bytes/8TB/s))",
                                        "roof_ms": round(r_roof_ms, 4), "frac": round(r_roof_ms / r_ms, 4)},
                           "layers": per, "cpu_baseline": cpu_r18},
+        "resnet50_conv": {"value": round(64 / r50_ms * 1e3, 1), "unit": "img/s", "batch": 64, "ms_per_batch": round(r50_ms, 4),
+                          "tflops": round(r50_flops / r50_ms / 1e9, 2),
+                          "roofline": {"roof_ms": round(r50_roof, 4), "frac": round(r50_roof / r50_ms, 4)},
+                          "cpu_baseline": cpu_extra.get("resnet50")},
+        "vit_b16_gemms": {"batch": 64, "tokens": 197, "hidden": 768, "heads": 12, **vit,
+                          "cpu_baseline": cpu_extra.get("vit")},
+        "mlp_784_256_128_10": {"batch": 128, "us_per_step": round(mlp_ms * 1e3, 2),
+                               "gflops": round(mlp_flops / mlp_ms / 1e6, 1), "cpu_baseline": cpu_extra.get("mlp")},
     }
     print(json.dumps(line), flush=True)
 
