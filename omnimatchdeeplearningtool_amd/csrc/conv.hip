@@ -162,10 +162,12 @@ struct WeightLoader {
     }
 };
 
-// Implicit im2col loader -> LDS [BK][BN+4]. Thread t owns pixel column
+// Implicit im2col loader -> LDS [BN][BK+4] (K contiguous, like the weights,
+// so both MFMA operands are read 4 k at a time). Thread t owns pixel column
 // c = t % BN and the RPT consecutive rows g*RPT .. g*RPT+RPT-1 of each slice
 // (g = t / BN, the same for all lanes of a wave since BN >= 64), so the rows'
-// table entries are wave-uniform scalar loads. Per pixel: one byte offset
+// table entries are wave-uniform scalar loads and the thread's RPT values are
+// contiguous in its pixel's LDS row (128-bit stores). Per pixel: one byte offset
 // (into a buffer view that starts pad*W+pad floats before x, so it is never
 // negative) and the mask of taps that fall outside the image.
 //   MODE 0: KH*KW <= 32 (one 32-bit mask), MODE 1: <= 64 (64-bit mask),
@@ -174,8 +176,8 @@ template <int BN, int BK, int NT, int MODE>
 struct GatherLoader {
     static constexpr int TPC = NT / BN;
     static constexpr int RPT = BK / TPC;
-    static_assert(NT % BN == 0 && BK % TPC == 0 && BN >= 64, "gather mapping");
-    using Shape = LdsShape<false, BN, BK>;
+    static_assert(NT % BN == 0 && BK % TPC == 0 && BN >= 64 && RPT % 4 == 0, "gather mapping");
+    using Shape = LdsShape<true, BN, BK>;
     __amdgpu_buffer_rsrc_t r;
     uint32_t voffPix;
     uint32_t invLo, invHi;
@@ -230,7 +232,10 @@ struct GatherLoader {
     __device__ void store(float* s, int tid) const {
         const int c = tid % BN, g = tid / BN;
 #pragma unroll
-        for (int j = 0; j < RPT; ++j) s[(g * RPT + j) * Shape::LD + c] = v[j];
+        for (int j = 0; j < RPT; j += 4) {
+            const f32x4 q = {v[j], v[j + 1], v[j + 2], v[j + 3]};
+            *reinterpret_cast<f32x4*>(s + c * Shape::LD + g * RPT + j) = q;
+        }
     }
 };
 
@@ -238,7 +243,7 @@ template <class Cfg, bool VA, int MODE>
 __global__ __launch_bounds__(Cfg::NT) void conv_igemm_kernel(ConvParams p) {
     extern __shared__ float smem[];
     using SA = LdsShape<true, Cfg::BM, Cfg::BK>;
-    using SB = LdsShape<false, Cfg::BN, Cfg::BK>;
+    using SB = LdsShape<true, Cfg::BN, Cfg::BK>;
     constexpr int STAGE = SA::SIZE + SB::SIZE;
     float* sEpi = smem + 2 * STAGE;   // [5][BM]: bias, mean, invStd, gamma, beta
 
@@ -295,7 +300,7 @@ __global__ __launch_bounds__(Cfg::NT) void conv_igemm_kernel(ConvParams p) {
                 lb.load(kBeg + (t + 1) * Cfg::BK, tid);
                 la.load(kBeg + (t + 1) * Cfg::BK, kEnd, tid);
             }
-            mma_slice<Cfg, true, false>(smem, smem + SA::SIZE, acc, wm, wn, lane);
+            mma_slice<Cfg, true, true>(smem, smem + SA::SIZE, acc, wm, wn, lane);
             if (more) {
                 la.store(smem + STAGE, tid);
                 lb.store(smem + STAGE + SA::SIZE, tid);
@@ -308,7 +313,7 @@ __global__ __launch_bounds__(Cfg::NT) void conv_igemm_kernel(ConvParams p) {
                 lb.load(kBeg + (t + 2) * Cfg::BK, tid);
                 la.load(kBeg + (t + 2) * Cfg::BK, kEnd, tid);
             }
-            mma_slice<Cfg, true, false>(smem + STAGE, smem + STAGE + SA::SIZE, acc, wm, wn, lane);
+            mma_slice<Cfg, true, true>(smem + STAGE, smem + STAGE + SA::SIZE, acc, wm, wn, lane);
             if (more) {
                 la.store(smem, tid);
                 lb.store(smem + SA::SIZE, tid);
@@ -390,13 +395,18 @@ __global__ void conv_splitk_finish(ConvParams p) {
 #ifndef OMHIP_CONV_BK
 #define OMHIP_CONV_BK 16
 #endif
+#ifndef OMHIP_CONV_TILE
+#define OMHIP_CONV_TILE 64, 64, 32, 32   // BM, BN, WM, WN
+#endif
 constexpr int kConvBK = OMHIP_CONV_BK;
-using ConvCfg = TileCfg<64, 64, kConvBK, 32, 32>;
+template <int BM, int BN, int WM, int WN>
+using ConvCfgT = TileCfg<BM, BN, kConvBK, WM, WN>;
+using ConvCfg = ConvCfgT<OMHIP_CONV_TILE>;
 
 template <class Cfg>
 static size_t convLds() {
     // two A+B stages and the epilogue vectors
-    return (2 * (LdsShape<true, Cfg::BM, Cfg::BK>::SIZE + LdsShape<false, Cfg::BN, Cfg::BK>::SIZE) + 5 * Cfg::BM) *
+    return (2 * (LdsShape<true, Cfg::BM, Cfg::BK>::SIZE + LdsShape<true, Cfg::BN, Cfg::BK>::SIZE) + 5 * Cfg::BM) *
            sizeof(float);
 }
 

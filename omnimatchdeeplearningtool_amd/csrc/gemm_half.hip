@@ -6,15 +6,29 @@
 // fp32 (cpu_backend.ixx:239-286). These entries compute what
 // halfToFloat(A), halfToFloat(B), matmul would, with fp32 accumulation.
 //
-// Same block structure as the fp32 tile (double-buffered LDS slices, 32x32
-// MFMA blocks per wave, the two lane halves reducing the two halves of a
-// slice). Both operands are kept K-contiguous in LDS ([R][BK+8] halves) so a
-// fragment (8 consecutive k of one row) is one ds_read_b128; an operand that is
-// R-contiguous in HBM (B of A*B, A of A^T*B) is transposed on its way into LDS.
+// Two kernels:
+//  * gemm_half_fast: operands whose contiguous axis, leading dimension and base
+//    are multiples of 8 halves (every layout the networks produce). Slices are
+//    fetched with raw buffer loads whose per-lane offset is fixed for the whole
+//    K walk (the slice start rides in the scalar offset; rows past the matrix
+//    fall outside the buffer range and read 0), so the mainloop spends almost
+//    no VALU on addressing. Both operands sit K-contiguous in LDS ([R][BK+8]
+//    halves), so an MFMA fragment (8 consecutive k of one row) is one
+//    ds_read_b128. An operand that is R-contiguous in HBM (B of A*B, A of
+//    A^T*B) is loaded as 8x8 blocks and transposed in registers with v_perm
+//    before the LDS store. The MFMA takes the B fragment as its first operand,
+//    so each lane ends up holding 4 consecutive output columns and the fp32
+//    tile leaves in 128-bit stores.
+//  * gemm_half_generic: any other layout (element loads with bounds checks).
+//
+// Within a 16-deep MFMA step the two 32-lane halves supply k = 0..7 and
+// k = 8..15 of the step; the sum over k is order-free, so this only changes
+// rounding order.
 #include "omhip_internal.hpp"
 #include "../../include/omhip.h"
 
 #include <algorithm>
+#include <type_traits>
 
 namespace omhip {
 
@@ -22,6 +36,8 @@ typedef float f32x16h __attribute__((ext_vector_type(16)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef uint16_t u16x8 __attribute__((ext_vector_type(8)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4h __attribute__((ext_vector_type(4)));
 
 struct GemmHalfParams {
     const uint16_t* A;
@@ -131,7 +147,7 @@ __device__ __forceinline__ void tileCoordsH(int bid, int total, int tilesM, int 
 }
 
 template <class Cfg, bool BF16, bool TA, bool TB, bool VA, bool VB>
-__global__ __launch_bounds__(Cfg::NT) void gemm_half_kernel(GemmHalfParams p) {
+__global__ __launch_bounds__(Cfg::NT) void gemm_half_generic(GemmHalfParams p) {
     extern __shared__ uint16_t hsmem[];
     constexpr int SA = Cfg::BM * Cfg::LD, SB = Cfg::BN * Cfg::LD, STAGE = SA + SB;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -208,13 +224,12 @@ __global__ __launch_bounds__(Cfg::NT) void gemm_half_kernel(GemmHalfParams p) {
         }
 }
 
-using HCfgL = HCfg<256, 256, 32, 128, 128>;
 using HCfgM = HCfg<128, 128, 32, 64, 64>;
 using HCfgS = HCfg<64, 64, 32, 32, 32>;
 
 template <class Cfg, bool BF16, bool TA, bool TB, bool VA, bool VB>
-static int launchH(GemmHalfParams prm, int batch) {
-    auto kern = gemm_half_kernel<Cfg, BF16, TA, TB, VA, VB>;
+static int launchGeneric(GemmHalfParams prm, int batch) {
+    auto kern = gemm_half_generic<Cfg, BF16, TA, TB, VA, VB>;
     const size_t lds = 2 * (size_t)(Cfg::BM + Cfg::BN) * Cfg::LD * sizeof(uint16_t);
     static bool s_attr = false;
     if (!s_attr) {
@@ -230,31 +245,429 @@ static int launchH(GemmHalfParams prm, int batch) {
 }
 
 template <class Cfg, bool BF16, bool TA, bool TB>
-static int launchHV(const GemmHalfParams& prm, int batch, bool va, bool vb) {
-    if (va && vb) return launchH<Cfg, BF16, TA, TB, true, true>(prm, batch);
-    if (va) return launchH<Cfg, BF16, TA, TB, true, false>(prm, batch);
-    if (vb) return launchH<Cfg, BF16, TA, TB, false, true>(prm, batch);
-    return launchH<Cfg, BF16, TA, TB, false, false>(prm, batch);
+static int launchGenericV(const GemmHalfParams& prm, int batch, bool va, bool vb) {
+    if (va && vb) return launchGeneric<Cfg, BF16, TA, TB, true, true>(prm, batch);
+    if (va) return launchGeneric<Cfg, BF16, TA, TB, true, false>(prm, batch);
+    if (vb) return launchGeneric<Cfg, BF16, TA, TB, false, true>(prm, batch);
+    return launchGeneric<Cfg, BF16, TA, TB, false, false>(prm, batch);
 }
 
 template <bool BF16, bool TA, bool TB>
-static int launchHC(const GemmHalfParams& prm, int batch, bool va, bool vb) {
-    const long long cus = cuCount();
-    auto tiles = [&](int bm, int bn) {
-        return (long long)((prm.M + bm - 1) / bm) * ((prm.N + bn - 1) / bn) * batch;
+static int launchGenericC(const GemmHalfParams& prm, int batch, bool va, bool vb) {
+    const long long tiles = (long long)((prm.M + 127) / 128) * ((prm.N + 127) / 128) * batch;
+    if (tiles >= cuCount()) return launchGenericV<HCfgM, BF16, TA, TB>(prm, batch, va, vb);
+    return launchGenericV<HCfgS, BF16, TA, TB>(prm, batch, va, vb);
+}
+
+// ---- fast kernel -------------------------------------------------------------
+
+// Offsets at or above this byte count are outside every buffer view used by the
+// fast kernel (views are limited to 2^30 bytes), so two such terms never wrap.
+constexpr uint32_t kOOBH = 0x40000000u;
+constexpr long long kMaxViewBytes = 0x40000000LL;
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t halfRsrc(const void* base, uint32_t bytes) {
+    // raw buffer, stride 0, range-checked against `bytes`
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)bytes, 0x00020000);
+}
+__device__ __forceinline__ u32x4 ld128(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+    return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
+}
+
+struct HalfFastParams {
+    const uint16_t* A;
+    const uint16_t* B;
+    float* C;
+    int M, N, K;
+    int lda, ldb;        // < 2^21
+    long long ldc, sA, sB, sC;
+    int tilesM, tilesN;
+};
+
+// K-major operand: element (r,k) at P[r*ld + k]. An R x BK slice is R*BK/8
+// 16-byte chunks; chunk e is (row e / (BK/8), k 8*(e % (BK/8))), so 8
+// consecutive lanes read one row's 128 contiguous bytes. The buffer view starts
+// at the tile's first row and ends after row rowsValid-1's K-th element, so
+// rows past the matrix read 0; chunks past K are masked on the last slice.
+template <int R, int BK, int NT>
+struct KMajorSlice {
+    static constexpr int CH = BK / 8;
+    static constexpr int PER_T = R * CH / NT;
+    static_assert(R * CH % NT == 0, "slice must split evenly");
+    static constexpr int NLOADS = PER_T, NSTORES = PER_T;   // per thread and slice
+    struct Regs {
+        u32x4 v[PER_T];
     };
-    // the 256x256 tile is only register-clean with 128-bit loads on both operands
-    if (va && vb && tiles(256, 256) >= cus) return launchHV<HCfgL, BF16, TA, TB>(prm, batch, va, vb);
-    if (tiles(128, 128) >= cus) return launchHV<HCfgM, BF16, TA, TB>(prm, batch, va, vb);
-    return launchHV<HCfgS, BF16, TA, TB>(prm, batch, va, vb);
+    __amdgpu_buffer_rsrc_t r;
+    uint32_t voff[PER_T];
+
+    __device__ void init(const uint16_t* base, int ld, int rowsValid, int K, int tid) {
+        const int rv = rowsValid < R ? rowsValid : R;
+        r = halfRsrc(base, ((uint32_t)(rv - 1) * (uint32_t)ld + (uint32_t)K) * 2u);
+#pragma unroll
+        for (int i = 0; i < PER_T; ++i) {
+            const int e = tid + i * NT;
+            voff[i] = ((uint32_t)(e / CH) * (uint32_t)ld + (uint32_t)(e % CH) * 8u) * 2u;
+        }
+    }
+    // FULL: the slice lies inside K (no per-chunk test).
+    template <bool FULL>
+    __device__ void load(int k0, int K, int tid, Regs& g) const {
+        const uint32_t soff = (uint32_t)k0 * 2u;
+        if (FULL || k0 + BK <= K) {
+#pragma unroll
+            for (int i = 0; i < PER_T; ++i) g.v[i] = ld128(r, voff[i], soff);
+        } else {
+#pragma unroll
+            for (int i = 0; i < PER_T; ++i) {
+                const int kc = ((tid + i * NT) % CH) * 8;
+                g.v[i] = ld128(r, (k0 + kc < K) ? voff[i] : kOOBH, soff);   // K % 8 == 0: all-or-none
+            }
+        }
+    }
+    template <int LD>
+    __device__ void store(uint16_t* s, int tid, const Regs& g) const {
+#pragma unroll
+        for (int i = 0; i < PER_T; ++i) {
+            const int e = tid + i * NT;
+            *reinterpret_cast<u32x4*>(s + (e / CH) * LD + (e % CH) * 8) = g.v[i];
+        }
+    }
+};
+
+// R-major operand: element (r,k) at P[k*ld + r]. A slice is (R/8) x (BK/8)
+// blocks of 8 k x 8 r; block e is (rb = e / (BK/8), kb = e % (BK/8)). A thread
+// loads its block's 8 rows (one 16-byte load each; the row step rides in the
+// scalar offset) and transposes it in registers into 8 K-contiguous 16-byte
+// LDS rows. The view starts at the tile's first column and ends after row
+// K-1's last valid column, so rows past K read 0; blocks past the matrix's
+// columns are pointed outside the view.
+template <int R, int BK, int NT>
+struct RMajorSlice {
+    static constexpr int KB = BK / 8;
+    static constexpr int BLKS = (R / 8) * KB;
+    static constexpr bool PARTIAL = BLKS < NT;   // only threads < BLKS carry a block
+    static constexpr int PER_T = PARTIAL ? 1 : BLKS / NT;
+    static_assert(PARTIAL ? (BLKS % 64 == 0) : (BLKS % NT == 0), "blocks must split evenly over waves");
+    static constexpr int NLOADS = 8 * PER_T, NSTORES = 8 * PER_T;   // per loading thread and slice
+    struct Regs {
+        u32x4 v[PER_T][8];
+    };
+    __amdgpu_buffer_rsrc_t r;
+    uint32_t voff[PER_T];
+    uint32_t ld2;
+
+    __device__ void init(const uint16_t* base, int ld, int colsValid, int K, int tid) {
+        ld2 = (uint32_t)ld * 2u;
+        const int cv = colsValid < R ? colsValid : R;
+        r = halfRsrc(base, (uint32_t)(K - 1) * ld2 + (uint32_t)cv * 2u);
+#pragma unroll
+        for (int i = 0; i < PER_T; ++i) {
+            const int e = tid + i * NT;
+            const int rb = e / KB, kb = e % KB;
+            voff[i] = (rb * 8 < cv) ? (uint32_t)(kb * 8) * ld2 + (uint32_t)(rb * 16) : kOOBH;   // cols % 8 == 0
+        }
+    }
+    template <bool FULL>   // rows past K read 0 either way
+    __device__ void load(int k0, int /*K*/, int tid, Regs& g) const {
+        if (PARTIAL && tid >= BLKS) return;
+#pragma unroll
+        for (int i = 0; i < PER_T; ++i)
+#pragma unroll
+            for (int j = 0; j < 8; ++j) g.v[i][j] = ld128(r, voff[i], (uint32_t)(k0 + j) * ld2);
+    }
+    static __device__ __forceinline__ uint32_t pair(uint32_t lo, uint32_t hi, bool upper) {
+        // (lo.half[upper], hi.half[upper]) packed low-to-high
+        return __builtin_amdgcn_perm(hi, lo, upper ? 0x07060302u : 0x05040100u);
+    }
+    template <int LD>
+    __device__ void store(uint16_t* s, int tid, const Regs& g) const {
+        if (PARTIAL && tid >= BLKS) return;
+#pragma unroll
+        for (int i = 0; i < PER_T; ++i) {
+            const int e = tid + i * NT;
+            const int rb = e / KB, kb = e % KB;
+#pragma unroll
+            for (int n = 0; n < 8; ++n) {
+                const int d = n >> 1;
+                const bool up = (n & 1) != 0;
+                const u32x4 col = {pair(g.v[i][0][d], g.v[i][1][d], up), pair(g.v[i][2][d], g.v[i][3][d], up),
+                                   pair(g.v[i][4][d], g.v[i][5][d], up), pair(g.v[i][6][d], g.v[i][7][d], up)};
+                *reinterpret_cast<u32x4*>(s + (rb * 8 + n) * LD + kb * 8) = col;
+            }
+        }
+    }
+};
+
+template <int BM_, int BN_, int BK_, int WM_, int WN_>
+struct FCfg {
+    static constexpr int BM = BM_, BN = BN_, BK = BK_, WM = WM_, WN = WN_;
+    static constexpr int WAVES_N = BN / WN;
+    static constexpr int NT = (BM / WM) * (BN / WN) * 64;
+    static constexpr int FM = WM / 32, FN = WN / 32;
+    static constexpr int LD = BK + 8;   // halves per LDS row
+    static constexpr int SA = BM * LD, SB = BN * LD, STAGE = SA + SB;
+    static constexpr size_t LDS_BYTES = 2 * (size_t)STAGE * sizeof(uint16_t);
+    static_assert(BK % 16 == 0 && WM % 32 == 0 && WN % 32 == 0, "tile shape");
+};
+
+template <bool BF16>
+__device__ __forceinline__ f32x16h mfma16u(const u32x4& a, const u32x4& b, const f32x16h& c) {
+    return mfma16<BF16>(__builtin_bit_cast(u16x8, a), __builtin_bit_cast(u16x8, b), c);
+}
+
+// Scheduling-group masks of __builtin_amdgcn_sched_group_barrier.
+constexpr int kSgMfma = 0x008, kSgVmemRead = 0x020, kSgDsRead = 0x100, kSgDsWrite = 0x200;
+
+template <int I, int N, class F>
+__device__ __forceinline__ void staticFor(F&& f) {
+    if constexpr (I < N) {
+        f(std::integral_constant<int, I>{});
+        staticFor<I + 1, N>(f);
+    }
+}
+
+// Fragments of 16-deep MFMA step s: 8 consecutive k (lane half h: k = 16s+8h ..)
+// of rows li of each 32-row block of the wave's sub-tile.
+template <class Cfg>
+__device__ __forceinline__ void readFrags(const uint16_t* sA, const uint16_t* sB, int s, u32x4 (&a)[Cfg::FM],
+                                          u32x4 (&b)[Cfg::FN], int wm, int wn, int li, int h) {
+    const int kc = s * 16 + h * 8;
+#pragma unroll
+    for (int fm = 0; fm < Cfg::FM; ++fm)
+        a[fm] = *reinterpret_cast<const u32x4*>(sA + (wm * Cfg::WM + fm * 32 + li) * Cfg::LD + kc);
+#pragma unroll
+    for (int fn = 0; fn < Cfg::FN; ++fn)
+        b[fn] = *reinterpret_cast<const u32x4*>(sB + (wn * Cfg::WN + fn * 32 + li) * Cfg::LD + kc);
+}
+
+template <class Cfg, bool BF16, bool SWAP>
+__device__ __forceinline__ void mfmaStep(const u32x4 (&a)[Cfg::FM], const u32x4 (&b)[Cfg::FN],
+                                         f32x16h (&acc)[Cfg::FM][Cfg::FN]) {
+    // SWAP: B first, so the 32x32 result has n along its rows and m along lanes.
+#pragma unroll
+    for (int fm = 0; fm < Cfg::FM; ++fm)
+#pragma unroll
+        for (int fn = 0; fn < Cfg::FN; ++fn)
+            acc[fm][fn] = SWAP ? mfma16u<BF16>(b[fn], a[fm], acc[fm][fn]) : mfma16u<BF16>(a[fm], b[fn], acc[fm][fn]);
+}
+
+// Interleaves NMEM memory instructions of kind MASK with NMFMA MFMAs (spread
+// evenly), so LDS traffic overlaps matrix-core execution.
+template <int MASK, int NMEM, int NMFMA, int I = 0, int LEFT = NMFMA>
+__device__ __forceinline__ void interleave() {
+    if constexpr (I < NMEM) {
+        constexpr int m = (LEFT + (NMEM - I) - 1) / (NMEM - I);
+        __builtin_amdgcn_sched_group_barrier(MASK, 1, 0);
+        if constexpr (m > 0) __builtin_amdgcn_sched_group_barrier(kSgMfma, m, 0);
+        interleave<MASK, NMEM, NMFMA, I + 1, LEFT - m>();
+    } else if constexpr (LEFT > 0) {
+        __builtin_amdgcn_sched_group_barrier(kSgMfma, LEFT, 0);
+    }
+}
+
+// SWAP (C rows allow 128-bit stores: N, ldc, batch stride multiples of 4 and a
+// 16-byte aligned base) puts the B fragment first so each lane holds 4
+// consecutive columns; otherwise lanes run along n for coalesced 32-bit stores.
+template <class Cfg, bool BF16, bool TA, bool TB, bool SWAP>
+__global__ __launch_bounds__(Cfg::NT) void gemm_half_fast(HalfFastParams p) {
+    extern __shared__ uint16_t hsm[];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave / Cfg::WAVES_N, wn = wave % Cfg::WAVES_N;
+    const int li = lane & 31, h = lane >> 5;
+    int tm, tn;
+    tileCoordsH(blockIdx.x, p.tilesM * p.tilesN, p.tilesM, p.tilesN, tm, tn);
+    const long long batch = blockIdx.z;
+    const int m0 = tm * Cfg::BM, n0 = tn * Cfg::BN;
+    const uint16_t* Ab = p.A + batch * p.sA;
+    const uint16_t* Bb = p.B + batch * p.sB;
+
+    // A's rows are m: K-major unless transposed. B's rows are n: K-major when transposed.
+    using LA = std::conditional_t<TA, RMajorSlice<Cfg::BM, Cfg::BK, Cfg::NT>, KMajorSlice<Cfg::BM, Cfg::BK, Cfg::NT>>;
+    using LB = std::conditional_t<TB, KMajorSlice<Cfg::BN, Cfg::BK, Cfg::NT>, RMajorSlice<Cfg::BN, Cfg::BK, Cfg::NT>>;
+    LA la;
+    LB lb;
+    la.init(TA ? Ab + m0 : Ab + (long long)m0 * p.lda, p.lda, p.M - m0, p.K, tid);
+    lb.init(TB ? Bb + (long long)n0 * p.ldb : Bb + n0, p.ldb, p.N - n0, p.K, tid);
+    typename LA::Regs ra;
+    typename LB::Regs rb;
+
+    f32x16h acc[Cfg::FM][Cfg::FN];
+#pragma unroll
+    for (int i = 0; i < Cfg::FM; ++i)
+#pragma unroll
+        for (int j = 0; j < Cfg::FN; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+
+    const int nk = (p.K + Cfg::BK - 1) / Cfg::BK;
+    const int nFull = p.K / Cfg::BK;   // slices entirely inside K
+    la.template load<false>(0, p.K, tid, ra);
+    lb.template load<false>(0, p.K, tid, rb);
+    la.template store<Cfg::LD>(hsm, tid, ra);
+    lb.template store<Cfg::LD>(hsm + Cfg::SA, tid, rb);
+    __syncthreads();
+    // One slice per trip: fetch slice t+1 into registers, run slice t from LDS
+    // stage t&1, park slice t+1 in the other stage. (Unrolling two slices to
+    // make the stage offset a constant lets the scheduler interleave both
+    // bodies and run out of VGPRs.)
+    constexpr int STEPS = Cfg::BK / 16;
+    constexpr int NFRAG = Cfg::FM + Cfg::FN;
+    // Runs slice t from LDS stage t&1 as a software pipeline: the fragments of
+    // step s+1 are read while the MFMAs of step s run, and the next slice's
+    // registers (fetched at the top) are written to the other stage during the
+    // last step. The group barriers pin that interleave.
+    auto runSlice = [&](int t, bool more) {
+        const uint16_t* sA = hsm + (t & 1) * Cfg::STAGE;
+        const uint16_t* sB = sA + Cfg::SA;
+        uint16_t* nxt = hsm + ((t & 1) ^ 1) * Cfg::STAGE;
+        u32x4 fa[2][Cfg::FM], fb[2][Cfg::FN];
+        readFrags<Cfg>(sA, sB, 0, fa[0], fb[0], wm, wn, li, h);
+        __builtin_amdgcn_sched_group_barrier(kSgDsRead, NFRAG, 0);
+        staticFor<0, STEPS>([&](auto I) {
+            constexpr int st = decltype(I)::value;
+            if constexpr (st + 1 < STEPS) {
+                readFrags<Cfg>(sA, sB, st + 1, fa[(st + 1) & 1], fb[(st + 1) & 1], wm, wn, li, h);
+                mfmaStep<Cfg, BF16, SWAP>(fa[st & 1], fb[st & 1], acc);
+                interleave<kSgDsRead, NFRAG, Cfg::FM * Cfg::FN>();
+            } else {
+                if (more) {
+                    la.template store<Cfg::LD>(nxt, tid, ra);
+                    lb.template store<Cfg::LD>(nxt + Cfg::SA, tid, rb);
+                }
+                mfmaStep<Cfg, BF16, SWAP>(fa[st & 1], fb[st & 1], acc);
+                interleave<kSgDsWrite, LA::NSTORES + LB::NSTORES, Cfg::FM * Cfg::FN>();
+            }
+        });
+    };
+    auto step = [&](int t, auto fullTag) {
+        constexpr bool FULL = decltype(fullTag)::value;
+        la.template load<FULL>((t + 1) * Cfg::BK, p.K, tid, ra);
+        lb.template load<FULL>((t + 1) * Cfg::BK, p.K, tid, rb);
+        __builtin_amdgcn_sched_group_barrier(kSgVmemRead, LA::NLOADS + LB::NLOADS, 0);
+        runSlice(t, true);
+        __syncthreads();
+    };
+    int t = 0;
+    for (; t + 1 < nFull; ++t) step(t, std::true_type{});
+    if (t + 1 < nk) step(t++, std::false_type{});   // the one partial slice at the end of K
+    runSlice(t, false);
+
+    float* Cb = p.C + batch * p.sC;
+    if constexpr (SWAP) {
+        // Lane (li, h) holds, for block (fm, fn), C[m][n .. n+3] at
+        // m = mBase + li, n = nBase + 8*g + 4*h (registers 4g .. 4g+3).
+#pragma unroll
+        for (int fm = 0; fm < Cfg::FM; ++fm) {
+            const int m = m0 + wm * Cfg::WM + fm * 32 + li;
+            if (m >= p.M) continue;
+            float* crow = Cb + (long long)m * p.ldc;
+#pragma unroll
+            for (int fn = 0; fn < Cfg::FN; ++fn)
+#pragma unroll
+                for (int g = 0; g < 4; ++g) {
+                    const int n = n0 + wn * Cfg::WN + fn * 32 + 8 * g + 4 * h;
+                    const f32x4h v = {acc[fm][fn][4 * g], acc[fm][fn][4 * g + 1], acc[fm][fn][4 * g + 2],
+                                      acc[fm][fn][4 * g + 3]};
+                    if (n < p.N) *reinterpret_cast<f32x4h*>(crow + n) = v;   // N % 4 == 0
+                }
+        }
+    } else {
+        // Lane (li, h) holds C[m][n] at n = nBase + li,
+        // m = mBase + 8*(r/4) + 4*h + (r%4): 32 lanes store one row's 128 bytes.
+#pragma unroll
+        for (int fn = 0; fn < Cfg::FN; ++fn) {
+            const int n = n0 + wn * Cfg::WN + fn * 32 + li;
+            if (n >= p.N) continue;
+#pragma unroll
+            for (int fm = 0; fm < Cfg::FM; ++fm)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int m = m0 + wm * Cfg::WM + fm * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
+                    if (m < p.M) Cb[(long long)m * p.ldc + n] = acc[fm][fn][r];
+                }
+        }
+    }
+}
+
+// 256 x 256 x 64 with 8 waves of 64 x 128 (one workgroup per CU, two waves
+// per SIMD) for large problems: measured on MI355X it beats 4 waves of
+// 128 x 128 (one wave per SIMD cannot hide its own LDS and barrier latency)
+// and BK = 32 (twice the barriers). 128 x 128 x 64 (4 waves of 64 x 64, two
+// workgroups per CU) and 64 x 64 x 64 (4 waves of 32 x 32) serve problems
+// whose large-tile count would leave CUs idle.
+#ifndef OMHIP_HALF_L
+#define OMHIP_HALF_L 256, 256, 64, 64, 128
+#endif
+using FCfgL = FCfg<OMHIP_HALF_L>;
+using FCfgM = FCfg<128, 128, 64, 64, 64>;
+using FCfgS = FCfg<64, 64, 64, 32, 32>;
+
+template <class Cfg, bool BF16, bool TA, bool TB, bool SWAP>
+static int launchFast(HalfFastParams prm, int batch) {
+    auto kern = gemm_half_fast<Cfg, BF16, TA, TB, SWAP>;
+    static bool s_attr = false;
+    if (!s_attr) {
+        OMHIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                        hipFuncAttributeMaxDynamicSharedMemorySize,
+                                        static_cast<int>(Cfg::LDS_BYTES)));
+        s_attr = true;
+    }
+    prm.tilesM = (prm.M + Cfg::BM - 1) / Cfg::BM;
+    prm.tilesN = (prm.N + Cfg::BN - 1) / Cfg::BN;
+    hipLaunchKernelGGL(kern, dim3(prm.tilesM * prm.tilesN, 1, batch), dim3(Cfg::NT), Cfg::LDS_BYTES, stream(), prm);
+    OMHIP_CHECK_LAUNCH();
+    return 0;
+}
+
+// Tile choice: the large tile once it covers at least half the CUs (its
+// higher per-CU rate outweighs the idle half, e.g. 12608 x 768), then the
+// 128x128 tile once it gives every CU a workgroup, else the 64x64 tile.
+static int pickFastTile(int M, int N, int batch) {
+    const long long cus = cuCount();
+    auto tiles = [&](int bm, int bn) { return (long long)((M + bm - 1) / bm) * ((N + bn - 1) / bn) * batch; };
+    // TILE-HOOK
+    if (2 * tiles(256, 256) >= cus) return 0;
+    if (tiles(128, 128) >= cus) return 1;
+    return 2;
+}
+
+template <bool BF16, bool TA, bool TB, bool SWAP>
+static int launchFastT(const HalfFastParams& prm, int batch) {
+    switch (pickFastTile(prm.M, prm.N, batch)) {
+        case 0: return launchFast<FCfgL, BF16, TA, TB, SWAP>(prm, batch);
+        case 1: return launchFast<FCfgM, BF16, TA, TB, SWAP>(prm, batch);
+        default: return launchFast<FCfgS, BF16, TA, TB, SWAP>(prm, batch);
+    }
+}
+
+template <bool BF16, bool TA, bool TB>
+static int launchFastC(const HalfFastParams& prm, int batch, bool vecC) {
+    return vecC ? launchFastT<BF16, TA, TB, true>(prm, batch) : launchFastT<BF16, TA, TB, false>(prm, batch);
 }
 
 template <bool BF16>
 static int dispatchH(bool ta, bool tb, const GemmHalfParams& prm, int batch, bool va, bool vb) {
-    if (!ta && !tb) return launchHC<BF16, false, false>(prm, batch, va, vb);
-    if (!ta && tb) return launchHC<BF16, false, true>(prm, batch, va, vb);
-    if (ta && !tb) return launchHC<BF16, true, false>(prm, batch, va, vb);
-    return launchHC<BF16, true, true>(prm, batch, va, vb);
+    // The fast kernel needs 16-byte operand chunks and every buffer view
+    // (a 256-row K-major tile, or all K rows of an R-major operand) below 2^30 bytes.
+    const bool ldOk = prm.lda < (1LL << 21) && prm.ldb < (1LL << 21);
+    const long long viewA = ta ? (long long)prm.K * prm.lda * 2 : 256LL * prm.lda * 2;
+    const long long viewB = tb ? 256LL * prm.ldb * 2 : (long long)prm.K * prm.ldb * 2;
+    if (va && vb && ldOk && viewA < kMaxViewBytes && viewB < kMaxViewBytes) {
+        HalfFastParams f{};
+        f.A = prm.A; f.B = prm.B; f.C = prm.C; f.M = prm.M; f.N = prm.N; f.K = prm.K;
+        f.lda = (int)prm.lda; f.ldb = (int)prm.ldb; f.ldc = prm.ldc; f.sA = prm.sA; f.sB = prm.sB; f.sC = prm.sC;
+        const bool vecC = (prm.N % 4 == 0) && (prm.ldc % 4 == 0) && (prm.sC % 4 == 0) &&
+                          ((reinterpret_cast<uintptr_t>(prm.C) & 15u) == 0);
+        if (!ta && !tb) return launchFastC<BF16, false, false>(f, batch, vecC);
+        if (!ta && tb) return launchFastC<BF16, false, true>(f, batch, vecC);
+        if (ta && !tb) return launchFastC<BF16, true, false>(f, batch, vecC);
+        return launchFastC<BF16, true, true>(f, batch, vecC);
+    }
+    if (!ta && !tb) return launchGenericC<BF16, false, false>(prm, batch, va, vb);
+    if (!ta && tb) return launchGenericC<BF16, false, true>(prm, batch, va, vb);
+    if (ta && !tb) return launchGenericC<BF16, true, false>(prm, batch, va, vb);
+    return launchGenericC<BF16, true, true>(prm, batch, va, vb);
 }
 
 int zeroOutput(float* C, int batch, int M, int N, long long ldc, long long sC);

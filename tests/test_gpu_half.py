@@ -69,6 +69,55 @@ def test_attention_batched(hip, bf16):
     assert O.normalized_error(dS.numpy(), O.batched_matmul_transB(Q, Kt), bS32) <= O.TOL_HALF
 
 
+# (batch, M, N, K): on a 256-CU MI355X these select the 256x256 tile (first),
+# the 128x128 tile (second) and the 64x64 tile (third); every one has ragged
+# M, N and a K that ends inside a 64-deep slice. The last shape has N % 4 != 0,
+# so C leaves through 32-bit stores.
+FAST_SHAPES = [(32, 296, 264, 136), (20, 392, 392, 72), (4, 296, 264, 136), (3, 104, 262, 200)]
+
+
+@pytest.mark.parametrize("bf16", [False, True], ids=["f16", "bf16"])
+@pytest.mark.parametrize("transA,transB", [(0, 0), (0, 1), (1, 0), (1, 1)], ids=["NN", "NT", "TN", "TT"])
+@pytest.mark.parametrize("batch,M,N,K", FAST_SHAPES)
+def test_half_layouts_tiles(hip, bf16, transA, transB, batch, M, N, K):
+    """Every operand layout through gemmStridedBatchedHalf, against float64 on the rounded inputs."""
+    seed = batch * 7 + M + N + K + 2 * transA + transB
+    A = O.randn((batch, K, M) if transA else (batch, M, K), seed)
+    B = O.randn((batch, N, K) if transB else (batch, K, N), seed + 1)
+    dA, dB = to_dev(hip, _bits(A, bf16)), to_dev(hip, _bits(B, bf16))
+    dC = empty_dev(hip, (batch, M, N))
+    lda = M if transA else K
+    ldb = K if transB else N
+    hip.HIPBackend.gemmStridedBatchedHalf(1 if bf16 else 0, transA, transB, batch, M, N, K, dA, lda, M * K, dB, ldb,
+                                          N * K, dC, N, M * N)
+    C64, bound = O.gemm_f64(_round(A, bf16), _round(B, bf16), transA=bool(transA), transB=bool(transB))
+    assert O.normalized_error(dC.numpy(), C64, bound) <= 1e-4
+
+
+def test_half_strided_views(hip):
+    """Leading dimensions wider than the rows and batch strides with gaps (sub-matrix views)."""
+    batch, M, N, K = 3, 72, 80, 96
+    lda, ldb, ldc = K + 24, N + 16, N + 8
+    sA, sB, sC = M * lda + 64, K * ldb + 32, M * ldc + 16
+    A = O.randn((batch * sA,), 11)
+    B = O.randn((batch * sB,), 12)
+    dA, dB = to_dev(hip, _bits(A, False)), to_dev(hip, _bits(B, False))
+    C0 = np.full(batch * sC, -7.0, np.float32)
+    dC = to_dev(hip, C0)
+    hip.HIPBackend.gemmStridedBatchedHalf(0, 0, 0, batch, M, N, K, dA, lda, sA, dB, ldb, sB, dC, ldc, sC)
+    C = dC.numpy()
+    Ar, Br = _round(A, False), _round(B, False)
+    for b in range(batch):
+        a = Ar[b * sA:b * sA + M * lda].reshape(M, lda)[:, :K]
+        bm = Br[b * sB:b * sB + K * ldb].reshape(K, ldb)[:, :N]
+        C64, bound = O.gemm_f64(a, bm)
+        got = C[b * sC:b * sC + M * ldc].reshape(M, ldc)
+        assert O.normalized_error(got[:, :N], C64, bound) <= 1e-4
+        assert np.all(got[:, N:] == -7.0), "columns past N must stay untouched"
+    for b in range(batch - 1):
+        assert np.all(C[b * sC + M * ldc:(b + 1) * sC] == -7.0), "batch gaps must stay untouched"
+
+
 def test_half_known_answer(hip):
     A = np.array([[1, 2], [3, 4]], np.float16).view(np.uint16)
     B = np.array([[5, 6], [7, 8]], np.float16).view(np.uint16)
