@@ -85,6 +85,46 @@ def bench_gemm(om, steps: int, warmup: int):
     return ms, flops, wall, err
 
 
+GEMM_SWEEP = [(512, 512, 512), (1024, 1024, 1024), (2048, 2048, 2048), (4096, 4096, 4096), (8192, 8192, 8192),
+              (128, 4096, 4096), (8192, 256, 2048)]   # (M, N, K)
+
+
+def bench_gemm_sweep(om, steps: int, warmup: int):
+    """The fp32 GEMM sweep in both layouts: row-major A x B and A x B^T (Linear weight)."""
+    from omnimatchdeeplearningtool_amd.hiptime import StreamTimer
+    import oracle as O
+    H = om.HIPBackend
+    timer = StreamTimer(om.stream_handle())
+    out = []
+    for (m, n, k) in GEMM_SWEEP:
+        A = O.randn((m, k), 21 + m)
+        dA = om.DeviceBuffer.from_numpy(A)
+        dC = om.DeviceBuffer.empty((m, n))
+        reps = max(3, min(steps, int(2e12 / (2.0 * m * n * k))))   # about 2 TFLOP of work per shape
+        for layout in ("NN", "NT"):
+            B = O.randn((k, n) if layout == "NN" else (n, k), 22 + n)
+            dB = om.DeviceBuffer.from_numpy(B)
+            f = (lambda: H.matmul(dA, dB, dC, m, k, n)) if layout == "NN" else (lambda: H.matmulTransB(dA, dB, dC, m, k, n))
+            for _ in range(warmup):
+                f()
+            om.synchronize()
+            timer.start()
+            for _ in range(reps):
+                f()
+            timer.stop()
+            ms = timer.ms() / reps
+            rows = np.unique(np.r_[0, m // 2, m - 1])
+            C64, bound = O.gemm_f64(A[rows], B, transB=(layout == "NT"))
+            err = O.normalized_error(dC.numpy()[rows], C64, bound)
+            tf = 2.0 * m * n * k / ms / 1e9
+            out.append({"M": m, "N": n, "K": k, "layout": layout, "ms": round(ms, 4), "tflops": round(tf, 1),
+                        "frac_of_157_3": round(tf / 157.3, 3), "parity": err})
+            log(f"gemm sweep {m}x{n}x{k} {layout}: {ms:.4f} ms  {tf:.1f} TFLOP/s  parity {err:.1e}")
+            dB.free()
+        dA.free(); dC.free()
+    return out
+
+
 def bench_resnet18(om, steps: int, warmup: int, batch: int = 32):
     from omnimatchdeeplearningtool_amd.hiptime import StreamTimer
     from resnet_shapes import conv_bytes, conv_flops, out_hw, resnet18_convs
@@ -458,6 +498,8 @@ def main():
     tflops = flops / ms / 1e9
     log(f"gemm {ms:.4f} ms/step  {tflops:.1f} TFLOP/s  parity {gemm_err:.2e}")
 
+    sweep = bench_gemm_sweep(om, args.steps, 2)
+
     log("resnet18 conv stack b32")
     r_steps = max(5, args.steps // 2)
     r_ms, r_flops, r_roof_ms, per, conv_err = bench_resnet18(om, r_steps, max(2, args.warmup))
@@ -525,6 +567,7 @@ def main():
                      "unit": "TFLOP/s", "frac": round(flops / gemm_kernel_ms / 1e9 / 157.3, 4),
                      "traffic": traffic},
         "cpu_baseline": cpu,
+        "gemm_sweep": sweep,
         "parity": {"gemm_sampled_rows_max_err": gemm_err, "conv_sampled_max_err": conv_err, "tol": 1e-4},
         "resnet18_conv": {"value": round(img_s, 1), "unit": "img/s", "batch": 32, "ms_per_batch": round(r_ms, 4),
                           "tflops": round(r_flops / r_ms / 1e9, 2),

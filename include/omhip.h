@@ -143,15 +143,40 @@ int omHipConv2dBiasBnAct(const float* pInput, const float* pWeight, const float*
 /* NEW: im2col of one image, col[(c*KH+kh)*KW+kw, oh*Wout+ow]; CPUBackend::im2col cpu_backend.ixx:544-575 */
 int omHipIm2col(const float* pInput, int nCin, int nH, int nW, int nKH, int nKW,
                 int nPadH, int nPadW, int nStrideH, int nStrideW, float* pCol);
-/* replaces omCudaBatchNorm2d (cuh:165). Inference mode only (bTraining == 0):
- * y = gamma*((x-runMean)*invStd)+beta, invStd = 1/sqrt(runVar+eps), savedMean/
- * savedInvStd written as cpu_backend.ixx:823-840. bTraining != 0 returns -1. */
+/* replaces omCudaBatchNorm2d (cuh:165); CPUBackend::batchNorm2d cpu_backend.ixx:781-842.
+ * bTraining == 0: y = gamma*((x-runMean)*invStd)+beta, invStd = 1/sqrt(runVar+eps),
+ * savedMean/savedInvStd (may be NULL) = runMean and invStd (:823-840).
+ * bTraining != 0: batch mean and biased variance (two passes, :796-810), savedMean /
+ * savedInvStd (may be NULL), runMean/runVar = (1-momentum)*run + momentum*batch (:818-821),
+ * y normalised with the batch statistics. */
 int omHipBatchNorm2d(const float* pInput, float* pOutput,
                      const float* pGamma, const float* pBeta,
                      float* pRunMean, float* pRunVar,
                      float* pSavedMean, float* pSavedInvStd,
                      int nBatch, int nChannels, int nH, int nW,
                      float fEps, float fMomentum, int bTraining);
+
+/* ===== conv2d / batchnorm training (cuda_kernels.cuh:295-316) ===== */
+
+/* replaces omCudaConv2dBackwardInput (cuh:295); CPUBackend::conv2dBackwardInput
+ * cpu_backend.ixx:666-705. pGradInput [N,Cin,H,W] is overwritten. */
+int omHipConv2dBackwardInput(const float* pGradOutput, const float* pWeight, float* pGradInput,
+                             int nBatch, int nCin, int nH, int nW,
+                             int nCout, int nKH, int nKW, int nStride, int nPad);
+/* replaces omCudaConv2dBackwardWeight (cuh:301); CPUBackend::conv2dBackwardWeight
+ * cpu_backend.ixx:710-772. pGradWeight [Cout,Cin,KH,KW] and pGradBias [Cout] (may be
+ * NULL) are overwritten with the sums over the batch. */
+int omHipConv2dBackwardWeight(const float* pInput, const float* pGradOutput,
+                              float* pGradWeight, float* pGradBias,
+                              int nBatch, int nCin, int nH, int nW,
+                              int nCout, int nKH, int nKW, int nStride, int nPad);
+/* replaces omCudaBatchNorm2dBackward (cuh:310); CPUBackend::batchNorm2dBackward
+ * cpu_backend.ixx:847-890 with the saved mean / inverse std of the training forward.
+ * pGradGamma / pGradBeta may be NULL. fEps is unused (pInvStd already holds it). */
+int omHipBatchNorm2dBackward(const float* pGradOutput, const float* pInput,
+                             const float* pMean, const float* pInvStd, const float* pGamma,
+                             float* pGradInput, float* pGradGamma, float* pGradBeta,
+                             int nBatch, int nChannels, int nH, int nW, float fEps);
 
 /* ===== fp16 / bf16 GEMM, fp32 accumulate (NEW; the reference has only the software
  * converter om.engine.fp16.ixx:36-164) ===== */

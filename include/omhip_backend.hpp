@@ -74,13 +74,35 @@ public:
         check(omHipConv2d(pInput, pWeight, pBias, pOutput, nBatch, nCin, nH, nW, nCout, nKH, nKW, nStride, nPad),
               "conv2d");
     }
-    // Inference mode only: bTraining == true throws (batch statistics are not provided).
+    // bTraining: batch statistics, saved mean / inverse std and running averages (:796-822).
     static void batchNorm2d(const float* pInput, float* pOutput, const float* pGamma, const float* pBeta,
                             float* pRunMean, float* pRunVar, float* pSavedMean, float* pSavedInvStd, int nBatch,
                             int nChannels, int nH, int nW, float fEps, float fMomentum, bool bTraining) {
         check(omHipBatchNorm2d(pInput, pOutput, pGamma, pBeta, pRunMean, pRunVar, pSavedMean, pSavedInvStd, nBatch,
                                nChannels, nH, nW, fEps, fMomentum, bTraining ? 1 : 0),
               "batchNorm2d");
+    }
+
+    // ---- conv / BN training (cpu_backend.ixx:666-772, :847-890) ----
+    static void conv2dBackwardInput(const float* pGradOutput, const float* pWeight, float* pGradInput, int nBatch,
+                                    int nCin, int nH, int nW, int nCout, int nKH, int nKW, int nStride, int nPad) {
+        check(omHipConv2dBackwardInput(pGradOutput, pWeight, pGradInput, nBatch, nCin, nH, nW, nCout, nKH, nKW,
+                                       nStride, nPad),
+              "conv2dBackwardInput");
+    }
+    static void conv2dBackwardWeight(const float* pInput, const float* pGradOutput, float* pGradWeight,
+                                     float* pGradBias, int nBatch, int nCin, int nH, int nW, int nCout, int nKH,
+                                     int nKW, int nStride, int nPad) {
+        check(omHipConv2dBackwardWeight(pInput, pGradOutput, pGradWeight, pGradBias, nBatch, nCin, nH, nW, nCout, nKH,
+                                        nKW, nStride, nPad),
+              "conv2dBackwardWeight");
+    }
+    static void batchNorm2dBackward(const float* pGradOutput, const float* pInput, const float* pSavedMean,
+                                    const float* pSavedInvStd, const float* pGamma, float* pGradInput,
+                                    float* pGradGamma, float* pGradBeta, int nBatch, int nChannels, int nH, int nW) {
+        check(omHipBatchNorm2dBackward(pGradOutput, pInput, pSavedMean, pSavedInvStd, pGamma, pGradInput, pGradGamma,
+                                       pGradBeta, nBatch, nChannels, nH, nW, 1e-5f),
+              "batchNorm2dBackward");
     }
 
     // ---- entries the reference builds by composition ----

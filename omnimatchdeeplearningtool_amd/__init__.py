@@ -80,6 +80,9 @@ _SIGS = {
     "omHipConv2dBiasBnAct": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _fl, _i, _vp] + [_i] * 9,
     "omHipIm2col": [_vp] + [_i] * 9 + [_vp],
     "omHipBatchNorm2d": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _fl, _fl, _i],
+    "omHipConv2dBackwardInput": [_vp, _vp, _vp] + [_i] * 9,
+    "omHipConv2dBackwardWeight": [_vp, _vp, _vp, _vp] + [_i] * 9,
+    "omHipBatchNorm2dBackward": [_vp] * 8 + [_i] * 4 + [_fl],
     "omHipConvertF32ToF16": [_vp, _vp, _i],
     "omHipConvertF32ToBF16": [_vp, _vp, _i],
     "omHipConvertF16ToF32": [_vp, _vp, _i],
@@ -273,6 +276,27 @@ class HIPBackend:
         call("omHipBatchNorm2d", _ptr(pInput), _ptr(pOutput), _ptr(pGamma), _ptr(pBeta), _ptr(pRunMean),
              _ptr(pRunVar), _ptr(pSavedMean), _ptr(pSavedInvStd), nBatch, nChannels, nH, nW, fEps, fMomentum,
              1 if bTraining else 0)
+
+    @staticmethod
+    def conv2dBackwardInput(pGradOutput, pWeight, pGradInput, nBatch, nCin, nH, nW, nCout, nKH, nKW, nStride,
+                            nPad) -> None:
+        """CPUBackend::conv2dBackwardInput (cpu_backend.ixx:666-705)."""
+        call("omHipConv2dBackwardInput", _ptr(pGradOutput), _ptr(pWeight), _ptr(pGradInput), nBatch, nCin, nH, nW,
+             nCout, nKH, nKW, nStride, nPad)
+
+    @staticmethod
+    def conv2dBackwardWeight(pInput, pGradOutput, pGradWeight, pGradBias, nBatch, nCin, nH, nW, nCout, nKH, nKW,
+                             nStride, nPad) -> None:
+        """CPUBackend::conv2dBackwardWeight (cpu_backend.ixx:710-772); pGradBias may be None."""
+        call("omHipConv2dBackwardWeight", _ptr(pInput), _ptr(pGradOutput), _ptr(pGradWeight), _ptr(pGradBias),
+             nBatch, nCin, nH, nW, nCout, nKH, nKW, nStride, nPad)
+
+    @staticmethod
+    def batchNorm2dBackward(pGradOutput, pInput, pSavedMean, pSavedInvStd, pGamma, pGradInput, pGradGamma,
+                            pGradBeta, nBatch, nChannels, nH, nW, fEps: float = 1e-5) -> None:
+        """CPUBackend::batchNorm2dBackward (cpu_backend.ixx:847-890)."""
+        call("omHipBatchNorm2dBackward", _ptr(pGradOutput), _ptr(pInput), _ptr(pSavedMean), _ptr(pSavedInvStd),
+             _ptr(pGamma), _ptr(pGradInput), _ptr(pGradGamma), _ptr(pGradBeta), nBatch, nChannels, nH, nW, fEps)
 
     # ---- entries the reference builds by composition ----
     @staticmethod

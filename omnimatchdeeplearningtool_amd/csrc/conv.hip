@@ -28,6 +28,7 @@
 #include "omhip_internal.hpp"
 #include "mfma_f32_tile.hpp"
 #include "gemm_f32.hpp"
+#include "conv.hpp"
 #include "../../include/omhip.h"
 
 #include <algorithm>
@@ -37,9 +38,6 @@
 #include <tuple>
 
 namespace omhip {
-
-int im2colBatched(const float* x, float* col, int N, int Cin, int H, int W, int KH, int KW, int pad, int strd,
-                  int Ho, int Wo);
 
 // Offsets at or above this byte count are out of range for every buffer used
 // here (buffers are limited to 2^30 bytes), so two such terms never wrap.

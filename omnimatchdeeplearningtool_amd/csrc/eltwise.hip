@@ -4,6 +4,7 @@
 // All are HBM-bound streams: each thread handles 4 consecutive floats with
 // 128-bit loads/stores where the pointers allow, grid-stride over the array.
 #include "omhip_internal.hpp"
+#include "conv.hpp"
 #include "../../include/omhip.h"
 
 #include <algorithm>
@@ -270,11 +271,12 @@ int omHipBatchNorm2d(const float* pInput, float* pOutput, const float* pGamma, c
                      float* pRunMean, float* pRunVar, float* pSavedMean, float* pSavedInvStd,
                      int nBatch, int nChannels, int nH, int nW, float fEps, float fMomentum, int bTraining) {
     clearError();
-    (void)fMomentum;
-    if (bTraining) return fail("omHipBatchNorm2d: training mode is not provided by this backend (inference only)");
     if (nBatch <= 0 || nChannels <= 0 || nH <= 0 || nW <= 0) return 0;
     if (!pInput || !pOutput || !pGamma || !pBeta || !pRunMean || !pRunVar)
         return fail("omHipBatchNorm2d: null pointer");
+    if (bTraining)
+        return batchNorm2dTrain(pInput, pOutput, pGamma, pBeta, pRunMean, pRunVar, pSavedMean, pSavedInvStd, nBatch,
+                                nChannels, nH, nW, fEps, fMomentum);
     if (pSavedMean || pSavedInvStd) {
         hipLaunchKernelGGL(bn_stats_kernel, dim3((nChannels + 255) / 256), dim3(256), 0, stream(), pRunMean, pRunVar,
                            pSavedMean, pSavedInvStd, nChannels, fEps);

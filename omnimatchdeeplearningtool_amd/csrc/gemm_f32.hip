@@ -12,6 +12,8 @@
 #include "gemm_f32.hpp"
 #include "../../include/omhip.h"
 
+#include <algorithm>
+
 namespace omhip {
 
 template <class Cfg, bool TA, bool TB, bool VA, bool VB>
@@ -32,13 +34,17 @@ __global__ __launch_bounds__(Cfg::NT) void gemm_f32_kernel(GemmF32Params p) {
     int tm, tn;
     tile_coords(blockIdx.x, p.tilesM * p.tilesN, p.tilesM, p.tilesN, 8, tm, tn);
     const long long batch = blockIdx.z;
+    const int split = blockIdx.y;
     const int m0 = tm * Cfg::BM;
     const int n0 = tn * Cfg::BN;
+    // This split's K range; the loaders treat kEnd as the end of K.
+    const int kBeg = split * p.kChunk;
+    const int kEnd = min(p.K, kBeg + p.kChunk);
 
     DenseLoader<A_KMAJOR, VA, Cfg::BM, Cfg::BK, Cfg::NT> la;
-    la.p = p.A + batch * p.sA; la.ld = p.lda; la.rows = p.M; la.K = p.K; la.r0 = m0;
+    la.p = p.A + batch * p.sA; la.ld = p.lda; la.rows = p.M; la.K = kEnd; la.r0 = m0;
     DenseLoader<B_KMAJOR, VB, Cfg::BN, Cfg::BK, Cfg::NT> lb;
-    lb.p = p.B + batch * p.sB; lb.ld = p.ldb; lb.rows = p.N; lb.K = p.K; lb.r0 = n0;
+    lb.p = p.B + batch * p.sB; lb.ld = p.ldb; lb.rows = p.N; lb.K = kEnd; lb.r0 = n0;
 
     f32x16 acc[Cfg::FM][Cfg::FN];
 #pragma unroll
@@ -48,9 +54,9 @@ __global__ __launch_bounds__(Cfg::NT) void gemm_f32_kernel(GemmF32Params p) {
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
-    const int nk = (p.K + Cfg::BK - 1) / Cfg::BK;
-    la.load(0, tid);
-    lb.load(0, tid);
+    const int nk = (kEnd - kBeg + Cfg::BK - 1) / Cfg::BK;
+    la.load(kBeg, tid);
+    lb.load(kBeg, tid);
     la.store(smem, tid);
     lb.store(smem + SA::SIZE, tid);
     __syncthreads();
@@ -58,8 +64,8 @@ __global__ __launch_bounds__(Cfg::NT) void gemm_f32_kernel(GemmF32Params p) {
         const int cur = t & 1;
         const bool more = (t + 1) < nk;
         if (more) {
-            la.load((t + 1) * Cfg::BK, tid);
-            lb.load((t + 1) * Cfg::BK, tid);
+            la.load(kBeg + (t + 1) * Cfg::BK, tid);
+            lb.load(kBeg + (t + 1) * Cfg::BK, tid);
         }
         float* sCur = smem + cur * STAGE;
         float* sNxt = smem + (cur ^ 1) * STAGE;
@@ -71,7 +77,10 @@ __global__ __launch_bounds__(Cfg::NT) void gemm_f32_kernel(GemmF32Params p) {
         __syncthreads();
     }
 
-    float* C = p.C + batch * p.sC;
+    // Split-K / batch-reduce partials go densely to [split][batch][M][N].
+    const bool partial = p.ws != nullptr;
+    float* C = partial ? p.ws + ((long long)split * gridDim.z + batch) * p.M * p.N : p.C + batch * p.sC;
+    const long long ldc = partial ? p.N : p.ldc;
     const int li = lane & 31, h = lane >> 5;
 #pragma unroll
     for (int fm = 0; fm < Cfg::FM; ++fm) {
@@ -82,9 +91,33 @@ __global__ __launch_bounds__(Cfg::NT) void gemm_f32_kernel(GemmF32Params p) {
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const int row = m0 + wm * Cfg::WM + fm * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
-                if (row < p.M) C[(long long)row * p.ldc + col] = acc[fm][fn][r];
+                if (row < p.M) C[(long long)row * ldc + col] = acc[fm][fn][r];
             }
         }
+    }
+}
+
+// Sums the partials of every split (and, when reduceBatch, every batch item)
+// in a fixed order and writes C. Thread per element, columns fastest.
+__global__ void gemm_splitk_finish(const float* ws, float* C, int splits, int batch, int M, int N, long long ldc,
+                                   long long sC, int reduceBatch, int accumulate) {
+    const long long plane = (long long)M * N;
+    const int outBatch = reduceBatch ? 1 : batch;
+    const long long total = plane * outBatch;
+    for (long long i = blockIdx.x * (long long)blockDim.x + threadIdx.x; i < total;
+         i += (long long)gridDim.x * blockDim.x) {
+        const long long b = i / plane, e = i - b * plane;
+        const long long r = e / N, c = e - r * N;
+        float* out = C + b * sC + r * ldc + c;
+        float v = accumulate ? *out : 0.f;
+        for (int s = 0; s < splits; ++s) {
+            if (reduceBatch) {
+                for (int bb = 0; bb < batch; ++bb) v += ws[((long long)s * batch + bb) * plane + e];
+            } else {
+                v += ws[((long long)s * batch + b) * plane + e];
+            }
+        }
+        *out = v;
     }
 }
 
@@ -96,7 +129,7 @@ static size_t ldsBytesFor() {
 }
 
 template <class Cfg, bool TA, bool TB, bool VA, bool VB>
-static int launchOne(const GemmF32Params& prm, int batch) {
+static int launchOne(const GemmF32Params& prm, int batch, int splits) {
     auto kern = gemm_f32_kernel<Cfg, TA, TB, VA, VB>;
     const size_t lds = ldsBytesFor<Cfg, TA, TB>();
     static bool s_attr = false;
@@ -105,20 +138,20 @@ static int launchOne(const GemmF32Params& prm, int batch) {
                                         hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds)));
         s_attr = true;
     }
-    dim3 grid(prm.tilesM * prm.tilesN, 1, batch);
+    dim3 grid(prm.tilesM * prm.tilesN, splits, batch);
     hipLaunchKernelGGL(kern, grid, dim3(Cfg::NT), lds, stream(), prm);
     OMHIP_CHECK_LAUNCH();
     return 0;
 }
 
 template <class Cfg, bool TA, bool TB>
-static int launchVec(GemmF32Params prm, int batch, bool va, bool vb) {
+static int launchVec(GemmF32Params prm, int batch, int splits, bool va, bool vb) {
     prm.tilesM = (prm.M + Cfg::BM - 1) / Cfg::BM;
     prm.tilesN = (prm.N + Cfg::BN - 1) / Cfg::BN;
-    if (va && vb) return launchOne<Cfg, TA, TB, true, true>(prm, batch);
-    if (va) return launchOne<Cfg, TA, TB, true, false>(prm, batch);
-    if (vb) return launchOne<Cfg, TA, TB, false, true>(prm, batch);
-    return launchOne<Cfg, TA, TB, false, false>(prm, batch);
+    if (va && vb) return launchOne<Cfg, TA, TB, true, true>(prm, batch, splits);
+    if (va) return launchOne<Cfg, TA, TB, true, false>(prm, batch, splits);
+    if (vb) return launchOne<Cfg, TA, TB, false, true>(prm, batch, splits);
+    return launchOne<Cfg, TA, TB, false, false>(prm, batch, splits);
 }
 
 // Slice depth of the large tile is a build-time constant (LDS: 2 x (256x(BK+4) + BKx260) floats).
@@ -129,35 +162,103 @@ using CfgL = TileCfg<256, 256, OMHIP_GEMM_BK, 128, 128>;
 using CfgM = TileCfg<128, 128, 16, 64, 64>;
 using CfgS = TileCfg<64, 64, 16, 32, 32>;
 
-template <bool TA, bool TB>
-static int launchCfg(const GemmF32Params& prm, int batch, bool va, bool vb) {
+struct GemmPlan {
+    int cfg;      // 0: 256x256, 1: 128x128, 2: 64x64
+    int splits;   // K splits (1: none)
+};
+
+// Tile and split-K choice: the largest tile that gives every CU a workgroup.
+// When even 64x64 tiles leave CUs idle and K is long (few rows or columns:
+// 128 x 4096 x 4096, weight gradients), K is split: the smallest power of two
+// (at most 64) that gives every CU a workgroup while each split keeps >= 256
+// of K, over the 128x128 tile (64x64 when M or N is below 128). The partials
+// cost one fp32 write and read of C per split. Measured on MI355X:
+// 128 x 4096 x 4096 runs at 72 TFLOP/s split 8 ways against 34 unsplit;
+// K = 512 problems run faster unsplit.
+static GemmPlan planGemm(int M, int N, int K, int batch, bool wsOk) {
     const long long cus = cuCount();
-    auto tiles = [&](int bm, int bn) {
-        return (long long)((prm.M + bm - 1) / bm) * ((prm.N + bn - 1) / bn) * batch;
-    };
-    if (tiles(256, 256) >= cus) return launchVec<CfgL, TA, TB>(prm, batch, va, vb);
-    if (tiles(128, 128) >= cus) return launchVec<CfgM, TA, TB>(prm, batch, va, vb);
-    return launchVec<CfgS, TA, TB>(prm, batch, va, vb);
+    auto tiles = [&](int bm, int bn) { return (long long)((M + bm - 1) / bm) * ((N + bn - 1) / bn) * batch; };
+    // TUNE-HOOK-GEMM
+    if (tiles(256, 256) >= cus) return {0, 1};
+    if (tiles(128, 128) >= cus) return {1, 1};
+    if (tiles(64, 64) >= cus || !wsOk || K < 1024) return {2, 1};
+    const int cfg = (M >= 128 && N >= 128) ? 1 : 2;
+    const long long t = cfg == 1 ? tiles(128, 128) : tiles(64, 64);
+    int s = 1;
+    while (s < 64 && t * s < cus && K / (2 * s) >= 256) s *= 2;
+    return {cfg, s};
+}
+
+template <bool TA, bool TB>
+static int launchCfg(const GemmF32Params& prm, int batch, int splits, int cfg, bool va, bool vb) {
+    if (cfg == 0) return launchVec<CfgL, TA, TB>(prm, batch, splits, va, vb);
+    if (cfg == 1) return launchVec<CfgM, TA, TB>(prm, batch, splits, va, vb);
+    return launchVec<CfgS, TA, TB>(prm, batch, splits, va, vb);
 }
 
 static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
-int gemmF32(bool ta, bool tb, int batch, int M, int N, int K,
-            const float* A, long long lda, long long sA,
-            const float* B, long long ldb, long long sB,
-            float* C, long long ldc, long long sC) {
+// Launches the GEMM (partials to ws when splits > 1 or the batch is reduced)
+// and, if needed, the finishing sum.
+static int gemmF32Run(bool ta, bool tb, int batch, int M, int N, int K, const float* A, long long lda, long long sA,
+                      const float* B, long long ldb, long long sB, float* C, long long ldc, long long sC,
+                      GemmPlan plan, bool reduceBatch, bool accumulate = false) {
     GemmF32Params prm{};
     prm.A = A; prm.B = B; prm.C = C;
     prm.M = M; prm.N = N; prm.K = K;
     prm.lda = lda; prm.ldb = ldb; prm.ldc = ldc;
     prm.sA = sA; prm.sB = sB; prm.sC = sC;
+    const int bk = 16;
+    int splits = plan.splits;
+    prm.kChunk = ((K + splits - 1) / splits + bk - 1) / bk * bk;
+    splits = (K + prm.kChunk - 1) / prm.kChunk;
+    const bool partial = splits > 1 || reduceBatch;
+    if (partial) {
+        prm.ws = static_cast<float*>(workspace((size_t)splits * batch * M * N * sizeof(float)));
+        if (!prm.ws) return fail("gemm: no workspace for %d x %d partial products", splits * batch, M * N);
+    }
     // A is K-contiguous unless transposed; the vector axis is K (A) or M (A^T).
     const bool va = aligned16(A) && lda % 4 == 0 && sA % 4 == 0 && (ta ? M % 4 == 0 : K % 4 == 0);
     const bool vb = aligned16(B) && ldb % 4 == 0 && sB % 4 == 0 && (tb ? K % 4 == 0 : N % 4 == 0);
-    if (!ta && !tb) return launchCfg<false, false>(prm, batch, va, vb);
-    if (!ta && tb) return launchCfg<false, true>(prm, batch, va, vb);
-    if (ta && !tb) return launchCfg<true, false>(prm, batch, va, vb);
-    return launchCfg<true, true>(prm, batch, va, vb);
+    int rc;
+    if (!ta && !tb) rc = launchCfg<false, false>(prm, batch, splits, plan.cfg, va, vb);
+    else if (!ta && tb) rc = launchCfg<false, true>(prm, batch, splits, plan.cfg, va, vb);
+    else if (ta && !tb) rc = launchCfg<true, false>(prm, batch, splits, plan.cfg, va, vb);
+    else rc = launchCfg<true, true>(prm, batch, splits, plan.cfg, va, vb);
+    if (rc || !partial) return rc;
+    const long long total = (long long)M * N * (reduceBatch ? 1 : batch);
+    const int blocks = (int)std::min<long long>((total + 255) / 256, (long long)cuCount() * 16);
+    hipLaunchKernelGGL(gemm_splitk_finish, dim3(blocks), dim3(256), 0, stream(), prm.ws, C, splits, batch, M, N, ldc,
+                       sC, reduceBatch ? 1 : 0, accumulate ? 1 : 0);
+    OMHIP_CHECK_LAUNCH();
+    return 0;
+}
+
+// Split-K partials are kept to at most this many bytes of workspace.
+constexpr size_t kMaxSplitWorkspace = (size_t)256 << 20;
+
+int gemmF32(bool ta, bool tb, int batch, int M, int N, int K,
+            const float* A, long long lda, long long sA,
+            const float* B, long long ldb, long long sB,
+            float* C, long long ldc, long long sC) {
+    const bool wsOk = (size_t)64 * batch * M * N * sizeof(float) <= kMaxSplitWorkspace;
+    const GemmPlan plan = planGemm(M, N, K, batch, wsOk);
+    return gemmF32Run(ta, tb, batch, M, N, K, A, lda, sA, B, ldb, sB, C, ldc, sC, plan, false);
+}
+
+int gemmF32BatchReduce(bool ta, bool tb, int batch, int M, int N, int K,
+                       const float* A, long long lda, long long sA,
+                       const float* B, long long ldb, long long sB,
+                       float* C, long long ldc, bool accumulate) {
+    // Each batch item is one more partial; split K only while the partials stay small.
+    const long long cus = cuCount();
+    GemmPlan plan{2, 1};
+    auto tiles = [&](int bm, int bn) { return (long long)((M + bm - 1) / bm) * ((N + bn - 1) / bn) * batch; };
+    if (tiles(256, 256) >= cus) plan.cfg = 0;
+    else if (tiles(128, 128) >= cus) plan.cfg = 1;
+    if ((size_t)batch * M * N * sizeof(float) > kMaxSplitWorkspace)
+        return fail("gemm: batch-reduce partials (%d x %d x %d floats) exceed the workspace limit", batch, M, N);
+    return gemmF32Run(ta, tb, batch, M, N, K, A, lda, sA, B, ldb, sB, C, ldc, 0, plan, true, accumulate);
 }
 
 __global__ void zero_rows_kernel(float* C, int rows, int cols, long long ldc, long long sC) {

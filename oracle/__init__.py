@@ -45,6 +45,7 @@ _REF_TRIED = False
 
 _f = ctypes.POINTER(ctypes.c_float)
 _u16 = ctypes.POINTER(ctypes.c_uint16)
+_ip = ctypes.POINTER(ctypes.c_int)
 _i = ctypes.c_int
 _sz = ctypes.c_size_t
 
@@ -83,6 +84,17 @@ def lib() -> ctypes.CDLL:
             "omrefConvBnRelu": [_f, _f, _f, _f, _f, _f, _f, ctypes.c_float, _i, _f] + [_i] * 9,
             "omrefFloatToHalfTruncN": [_f, _u16, _sz],
             "omrefFillValue": [_f, _sz, ctypes.c_float],
+            "omrefCol2im": [_f, _i, _i, _i, _i, _i, _i, _i, _i, _i, _f],
+            "omrefConv2dBackwardInput": [_f, _f, _f] + [_i] * 9,
+            "omrefConv2dBackwardWeight": [_f, _f, _f, _f] + [_i] * 9,
+            "omrefBatchNorm2dBackward": [_f] * 8 + [_i] * 4,
+            "omrefMaxPool2d": [_f, _f, _ip] + [_i] * 8,
+            "omrefMaxPool2dBackward": [_f, _ip, _f] + [_i] * 6,
+            "omrefAvgPool2d": [_f, _f] + [_i] * 8,
+            "omrefAvgPool2dBackward": [_f, _f] + [_i] * 10,
+            "omrefAdaptiveAvgPool2d": [_f, _f] + [_i] * 6,
+            "omrefAdaptiveAvgPool2dBackward": [_f, _f] + [_i] * 6,
+            "omrefAdd": [_f, _f, _f, _sz],
         }
         for name, args in sig.items():
             fn = getattr(L, name)
@@ -113,6 +125,16 @@ def ref_lib() -> Optional[ctypes.CDLL]:
                 "refRelu": [_f, _f, _sz],
                 "refReluBackward": [_f, _f, _f, _sz],
                 "refAddBias": [_f, _f, _f, _i, _i],
+                "refConv2dBackwardInput": [_f, _f, _f] + [_i] * 9,
+                "refConv2dBackwardWeight": [_f, _f, _f, _f] + [_i] * 9,
+                "refBatchNorm2dBackward": [_f] * 8 + [_i] * 4,
+                "refMaxPool2d": [_f, _f, _ip] + [_i] * 8,
+                "refMaxPool2dBackward": [_f, _ip, _f] + [_i] * 6,
+                "refAvgPool2d": [_f, _f] + [_i] * 8,
+                "refAvgPool2dBackward": [_f, _f] + [_i] * 10,
+                "refAdaptiveAvgPool2d": [_f, _f] + [_i] * 6,
+                "refAdaptiveAvgPool2dBackward": [_f, _f] + [_i] * 6,
+                "refAdd": [_f, _f, _f, _sz],
             }
             for name, args in sig.items():
                 fn = getattr(R, name)
@@ -311,6 +333,116 @@ def conv_bn_act(x, w, bias, gamma, beta, mean, var, eps=1e-5, act=1, stride=1, p
     return out
 
 
+def _fn(name: str, backend: str):
+    return getattr(ref_lib(), "ref" + name) if backend == "reference" else getattr(lib(), "omref" + name)
+
+
+def conv2d_backward_input(gO, w, H, W, stride=1, pad=0, backend: str = "oracle") -> np.ndarray:
+    """CPUBackend::conv2dBackwardInput (cpu_backend.ixx:666-705): col2im(W^T gO) per image."""
+    gO, w = _f32(gO), _f32(w)
+    N, Cout, Ho, Wo = gO.shape
+    Cout2, Cin, KH, KW = w.shape
+    assert Cout == Cout2 and out_hw(H, W, KH, KW, stride, pad) == (Ho, Wo)
+    gI = np.empty((N, Cin, H, W), np.float32)
+    _fn("Conv2dBackwardInput", backend)(_p(gO), _p(w), _p(gI), N, Cin, H, W, Cout, KH, KW, stride, pad)
+    return gI
+
+
+def conv2d_backward_weight(x, gO, KH, KW, stride=1, pad=0, bias=True, backend: str = "oracle"):
+    """CPUBackend::conv2dBackwardWeight (cpu_backend.ixx:710-772): (gradWeight, gradBias or None)."""
+    x, gO = _f32(x), _f32(gO)
+    N, Cin, H, W = x.shape
+    N2, Cout, Ho, Wo = gO.shape
+    assert N == N2 and out_hw(H, W, KH, KW, stride, pad) == (Ho, Wo)
+    gW = np.empty((Cout, Cin, KH, KW), np.float32)
+    gB = np.empty(Cout, np.float32) if bias else None
+    _fn("Conv2dBackwardWeight", backend)(_p(x), _p(gO), _p(gW), _p(gB), N, Cin, H, W, Cout, KH, KW, stride, pad)
+    return gW, gB
+
+
+def batchnorm2d_backward(gO, x, mean, inv_std, gamma, backend: str = "oracle"):
+    """CPUBackend::batchNorm2dBackward (cpu_backend.ixx:847-890): (gradInput, gradGamma, gradBeta)."""
+    gO, x = _f32(gO), _f32(x)
+    N, C, H, W = x.shape
+    gI = np.empty_like(x)
+    gG = np.empty(C, np.float32)
+    gB = np.empty(C, np.float32)
+    _fn("BatchNorm2dBackward", backend)(_p(gO), _p(x), _p(_f32(mean)), _p(_f32(inv_std)), _p(_f32(gamma)), _p(gI),
+                                        _p(gG), _p(gB), N, C, H, W)
+    return gI, gG, gB
+
+
+def _ipt(a: np.ndarray):
+    assert a.dtype == np.int32 and a.flags["C_CONTIGUOUS"]
+    return a.ctypes.data_as(_ip)
+
+
+def maxpool2d(x, K, stride, pad, backend: str = "oracle"):
+    """CPUBackend::maxPool2d (cpu_backend.ixx:897-934): (output, flat input index per output)."""
+    x = _f32(x)
+    N, C, H, W = x.shape
+    Ho, Wo = out_hw(H, W, K, K, stride, pad)
+    y = np.empty((N, C, Ho, Wo), np.float32)
+    idx = np.empty((N, C, Ho, Wo), np.int32)
+    _fn("MaxPool2d", backend)(_p(x), _p(y), _ipt(idx), N, C, H, W, K, K, stride, pad)
+    return y, idx
+
+
+def maxpool2d_backward(gO, idx, H, W, backend: str = "oracle") -> np.ndarray:
+    """CPUBackend::maxPool2dBackward (cpu_backend.ixx:937-955)."""
+    gO = _f32(gO)
+    idx = np.ascontiguousarray(idx, np.int32)
+    N, C, Ho, Wo = gO.shape
+    gI = np.empty((N, C, H, W), np.float32)
+    _fn("MaxPool2dBackward", backend)(_p(gO), _ipt(idx), _p(gI), N, C, Ho, Wo, H, W)
+    return gI
+
+
+def avgpool2d(x, K, stride, pad, backend: str = "oracle") -> np.ndarray:
+    """CPUBackend::avgPool2d (cpu_backend.ixx:958-990): padding counts in the divisor."""
+    x = _f32(x)
+    N, C, H, W = x.shape
+    Ho, Wo = out_hw(H, W, K, K, stride, pad)
+    y = np.empty((N, C, Ho, Wo), np.float32)
+    _fn("AvgPool2d", backend)(_p(x), _p(y), N, C, H, W, K, K, stride, pad)
+    return y
+
+
+def avgpool2d_backward(gO, H, W, K, stride, pad, backend: str = "oracle") -> np.ndarray:
+    """CPUBackend::avgPool2dBackward (cpu_backend.ixx:994-1023)."""
+    gO = _f32(gO)
+    N, C, Ho, Wo = gO.shape
+    gI = np.empty((N, C, H, W), np.float32)
+    _fn("AvgPool2dBackward", backend)(_p(gO), _p(gI), N, C, H, W, Ho, Wo, K, K, stride, pad)
+    return gI
+
+
+def adaptive_avgpool2d(x, OH, OW, backend: str = "oracle") -> np.ndarray:
+    """CPUBackend::adaptiveAvgPool2d (cpu_backend.ixx:1467-1488)."""
+    x = _f32(x)
+    N, C, H, W = x.shape
+    y = np.empty((N, C, OH, OW), np.float32)
+    _fn("AdaptiveAvgPool2d", backend)(_p(x), _p(y), N, C, H, W, OH, OW)
+    return y
+
+
+def adaptive_avgpool2d_backward(gO, H, W, backend: str = "oracle") -> np.ndarray:
+    """CPUBackend::adaptiveAvgPool2dBackward (cpu_backend.ixx:1491-1510)."""
+    gO = _f32(gO)
+    N, C, OH, OW = gO.shape
+    gI = np.empty((N, C, H, W), np.float32)
+    _fn("AdaptiveAvgPool2dBackward", backend)(_p(gO), _p(gI), N, C, H, W, OH, OW)
+    return gI
+
+
+def add(a, b, backend: str = "oracle") -> np.ndarray:
+    """CPUBackend::add (cpu_backend.ixx:147-160)."""
+    a, b = _f32(a), _f32(b)
+    out = np.empty_like(a)
+    _fn("Add", backend)(_p(a), _p(b), _p(out), a.size)
+    return out
+
+
 def float_to_half_trunc(x) -> np.ndarray:
     """FP16Converter::floatToHalf (fp16.ixx:36-100): truncating fp32 -> fp16 bits."""
     x = _f32(x)
@@ -373,6 +505,69 @@ def conv_f64(x, w, bias=None, stride=1, pad=0, gamma=None, beta=None, mean=None,
     if act == 1:
         out = np.maximum(out, 0.0)
     return out, bound
+
+
+def conv_backward_f64(x, w, gO, stride=1, pad=0):
+    """float64 gradients of out = conv(x, w) for upstream gO, and their error budgets.
+
+    dX = W^T gO scattered back (col2im), dW = gO im2col(x)^T, dB = sum gO; the
+    budgets are the same contractions over absolute values."""
+    x64 = np.asarray(x, np.float64)
+    w64 = np.asarray(w, np.float64)
+    g64 = np.asarray(gO, np.float64)
+    N, Cin, H, W = x64.shape
+    Cout, _, KH, KW = w64.shape
+    cols, Ho, Wo = _im2col64(x64, KH, KW, stride, pad)
+    wm = w64.reshape(Cout, -1)
+    gm = g64.reshape(N, Cout, Ho * Wo)
+    dW = np.einsum("nop,nkp->ok", gm, cols).reshape(w64.shape)
+    dWb = np.einsum("nop,nkp->ok", np.abs(gm), np.abs(cols)).reshape(w64.shape)
+    dB = gm.sum(axis=(0, 2))
+    dBb = np.abs(gm).sum(axis=(0, 2))
+    dcol = np.matmul(wm.T[None], gm)
+    dcolb = np.matmul(np.abs(wm).T[None], np.abs(gm))
+    dX = _col2im64(dcol, N, Cin, H, W, KH, KW, stride, pad)
+    dXb = _col2im64(dcolb, N, Cin, H, W, KH, KW, stride, pad)
+    return (dX, dXb), (dW, dWb), (dB, dBb)
+
+
+def _col2im64(cols, N, C, H, W, KH, KW, stride, pad):
+    Ho, Wo = out_hw(H, W, KH, KW, stride, pad)
+    cols = cols.reshape(N, C, KH, KW, Ho, Wo)
+    xp = np.zeros((N, C, H + 2 * pad, W + 2 * pad), np.float64)
+    for kh in range(KH):
+        for kw in range(KW):
+            xp[:, :, kh:kh + stride * (Ho - 1) + 1:stride, kw:kw + stride * (Wo - 1) + 1:stride] += cols[:, :, kh, kw]
+    return xp[:, :, pad:pad + H, pad:pad + W]
+
+
+def bn_train_f64(x, gamma, beta, eps=1e-5):
+    """float64 BN training forward: (y, batch mean, biased var, invStd)."""
+    x64 = np.asarray(x, np.float64)
+    mean = x64.mean(axis=(0, 2, 3))
+    var = ((x64 - mean[None, :, None, None]) ** 2).mean(axis=(0, 2, 3))
+    inv = 1.0 / np.sqrt(var + eps)
+    y = np.asarray(gamma, np.float64)[None, :, None, None] * (x64 - mean[None, :, None, None]) * inv[None, :, None, None] \
+        + np.asarray(beta, np.float64)[None, :, None, None]
+    return y, mean, var, inv
+
+
+def bn_backward_f64(gO, x, mean, inv_std, gamma):
+    """float64 BN backward with the given statistics: (dX, dGamma, dBeta) and dX's error budget."""
+    g64 = np.asarray(gO, np.float64)
+    x64 = np.asarray(x, np.float64)
+    m = np.asarray(mean, np.float64)[None, :, None, None]
+    inv = np.asarray(inv_std, np.float64)[None, :, None, None]
+    gam = np.asarray(gamma, np.float64)[None, :, None, None]
+    cnt = x64.shape[0] * x64.shape[2] * x64.shape[3]
+    xh = (x64 - m) * inv
+    dG = (g64 * xh).sum(axis=(0, 2, 3))
+    dB = g64.sum(axis=(0, 2, 3))
+    dX = gam * inv / cnt * (cnt * g64 - dB[None, :, None, None] - xh * dG[None, :, None, None])
+    absG = np.abs(g64).sum(axis=(0, 2, 3))
+    absGX = (np.abs(g64) * np.abs(xh)).sum(axis=(0, 2, 3))
+    bound = np.abs(gam) * inv / cnt * (cnt * np.abs(g64) + absG[None, :, None, None] + np.abs(xh) * absGX[None, :, None, None])
+    return dX, dG, dB, bound, absGX, absG
 
 
 def normalized_error(C, C64, bound) -> float:

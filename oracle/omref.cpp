@@ -255,6 +255,200 @@ void omrefConvBnRelu(const float* x, const float* w, const float* bias, const fl
 // FP16Converter::floatToHalf (src/engine/om.engine.fp16.ixx:36-100): the
 // reference's software converter TRUNCATES the mantissa (>>13) and flushes
 // fp32 subnormals to signed zero. Restated for documentation of the rounding
+// ---- training path and pooling -------------------------------------------------
+
+// cpu_backend.ixx:581-607 — scatter-add of a column matrix back onto one image.
+void omrefCol2im(const float* col, int Cin, int H, int W, int KH, int KW, int ph, int pw, int sh, int sw, float* x) {
+    const int Ho = (H + 2 * ph - KH) / sh + 1, Wo = (W + 2 * pw - KW) / sw + 1;
+    const int cols = Ho * Wo;
+    for (int c = 0; c < Cin; ++c)
+        for (int kh = 0; kh < KH; ++kh)
+            for (int kw = 0; kw < KW; ++kw) {
+                const int row = (c * KH + kh) * KW + kw;
+                for (int oh = 0; oh < Ho; ++oh)
+                    for (int ow = 0; ow < Wo; ++ow) {
+                        const int ih = oh * sh - ph + kh, iw = ow * sw - pw + kw;
+                        if (ih >= 0 && ih < H && iw >= 0 && iw < W)
+                            x[((size_t)c * H + ih) * W + iw] += col[(size_t)row * cols + oh * Wo + ow];
+                    }
+            }
+}
+
+// cpu_backend.ixx:666-705 — gradInput = col2im(W^T x gradOutput), per image.
+void omrefConv2dBackwardInput(const float* gO, const float* w, float* gI, int N, int Cin, int H, int W, int Cout,
+                              int KH, int KW, int stride, int pad) {
+    const int Ho = (H + 2 * pad - KH) / stride + 1, Wo = (W + 2 * pad - KW) / stride + 1;
+    const int rows = Cin * KH * KW, cols = Ho * Wo;
+    std::memset(gI, 0, (size_t)N * Cin * H * W * sizeof(float));
+    std::vector<float> wt((size_t)rows * Cout), col((size_t)rows * cols);
+    omrefTranspose2d(w, wt.data(), Cout, rows);
+    for (int n = 0; n < N; ++n) {
+        omrefMatmul(wt.data(), gO + (size_t)n * Cout * cols, col.data(), rows, Cout, cols);
+        omrefCol2im(col.data(), Cin, H, W, KH, KW, pad, pad, stride, stride, gI + (size_t)n * Cin * H * W);
+    }
+}
+
+// cpu_backend.ixx:710-772 — gradWeight = sum_n gradOutput[n] x im2col(x[n])^T,
+// gradBias[co] = sum_n (sum_hw gradOutput[n][co][hw]).
+void omrefConv2dBackwardWeight(const float* x, const float* gO, float* gW, float* gB, int N, int Cin, int H, int W,
+                               int Cout, int KH, int KW, int stride, int pad) {
+    const int Ho = (H + 2 * pad - KH) / stride + 1, Wo = (W + 2 * pad - KW) / stride + 1;
+    const int rows = Cin * KH * KW, cols = Ho * Wo;
+    const size_t wsz = (size_t)Cout * rows;
+    std::memset(gW, 0, wsz * sizeof(float));
+    if (gB) std::memset(gB, 0, (size_t)Cout * sizeof(float));
+    std::vector<float> col((size_t)rows * cols), colT((size_t)rows * cols), tmp(wsz);
+    for (int n = 0; n < N; ++n) {
+        omrefIm2col(x + (size_t)n * Cin * H * W, Cin, H, W, KH, KW, pad, pad, stride, stride, col.data());
+        omrefTranspose2d(col.data(), colT.data(), rows, cols);
+        omrefMatmul(gO + (size_t)n * Cout * cols, colT.data(), tmp.data(), Cout, cols, rows);
+        for (size_t i = 0; i < wsz; ++i) gW[i] += tmp[i];
+        if (gB) {
+            const float* g = gO + (size_t)n * Cout * cols;
+            for (int co = 0; co < Cout; ++co) {
+                float b = 0.f;
+                for (int hw = 0; hw < cols; ++hw) b += g[(size_t)co * cols + hw];
+                gB[co] += b;
+            }
+        }
+    }
+}
+
+// cpu_backend.ixx:847-890 — per channel: gradGamma = sum(dy * xhat), gradBeta = sum(dy),
+// dx = gamma*invStd/cnt * (cnt*dy - gradBeta - xhat*gradGamma) (clang contracts the
+// sums and the bracket into fmas).
+void omrefBatchNorm2dBackward(const float* gO, const float* x, const float* mean, const float* invStd,
+                              const float* gamma, float* gI, float* gG, float* gBeta, int N, int C, int H, int W) {
+    const int S = H * W;
+    const int cnt = N * S;
+    const float invCnt = 1.0f / (float)cnt;
+#pragma omp parallel for schedule(static)
+    for (int c = 0; c < C; ++c) {
+        const float m = mean[c], is = invStd[c], g = gamma[c];
+        float sg = 0.f, sb = 0.f;
+        for (int n = 0; n < N; ++n)
+            for (int s = 0; s < S; ++s) {
+                const size_t i = ((size_t)n * C + c) * S + s;
+                const float xh = (x[i] - m) * is;
+                sg = std::fma(gO[i], xh, sg);
+                sb += gO[i];
+            }
+        gG[c] = sg;
+        gBeta[c] = sb;
+        for (int n = 0; n < N; ++n)
+            for (int s = 0; s < S; ++s) {
+                const size_t i = ((size_t)n * C + c) * S + s;
+                const float xh = (x[i] - m) * is;
+                gI[i] = g * is * invCnt * std::fma(-xh, sg, std::fma((float)cnt, gO[i], -sb));
+            }
+    }
+}
+
+// cpu_backend.ixx:897-934 — max over the window (strictly greater wins, so the
+// first maximum in kh, kw order is kept); the index is the flat input index, -1
+// for a window entirely in the padding (output -1e30).
+void omrefMaxPool2d(const float* x, float* y, int* idx, int N, int C, int H, int W, int KH, int KW, int stride,
+                    int pad) {
+    const int Ho = (H + 2 * pad - KH) / stride + 1, Wo = (W + 2 * pad - KW) / stride + 1;
+    for (int nc = 0; nc < N * C; ++nc)
+        for (int oh = 0; oh < Ho; ++oh)
+            for (int ow = 0; ow < Wo; ++ow) {
+                float best = -1e30f;
+                int bi = -1;
+                for (int kh = 0; kh < KH; ++kh)
+                    for (int kw = 0; kw < KW; ++kw) {
+                        const int ih = oh * stride - pad + kh, iw = ow * stride - pad + kw;
+                        if (ih >= 0 && ih < H && iw >= 0 && iw < W) {
+                            const int ii = (nc * H + ih) * W + iw;
+                            if (x[ii] > best) {
+                                best = x[ii];
+                                bi = ii;
+                            }
+                        }
+                    }
+                const size_t o = ((size_t)nc * Ho + oh) * Wo + ow;
+                y[o] = best;
+                idx[o] = bi;
+            }
+}
+
+// cpu_backend.ixx:937-955 — scatter-add through the saved indices in output order.
+void omrefMaxPool2dBackward(const float* gO, const int* idx, float* gI, int N, int C, int Ho, int Wo, int H, int W) {
+    const size_t nin = (size_t)N * C * H * W, nout = (size_t)N * C * Ho * Wo;
+    for (size_t i = 0; i < nin; ++i) gI[i] = 0.f;
+    for (size_t i = 0; i < nout; ++i)
+        if (idx[i] >= 0) gI[idx[i]] += gO[i];
+}
+
+// cpu_backend.ixx:958-990 — window sum over the valid taps divided by KH*KW
+// (padding counts in the divisor).
+void omrefAvgPool2d(const float* x, float* y, int N, int C, int H, int W, int KH, int KW, int stride, int pad) {
+    const int Ho = (H + 2 * pad - KH) / stride + 1, Wo = (W + 2 * pad - KW) / stride + 1;
+    for (int nc = 0; nc < N * C; ++nc)
+        for (int oh = 0; oh < Ho; ++oh)
+            for (int ow = 0; ow < Wo; ++ow) {
+                float sum = 0.f;
+                for (int kh = 0; kh < KH; ++kh)
+                    for (int kw = 0; kw < KW; ++kw) {
+                        const int ih = oh * stride - pad + kh, iw = ow * stride - pad + kw;
+                        if (ih >= 0 && ih < H && iw >= 0 && iw < W) sum += x[((size_t)nc * H + ih) * W + iw];
+                    }
+                y[((size_t)nc * Ho + oh) * Wo + ow] = sum / (float)(KH * KW);
+            }
+}
+
+// cpu_backend.ixx:994-1023 — each output's gradient times 1/(KH*KW) added to its valid taps.
+void omrefAvgPool2dBackward(const float* gO, float* gI, int N, int C, int H, int W, int Ho, int Wo, int KH, int KW,
+                            int stride, int pad) {
+    for (size_t i = 0; i < (size_t)N * C * H * W; ++i) gI[i] = 0.f;
+    const float scale = 1.0f / (float)(KH * KW);
+    for (int nc = 0; nc < N * C; ++nc)
+        for (int oh = 0; oh < Ho; ++oh)
+            for (int ow = 0; ow < Wo; ++ow) {
+                const float g = gO[((size_t)nc * Ho + oh) * Wo + ow] * scale;
+                for (int kh = 0; kh < KH; ++kh)
+                    for (int kw = 0; kw < KW; ++kw) {
+                        const int ih = oh * stride - pad + kh, iw = ow * stride - pad + kw;
+                        if (ih >= 0 && ih < H && iw >= 0 && iw < W) gI[((size_t)nc * H + ih) * W + iw] += g;
+                    }
+            }
+}
+
+// cpu_backend.ixx:1467-1488 — region [floor(o*H/OH), floor((o+1)*H/OH)) per axis, mean.
+void omrefAdaptiveAvgPool2d(const float* x, float* y, int N, int C, int H, int W, int OH, int OW) {
+    for (int nc = 0; nc < N * C; ++nc)
+        for (int oh = 0; oh < OH; ++oh)
+            for (int ow = 0; ow < OW; ++ow) {
+                const int h0 = oh * H / OH, h1 = (oh + 1) * H / OH, w0 = ow * W / OW, w1 = (ow + 1) * W / OW;
+                float sum = 0.f;
+                int cnt = 0;
+                for (int ih = h0; ih < h1; ++ih)
+                    for (int iw = w0; iw < w1; ++iw) {
+                        sum += x[((size_t)nc * H + ih) * W + iw];
+                        ++cnt;
+                    }
+                y[((size_t)nc * OH + oh) * OW + ow] = sum / (float)cnt;
+            }
+}
+
+// cpu_backend.ixx:1491-1510 — gradient / region size added over the region.
+void omrefAdaptiveAvgPool2dBackward(const float* gO, float* gI, int N, int C, int H, int W, int OH, int OW) {
+    for (size_t i = 0; i < (size_t)N * C * H * W; ++i) gI[i] = 0.f;
+    for (int nc = 0; nc < N * C; ++nc)
+        for (int oh = 0; oh < OH; ++oh)
+            for (int ow = 0; ow < OW; ++ow) {
+                const int h0 = oh * H / OH, h1 = (oh + 1) * H / OH, w0 = ow * W / OW, w1 = (ow + 1) * W / OW;
+                const float g = gO[((size_t)nc * OH + oh) * OW + ow] / (float)((h1 - h0) * (w1 - w0));
+                for (int ih = h0; ih < h1; ++ih)
+                    for (int iw = w0; iw < w1; ++iw) gI[((size_t)nc * H + ih) * W + iw] += g;
+            }
+}
+
+// cpu_backend.ixx:147-160, simd.ixx:180-200 — elementwise a + b.
+void omrefAdd(const float* a, const float* b, float* out, size_t n) {
+    for (size_t i = 0; i < n; ++i) out[i] = a[i] + b[i];
+}
+
 // difference; the GPU path converts with round-to-nearest-even instead.
 uint16_t omrefFloatToHalfTrunc(float f) {
     uint32_t b;

@@ -29,4 +29,36 @@ void refReluBackward(const float* x, const float* g, float* gi, size_t n) { om::
 void refAddBias(const float* a, const float* bias, float* out, int batch, int cols) {
     om::CPUBackend::addBias(a, bias, out, batch, cols);
 }
+void refConv2dBackwardInput(const float* gO, const float* w, float* gI, int n, int cin, int h, int wd, int cout, int kh,
+                            int kw, int stride, int pad) {
+    om::CPUBackend::conv2dBackwardInput(gO, w, gI, n, cin, h, wd, cout, kh, kw, stride, pad);
+}
+void refConv2dBackwardWeight(const float* x, const float* gO, float* gW, float* gB, int n, int cin, int h, int wd,
+                             int cout, int kh, int kw, int stride, int pad) {
+    om::CPUBackend::conv2dBackwardWeight(x, gO, gW, gB, n, cin, h, wd, cout, kh, kw, stride, pad);
+}
+void refBatchNorm2dBackward(const float* gO, const float* x, const float* mean, const float* invStd, const float* g,
+                            float* gI, float* gG, float* gB, int n, int c, int h, int w) {
+    om::CPUBackend::batchNorm2dBackward(gO, x, mean, invStd, g, gI, gG, gB, n, c, h, w);
+}
+void refMaxPool2d(const float* x, float* y, int* idx, int n, int c, int h, int w, int kh, int kw, int stride, int pad) {
+    om::CPUBackend::maxPool2d(x, y, idx, n, c, h, w, kh, kw, stride, pad);
+}
+void refMaxPool2dBackward(const float* gO, const int* idx, float* gI, int n, int c, int ho, int wo, int h, int w) {
+    om::CPUBackend::maxPool2dBackward(gO, idx, gI, n, c, ho, wo, h, w);
+}
+void refAvgPool2d(const float* x, float* y, int n, int c, int h, int w, int kh, int kw, int stride, int pad) {
+    om::CPUBackend::avgPool2d(x, y, n, c, h, w, kh, kw, stride, pad);
+}
+void refAvgPool2dBackward(const float* gO, float* gI, int n, int c, int h, int w, int ho, int wo, int kh, int kw,
+                          int stride, int pad) {
+    om::CPUBackend::avgPool2dBackward(gO, gI, n, c, h, w, ho, wo, kh, kw, stride, pad);
+}
+void refAdaptiveAvgPool2d(const float* x, float* y, int n, int c, int h, int w, int oh, int ow) {
+    om::CPUBackend::adaptiveAvgPool2d(x, y, n, c, h, w, oh, ow);
+}
+void refAdaptiveAvgPool2dBackward(const float* gO, float* gI, int n, int c, int h, int w, int oh, int ow) {
+    om::CPUBackend::adaptiveAvgPool2dBackward(gO, gI, n, c, h, w, oh, ow);
+}
+void refAdd(const float* a, const float* b, float* out, size_t n) { om::CPUBackend::add(a, b, out, n); }
 }

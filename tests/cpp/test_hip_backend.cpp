@@ -7,6 +7,7 @@
 // (tests/test_phase5.cpp:206-222), LinearWithBias zero input
 // (tests/test_nn.cpp:34-48), Conv2dForward shapes on all-ones input
 // (tests/test_conv.cpp:21-49; interior value = sum of weights).
+#include <algorithm>
 #include <cmath>
 #include <cstdio>
 #include <stdexcept>
@@ -111,13 +112,44 @@ static void testReluAndErrors() {
     EXPECT_NEAR(std::signbit(h[4]) ? 1 : 0, 0, 0);
     bool threw = false;
     try {
-        HIPBackend::batchNorm2d(x.p, y.p, x.p, x.p, x.p, x.p, nullptr, nullptr, 1, 1, 1, 1, 1e-5f, 0.1f, true);
+        HIPBackend::conv2d(x.p, x.p, nullptr, y.p, 1, 1, 1, 1, 1, 1, 1, 0, 0);   // stride 0
     } catch (const std::runtime_error& e) {
         threw = true;
         std::printf("expected error: %s\n", e.what());
     }
-    if (!threw) { std::printf("FAIL: training-mode batchNorm2d did not throw\n"); ++g_fail; }
+    if (!threw) { std::printf("FAIL: conv2d with stride 0 did not throw\n"); ++g_fail; }
     std::printf("ReluAndErrors done\n");
+}
+
+// One training step's pieces on closed-form inputs.
+static void testTrainingPieces() {
+    // BN training on one channel holding 1, 2, 3, 4: mean 2.5, biased var 1.25
+    Dev x(std::vector<float>{1.f, 2.f, 3.f, 4.f}), y(4), g(std::vector<float>{1.f}), b(std::vector<float>{0.f});
+    Dev rm(std::vector<float>{0.f}), rv(std::vector<float>{1.f}), sm(1), si(1);
+    HIPBackend::batchNorm2d(x.p, y.p, g.p, b.p, rm.p, rv.p, sm.p, si.p, 1, 1, 2, 2, 1e-5f, 0.1f, true);
+    const double inv = 1.0 / std::sqrt(1.25 + 1e-5);
+    auto yh = y.host();
+    for (int i = 0; i < 4; ++i) EXPECT_NEAR(yh[i], (i + 1 - 2.5) * inv, 1e-6);
+    EXPECT_NEAR(sm.host()[0], 2.5, 1e-7);
+    EXPECT_NEAR(rm.host()[0], 0.25, 1e-7);
+    EXPECT_NEAR(rv.host()[0], 0.9 + 0.125, 1e-6);
+    // input gradient of a 3x3 all-ones conv (8x8 input, no padding) for an all-ones
+    // output gradient: each input element counts the windows covering it
+    std::vector<float> ones9(9, 1.f), ones36(36, 1.f);
+    Dev w(ones9), go(ones36), gi(64);
+    HIPBackend::conv2dBackwardInput(go.p, w.p, gi.p, 1, 1, 8, 8, 1, 3, 3, 1, 0);
+    auto gh = gi.host();
+    auto cover = [](int i) { return std::min(i, 2) - std::max(0, i - 5) + 1; };
+    for (int i = 0; i < 8; ++i)
+        for (int j = 0; j < 8; ++j) EXPECT_NEAR(gh[i * 8 + j], cover(i) * cover(j), 0);
+    // weight gradient: every tap sees the 6x6 window of an all-ones input
+    std::vector<float> ones64(64, 1.f);
+    Dev xi(ones64), gw(9), gb(1);
+    HIPBackend::conv2dBackwardWeight(xi.p, go.p, gw.p, gb.p, 1, 1, 8, 8, 1, 3, 3, 1, 0);
+    auto wh = gw.host();
+    for (int t = 0; t < 9; ++t) EXPECT_NEAR(wh[t], 36, 0);
+    EXPECT_NEAR(gb.host()[0], 36, 0);
+    std::printf("TrainingPieces done\n");
 }
 
 int main() {
@@ -129,6 +161,7 @@ int main() {
         testLinearZeroInput();
         testConvAllOnes();
         testReluAndErrors();
+        testTrainingPieces();
         HIPBackend::synchronize();
     } catch (const std::exception& e) {
         std::printf("FAIL: exception %s\n", e.what());

@@ -76,6 +76,36 @@ def main() -> None:
     bb = O.randn((11,), 52)
     put("add_bias", A=A, bias=bb, out=O.add_bias(A, bb, backend="reference"))
 
+    # training path: conv gradients (stride 1 and 2), BN backward
+    xg = O.randn((2, 3, 9, 9), 60)
+    wg = O.randn((4, 3, 3, 3), 61)
+    for (s, p) in [(1, 1), (2, 1)]:
+        Ho = (9 + 2 * p - 3) // s + 1
+        go = O.randn((2, 4, Ho, Ho), 62 + s)
+        gi = O.conv2d_backward_input(go, wg, 9, 9, s, p, backend="reference")
+        gw, gb = O.conv2d_backward_weight(xg, go, 3, 3, s, p, backend="reference")
+        put(f"conv_bwd_s{s}p{p}", x=xg, w=wg, gO=go, gI=gi, gW=gw, gB=gb)
+    xb2 = O.randn((3, 4, 5, 6), 64)
+    g2, b2 = O.uniform((4,), 65, 0.5, 1.5), O.randn((4,), 66, 0.1)
+    _, _, _, sm2, si2 = O.batchnorm2d_train(xb2, g2, b2, np.zeros(4, np.float32), np.ones(4, np.float32),
+                                            backend="reference")
+    gy = O.randn(xb2.shape, 67)
+    gi, gg, gbt = O.batchnorm2d_backward(gy, xb2, sm2, si2, g2, backend="reference")
+    put("bn_backward", x=xb2, gO=gy, mean=sm2, invStd=si2, gamma=g2, gI=gi, gGamma=gg, gBeta=gbt)
+    # pooling (with ties and padding) and add
+    xp = O.randn((2, 3, 11, 11), 68)
+    xp[0, 0, :4, :4] = 1.0                                    # ties: the first maximum wins
+    y, idx = O.maxpool2d(xp, 3, 2, 1, backend="reference")
+    gp = O.randn(y.shape, 69)
+    put("maxpool_k3s2p1", x=xp, y=y, idx=idx, gO=gp, gI=O.maxpool2d_backward(gp, idx, 11, 11, backend="reference"))
+    ya = O.avgpool2d(xp, 3, 2, 1, backend="reference")
+    put("avgpool_k3s2p1", x=xp, y=ya, gO=gp, gI=O.avgpool2d_backward(gp, 11, 11, 3, 2, 1, backend="reference"))
+    yad = O.adaptive_avgpool2d(xp, 3, 4, backend="reference")
+    gad = O.randn(yad.shape, 70)
+    put("adaptive_3x4", x=xp, y=yad, gO=gad, gI=O.adaptive_avgpool2d_backward(gad, 11, 11, backend="reference"))
+    a1, a2 = O.randn((37,), 71), O.randn((37,), 72)
+    put("add", a=a1, b=a2, out=O.add(a1, a2, backend="reference"))
+
     path = os.path.join(HERE, "reference_cpubackend.npz")
     np.savez_compressed(path, **out)
     print(f"wrote {path} ({os.path.getsize(path)} bytes, {len(out)} arrays)")

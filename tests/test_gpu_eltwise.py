@@ -96,10 +96,10 @@ def test_batchnorm_eval_bitexact(hip, geom):
     assert np.array_equal(dm.numpy(), m) and np.array_equal(dv.numpy(), v)
 
 
-def test_batchnorm_training_rejected(hip):
+def test_batchnorm_null_pointer_rejected(hip):
     d = to_dev(hip, np.ones(4, np.float32))
-    with pytest.raises(hip.OmHipError, match="inference only"):
-        hip.HIPBackend.batchNorm2d(d, d, d, d, d, d, d, d, 1, 1, 2, 2, 1e-5, 0.1, True)
+    with pytest.raises(hip.OmHipError, match="null pointer"):
+        hip.HIPBackend.batchNorm2d(d, d, None, d, d, d, d, d, 1, 1, 2, 2, 1e-5, 0.1, True)
 
 
 @pytest.mark.parametrize("geom", [(3, 9, 9, 3, 3, 1, 1), (3, 9, 9, 3, 3, 2, 1), (2, 8, 8, 1, 1, 2, 0),

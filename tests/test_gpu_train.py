@@ -1,0 +1,179 @@
+"""Training half of the conv / BatchNorm path: conv2d input and weight
+gradients, BatchNorm2d training statistics and its backward pass, against
+float64 and against the oracle (CPUBackend restated: conv2dBackwardInput /
+conv2dBackwardWeight cpu_backend.ixx:666-772, batchNorm2d training
+:796-822, batchNorm2dBackward :847-890).
+
+Tolerances (written here, all 1e-4 relative to an error budget):
+  * conv gradients: the same contraction over absolute values — dX against
+    col2im(|W|^T |gO|), dW against sum |gO| im2col(|x|)^T, dB against sum |gO|;
+  * BN statistics: mean against mean|x|, variance against var + mean|x|^2,
+    y against |gamma| invStd (|x| + |mean| + mean|x|) + |beta|;
+  * BN backward: dX against |gamma| invStd / cnt (cnt |dy| + sum|dy| + |xhat| sum|dy xhat|),
+    dGamma against sum |dy xhat|, dBeta against sum |dy|.
+"""
+import numpy as np
+import pytest
+
+import oracle as O
+from conftest import empty_dev, to_dev
+
+pytestmark = pytest.mark.gpu
+TOL = O.TOL_FP32
+
+# (N, Cin, H, W, Cout, KH, KW, stride, pad): stride-1 shapes take the flipped-weight
+# convolution, the others the GEMM + col2im gather.
+GRAD_SHAPES = [
+    (2, 16, 14, 14, 32, 3, 3, 1, 1),    # ResNet 3x3 s1
+    (2, 16, 15, 15, 32, 3, 3, 2, 1),    # 3x3 s2, odd input
+    (2, 32, 14, 14, 64, 1, 1, 2, 0),    # 1x1 s2 downsample
+    (1, 3, 32, 32, 16, 7, 7, 2, 3),     # 7x7 s2 stem
+    (2, 8, 11, 11, 8, 5, 5, 1, 1),      # 5x5 s1 pad 1 (flipped pad 3)
+    (2, 8, 12, 10, 16, 3, 1, 1, 0),     # KH != KW
+    (2, 8, 9, 9, 8, 1, 1, 1, 1),        # pad > K-1
+    (3, 5, 7, 9, 6, 3, 3, 3, 2),        # stride 3, ragged
+]
+
+
+def _ids(s):
+    return "N{}C{}H{}W{}o{}k{}x{}s{}p{}".format(*s)
+
+
+def _data(shape, seed):
+    N, Cin, H, W, Cout, KH, KW, s, p = shape
+    Ho, Wo = O.out_hw(H, W, KH, KW, s, p)
+    x = O.randn((N, Cin, H, W), seed)
+    w = O.randn((Cout, Cin, KH, KW), seed + 1, 0.2)
+    g = O.randn((N, Cout, Ho, Wo), seed + 2)
+    return x, w, g, Ho, Wo
+
+
+@pytest.mark.parametrize("shape", GRAD_SHAPES, ids=_ids)
+def test_conv_backward_input(hip, shape):
+    N, Cin, H, W, Cout, KH, KW, s, p = shape
+    x, w, g, Ho, Wo = _data(shape, 31 + sum(shape))
+    dG, dW = to_dev(hip, g), to_dev(hip, w)
+    dX = empty_dev(hip, (N, Cin, H, W))
+    hip.HIPBackend.conv2dBackwardInput(dG, dW, dX, N, Cin, H, W, Cout, KH, KW, s, p)
+    got = dX.numpy()
+    (X64, Xb), _, _ = O.conv_backward_f64(x, w, g, s, p) if KH == KW else _f64_rect(x, w, g, s, p)
+    assert O.normalized_error(got, X64, Xb) <= TOL
+    ref = O.conv2d_backward_input(g, w, H, W, s, p)
+    assert O.normalized_error(got, ref, Xb) <= TOL
+
+
+@pytest.mark.parametrize("shape", GRAD_SHAPES, ids=_ids)
+def test_conv_backward_weight(hip, shape):
+    N, Cin, H, W, Cout, KH, KW, s, p = shape
+    x, w, g, Ho, Wo = _data(shape, 57 + sum(shape))
+    dx, dg = to_dev(hip, x), to_dev(hip, g)
+    dW = empty_dev(hip, (Cout, Cin, KH, KW))
+    dB = empty_dev(hip, (Cout,))
+    hip.HIPBackend.conv2dBackwardWeight(dx, dg, dW, dB, N, Cin, H, W, Cout, KH, KW, s, p)
+    _, (W64, Wb), (B64, Bb) = O.conv_backward_f64(x, w, g, s, p) if KH == KW else _f64_rect(x, w, g, s, p)
+    gw, gb = dW.numpy(), dB.numpy()
+    assert O.normalized_error(gw, W64, Wb) <= TOL
+    assert O.normalized_error(gb, B64, Bb) <= TOL
+    rw, rb = O.conv2d_backward_weight(x, g, KH, KW, s, p)
+    assert O.normalized_error(gw, rw, Wb) <= TOL
+    assert O.normalized_error(gb, rb, Bb) <= TOL
+    # the bias pointer is optional
+    dW2 = empty_dev(hip, (Cout, Cin, KH, KW))
+    hip.HIPBackend.conv2dBackwardWeight(dx, dg, dW2, None, N, Cin, H, W, Cout, KH, KW, s, p)
+    assert np.array_equal(dW2.numpy(), gw), "weight gradient must not depend on the bias request"
+
+
+def _f64_rect(x, w, g, s, p):
+    """float64 gradients for rectangular kernels (direct loops over taps)."""
+    x64, w64, g64 = (np.asarray(a, np.float64) for a in (x, w, g))
+    N, Cin, H, W = x64.shape
+    Cout, _, KH, KW = w64.shape
+    Ho, Wo = g64.shape[2:]
+    xp = np.zeros((N, Cin, H + 2 * p, W + 2 * p))
+    xp[:, :, p:p + H, p:p + W] = x64
+    dXp, dXpb = np.zeros_like(xp), np.zeros_like(xp)
+    dW, dWb = np.zeros_like(w64), np.zeros_like(w64)
+    for kh in range(KH):
+        for kw in range(KW):
+            win = xp[:, :, kh:kh + s * (Ho - 1) + 1:s, kw:kw + s * (Wo - 1) + 1:s]   # N Cin Ho Wo
+            dW[:, :, kh, kw] = np.einsum("nohw,nchw->oc", g64, win)
+            dWb[:, :, kh, kw] = np.einsum("nohw,nchw->oc", np.abs(g64), np.abs(win))
+            dXp[:, :, kh:kh + s * (Ho - 1) + 1:s, kw:kw + s * (Wo - 1) + 1:s] += np.einsum("oc,nohw->nchw", w64[:, :, kh, kw], g64)
+            dXpb[:, :, kh:kh + s * (Ho - 1) + 1:s, kw:kw + s * (Wo - 1) + 1:s] += np.einsum("oc,nohw->nchw", np.abs(w64[:, :, kh, kw]), np.abs(g64))
+    sl = (slice(None), slice(None), slice(p, p + H), slice(p, p + W))
+    return (dXp[sl], dXpb[sl]), (dW, dWb), (g64.sum(axis=(0, 2, 3)), np.abs(g64).sum(axis=(0, 2, 3)))
+
+
+def test_conv_backward_weight_chunked(hip):
+    """ResNet-18 layer-4 conv at batch 32: the per-image partial products exceed one
+    workspace, so the batch is reduced in two chunks (the second accumulates)."""
+    N, Cin, H, W, Cout, K, s, p = 32, 512, 7, 7, 512, 3, 1, 1
+    x = O.randn((N, Cin, H, W), 71)
+    g = O.randn((N, Cout, H, W), 72)
+    dW = empty_dev(hip, (Cout, Cin, K, K))
+    hip.HIPBackend.conv2dBackwardWeight(to_dev(hip, x), to_dev(hip, g), dW, None, N, Cin, H, W, Cout, K, K, s, p)
+    got = dW.numpy().reshape(Cout, -1)
+    rows = np.array([0, 1, 255, 511])
+    cols, _, _ = O._im2col64(np.asarray(x, np.float64), K, K, s, p)     # N x Kc x HW
+    g64 = np.asarray(g, np.float64).reshape(N, Cout, H * W)[:, rows]
+    ref = np.einsum("nop,nkp->ok", g64, cols)
+    bound = np.einsum("nop,nkp->ok", np.abs(g64), np.abs(cols))
+    assert O.normalized_error(got[rows], ref, bound) <= TOL
+
+
+BN_SHAPES = [(4, 8, 7, 9), (8, 64, 28, 28), (32, 16, 7, 7), (1, 3, 1, 1), (2, 300, 5, 5)]
+
+
+@pytest.mark.parametrize("shape", BN_SHAPES, ids=lambda s: "N{}C{}H{}W{}".format(*s))
+def test_batchnorm_training(hip, shape):
+    N, C, H, W = shape
+    x = O.randn(shape, 81 + C) * 2.0 + 0.5
+    gamma, beta = O.uniform((C,), 82, 0.5, 1.5), O.randn((C,), 83, 0.1)
+    rm0, rv0 = O.randn((C,), 84, 0.1), O.uniform((C,), 85, 0.5, 1.5)
+    dx, dy = to_dev(hip, x), empty_dev(hip, shape)
+    drm, drv = to_dev(hip, rm0), to_dev(hip, rv0)
+    dsm, dsi = empty_dev(hip, (C,)), empty_dev(hip, (C,))
+    hip.HIPBackend.batchNorm2d(dx, dy, to_dev(hip, gamma), to_dev(hip, beta), drm, drv, dsm, dsi, N, C, H, W,
+                               1e-5, 0.1, True)
+    y, rm, rv, sm, si = dy.numpy(), drm.numpy(), drv.numpy(), dsm.numpy(), dsi.numpy()
+    y64, mean64, var64, inv64 = O.bn_train_f64(x, gamma, beta)
+    absmean = np.abs(np.asarray(x, np.float64)).mean(axis=(0, 2, 3))
+    assert np.max(np.abs(sm - mean64) / absmean) <= TOL
+    assert np.max(np.abs(1.0 / si.astype(np.float64) ** 2 - 1e-5 - var64) / (var64 + absmean ** 2)) <= TOL
+    assert np.max(np.abs(rm - (0.9 * rm0 + 0.1 * mean64)) / (np.abs(rm0) + absmean)) <= TOL
+    assert np.max(np.abs(rv - (0.9 * rv0 + 0.1 * var64)) / (rv0 + var64 + absmean ** 2)) <= TOL
+    ybound = (np.abs(gamma)[None, :, None, None] * inv64[None, :, None, None] *
+              (np.abs(np.asarray(x, np.float64)) + np.abs(mean64)[None, :, None, None] + absmean[None, :, None, None])
+              + np.abs(beta)[None, :, None, None])
+    assert O.normalized_error(y, y64, ybound) <= TOL
+    # against the oracle (the reference's sequential sums)
+    ry, rrm, rrv, rsm, rsi = O.batchnorm2d_train(x, gamma, beta, rm0, rv0)
+    assert O.normalized_error(y, ry, ybound) <= TOL
+    assert np.max(np.abs(sm - rsm) / absmean) <= TOL
+    assert np.max(np.abs(si - rsi) / rsi) <= TOL
+    # saved-statistics pointers are optional
+    dy2, drm2, drv2 = empty_dev(hip, shape), to_dev(hip, rm0), to_dev(hip, rv0)
+    hip.HIPBackend.batchNorm2d(dx, dy2, to_dev(hip, gamma), to_dev(hip, beta), drm2, drv2, None, None, N, C, H, W,
+                               1e-5, 0.1, True)
+    assert np.array_equal(dy2.numpy(), y) and np.array_equal(drm2.numpy(), rm) and np.array_equal(drv2.numpy(), rv)
+
+
+@pytest.mark.parametrize("shape", BN_SHAPES, ids=lambda s: "N{}C{}H{}W{}".format(*s))
+def test_batchnorm_backward(hip, shape):
+    N, C, H, W = shape
+    x = O.randn(shape, 91 + C)
+    gy = O.randn(shape, 92 + C)
+    gamma, beta = O.uniform((C,), 93, 0.5, 1.5), O.randn((C,), 94, 0.1)
+    _, _, _, sm, si = O.batchnorm2d_train(x, gamma, beta, np.zeros(C, np.float32), np.ones(C, np.float32))
+    dgi, dgg, dgb = empty_dev(hip, shape), empty_dev(hip, (C,)), empty_dev(hip, (C,))
+    hip.HIPBackend.batchNorm2dBackward(to_dev(hip, gy), to_dev(hip, x), to_dev(hip, sm), to_dev(hip, si),
+                                       to_dev(hip, gamma), dgi, dgg, dgb, N, C, H, W)
+    gi, gg, gb = dgi.numpy(), dgg.numpy(), dgb.numpy()
+    dX, dG, dB, bound, absGX, absG = O.bn_backward_f64(gy, x, sm, si, gamma)
+    assert O.normalized_error(gi, dX, bound) <= TOL
+    assert O.normalized_error(gg, dG, absGX) <= TOL
+    assert O.normalized_error(gb, dB, absG) <= TOL
+    ri, rg, rb = O.batchnorm2d_backward(gy, x, sm, si, gamma)
+    assert O.normalized_error(gi, ri, bound) <= TOL
+    assert O.normalized_error(gg, rg, absGX) <= TOL
+    assert O.normalized_error(gb, rb, absG) <= TOL

@@ -76,6 +76,34 @@ def test_golden_relu_bias(gold):
     assert np.array_equal(bits(O.add_bias(gold["add_bias.A"], gold["add_bias.bias"])), bits(gold["add_bias.out"]))
 
 
+def test_golden_training(gold):
+    for g, (s, p) in (("conv_bwd_s1p1", (1, 1)), ("conv_bwd_s2p1", (2, 1))):
+        gi = O.conv2d_backward_input(gold[f"{g}.gO"], gold[f"{g}.w"], 9, 9, s, p)
+        assert np.array_equal(bits(gi), bits(gold[f"{g}.gI"])), g
+        gw, gb = O.conv2d_backward_weight(gold[f"{g}.x"], gold[f"{g}.gO"], 3, 3, s, p)
+        assert np.array_equal(bits(gw), bits(gold[f"{g}.gW"])), g
+        assert np.array_equal(bits(gb), bits(gold[f"{g}.gB"])), g
+    k = "bn_backward"
+    res = O.batchnorm2d_backward(gold[f"{k}.gO"], gold[f"{k}.x"], gold[f"{k}.mean"], gold[f"{k}.invStd"],
+                                 gold[f"{k}.gamma"])
+    for a, n in zip(res, ("gI", "gGamma", "gBeta")):
+        assert np.array_equal(bits(a), bits(gold[f"{k}.{n}"])), n
+
+
+def test_golden_pooling(gold):
+    k = "maxpool_k3s2p1"
+    y, idx = O.maxpool2d(gold[f"{k}.x"], 3, 2, 1)
+    assert np.array_equal(bits(y), bits(gold[f"{k}.y"])) and np.array_equal(idx, gold[f"{k}.idx"])
+    assert np.array_equal(bits(O.maxpool2d_backward(gold[f"{k}.gO"], idx, 11, 11)), bits(gold[f"{k}.gI"]))
+    k = "avgpool_k3s2p1"
+    assert np.array_equal(bits(O.avgpool2d(gold[f"{k}.x"], 3, 2, 1)), bits(gold[f"{k}.y"]))
+    assert np.array_equal(bits(O.avgpool2d_backward(gold[f"{k}.gO"], 11, 11, 3, 2, 1)), bits(gold[f"{k}.gI"]))
+    k = "adaptive_3x4"
+    assert np.array_equal(bits(O.adaptive_avgpool2d(gold[f"{k}.x"], 3, 4)), bits(gold[f"{k}.y"]))
+    assert np.array_equal(bits(O.adaptive_avgpool2d_backward(gold[f"{k}.gO"], 11, 11)), bits(gold[f"{k}.gI"]))
+    assert np.array_equal(bits(O.add(gold["add.a"], gold["add.b"])), bits(gold["add.out"]))
+
+
 # ---------------------------------------------------------- 2. known answers
 def test_known_answers():
     assert O.matmul(np.array([[1, 2], [3, 4]]), np.array([[5, 6], [7, 8]])).tolist() == [[19, 22], [43, 50]]
@@ -123,6 +151,33 @@ def test_vs_reference_conv_bn_relu(geom):
     bb = O.batchnorm2d_eval(y2, g, be, m, v, backend="reference")
     assert all(np.array_equal(bits(u), bits(t)) for u, t in zip(a, bb))
     assert np.array_equal(bits(O.relu(a[0])), bits(O.relu(bb[0], backend="reference")))
+
+
+@ref_built
+@pytest.mark.parametrize("geom", [(2, 3, 11, 13, 5, 3, 2, 1), (1, 8, 7, 7, 16, 1, 1, 0), (2, 4, 12, 12, 6, 7, 2, 3),
+                                  (3, 4, 8, 8, 4, 3, 1, 1)])
+def test_vs_reference_training(geom):
+    N, cin, h, w, cout, k, s, p = geom
+    x, wt = O.randn((N, cin, h, w), 21), O.randn((cout, cin, k, k), 22)
+    Ho, Wo = O.out_hw(h, w, k, k, s, p)
+    g = O.randn((N, cout, Ho, Wo), 23)
+    assert np.array_equal(bits(O.conv2d_backward_input(g, wt, h, w, s, p)),
+                          bits(O.conv2d_backward_input(g, wt, h, w, s, p, backend="reference")))
+    a = O.conv2d_backward_weight(x, g, k, k, s, p)
+    b = O.conv2d_backward_weight(x, g, k, k, s, p, backend="reference")
+    assert np.array_equal(bits(a[0]), bits(b[0])) and np.array_equal(bits(a[1]), bits(b[1]))
+    gam = O.uniform((cin,), 24, 0.5, 1.5)
+    _, _, _, sm, si = O.batchnorm2d_train(x, gam, np.zeros(cin, np.float32), np.zeros(cin, np.float32),
+                                          np.ones(cin, np.float32))
+    gy = O.randn(x.shape, 25)
+    r1 = O.batchnorm2d_backward(gy, x, sm, si, gam)
+    r2 = O.batchnorm2d_backward(gy, x, sm, si, gam, backend="reference")
+    assert all(np.array_equal(bits(u), bits(t)) for u, t in zip(r1, r2))
+    y1, i1 = O.maxpool2d(x, 3, 2, 1)
+    y2, i2 = O.maxpool2d(x, 3, 2, 1, backend="reference")
+    assert np.array_equal(bits(y1), bits(y2)) and np.array_equal(i1, i2)
+    assert np.array_equal(bits(O.avgpool2d(x, 3, 2, 1)), bits(O.avgpool2d(x, 3, 2, 1, backend="reference")))
+    assert np.array_equal(bits(O.adaptive_avgpool2d(x, 2, 3)), bits(O.adaptive_avgpool2d(x, 2, 3, backend="reference")))
 
 
 # ----------------------------------------------- 4. float64 and closed forms
@@ -190,6 +245,119 @@ def test_half_truncation_rule():
     assert t[5] == 0                           # fp32 subnormal flushed
     assert t[6] == 0x7C00                      # overflow -> inf
     assert t[7] == (x[7:8].astype(np.float16).view(np.uint16)[0])   # exact fp16 subnormal
+
+
+# ------------------------------------------- training path: closed forms
+@pytest.mark.parametrize("geom", [(2, 3, 9, 9, 4, 3, 1, 1), (2, 3, 9, 9, 4, 3, 2, 1), (1, 4, 8, 8, 6, 1, 2, 0),
+                                  (1, 2, 12, 12, 3, 7, 2, 3)])
+def test_conv_gradients_adjoint(geom):
+    """<conv(x, w), g> = <x, dX(g)> = <w, dW(x, g)> (the gradients are the adjoints of
+    the forward conv in x and in w), in float64 for the checker and within the
+    K-scaled bar for the oracle; dB = sum of g."""
+    N, C, H, W, Co, K, s, p = geom
+    x, w = O.randn((N, C, H, W), 1), O.randn((Co, C, K, K), 2)
+    Ho, Wo = O.out_hw(H, W, K, K, s, p)
+    g = O.randn((N, Co, Ho, Wo), 3)
+    y64, _ = O.conv_f64(x, w, None, s, p)
+    (dX, dXb), (dW, dWb), (dB, dBb) = O.conv_backward_f64(x, w, g, s, p)
+    lhs = float((y64 * g).sum())
+    assert abs(lhs - float((np.asarray(x, np.float64) * dX).sum())) <= 1e-9 * (1 + abs(lhs))
+    assert abs(lhs - float((np.asarray(w, np.float64) * dW).sum())) <= 1e-9 * (1 + abs(lhs))
+    assert np.allclose(dB, np.asarray(g, np.float64).sum(axis=(0, 2, 3)))
+    assert O.normalized_error(O.conv2d_backward_input(g, w, H, W, s, p), dX, dXb) <= O.TOL_FP32
+    gw, gb = O.conv2d_backward_weight(x, g, K, K, s, p)
+    assert O.normalized_error(gw, dW, dWb) <= O.TOL_FP32
+    assert O.normalized_error(gb, dB, dBb) <= O.TOL_FP32
+
+
+def test_bn_backward_numeric_gradient():
+    """The float64 BN backward equals central differences of the float64 BN training
+    forward (loss = sum(y * r)) in x, gamma and beta; the oracle meets it."""
+    rng = np.random.default_rng(5)
+    x = rng.standard_normal((2, 3, 3, 2))
+    gamma, beta = rng.uniform(0.5, 1.5, 3), rng.standard_normal(3)
+    r = rng.standard_normal(x.shape)
+
+    def loss(xv, gv, bv):
+        y, _, _, _ = O.bn_train_f64(xv, gv, bv)
+        return float((y * r).sum())
+
+    _, mean, _, inv = O.bn_train_f64(x, gamma, beta)
+    dX, dG, dB, bound, absGX, absG = O.bn_backward_f64(r, x, mean, inv, gamma)
+    h = 1e-6
+    num = np.zeros_like(x)
+    for i in np.ndindex(*x.shape):
+        xp, xm = x.copy(), x.copy()
+        xp[i] += h
+        xm[i] -= h
+        num[i] = (loss(xp, gamma, beta) - loss(xm, gamma, beta)) / (2 * h)
+    assert np.max(np.abs(num - dX)) < 1e-6
+    for c in range(3):
+        e = np.eye(3)[c] * h
+        assert abs((loss(x, gamma + e, beta) - loss(x, gamma - e, beta)) / (2 * h) - dG[c]) < 1e-6
+        assert abs((loss(x, gamma, beta + e) - loss(x, gamma, beta - e)) / (2 * h) - dB[c]) < 1e-6
+    x32 = x.astype(np.float32)
+    _, _, _, sm, si = O.batchnorm2d_train(x32, gamma.astype(np.float32), beta.astype(np.float32),
+                                          np.zeros(3, np.float32), np.ones(3, np.float32))
+    gi, gg, gb = O.batchnorm2d_backward(r.astype(np.float32), x32, sm, si, gamma.astype(np.float32))
+    dX2, dG2, dB2, bound2, absGX2, absG2 = O.bn_backward_f64(r, x32, sm, si, gamma)
+    assert O.normalized_error(gi, dX2, bound2) <= O.TOL_FP32
+    assert O.normalized_error(gg, dG2, absGX2) <= O.TOL_FP32
+    assert O.normalized_error(gb, dB2, absG2) <= O.TOL_FP32
+
+
+def test_pooling_closed_forms():
+    """Pools against numpy sliding windows: max (first maximum's flat index), average
+    with padding counted in the divisor, adaptive regions; backward = transpose."""
+    x = O.randn((2, 3, 9, 10), 7)
+    K, s, p = 3, 2, 1
+    Ho, Wo = O.out_hw(9, 10, K, K, s, p)
+    xp = np.full((2, 3, 9 + 2 * p, 10 + 2 * p), -np.inf, np.float64)
+    xp[:, :, p:p + 9, p:p + 10] = x
+    y, idx = O.maxpool2d(x, K, s, p)
+    for oh in range(Ho):
+        for ow in range(Wo):
+            win = xp[:, :, oh * s:oh * s + K, ow * s:ow * s + K].reshape(2, 3, -1)
+            assert np.array_equal(y[:, :, oh, ow], win.max(axis=2).astype(np.float32))
+            a = win.argmax(axis=2)
+            ih, iw = oh * s - p + a // K, ow * s - p + a % K
+            flat = ((np.arange(2)[:, None] * 3 + np.arange(3)[None, :]) * 9 + ih) * 10 + iw
+            assert np.array_equal(idx[:, :, oh, ow], flat)
+    xz = np.zeros_like(xp)
+    xz[:, :, p:p + 9, p:p + 10] = x
+    ya = O.avgpool2d(x, K, s, p)
+    for oh in range(Ho):
+        for ow in range(Wo):
+            ref = xz[:, :, oh * s:oh * s + K, ow * s:ow * s + K].sum(axis=(2, 3)) / 9.0
+            assert np.allclose(ya[:, :, oh, ow], ref, rtol=1e-6, atol=1e-6)
+    g = O.randn(ya.shape, 8)
+    ga = O.avgpool2d_backward(g, 9, 10, K, s, p)
+    assert np.isclose(float((ya.astype(np.float64) * g).sum()), float((x.astype(np.float64) * ga).sum()), rtol=1e-5)
+    gm = O.maxpool2d_backward(g, idx, 9, 10)
+    assert np.isclose(float((y.astype(np.float64) * g).sum()), float((x.astype(np.float64) * gm).sum()), rtol=1e-5)
+    yad = O.adaptive_avgpool2d(x, 1, 1)
+    assert np.allclose(yad[:, :, 0, 0], x.mean(axis=(2, 3)), rtol=1e-5, atol=1e-6)
+    gad = O.randn(yad.shape, 9)
+    assert np.allclose(O.adaptive_avgpool2d_backward(gad, 9, 10), np.broadcast_to(gad / 90.0, x.shape), rtol=1e-6)
+
+
+def test_training_planted_mistakes():
+    """A conv gradient with a shifted tap or a dropped image, or BN backward without
+    the mean-gradient term, must fail the bar."""
+    x, w = O.randn((2, 3, 9, 9), 11), O.randn((4, 3, 3, 3), 12)
+    g = O.randn((2, 4, 5, 5), 13)
+    (dX, dXb), (dW, dWb), _ = O.conv_backward_f64(x, w, g, 2, 1)
+    gi = O.conv2d_backward_input(g, w, 9, 9, 2, 1)
+    assert O.normalized_error(np.roll(gi, 1, axis=3), dX, dXb) > O.TOL_FP32
+    gw, _ = O.conv2d_backward_weight(x[:1], g[:1], 3, 3, 2, 1)           # second image dropped
+    assert O.normalized_error(gw, dW, dWb) > O.TOL_FP32
+    xb, gy = O.randn((2, 3, 4, 4), 14), O.randn((2, 3, 4, 4), 15)
+    gam = O.uniform((3,), 16, 0.5, 1.5)
+    _, _, _, sm, si = O.batchnorm2d_train(xb, gam, np.zeros(3, np.float32), np.zeros(3, np.float32),
+                                          np.ones(3, np.float32))
+    dX, _, _, bound, _, _ = O.bn_backward_f64(gy, xb, sm, si, gam)
+    naive = gam[None, :, None, None] * si[None, :, None, None] * gy              # ignores the batch statistics
+    assert O.normalized_error(naive, dX, bound) > O.TOL_FP32
 
 
 # ---------------------------------------- planted mistakes are caught (CPU)
