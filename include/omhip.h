@@ -178,6 +178,53 @@ int omHipBatchNorm2dBackward(const float* pGradOutput, const float* pInput,
                              float* pGradInput, float* pGradGamma, float* pGradBeta,
                              int nBatch, int nChannels, int nH, int nW, float fEps);
 
+/* ===== pooling and the residual sum (cuda_kernels.cuh:218-245, :74) ===== */
+
+/* replaces omCudaMaxPool2d (cuh:218); CPUBackend::maxPool2d cpu_backend.ixx:897-934:
+ * first maximum (strict >) in (kh, kw) order; pIndices (may be NULL) receives the flat
+ * input index ((n*C+c)*H+ih)*W+iw, -1 for a window wholly in the padding (value -1e30). */
+int omHipMaxPool2d(const float* pIn, float* pOut, int* pIndices,
+                   int nN, int nC, int nH, int nW,
+                   int nKH, int nKW, int nSH, int nSW, int nPH, int nPW);
+/* replaces omCudaMaxPool2dBackward (cuh:224); CPUBackend::maxPool2dBackward
+ * cpu_backend.ixx:937-955: pGradIn zeroed, then gradients scattered through the
+ * indices. An input that is the maximum of several windows receives their
+ * gradients in an unspecified order (atomic adds). */
+int omHipMaxPool2dBackward(const float* pGradOut, const int* pIndices, float* pGradIn,
+                           int nN, int nC, int nH, int nW, int nHout, int nWout);
+/* NEW: as omHipMaxPool2dBackward with the window geometry given, computed as an
+ * ordered gather: bit-identical to CPUBackend::maxPool2dBackward. */
+int omHipMaxPool2dBackwardEx(const float* pGradOut, const int* pIndices, float* pGradIn,
+                             int nN, int nC, int nH, int nW,
+                             int nKH, int nKW, int nSH, int nSW, int nPH, int nPW);
+/* replaces omCudaAvgPool2d (cuh:230); CPUBackend::avgPool2d cpu_backend.ixx:958-990
+ * (sum of the valid taps / (KH*KW)) */
+int omHipAvgPool2d(const float* pIn, float* pOut, int nN, int nC, int nH, int nW,
+                   int nKH, int nKW, int nSH, int nSW, int nPH, int nPW);
+/* replaces omCudaAvgPool2dBackward (cuh:236); CPUBackend::avgPool2dBackward
+ * cpu_backend.ixx:994-1023; pGradIn [N,C,H,W] is overwritten */
+int omHipAvgPool2dBackward(const float* pGradOut, float* pGradIn, int nN, int nC, int nH, int nW,
+                           int nKH, int nKW, int nSH, int nSW, int nPH, int nPW);
+/* replaces omCudaAdaptiveAvgPool2d (cuh:242); CPUBackend::adaptiveAvgPool2d
+ * cpu_backend.ixx:1467-1488 (regions [floor(o*H/OH), floor((o+1)*H/OH))) */
+int omHipAdaptiveAvgPool2d(const float* pIn, float* pOut, int nN, int nC, int nH, int nW,
+                           int nOutH, int nOutW);
+/* NEW: CPUBackend::adaptiveAvgPool2dBackward cpu_backend.ixx:1491-1510 */
+int omHipAdaptiveAvgPool2dBackward(const float* pGradOut, float* pGradIn, int nN, int nC, int nH, int nW,
+                                   int nOutH, int nOutW);
+/* replaces omCudaAdd (cuh:74); CPUBackend::add cpu_backend.ixx:147-160 */
+int omHipAdd(const float* pA, const float* pB, float* pC, int nCount);
+/* NEW: omHipConv2dBiasBnAct with the residual added after BN and before the
+ * activation: out = act(BN(conv(x) + bias) + residual). Reference composition: the
+ * BasicBlock / Bottleneck tail bn2(conv2(.)) + shortcut -> relu (resnet.ixx:55-79,
+ * resnet50.ixx:57-83). pResidual [N,Cout,Ho,Wo] must not alias pOutput. */
+int omHipConv2dBiasBnAddAct(const float* pInput, const float* pWeight, const float* pBias,
+                            const float* pGamma, const float* pBeta,
+                            const float* pMean, const float* pVar, float fEps,
+                            const float* pResidual, int nAct, float* pOutput,
+                            int nBatch, int nCin, int nH, int nW,
+                            int nCout, int nKH, int nKW, int nStride, int nPad);
+
 /* ===== fp16 / bf16 GEMM, fp32 accumulate (NEW; the reference has only the software
  * converter om.engine.fp16.ixx:36-164) ===== */
 

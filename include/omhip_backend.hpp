@@ -105,6 +105,42 @@ public:
               "batchNorm2dBackward");
     }
 
+    // ---- pooling and add (cpu_backend.ixx:897-1023, :1467-1510, :147-160) ----
+    static void maxPool2d(const float* pInput, float* pOutput, int* pIndices, int nBatch, int nChannels, int nH,
+                          int nW, int nKH, int nKW, int nStride, int nPad) {
+        check(omHipMaxPool2d(pInput, pOutput, pIndices, nBatch, nChannels, nH, nW, nKH, nKW, nStride, nStride, nPad,
+                             nPad),
+              "maxPool2d");
+    }
+    static void maxPool2dBackward(const float* pGradOutput, const int* pIndices, float* pGradInput, int nBatch,
+                                  int nChannels, int nHout, int nWout, int nH, int nW) {
+        check(omHipMaxPool2dBackward(pGradOutput, pIndices, pGradInput, nBatch, nChannels, nH, nW, nHout, nWout),
+              "maxPool2dBackward");
+    }
+    static void avgPool2d(const float* pInput, float* pOutput, int nBatch, int nChannels, int nH, int nW, int nKH,
+                          int nKW, int nStride, int nPad) {
+        check(omHipAvgPool2d(pInput, pOutput, nBatch, nChannels, nH, nW, nKH, nKW, nStride, nStride, nPad, nPad),
+              "avgPool2d");
+    }
+    static void avgPool2dBackward(const float* pGradOutput, float* pGradInput, int nBatch, int nChannels, int nH,
+                                  int nW, int /*nHout*/, int /*nWout*/, int nKH, int nKW, int nStride, int nPad) {
+        check(omHipAvgPool2dBackward(pGradOutput, pGradInput, nBatch, nChannels, nH, nW, nKH, nKW, nStride, nStride,
+                                     nPad, nPad),
+              "avgPool2dBackward");
+    }
+    static void adaptiveAvgPool2d(const float* pInput, float* pOutput, int nBatch, int nChannels, int nH, int nW,
+                                  int nOutH, int nOutW) {
+        check(omHipAdaptiveAvgPool2d(pInput, pOutput, nBatch, nChannels, nH, nW, nOutH, nOutW), "adaptiveAvgPool2d");
+    }
+    static void adaptiveAvgPool2dBackward(const float* pGradOutput, float* pGradInput, int nBatch, int nChannels,
+                                          int nH, int nW, int nOutH, int nOutW) {
+        check(omHipAdaptiveAvgPool2dBackward(pGradOutput, pGradInput, nBatch, nChannels, nH, nW, nOutH, nOutW),
+              "adaptiveAvgPool2dBackward");
+    }
+    static void add(const float* pA, const float* pB, float* pOut, size_t nCount) {
+        check(omHipAdd(pA, pB, pOut, toInt(nCount)), "add");
+    }
+
     // ---- entries the reference builds by composition ----
     // transpose2d(B) + matmul (autograd.ixx:261-273)
     static void matmulTransB(const float* pA, const float* pB, float* pC, int nM, int nK, int nN) {
@@ -116,6 +152,15 @@ public:
     }
     static void batchedMatmulTransB(const float* pA, const float* pB, float* pC, int nBatch, int nM, int nK, int nN) {
         check(omHipBatchedMatmulTransB(pA, pB, pC, nBatch, nM, nK, nN), "batchedMatmulTransB");
+    }
+    // conv2d -> batchNorm2d(eval) -> add(shortcut) -> relu (resnet.ixx:55-79)
+    static void conv2dBiasBnAddAct(const float* pInput, const float* pWeight, const float* pBias,
+                                   const float* pGamma, const float* pBeta, const float* pMean, const float* pVar,
+                                   float fEps, const float* pResidual, int nAct, float* pOutput, int nBatch, int nCin,
+                                   int nH, int nW, int nCout, int nKH, int nKW, int nStride, int nPad) {
+        check(omHipConv2dBiasBnAddAct(pInput, pWeight, pBias, pGamma, pBeta, pMean, pVar, fEps, pResidual, nAct,
+                                      pOutput, nBatch, nCin, nH, nW, nCout, nKH, nKW, nStride, nPad),
+              "conv2dBiasBnAddAct");
     }
     // conv2d -> batchNorm2d(eval) -> relu (tensor_ops.ixx:672-833, :511-536)
     static void conv2dBiasBnAct(const float* pInput, const float* pWeight, const float* pBias, const float* pGamma,

@@ -83,6 +83,15 @@ _SIGS = {
     "omHipConv2dBackwardInput": [_vp, _vp, _vp] + [_i] * 9,
     "omHipConv2dBackwardWeight": [_vp, _vp, _vp, _vp] + [_i] * 9,
     "omHipBatchNorm2dBackward": [_vp] * 8 + [_i] * 4 + [_fl],
+    "omHipMaxPool2d": [_vp, _vp, _vp] + [_i] * 10,
+    "omHipMaxPool2dBackward": [_vp, _vp, _vp] + [_i] * 6,
+    "omHipMaxPool2dBackwardEx": [_vp, _vp, _vp] + [_i] * 10,
+    "omHipAvgPool2d": [_vp, _vp] + [_i] * 10,
+    "omHipAvgPool2dBackward": [_vp, _vp] + [_i] * 10,
+    "omHipAdaptiveAvgPool2d": [_vp, _vp] + [_i] * 6,
+    "omHipAdaptiveAvgPool2dBackward": [_vp, _vp] + [_i] * 6,
+    "omHipAdd": [_vp, _vp, _vp, _i],
+    "omHipConv2dBiasBnAddAct": [_vp] * 7 + [_fl, _vp, _i, _vp] + [_i] * 9,
     "omHipConvertF32ToF16": [_vp, _vp, _i],
     "omHipConvertF32ToBF16": [_vp, _vp, _i],
     "omHipConvertF16ToF32": [_vp, _vp, _i],
@@ -297,6 +306,62 @@ class HIPBackend:
         """CPUBackend::batchNorm2dBackward (cpu_backend.ixx:847-890)."""
         call("omHipBatchNorm2dBackward", _ptr(pGradOutput), _ptr(pInput), _ptr(pSavedMean), _ptr(pSavedInvStd),
              _ptr(pGamma), _ptr(pGradInput), _ptr(pGradGamma), _ptr(pGradBeta), nBatch, nChannels, nH, nW, fEps)
+
+    @staticmethod
+    def maxPool2d(pInput, pOutput, pIndices, nBatch, nChannels, nH, nW, nKH, nKW, nStride, nPad) -> None:
+        """CPUBackend::maxPool2d (cpu_backend.ixx:897-934); pIndices (int32) may be None."""
+        call("omHipMaxPool2d", _ptr(pInput), _ptr(pOutput), _ptr(pIndices), nBatch, nChannels, nH, nW, nKH, nKW,
+             nStride, nStride, nPad, nPad)
+
+    @staticmethod
+    def maxPool2dBackward(pGradOutput, pIndices, pGradInput, nBatch, nChannels, nHout, nWout, nH, nW) -> None:
+        """CPUBackend::maxPool2dBackward (cpu_backend.ixx:937-955): scatter through the indices."""
+        call("omHipMaxPool2dBackward", _ptr(pGradOutput), _ptr(pIndices), _ptr(pGradInput), nBatch, nChannels, nH,
+             nW, nHout, nWout)
+
+    @staticmethod
+    def maxPool2dBackwardEx(pGradOutput, pIndices, pGradInput, nBatch, nChannels, nH, nW, nKH, nKW, nStride,
+                            nPad) -> None:
+        """Ordered gather form of maxPool2dBackward (bit-identical to the reference)."""
+        call("omHipMaxPool2dBackwardEx", _ptr(pGradOutput), _ptr(pIndices), _ptr(pGradInput), nBatch, nChannels, nH,
+             nW, nKH, nKW, nStride, nStride, nPad, nPad)
+
+    @staticmethod
+    def avgPool2d(pInput, pOutput, nBatch, nChannels, nH, nW, nKH, nKW, nStride, nPad) -> None:
+        """CPUBackend::avgPool2d (cpu_backend.ixx:958-990)."""
+        call("omHipAvgPool2d", _ptr(pInput), _ptr(pOutput), nBatch, nChannels, nH, nW, nKH, nKW, nStride, nStride,
+             nPad, nPad)
+
+    @staticmethod
+    def avgPool2dBackward(pGradOutput, pGradInput, nBatch, nChannels, nH, nW, nHout, nWout, nKH, nKW, nStride,
+                          nPad) -> None:
+        """CPUBackend::avgPool2dBackward (cpu_backend.ixx:994-1023)."""
+        call("omHipAvgPool2dBackward", _ptr(pGradOutput), _ptr(pGradInput), nBatch, nChannels, nH, nW, nKH, nKW,
+             nStride, nStride, nPad, nPad)
+
+    @staticmethod
+    def adaptiveAvgPool2d(pInput, pOutput, nBatch, nChannels, nH, nW, nOutH, nOutW) -> None:
+        """CPUBackend::adaptiveAvgPool2d (cpu_backend.ixx:1467-1488)."""
+        call("omHipAdaptiveAvgPool2d", _ptr(pInput), _ptr(pOutput), nBatch, nChannels, nH, nW, nOutH, nOutW)
+
+    @staticmethod
+    def adaptiveAvgPool2dBackward(pGradOutput, pGradInput, nBatch, nChannels, nH, nW, nOutH, nOutW) -> None:
+        """CPUBackend::adaptiveAvgPool2dBackward (cpu_backend.ixx:1491-1510)."""
+        call("omHipAdaptiveAvgPool2dBackward", _ptr(pGradOutput), _ptr(pGradInput), nBatch, nChannels, nH, nW, nOutH,
+             nOutW)
+
+    @staticmethod
+    def add(pA, pB, pOut, nCount) -> None:
+        """CPUBackend::add (cpu_backend.ixx:147-160)."""
+        call("omHipAdd", _ptr(pA), _ptr(pB), _ptr(pOut), nCount)
+
+    @staticmethod
+    def conv2dBiasBnAddAct(pInput, pWeight, pBias, pGamma, pBeta, pMean, pVar, fEps, pResidual, nAct, pOutput,
+                           nBatch, nCin, nH, nW, nCout, nKH, nKW, nStride, nPad) -> None:
+        """conv2d -> batchNorm2d(eval) -> add(shortcut) -> relu in one kernel (resnet.ixx:55-79)."""
+        call("omHipConv2dBiasBnAddAct", _ptr(pInput), _ptr(pWeight), _ptr(pBias), _ptr(pGamma), _ptr(pBeta),
+             _ptr(pMean), _ptr(pVar), fEps, _ptr(pResidual), nAct, _ptr(pOutput), nBatch, nCin, nH, nW, nCout, nKH,
+             nKW, nStride, nPad)
 
     # ---- entries the reference builds by composition ----
     @staticmethod

@@ -54,6 +54,7 @@ struct ConvParams {
     const float* var;
     float eps;
     int act;             // 0 identity, 1 relu
+    const float* res;    // [N][Cout][Ho][Wo] added after BN, before the activation, or null
     float* out;          // [N][Cout][Ho][Wo]
     float* ws;           // split-K partials [splits][Cout][Nq]
     const uint2* tab;    // per K row: (byte offset ci*HW+kh*W+kw, tap code); kOOB past K
@@ -356,6 +357,7 @@ __global__ __launch_bounds__(Cfg::NT) void conv_igemm_kernel(ConvParams p) {
                 if (p.gamma)
                     v = __builtin_fmaf(sEpi[3 * Cfg::BM + rl], (v - sEpi[Cfg::BM + rl]) * sEpi[2 * Cfg::BM + rl],
                                        sEpi[4 * Cfg::BM + rl]);
+                if (p.res) v += p.res[(long long)n * p.Cout * HoWo + (long long)co * HoWo + pix];
                 if (p.act == 1) v = v > 0.f ? v : 0.f;
                 o[(long long)co * HoWo] = v;
             }
@@ -378,10 +380,12 @@ __global__ void conv_splitk_finish(ConvParams p) {
             const float inv = 1.0f / sqrtf(p.var[co] + p.eps);
             v = __builtin_fmaf(p.gamma[co], (v - p.mean[co]) * inv, p.beta[co]);
         }
-        if (p.act == 1) v = v > 0.f ? v : 0.f;
         const int n = q / HoWo;
         const int pix = q - n * HoWo;
-        p.out[((long long)n * p.Cout + co) * HoWo + pix] = v;
+        const long long o = ((long long)n * p.Cout + co) * HoWo + pix;
+        if (p.res) v += p.res[o];
+        if (p.act == 1) v = v > 0.f ? v : 0.f;
+        p.out[o] = v;
     }
 }
 
@@ -517,6 +521,7 @@ static int convChunk(ConvParams p, int n0, int nb) {
     // one batch chunk: x, out and the pixel axis restricted to images [n0, n0+nb)
     p.x = p.x + (long long)n0 * p.Cin * p.H * p.W;
     p.out = p.out + (long long)n0 * p.Cout * p.Ho * p.Wo;
+    if (p.res) p.res = p.res + (long long)n0 * p.Cout * p.Ho * p.Wo;
     p.N = nb;
     p.Nq = nb * p.Ho * p.Wo;
     p.padOff = p.pad * p.W + p.pad;
@@ -533,8 +538,8 @@ static int convChunk(ConvParams p, int n0, int nb) {
 }
 
 int conv2dFused(const char* name, const float* x, const float* w, const float* bias, const float* gamma,
-                const float* beta, const float* mean, const float* var, float eps, int act, float* out, int N, int Cin,
-                int H, int W, int Cout, int KH, int KW, int stride, int pad) {
+                const float* beta, const float* mean, const float* var, float eps, const float* res, int act,
+                float* out, int N, int Cin, int H, int W, int Cout, int KH, int KW, int stride, int pad) {
     clearError();
     int Ho, Wo;
     if (validateConv(name, x, w, out, N, Cin, H, W, Cout, KH, KW, stride, pad, Ho, Wo)) return -1;
@@ -544,7 +549,7 @@ int conv2dFused(const char* name, const float* x, const float* w, const float* b
     ConvParams p{};
     p.x = x; p.w = w; p.bias = bias;
     p.gamma = anyBn ? gamma : nullptr; p.beta = beta; p.mean = mean; p.var = var;
-    p.eps = eps; p.act = act; p.out = out;
+    p.eps = eps; p.act = act; p.res = res; p.out = out;
     p.N = N; p.Cin = Cin; p.H = H; p.W = W; p.Cout = Cout; p.KH = KH; p.KW = KW;
     p.stride = stride; p.pad = pad; p.Ho = Ho; p.Wo = Wo;
     p.K = Cin * KH * KW;
@@ -569,16 +574,32 @@ extern "C" {
 
 int omHipConv2d(const float* pInput, const float* pWeight, const float* pBias, float* pOutput, int nBatch, int nCin,
                 int nH, int nW, int nCout, int nKH, int nKW, int nStride, int nPad) {
-    return conv2dFused("omHipConv2d", pInput, pWeight, pBias, nullptr, nullptr, nullptr, nullptr, 0.f, 0, pOutput,
-                       nBatch, nCin, nH, nW, nCout, nKH, nKW, nStride, nPad);
+    return conv2dFused("omHipConv2d", pInput, pWeight, pBias, nullptr, nullptr, nullptr, nullptr, 0.f, nullptr, 0,
+                       pOutput, nBatch, nCin, nH, nW, nCout, nKH, nKW, nStride, nPad);
 }
 
 int omHipConv2dBiasBnAct(const float* pInput, const float* pWeight, const float* pBias, const float* pGamma,
                          const float* pBeta, const float* pMean, const float* pVar, float fEps, int nAct,
                          float* pOutput, int nBatch, int nCin, int nH, int nW, int nCout, int nKH, int nKW,
                          int nStride, int nPad) {
-    return conv2dFused("omHipConv2dBiasBnAct", pInput, pWeight, pBias, pGamma, pBeta, pMean, pVar, fEps, nAct,
-                       pOutput, nBatch, nCin, nH, nW, nCout, nKH, nKW, nStride, nPad);
+    return conv2dFused("omHipConv2dBiasBnAct", pInput, pWeight, pBias, pGamma, pBeta, pMean, pVar, fEps, nullptr,
+                       nAct, pOutput, nBatch, nCin, nH, nW, nCout, nKH, nKW, nStride, nPad);
+}
+
+int omHipConv2dBiasBnAddAct(const float* pInput, const float* pWeight, const float* pBias, const float* pGamma,
+                            const float* pBeta, const float* pMean, const float* pVar, float fEps,
+                            const float* pResidual, int nAct, float* pOutput, int nBatch, int nCin, int nH, int nW,
+                            int nCout, int nKH, int nKW, int nStride, int nPad) {
+    if (!pResidual) {
+        clearError();
+        return fail("omHipConv2dBiasBnAddAct: null residual");
+    }
+    if (pResidual == pOutput) {
+        clearError();
+        return fail("omHipConv2dBiasBnAddAct: the residual must not alias the output");
+    }
+    return conv2dFused("omHipConv2dBiasBnAddAct", pInput, pWeight, pBias, pGamma, pBeta, pMean, pVar, fEps,
+                       pResidual, nAct, pOutput, nBatch, nCin, nH, nW, nCout, nKH, nKW, nStride, nPad);
 }
 
 // Explicit lowering: im2col of every image into one buffer, then a batched

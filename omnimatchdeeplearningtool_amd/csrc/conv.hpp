@@ -4,11 +4,11 @@
 
 namespace omhip {
 
-// out = act(BN(conv(x, w) + bias)) in one pass (any of bias / BN may be null);
-// act 0 identity, 1 ReLU. `name` prefixes error messages. 0 or -1.
+// out = act(BN(conv(x, w) + bias) + res) in one pass (bias, BN and res may be
+// null); act 0 identity, 1 ReLU. `name` prefixes error messages. 0 or -1.
 int conv2dFused(const char* name, const float* x, const float* w, const float* bias, const float* gamma,
-                const float* beta, const float* mean, const float* var, float eps, int act, float* out, int N, int Cin,
-                int H, int W, int Cout, int KH, int KW, int stride, int pad);
+                const float* beta, const float* mean, const float* var, float eps, const float* res, int act,
+                float* out, int N, int Cin, int H, int W, int Cout, int KH, int KW, int stride, int pad);
 
 // col[n][(c*KH+kh)*KW+kw][oh*Wo+ow] for every image of x (zero outside the image).
 int im2colBatched(const float* x, float* col, int N, int Cin, int H, int W, int KH, int KW, int pad, int strd,

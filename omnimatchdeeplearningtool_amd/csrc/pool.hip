@@ -1,0 +1,337 @@
+// pool.hip — pooling and the elementwise add that join the conv layers of a
+// ResNet: max / average / adaptive-average pooling (forward and backward) and
+// a + b (the residual sum).
+//
+// Reference: CPUBackend::maxPool2d / maxPool2dBackward / avgPool2d /
+// avgPool2dBackward / adaptiveAvgPool2d / adaptiveAvgPool2dBackward / add
+// (src/hal/om.hal.cpu_backend.ixx:897-1023, :1467-1510, :147-160); C ABI
+// counterparts omCudaMaxPool2d ... omCudaAdaptiveAvgPool2d and omCudaAdd
+// (src/cuda/cuda_kernels.cuh:218-245, :74).
+//
+// All are HBM-bound. Forward kernels run one thread per output. The backward
+// kernels are gathers, one thread per input element: it visits the output
+// windows covering it in ascending (oh, ow) order and adds their
+// contributions in that order — the order in which the reference's scatter
+// loop (outputs ascending) adds into that element, so the results are
+// bit-identical and no atomics are involved.
+#include "omhip_internal.hpp"
+#include "../../include/omhip.h"
+
+#include <algorithm>
+
+namespace omhip {
+
+static int gridFor(long long n) {
+    return (int)std::max<long long>(1, std::min<long long>((n + 255) / 256, (long long)cuCount() * 16));
+}
+
+struct PoolGeom {
+    int N, C, H, W, KH, KW, SH, SW, PH, PW, Ho, Wo;
+};
+
+// Window range of outputs covering input coordinate i along one axis:
+// o*s - p <= i <= o*s - p + K - 1  ->  o in [ceil((i+p-K+1)/s), floor((i+p)/s)] within [0, O).
+__device__ __forceinline__ void coverRange(int i, int K, int s, int p, int O, int& o0, int& o1) {
+    const int hi = i + p;   // >= 0
+    const int lo = hi - K + 1;
+    o0 = lo <= 0 ? 0 : (lo + s - 1) / s;
+    o1 = min(hi / s, O - 1);
+}
+
+// cpu_backend.ixx:897-934: strict '>' keeps the first maximum in (kh, kw) order;
+// index = flat input index, -1 (value -1e30) for a window wholly in the padding.
+__global__ void maxpool_kernel(const float* __restrict__ x, float* __restrict__ y, int* __restrict__ idx, PoolGeom g) {
+    const long long total = (long long)g.N * g.C * g.Ho * g.Wo;
+    for (long long o = blockIdx.x * (long long)blockDim.x + threadIdx.x; o < total;
+         o += (long long)gridDim.x * blockDim.x) {
+        const int ow = (int)(o % g.Wo);
+        const int oh = (int)((o / g.Wo) % g.Ho);
+        const long long nc = o / ((long long)g.Wo * g.Ho);
+        float best = -1e30f;
+        int bi = -1;
+        for (int kh = 0; kh < g.KH; ++kh) {
+            const int ih = oh * g.SH - g.PH + kh;
+            if (ih < 0 || ih >= g.H) continue;
+            for (int kw = 0; kw < g.KW; ++kw) {
+                const int iw = ow * g.SW - g.PW + kw;
+                if (iw < 0 || iw >= g.W) continue;
+                const long long ii = (nc * g.H + ih) * g.W + iw;
+                const float v = x[ii];
+                if (v > best) {
+                    best = v;
+                    bi = (int)ii;
+                }
+            }
+        }
+        y[o] = best;
+        if (idx) idx[o] = bi;
+    }
+}
+
+// cpu_backend.ixx:937-955 as a gather: gI[i] = sum of gO[o] over the outputs o
+// (ascending) whose saved index is i.
+__global__ void maxpool_backward_kernel(const float* __restrict__ gO, const int* __restrict__ idx,
+                                        float* __restrict__ gI, PoolGeom g) {
+    const long long total = (long long)g.N * g.C * g.H * g.W;
+    for (long long i = blockIdx.x * (long long)blockDim.x + threadIdx.x; i < total;
+         i += (long long)gridDim.x * blockDim.x) {
+        const int iw = (int)(i % g.W);
+        const int ih = (int)((i / g.W) % g.H);
+        const long long nc = i / ((long long)g.W * g.H);
+        int oh0, oh1, ow0, ow1;
+        coverRange(ih, g.KH, g.SH, g.PH, g.Ho, oh0, oh1);
+        coverRange(iw, g.KW, g.SW, g.PW, g.Wo, ow0, ow1);
+        float v = 0.f;
+        for (int oh = oh0; oh <= oh1; ++oh)
+            for (int ow = ow0; ow <= ow1; ++ow) {
+                const long long o = (nc * g.Ho + oh) * g.Wo + ow;
+                if (idx[o] == (int)i) v += gO[o];
+            }
+        gI[i] = v;
+    }
+}
+
+__global__ void zero_kernel(float* __restrict__ p, long long n) {
+    for (long long i = blockIdx.x * (long long)blockDim.x + threadIdx.x; i < n; i += (long long)gridDim.x * blockDim.x)
+        p[i] = 0.f;
+}
+
+// cpu_backend.ixx:937-955 with the reference's signature (no window geometry):
+// scatter through the saved indices with atomic adds. An input that is the
+// maximum of several windows receives their gradients in an unspecified order
+// (at most ceil(K/s)^2 of them); omHipMaxPool2dBackwardEx is the ordered,
+// bit-reproducible gather when the window geometry is known.
+__global__ void maxpool_scatter_kernel(const float* __restrict__ gO, const int* __restrict__ idx, float* gI,
+                                       long long nout, long long nin) {
+    for (long long o = blockIdx.x * (long long)blockDim.x + threadIdx.x; o < nout;
+         o += (long long)gridDim.x * blockDim.x) {
+        const int t = idx[o];
+        if (t >= 0 && t < nin) atomicAdd(gI + t, gO[o]);
+    }
+}
+
+// cpu_backend.ixx:958-990: sum over the valid taps divided by KH*KW.
+__global__ void avgpool_kernel(const float* __restrict__ x, float* __restrict__ y, PoolGeom g) {
+    const long long total = (long long)g.N * g.C * g.Ho * g.Wo;
+    const float div = (float)(g.KH * g.KW);
+    for (long long o = blockIdx.x * (long long)blockDim.x + threadIdx.x; o < total;
+         o += (long long)gridDim.x * blockDim.x) {
+        const int ow = (int)(o % g.Wo);
+        const int oh = (int)((o / g.Wo) % g.Ho);
+        const long long nc = o / ((long long)g.Wo * g.Ho);
+        float sum = 0.f;
+        for (int kh = 0; kh < g.KH; ++kh) {
+            const int ih = oh * g.SH - g.PH + kh;
+            if (ih < 0 || ih >= g.H) continue;
+            for (int kw = 0; kw < g.KW; ++kw) {
+                const int iw = ow * g.SW - g.PW + kw;
+                if (iw < 0 || iw >= g.W) continue;
+                sum += x[(nc * g.H + ih) * g.W + iw];
+            }
+        }
+        y[o] = sum / div;
+    }
+}
+
+// cpu_backend.ixx:994-1023 as a gather: each covering output adds gO * (1/(KH*KW)).
+// The reference rounds the product before adding it (separate statements), so
+// the multiply must not be fused into the add here.
+__global__ void avgpool_backward_kernel(const float* __restrict__ gO, float* __restrict__ gI, PoolGeom g) {
+#pragma clang fp contract(off)
+    const long long total = (long long)g.N * g.C * g.H * g.W;
+    const float scale = 1.0f / (float)(g.KH * g.KW);
+    for (long long i = blockIdx.x * (long long)blockDim.x + threadIdx.x; i < total;
+         i += (long long)gridDim.x * blockDim.x) {
+        const int iw = (int)(i % g.W);
+        const int ih = (int)((i / g.W) % g.H);
+        const long long nc = i / ((long long)g.W * g.H);
+        int oh0, oh1, ow0, ow1;
+        coverRange(ih, g.KH, g.SH, g.PH, g.Ho, oh0, oh1);
+        coverRange(iw, g.KW, g.SW, g.PW, g.Wo, ow0, ow1);
+        float v = 0.f;
+        for (int oh = oh0; oh <= oh1; ++oh)
+            for (int ow = ow0; ow <= ow1; ++ow) v += gO[(nc * g.Ho + oh) * g.Wo + ow] * scale;
+        gI[i] = v;
+    }
+}
+
+// cpu_backend.ixx:1467-1488: region [floor(o*H/OH), floor((o+1)*H/OH)) per axis;
+// an empty region divides 0 by 0, as the reference does.
+__global__ void adaptive_avgpool_kernel(const float* __restrict__ x, float* __restrict__ y, int NC, int H, int W,
+                                        int OH, int OW) {
+    const long long total = (long long)NC * OH * OW;
+    for (long long o = blockIdx.x * (long long)blockDim.x + threadIdx.x; o < total;
+         o += (long long)gridDim.x * blockDim.x) {
+        const int ow = (int)(o % OW);
+        const int oh = (int)((o / OW) % OH);
+        const long long nc = o / ((long long)OW * OH);
+        const int h0 = (int)((long long)oh * H / OH), h1 = (int)((long long)(oh + 1) * H / OH);
+        const int w0 = (int)((long long)ow * W / OW), w1 = (int)((long long)(ow + 1) * W / OW);
+        float sum = 0.f;
+        int cnt = 0;
+        for (int ih = h0; ih < h1; ++ih)
+            for (int iw = w0; iw < w1; ++iw) {
+                sum += x[(nc * H + ih) * W + iw];
+                ++cnt;
+            }
+        y[o] = sum / (float)cnt;
+    }
+}
+
+// cpu_backend.ixx:1491-1510: the regions partition the input (each region's end
+// is the next one's start), so every input element takes gO / count of its one region.
+__global__ void adaptive_avgpool_backward_kernel(const float* __restrict__ gO, float* __restrict__ gI, int NC, int H,
+                                                 int W, int OH, int OW) {
+    const long long total = (long long)NC * H * W;
+    for (long long i = blockIdx.x * (long long)blockDim.x + threadIdx.x; i < total;
+         i += (long long)gridDim.x * blockDim.x) {
+        const int iw = (int)(i % W);
+        const int ih = (int)((i / W) % H);
+        const long long nc = i / ((long long)W * H);
+        // the region o with floor(o*H/OH) <= ih < floor((o+1)*H/OH)
+        int oh = (int)(((long long)ih * OH) / H);
+        while (oh + 1 < OH && (long long)(oh + 1) * H / OH <= ih) ++oh;
+        while (oh > 0 && (long long)oh * H / OH > ih) --oh;
+        int ow = (int)(((long long)iw * OW) / W);
+        while (ow + 1 < OW && (long long)(ow + 1) * W / OW <= iw) ++ow;
+        while (ow > 0 && (long long)ow * W / OW > iw) --ow;
+        const int h0 = (int)((long long)oh * H / OH), h1 = (int)((long long)(oh + 1) * H / OH);
+        const int w0 = (int)((long long)ow * W / OW), w1 = (int)((long long)(ow + 1) * W / OW);
+        const float g = gO[(nc * OH + oh) * OW + ow] / (float)((h1 - h0) * (w1 - w0));
+        gI[i] = g;
+    }
+}
+
+__global__ void add_kernel(const float* __restrict__ a, const float* __restrict__ b, float* __restrict__ c,
+                           long long n) {
+    const long long n4 = n / 4;
+    const long long stride = (long long)gridDim.x * blockDim.x;
+    const long long t = blockIdx.x * (long long)blockDim.x + threadIdx.x;
+    const bool vec = ((reinterpret_cast<uintptr_t>(a) | reinterpret_cast<uintptr_t>(b) |
+                       reinterpret_cast<uintptr_t>(c)) & 15u) == 0;
+    if (vec) {
+        typedef float f4 __attribute__((ext_vector_type(4)));
+        for (long long i = t; i < n4; i += stride) {
+            const f4 u = reinterpret_cast<const f4*>(a)[i], v = reinterpret_cast<const f4*>(b)[i];
+            reinterpret_cast<f4*>(c)[i] = u + v;
+        }
+        for (long long i = n4 * 4 + t; i < n; i += stride) c[i] = a[i] + b[i];
+    } else {
+        for (long long i = t; i < n; i += stride) c[i] = a[i] + b[i];
+    }
+}
+
+static int poolGeom(const char* name, int N, int C, int H, int W, int KH, int KW, int SH, int SW, int PH, int PW,
+                    PoolGeom& g) {
+    if (N <= 0 || C <= 0 || H <= 0 || W <= 0 || KH <= 0 || KW <= 0 || SH <= 0 || SW <= 0 || PH < 0 || PW < 0)
+        return fail("%s: invalid geometry", name);
+    g = {N, C, H, W, KH, KW, SH, SW, PH, PW, (H + 2 * PH - KH) / SH + 1, (W + 2 * PW - KW) / SW + 1};
+    if (g.Ho <= 0 || g.Wo <= 0) return fail("%s: window larger than the padded input", name);
+    if ((long long)N * C * H * W >= (1LL << 31)) return fail("%s: input exceeds 2^31 elements (int indices)", name);
+    return 0;
+}
+
+}  // namespace omhip
+
+using namespace omhip;
+
+extern "C" {
+
+int omHipMaxPool2d(const float* pIn, float* pOut, int* pIndices, int nN, int nC, int nH, int nW, int nKH, int nKW,
+                   int nSH, int nSW, int nPH, int nPW) {
+    clearError();
+    PoolGeom g;
+    if (poolGeom("omHipMaxPool2d", nN, nC, nH, nW, nKH, nKW, nSH, nSW, nPH, nPW, g)) return -1;
+    if (!pIn || !pOut) return fail("omHipMaxPool2d: null pointer");
+    hipLaunchKernelGGL(maxpool_kernel, dim3(gridFor((long long)nN * nC * g.Ho * g.Wo)), dim3(256), 0, stream(), pIn,
+                       pOut, pIndices, g);
+    OMHIP_CHECK_LAUNCH();
+    return 0;
+}
+
+int omHipMaxPool2dBackward(const float* pGradOut, const int* pIndices, float* pGradIn, int nN, int nC, int nH, int nW,
+                           int nHout, int nWout) {
+    clearError();
+    if (nN <= 0 || nC <= 0 || nH <= 0 || nW <= 0 || nHout <= 0 || nWout <= 0)
+        return fail("omHipMaxPool2dBackward: invalid geometry");
+    if (!pGradOut || !pIndices || !pGradIn) return fail("omHipMaxPool2dBackward: null pointer");
+    const long long nin = (long long)nN * nC * nH * nW, nout = (long long)nN * nC * nHout * nWout;
+    if (nin >= (1LL << 31)) return fail("omHipMaxPool2dBackward: input exceeds 2^31 elements (int indices)");
+    hipLaunchKernelGGL(zero_kernel, dim3(gridFor(nin)), dim3(256), 0, stream(), pGradIn, nin);
+    OMHIP_CHECK_LAUNCH();
+    hipLaunchKernelGGL(maxpool_scatter_kernel, dim3(gridFor(nout)), dim3(256), 0, stream(), pGradOut, pIndices,
+                       pGradIn, nout, nin);
+    OMHIP_CHECK_LAUNCH();
+    return 0;
+}
+
+int omHipMaxPool2dBackwardEx(const float* pGradOut, const int* pIndices, float* pGradIn, int nN, int nC, int nH,
+                             int nW, int nKH, int nKW, int nSH, int nSW, int nPH, int nPW) {
+    clearError();
+    PoolGeom g;
+    if (poolGeom("omHipMaxPool2dBackwardEx", nN, nC, nH, nW, nKH, nKW, nSH, nSW, nPH, nPW, g)) return -1;
+    if (!pGradOut || !pIndices || !pGradIn) return fail("omHipMaxPool2dBackwardEx: null pointer");
+    hipLaunchKernelGGL(maxpool_backward_kernel, dim3(gridFor((long long)nN * nC * nH * nW)), dim3(256), 0, stream(),
+                       pGradOut, pIndices, pGradIn, g);
+    OMHIP_CHECK_LAUNCH();
+    return 0;
+}
+
+int omHipAvgPool2d(const float* pIn, float* pOut, int nN, int nC, int nH, int nW, int nKH, int nKW, int nSH, int nSW,
+                   int nPH, int nPW) {
+    clearError();
+    PoolGeom g;
+    if (poolGeom("omHipAvgPool2d", nN, nC, nH, nW, nKH, nKW, nSH, nSW, nPH, nPW, g)) return -1;
+    if (!pIn || !pOut) return fail("omHipAvgPool2d: null pointer");
+    hipLaunchKernelGGL(avgpool_kernel, dim3(gridFor((long long)nN * nC * g.Ho * g.Wo)), dim3(256), 0, stream(), pIn,
+                       pOut, g);
+    OMHIP_CHECK_LAUNCH();
+    return 0;
+}
+
+int omHipAvgPool2dBackward(const float* pGradOut, float* pGradIn, int nN, int nC, int nH, int nW, int nKH, int nKW,
+                           int nSH, int nSW, int nPH, int nPW) {
+    clearError();
+    PoolGeom g;
+    if (poolGeom("omHipAvgPool2dBackward", nN, nC, nH, nW, nKH, nKW, nSH, nSW, nPH, nPW, g)) return -1;
+    if (!pGradOut || !pGradIn) return fail("omHipAvgPool2dBackward: null pointer");
+    hipLaunchKernelGGL(avgpool_backward_kernel, dim3(gridFor((long long)nN * nC * nH * nW)), dim3(256), 0, stream(),
+                       pGradOut, pGradIn, g);
+    OMHIP_CHECK_LAUNCH();
+    return 0;
+}
+
+int omHipAdaptiveAvgPool2d(const float* pIn, float* pOut, int nN, int nC, int nH, int nW, int nOutH, int nOutW) {
+    clearError();
+    if (nN <= 0 || nC <= 0 || nH <= 0 || nW <= 0 || nOutH <= 0 || nOutW <= 0)
+        return fail("omHipAdaptiveAvgPool2d: invalid geometry");
+    if (!pIn || !pOut) return fail("omHipAdaptiveAvgPool2d: null pointer");
+    hipLaunchKernelGGL(adaptive_avgpool_kernel, dim3(gridFor((long long)nN * nC * nOutH * nOutW)), dim3(256), 0,
+                       stream(), pIn, pOut, nN * nC, nH, nW, nOutH, nOutW);
+    OMHIP_CHECK_LAUNCH();
+    return 0;
+}
+
+int omHipAdaptiveAvgPool2dBackward(const float* pGradOut, float* pGradIn, int nN, int nC, int nH, int nW, int nOutH,
+                                   int nOutW) {
+    clearError();
+    if (nN <= 0 || nC <= 0 || nH <= 0 || nW <= 0 || nOutH <= 0 || nOutW <= 0)
+        return fail("omHipAdaptiveAvgPool2dBackward: invalid geometry");
+    if (!pGradOut || !pGradIn) return fail("omHipAdaptiveAvgPool2dBackward: null pointer");
+    hipLaunchKernelGGL(adaptive_avgpool_backward_kernel, dim3(gridFor((long long)nN * nC * nH * nW)), dim3(256), 0,
+                       stream(), pGradOut, pGradIn, nN * nC, nH, nW, nOutH, nOutW);
+    OMHIP_CHECK_LAUNCH();
+    return 0;
+}
+
+int omHipAdd(const float* pA, const float* pB, float* pC, int nCount) {
+    clearError();
+    if (nCount <= 0) return 0;
+    if (!pA || !pB || !pC) return fail("omHipAdd: null pointer");
+    hipLaunchKernelGGL(add_kernel, dim3(gridFor((nCount + 3) / 4)), dim3(256), 0, stream(), pA, pB, pC,
+                       (long long)nCount);
+    OMHIP_CHECK_LAUNCH();
+    return 0;
+}
+
+}  // extern "C"

@@ -299,8 +299,8 @@ int omHipConv2dBackwardInput(const float* pGradOutput, const float* pWeight, flo
                            nKH, nKW);
         int rc = hipGetLastError() == hipSuccess ? 0 : fail("%s: flip launch failed", name);
         if (!rc)
-            rc = conv2dFused(name, pGradOutput, wf, nullptr, nullptr, nullptr, nullptr, nullptr, 0.f, 0, pGradInput,
-                             nBatch, nCout, Ho, Wo, nCin, nKH, nKW, 1, nKH - 1 - nPad);
+            rc = conv2dFused(name, pGradOutput, wf, nullptr, nullptr, nullptr, nullptr, nullptr, 0.f, nullptr, 0,
+                             pGradInput, nBatch, nCout, Ho, Wo, nCin, nKH, nKW, 1, nKH - 1 - nPad);
         (void)omHipFree(wf);   // stream-ordered reuse: later work on the stream runs after the conv
         return rc;
     }
