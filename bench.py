@@ -187,6 +187,66 @@ def bench_resnet18(om, steps: int, warmup: int, batch: int = 32):
     return ms, flops, roof_ms, per, max(errs)
 
 
+def bench_resnet18_net(om, steps: int, warmup: int, batch: int = 32):
+    """The whole ResNet-18 at batch 32: fused inference forward, and one training
+    step (forward with batch statistics + backward to every weight)."""
+    from omnimatchdeeplearningtool_amd.hiptime import StreamTimer
+    from resnet_net import GpuResNet18, conv_list, cpu_forward, forward_flops, make_params
+    import oracle as O
+    P = make_params(seed=1)
+    img = O.randn((batch, 3, 224, 224), 900)
+    d_img = om.DeviceBuffer.from_numpy(img)
+    timer = StreamTimer(om.stream_handle())
+    net = GpuResNet18(om, P, batch)
+    for _ in range(warmup):
+        logits = net.forward(d_img)
+    om.synchronize()
+    timer.start()
+    for _ in range(steps):
+        net.forward(d_img)
+    timer.stop()
+    fwd_ms = timer.ms() / steps
+    got = logits.numpy()[:2]
+    err = O.frobenius_rel(got, cpu_forward(P, img[:2]))
+    # training step
+    tnet = GpuResNet18(om, P, batch, train=True)
+    g_logits = om.DeviceBuffer.from_numpy(O.randn((batch, 1000), 901, 0.01))
+    for _ in range(max(1, warmup // 2)):
+        tnet.forward_train(d_img)
+        tnet.backward(g_logits)
+    om.synchronize()
+    tsteps = max(3, steps // 2)
+    timer.start()
+    for _ in range(tsteps):
+        tnet.forward_train(d_img)
+        tnet.backward(g_logits)
+    timer.stop()
+    train_ms = timer.ms() / tsteps
+    fl = forward_flops(batch)
+    stem = 2.0 * batch * 64 * 112 * 112 * 3 * 49
+    train_fl = 3.0 * fl - stem        # forward + input gradients (none for the image) + weight gradients
+    return fwd_ms, fl, err, train_ms, train_fl
+
+
+def cpu_baseline_resnet18_net(n_img: int = 2, reps: int = 3):
+    from resnet_net import cpu_forward, cpu_train_step, make_params
+    import oracle as O
+    kind = "reference" if O.ref_lib() is not None else "oracle"
+    P = make_params(seed=1)
+    img = O.randn((n_img, 3, 224, 224), 900)
+    g = O.randn((n_img, 1000), 901, 0.01)
+    cpu_forward(P, img, backend=kind)
+    f, t = [], []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        cpu_forward(P, img, backend=kind)
+        f.append(time.perf_counter() - t0)
+        t0 = time.perf_counter()
+        cpu_train_step(P, img, g, backend=kind)
+        t.append(time.perf_counter() - t0)
+    return kind, n_img / float(np.median(f)), n_img / float(np.median(t)), float(np.median(f)), float(np.median(t))
+
+
 def bench_resnet50(om, steps: int, warmup: int, batch: int = 64):
     """ResNet-50 conv stack forward (53 convs, fused conv+BN+ReLU) at batch 64."""
     from omnimatchdeeplearningtool_amd.hiptime import StreamTimer
@@ -506,6 +566,11 @@ def main():
     img_s = 32.0 / (r_ms / 1e3)
     log(f"resnet18 {r_ms:.3f} ms/batch  {img_s:.0f} img/s  roof frac {r_roof_ms / r_ms:.3f}  parity {conv_err:.2e}")
 
+    log("resnet18 network b32 (inference forward, training step)")
+    n_fwd_ms, n_fl, n_err, n_train_ms, n_train_fl = bench_resnet18_net(om, max(5, args.steps // 5), 2)
+    log(f"resnet18 net forward {n_fwd_ms:.3f} ms  {32 / n_fwd_ms * 1e3:.0f} img/s  logits err {n_err:.1e}; "
+        f"train step {n_train_ms:.3f} ms  {32 / n_train_ms * 1e3:.0f} img/s")
+
     log("resnet50 conv stack b64")
     r50_ms, r50_flops, r50_roof = bench_resnet50(om, max(3, args.steps // 10), 1)
     log(f"resnet50 {r50_ms:.3f} ms/batch  {64 / r50_ms * 1e3:.0f} img/s  roof frac {r50_roof / r50_ms:.3f}")
@@ -541,6 +606,11 @@ def main():
         kv, tfv, dtv = cpu_baseline_vit()
         cpu_extra["vit"] = {"value": round(tfv, 4), "unit": "TFLOP/s", "cores": threads, "kind": kv if kv == "reference" else "port",
                             "sample": f"one image's share of the ViT GEMM set (197 tokens, fp16-rounded fp32 inputs), {dtv:.2f} s"}
+        kn, n_fwd_ips, n_train_ips, n_fdt, n_tdt = cpu_baseline_resnet18_net()
+        cpu_extra["resnet18_net"] = {"kind": kn if kn == "reference" else "port", "cores": threads,
+                                     "forward_img_s": round(n_fwd_ips, 3), "train_img_s": round(n_train_ips, 3),
+                                     "sample": f"2 images, median of 3: inference forward {n_fdt:.2f} s, "
+                                               f"training step {n_tdt:.2f} s (reference CPUBackend chain)"}
         km, msm = cpu_baseline_mlp()
         cpu_extra["mlp"] = {"value": round(msm, 3), "unit": "ms/step", "cores": threads, "kind": km if km == "reference" else "port",
                             "sample": "mean of 20 MLP fwd+bwd steps after one warm-up"}
@@ -574,6 +644,17 @@ def main():
                           "roofline": {"bound": "mfma (per-layer max(flops/157.3T, bytes/8TB/s))",
                                        "roof_ms": round(r_roof_ms, 4), "frac": round(r_roof_ms / r_ms, 4)},
                           "layers": per, "cpu_baseline": cpu_r18},
+        "resnet18_network": {"batch": 32, "data": "synthetic images N(0,1), Kaiming-uniform weights, seeded BN",
+                             "forward": {"ms": round(n_fwd_ms, 4), "img_s": round(32 / n_fwd_ms * 1e3, 1),
+                                         "tflops": round(n_fl / n_fwd_ms / 1e9, 2),
+                                         "frac_of_157_3": round(n_fl / n_fwd_ms / 1e9 / 157.3, 4),
+                                         "logits_rel_err_vs_cpu_chain": n_err},
+                             "train_step": {"ms": round(n_train_ms, 4), "img_s": round(32 / n_train_ms * 1e3, 1),
+                                            "tflops": round(n_train_fl / n_train_ms / 1e9, 2),
+                                            "frac_of_157_3": round(n_train_fl / n_train_ms / 1e9 / 157.3, 4),
+                                            "scope": "forward with batch statistics + backward to every weight; "
+                                                     "no optimizer update"},
+                             "cpu_baseline": cpu_extra.get("resnet18_net")},
         "resnet50_conv": {"value": round(64 / r50_ms * 1e3, 1), "unit": "img/s", "batch": 64, "ms_per_batch": round(r50_ms, 4),
                           "tflops": round(r50_flops / r50_ms / 1e9, 2),
                           "roofline": {"roof_ms": round(r50_roof, 4), "frac": round(r50_roof / r50_ms, 4)},
