@@ -331,7 +331,30 @@ def bench_vit_half(om, steps: int, warmup: int, bf16: bool):
         flops_total += f
         total_ms += ms
         per.append({"gemm": name, "shape": [b, m, n, k], "ms": round(ms, 4), "tflops": round(f / ms / 1e9, 1)})
-    return total_ms, flops_total, per
+    # Fused attention on the QKV projection's output layout [T, 3*768] (split + softmax(QK^T/8) V + merge),
+    # replacing the two batched products above plus the softmax between them.
+    batch, tokens, heads, dh = 64, 197, 12, 64
+    T = batch * tokens
+    qkv = om.DeviceBuffer.empty((T * 3 * heads * dh,), np.uint16)
+    src = om.DeviceBuffer.from_numpy((rng.standard_normal(T * 3 * heads * dh, dtype=np.float32) * 0.5))
+    H.convertToHalf(src, qkv, T * 3 * heads * dh, bf16=bf16)
+    ctx = om.DeviceBuffer.empty((T * heads * dh,), np.uint16)
+    for _ in range(warmup):
+        H.attentionHalf(qkv, ctx, batch, tokens, heads, dh, 0.125, bf16=bf16, outHalf=True)
+    om.synchronize()
+    t = StreamTimer(om.stream_handle())
+    t.start()
+    for _ in range(steps):
+        H.attentionHalf(qkv, ctx, batch, tokens, heads, dh, 0.125, bf16=bf16, outHalf=True)
+    t.stop()
+    attn_ms = t.ms() / steps
+    attn_bytes = 2.0 * T * 3 * heads * dh + 2.0 * T * heads * dh   # qkv read + context written (half)
+    attn_flops = 4.0 * batch * heads * tokens * tokens * dh
+    fused = {"op": "attention_fused", "shape": [batch, tokens, heads, dh], "ms": round(attn_ms, 4),
+             "hbm_gb_s": round(attn_bytes / attn_ms / 1e6, 1), "frac_of_8000_gb_s": round(attn_bytes / attn_ms / 8e9, 4),
+             "tflops": round(attn_flops / attn_ms / 1e9, 1),
+             "replaces_ms": round(sum(x["ms"] for x in per if x["gemm"] in ("qk_t", "pv")), 4)}
+    return total_ms, flops_total, per, fused
 
 
 def bench_mlp(om, steps: int, warmup: int, batch: int = 128):
@@ -576,10 +599,15 @@ def main():
     log(f"resnet50 {r50_ms:.3f} ms/batch  {64 / r50_ms * 1e3:.0f} img/s  roof frac {r50_roof / r50_ms:.3f}")
     vit = {}
     for bf in (False, True):
-        v_ms, v_flops, v_per = bench_vit_half(om, max(5, args.steps // 5), 2, bf)
+        v_ms, v_flops, v_per, v_fused = bench_vit_half(om, max(5, args.steps // 5), 2, bf)
+        lin_ms = sum(x["ms"] for x in v_per if x["gemm"] not in ("qk_t", "pv"))
         vit["bf16" if bf else "fp16"] = {"ms_per_set": round(v_ms, 4), "tflops": round(v_flops / v_ms / 1e9, 1),
-                                         "frac_of_2516_tflops": round(v_flops / v_ms / 1e9 / 2516.6, 4), "gemms": v_per}
-        log(f"vit {'bf16' if bf else 'fp16'} {v_ms:.3f} ms  {v_flops / v_ms / 1e9:.1f} TFLOP/s")
+                                         "frac_of_2516_tflops": round(v_flops / v_ms / 1e9 / 2516.6, 4), "gemms": v_per,
+                                         "attention_fused": v_fused,
+                                         "ms_per_layer_fused": round(lin_ms + v_fused["ms"], 4)}
+        log(f"vit {'bf16' if bf else 'fp16'} {v_ms:.3f} ms  {v_flops / v_ms / 1e9:.1f} TFLOP/s; fused attention "
+            f"{v_fused['ms'] * 1e3:.1f} us ({v_fused['hbm_gb_s']:.0f} GB/s) replaces {v_fused['replaces_ms'] * 1e3:.1f} us "
+            f"of Q.K^T + P.V")
     mlp_ms, mlp_flops = bench_mlp(om, max(20, args.steps), 5)
     log(f"mlp step {mlp_ms * 1e3:.1f} us")
 

@@ -248,6 +248,18 @@ int omHipGemmStridedBatchedHalf(int nDtype, int bTransA, int bTransB, int nBatch
                                 const uint16_t* pB, long long nLdb, long long nStrideB,
                                 float* pC, long long nLdc, long long nStrideC);
 
+/* NEW: fused multi-head attention on half-precision inputs (QKV split with Q scaled,
+ * Q x K^T, softmax over the keys, P x V, head merge). Reference composition:
+ * MultiHeadAttention::forward vit.ixx:150-239 after the QKV projection —
+ * qkvSplitHeads, tensorTranspose2dBatched + tensorBatchedMatmul, tensorSoftmaxLastDim
+ * (CPUBackend::softmax cpu_backend.ixx:352-370), tensorBatchedMatmul, mergeHeads.
+ * pQKV [nBatch*nSeq, 3*nHeads*nHeadDim] in nDtype (0 binary16, 1 bfloat16), 16-byte
+ * aligned; pOut [nBatch*nSeq, nHeads*nHeadDim], fp32 (nOutHalf 0) or nDtype (1).
+ * fScale multiplies the scores (1/sqrt(nHeadDim) for ViT). nHeadDim must be 64 and
+ * nSeq <= 384. P is rounded to nDtype before P x V (fp32 accumulate). */
+int omHipAttentionHalf(int nDtype, const uint16_t* pQKV, void* pOut, int nOutHalf,
+                       int nBatch, int nSeq, int nHeads, int nHeadDim, float fScale);
+
 #ifdef __cplusplus
 }
 #endif

@@ -141,6 +141,13 @@ public:
         check(omHipAdd(pA, pB, pOut, toInt(nCount)), "add");
     }
 
+    // ---- fused attention (vit.ixx:150-239): qkv [B*S, 3*H*D] half -> out [B*S, H*D] ----
+    static void attentionHalf(int nDtype, const uint16_t* pQKV, void* pOut, bool bOutHalf, int nBatch, int nSeq,
+                              int nHeads, int nHeadDim, float fScale) {
+        check(omHipAttentionHalf(nDtype, pQKV, pOut, bOutHalf ? 1 : 0, nBatch, nSeq, nHeads, nHeadDim, fScale),
+              "attentionHalf");
+    }
+
     // ---- entries the reference builds by composition ----
     // transpose2d(B) + matmul (autograd.ixx:261-273)
     static void matmulTransB(const float* pA, const float* pB, float* pC, int nM, int nK, int nN) {

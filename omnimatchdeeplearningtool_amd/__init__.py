@@ -92,6 +92,7 @@ _SIGS = {
     "omHipAdaptiveAvgPool2dBackward": [_vp, _vp] + [_i] * 6,
     "omHipAdd": [_vp, _vp, _vp, _i],
     "omHipConv2dBiasBnAddAct": [_vp] * 7 + [_fl, _vp, _i, _vp] + [_i] * 9,
+    "omHipAttentionHalf": [_i, _vp, _vp, _i, _i, _i, _i, _i, _fl],
     "omHipConvertF32ToF16": [_vp, _vp, _i],
     "omHipConvertF32ToBF16": [_vp, _vp, _i],
     "omHipConvertF16ToF32": [_vp, _vp, _i],
@@ -362,6 +363,13 @@ class HIPBackend:
         call("omHipConv2dBiasBnAddAct", _ptr(pInput), _ptr(pWeight), _ptr(pBias), _ptr(pGamma), _ptr(pBeta),
              _ptr(pMean), _ptr(pVar), fEps, _ptr(pResidual), nAct, _ptr(pOutput), nBatch, nCin, nH, nW, nCout, nKH,
              nKW, nStride, nPad)
+
+    @staticmethod
+    def attentionHalf(pQKV, pOut, nBatch, nSeq, nHeads, nHeadDim, fScale, bf16: bool = False,
+                      outHalf: bool = False) -> None:
+        """Fused QKV split + softmax(scale Q K^T) V + head merge (vit.ixx:150-239)."""
+        call("omHipAttentionHalf", 1 if bf16 else 0, _ptr(pQKV), _ptr(pOut), 1 if outHalf else 0, nBatch, nSeq, nHeads,
+             nHeadDim, fScale)
 
     # ---- entries the reference builds by composition ----
     @staticmethod

@@ -95,6 +95,8 @@ def lib() -> ctypes.CDLL:
             "omrefAdaptiveAvgPool2d": [_f, _f] + [_i] * 6,
             "omrefAdaptiveAvgPool2dBackward": [_f, _f] + [_i] * 6,
             "omrefAdd": [_f, _f, _f, _sz],
+            "omrefSoftmax": [_f, _f, _i, _i],
+            "omrefAttention": [_f, _f, _i, _i, _i, _i, ctypes.c_float],
         }
         for name, args in sig.items():
             fn = getattr(L, name)
@@ -135,6 +137,7 @@ def ref_lib() -> Optional[ctypes.CDLL]:
                 "refAdaptiveAvgPool2d": [_f, _f] + [_i] * 6,
                 "refAdaptiveAvgPool2dBackward": [_f, _f] + [_i] * 6,
                 "refAdd": [_f, _f, _f, _sz],
+                "refSoftmax": [_f, _f, _i, _i],
             }
             for name, args in sig.items():
                 fn = getattr(R, name)
@@ -441,6 +444,49 @@ def add(a, b, backend: str = "oracle") -> np.ndarray:
     out = np.empty_like(a)
     _fn("Add", backend)(_p(a), _p(b), _p(out), a.size)
     return out
+
+
+def softmax(x, backend: str = "oracle") -> np.ndarray:
+    """CPUBackend::softmax over the last axis (cpu_backend.ixx:352-370)."""
+    x = _f32(x)
+    out = np.empty_like(x)
+    _fn("Softmax", backend)(_p(x), _p(out), x.size // x.shape[-1], x.shape[-1])
+    return out
+
+
+def attention(qkv, B, S, H, D, scale, backend: str = "oracle") -> np.ndarray:
+    """MultiHeadAttention's core after the QKV projection (vit.ixx:193-236):
+    qkv [B*S, 3*H*D] -> merged-head context [B*S, H*D]. With backend="reference"
+    the matmuls, transposes and softmax are the compiled reference's own."""
+    qkv = _f32(qkv)
+    if backend != "reference":
+        out = np.empty((B * S, H * D), np.float32)
+        lib().omrefAttention(_p(qkv), _p(out), B, S, H, D, ctypes.c_float(scale))
+        return out
+    t = qkv.reshape(B, S, 3, H, D)
+    Q = np.ascontiguousarray((t[:, :, 0] * np.float32(scale)).transpose(0, 2, 1, 3)).reshape(B * H, S, D)
+    K = np.ascontiguousarray(t[:, :, 1].transpose(0, 2, 1, 3)).reshape(B * H, S, D)
+    V = np.ascontiguousarray(t[:, :, 2].transpose(0, 2, 1, 3)).reshape(B * H, S, D)
+    kT = np.stack([transpose2d(K[i], backend="reference") for i in range(B * H)])
+    sc = batched_matmul(Q, kT, backend="reference")
+    P = softmax(sc, backend="reference")
+    ctx = batched_matmul(P, V, backend="reference")
+    return np.ascontiguousarray(ctx.reshape(B, H, S, D).transpose(0, 2, 1, 3)).reshape(B * S, H * D)
+
+
+def attention_f64(qkv, B, S, H, D, scale):
+    """float64 attention from the given (rounded) inputs, and the error budget
+    sum_j P_ij |V_jd| of each context element."""
+    t = np.asarray(qkv, np.float64).reshape(B, S, 3, H, D).transpose(2, 0, 3, 1, 4)   # 3 B H S D
+    Q, K, V = t[0], t[1], t[2]
+    s = scale * np.matmul(Q, np.swapaxes(K, -1, -2))
+    s = s - s.max(axis=-1, keepdims=True)
+    e = np.exp(s)
+    P = e / e.sum(axis=-1, keepdims=True)
+    ctx = np.matmul(P, V)
+    bound = np.matmul(P, np.abs(V))
+    f = lambda a: np.ascontiguousarray(a.transpose(0, 2, 1, 3)).reshape(B * S, H * D)
+    return f(ctx), f(bound)
 
 
 def float_to_half_trunc(x) -> np.ndarray:

@@ -444,6 +444,53 @@ void omrefAdaptiveAvgPool2dBackward(const float* gO, float* gI, int N, int C, in
             }
 }
 
+// cpu_backend.ixx:352-370 — per row: max, exp(x - max), sequential sum, divide.
+void omrefSoftmax(const float* in, float* out, int rows, int cols) {
+    for (int b = 0; b < rows; ++b) {
+        const float* r = in + (size_t)b * cols;
+        float* o = out + (size_t)b * cols;
+        float m = r[0];
+        for (int j = 1; j < cols; ++j)
+            if (r[j] > m) m = r[j];
+        float sum = 0.f;
+        for (int j = 0; j < cols; ++j) {
+            o[j] = std::exp(r[j] - m);
+            sum += o[j];
+        }
+        for (int j = 0; j < cols; ++j) o[j] /= sum;
+    }
+}
+
+// om.engine.vit.ixx:193-236 (MultiHeadAttention::forward, CPU path, after the QKV
+// projection): split heads with Q scaled, scores = Q x K^T (transpose2d +
+// batchedMatmul), softmax over the last dim, context = P x V, merge heads.
+// qkv [B*S, 3*H*D] -> out [B*S, H*D].
+void omrefAttention(const float* qkv, float* out, int B, int S, int H, int D, float scale) {
+    const int Dm = H * D, BH = B * H;
+    std::vector<float> Q((size_t)BH * S * D), K((size_t)BH * S * D), V((size_t)BH * S * D);
+    for (int n = 0; n < B; ++n)
+        for (int s = 0; s < S; ++s) {
+            const float* row = qkv + ((size_t)n * S + s) * 3 * Dm;
+            for (int h = 0; h < H; ++h)
+                for (int d = 0; d < D; ++d) {
+                    const size_t o = (((size_t)n * H + h) * S + s) * D + d;
+                    Q[o] = row[h * D + d] * scale;
+                    K[o] = row[Dm + h * D + d];
+                    V[o] = row[2 * Dm + h * D + d];
+                }
+        }
+    std::vector<float> kT((size_t)D * S), sc((size_t)S * S), P((size_t)S * S), ctx((size_t)S * D);
+    for (int bh = 0; bh < BH; ++bh) {
+        omrefTranspose2d(K.data() + (size_t)bh * S * D, kT.data(), S, D);
+        omrefMatmul(Q.data() + (size_t)bh * S * D, kT.data(), sc.data(), S, D, S);
+        omrefSoftmax(sc.data(), P.data(), S, S);
+        omrefMatmul(P.data(), V.data() + (size_t)bh * S * D, ctx.data(), S, S, D);
+        const int n = bh / H, h = bh % H;
+        for (int s = 0; s < S; ++s)
+            for (int d = 0; d < D; ++d) out[((size_t)n * S + s) * Dm + h * D + d] = ctx[(size_t)s * D + d];
+    }
+}
+
 // cpu_backend.ixx:147-160, simd.ixx:180-200 — elementwise a + b.
 void omrefAdd(const float* a, const float* b, float* out, size_t n) {
     for (size_t i = 0; i < n; ++i) out[i] = a[i] + b[i];

@@ -61,4 +61,5 @@ void refAdaptiveAvgPool2dBackward(const float* gO, float* gI, int n, int c, int 
     om::CPUBackend::adaptiveAvgPool2dBackward(gO, gI, n, c, h, w, oh, ow);
 }
 void refAdd(const float* a, const float* b, float* out, size_t n) { om::CPUBackend::add(a, b, out, n); }
+void refSoftmax(const float* in, float* out, int rows, int cols) { om::CPUBackend::softmax(in, out, rows, cols); }
 }
