@@ -553,12 +553,51 @@ def traffic_probe():
     log("traffic probe done")
 
 
+def workload_probe(name: str):
+    """A short dispatch sequence for kernel-trace profiling (no timing, no JSON):
+    resnet18_train — three ResNet-18 b32 training steps; vit_attention — ten fused
+    attentions (ViT-B/16 b64, fp16) after the ten Q.K^T / P.V batched products they replace."""
+    import omnimatchdeeplearningtool_amd as om
+    import oracle as O
+    om.init(0)
+    H = om.HIPBackend
+    if name == "resnet18_train":
+        from resnet_net import GpuResNet18, make_params
+        img = om.DeviceBuffer.from_numpy(O.randn((32, 3, 224, 224), 900))
+        g = om.DeviceBuffer.from_numpy(O.randn((32, 1000), 901, 0.01))
+        net = GpuResNet18(om, make_params(seed=1), 32, train=True)
+        for _ in range(3):
+            net.forward_train(img)
+            net.backward(g)
+    elif name == "vit_attention":
+        T, S, heads, dh, b = 64 * 197, 197, 12, 64, 64
+        src = om.DeviceBuffer.from_numpy(O.randn((T * 3 * heads * dh,), 5, 0.5))
+        qkv = om.DeviceBuffer.empty((T * 3 * heads * dh,), np.uint16)
+        H.convertToHalf(src, qkv, T * 3 * heads * dh)
+        ctx = om.DeviceBuffer.empty((T * heads * dh,), np.uint16)
+        q = om.DeviceBuffer.empty((b * heads * S * dh,), np.uint16)
+        sc = om.DeviceBuffer.empty((b * heads * S * S,))
+        pv = om.DeviceBuffer.empty((b * heads * S * dh,))
+        p16 = om.DeviceBuffer.empty((b * heads * S * S,), np.uint16)
+        for _ in range(10):
+            H.gemmStridedBatchedHalf(0, 0, 1, b * heads, S, S, dh, q, dh, S * dh, q, dh, S * dh, sc, S, S * S)
+            H.gemmStridedBatchedHalf(0, 0, 0, b * heads, S, dh, S, p16, S, S * S, q, dh, S * dh, pv, dh, S * dh)
+        for _ in range(10):
+            H.attentionHalf(qkv, ctx, b, S, heads, dh, 0.125, outHalf=True)
+    else:
+        raise SystemExit(f"unknown probe {name}")
+    om.synchronize()
+    log(f"probe {name} done")
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--probe", choices=["resnet18_train", "vit_attention"],
+                    help="run only a short dispatch sequence for kernel-trace profiling (no JSON line)")
     ap.add_argument("--traffic-probe", action="store_true",
                     help="run only the dispatch sequence profiled for HBM traffic (no JSON line)")
     args = ap.parse_args()
@@ -569,6 +608,9 @@ def main():
     rank = int(os.environ.get("RANK", "0"))
     if args.traffic_probe:
         traffic_probe()
+        return
+    if args.probe:
+        workload_probe(args.probe)
         return
 
     import omnimatchdeeplearningtool_amd as om
