@@ -27,6 +27,7 @@
 // in a fixed order (deterministic) and applies the same epilogue.
 #include "omhip_internal.hpp"
 #include "mfma_f32_tile.hpp"
+#include "buffer_io.hpp"
 #include "gemm_f32.hpp"
 #include "conv.hpp"
 #include "../../include/omhip.h"
@@ -38,11 +39,6 @@
 #include <tuple>
 
 namespace omhip {
-
-// Offsets at or above this byte count are out of range for every buffer used
-// here (buffers are limited to 2^30 bytes), so two such terms never wrap.
-constexpr uint32_t kOOB = 0x40000000u;
-constexpr uint32_t kMaxBufferBytes = 0x40000000u;
 
 struct ConvParams {
     const float* x;      // [N][Cin][H][W] (this batch chunk)
@@ -57,7 +53,7 @@ struct ConvParams {
     const float* res;    // [N][Cout][Ho][Wo] added after BN, before the activation, or null
     float* out;          // [N][Cout][Ho][Wo]
     float* ws;           // split-K partials [splits][Cout][Nq]
-    const uint2* tab;    // per K row: (byte offset ci*HW+kh*W+kw, tap code); kOOB past K
+    const uint2* tab;    // per K row: (byte offset of tap (ci,kh,kw), tap code); "outside" code past K
     int N, Cin, H, W, Cout, KH, KW, stride, pad, Ho, Wo;
     int K;               // Cin*KH*KW
     int Nq;              // N*Ho*Wo
@@ -67,21 +63,12 @@ struct ConvParams {
     uint32_t xBytes;     // range of the x buffer view
 };
 
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t bufferRsrc(const void* base, uint32_t bytes) {
-    // raw buffer, stride 0, range-checked against `bytes` (data format 32-bit)
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)bytes, 0x00020000);
-}
-__device__ __forceinline__ float bufLoad1(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
-    return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0));
-}
-__device__ __forceinline__ f32x4 bufLoad4(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
-    return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
-}
-
 // Tap table: entry kk = (4*(ci*H*W + kh*W + kw), code), code = kh*KW+kw for
 // the mask modes or (kh << 16) | kw for the coordinate-compare mode. Rows past
-// K read (kOOB, 0), so a slice that runs past K gathers zeros.
-__global__ void build_tap_table(uint2* tab, int K, int Kpad, int KH, int KW, int H, int W, int compareMode) {
+// K get offset 0 and a code that tests "outside" for every pixel (mask bit
+// 31 / 63, or kh = kw = 0xffff with H + pad, W + pad < 65535), so a slice that
+// runs past K gathers zeros through the voffset range check.
+__global__ void build_tap_table(uint2* tab, int K, int Kpad, int KH, int KW, int H, int W, int mode) {
     const int kk = blockIdx.x * blockDim.x + threadIdx.x;
     if (kk >= Kpad) return;
     uint2 e;
@@ -92,10 +79,10 @@ __global__ void build_tap_table(uint2* tab, int K, int Kpad, int KH, int KW, int
         const int kh = t / KW;
         const int kw = t - kh * KW;
         e.x = (uint32_t)(ci * H * W + kh * W + kw) * 4u;
-        e.y = compareMode ? (uint32_t)((kh << 16) | kw) : (uint32_t)t;
+        e.y = mode == 2 ? (uint32_t)((kh << 16) | kw) : (uint32_t)t;
     } else {
-        e.x = kOOB;
-        e.y = 0;
+        e.x = 0;
+        e.y = mode == 0 ? 31u : (mode == 1 ? 63u : 0xffffffffu);
     }
     tab[kk] = e;
 }
@@ -169,8 +156,7 @@ struct WeightLoader {
 // contiguous in its pixel's LDS row (128-bit stores). Per pixel: one byte offset
 // (into a buffer view that starts pad*W+pad floats before x, so it is never
 // negative) and the mask of taps that fall outside the image.
-//   MODE 0: KH*KW <= 32 (one 32-bit mask), MODE 1: <= 64 (64-bit mask),
-//   MODE 2: larger kernels compare coordinates.
+//   MODE: gatherMode(KH*KW).
 template <int BN, int BK, int NT, int MODE>
 struct GatherLoader {
     static constexpr int TPC = NT / BN;
@@ -452,7 +438,7 @@ static int launchConv(ConvParams& p, int splits, float* wsBuf) {
     p.ws = wsBuf;
     const bool va = (p.K % 4 == 0) && ((reinterpret_cast<uintptr_t>(p.w) & 15u) == 0);
     const int khw = p.KH * p.KW;
-    const int mode = khw <= 32 ? 0 : (khw <= 64 ? 1 : 2);
+    const int mode = gatherMode(khw);
     int rc;
     if (va)
         rc = mode == 0 ? launchConvT<Cfg, true, 0>(p)
@@ -493,7 +479,7 @@ static const uint2* tapTable(int Cin, int H, int W, int KH, int KW) {
     if (omHipMalloc(&mem, (size_t)Kpad * sizeof(uint2)) != 0) return nullptr;
     uint2* tab = static_cast<uint2*>(mem);
     hipLaunchKernelGGL(build_tap_table, dim3((Kpad + 255) / 256), dim3(256), 0, stream(), tab, K, Kpad, KH, KW, H, W,
-                       KH * KW > 64 ? 1 : 0);
+                       gatherMode(KH * KW));
     if (hipGetLastError() != hipSuccess) return nullptr;
     g_tabs.emplace(key, tab);
     return tab;
@@ -512,7 +498,8 @@ static int validateConv(const char* name, const float* x, const float* w, float*
     // (the batch is split into chunks that do); KH, KW < 2^16 for the tap codes.
     const long long imgBytes = (long long)Cin * H * W * 4 + 8LL * ((long long)pad * W + pad + W + 1);
     if (K > (1LL << 26) || imgBytes > (long long)kMaxBufferBytes / 2 || (long long)Cout * K * 4 > kMaxBufferBytes ||
-        (long long)Cout * Ho * Wo > (1LL << 30) || KH >= 65536 || KW >= 65536)
+        (long long)Cout * Ho * Wo > (1LL << 30) || H + pad >= 65535 || W + pad >= 65535 || KH >= 65536 ||
+        KW >= 65536)
         return fail("%s: tensor exceeds the 2^30-byte buffer range of this kernel", name);
     return 0;
 }

@@ -2,13 +2,27 @@
 // the forward (conv.hip, eltwise.hip) and training (train.hip) entry points.
 #pragma once
 
+#include <hip/hip_runtime.h>
+
 namespace omhip {
+
+// Gather mode by kernel size: 0 = one 32-bit "tap outside the image" mask per
+// pixel, 1 = a 64-bit mask, 2 = coordinate compares. Each mask mode keeps its
+// top bit free (at most 31 / 63 taps): that bit is never an image tap, so it
+// reads as "outside" for every pixel and serves as the code of rows past K.
+__host__ __device__ constexpr int gatherMode(int taps) { return taps <= 31 ? 0 : (taps <= 63 ? 1 : 2); }
 
 // out = act(BN(conv(x, w) + bias) + res) in one pass (bias, BN and res may be
 // null); act 0 identity, 1 ReLU. `name` prefixes error messages. 0 or -1.
 int conv2dFused(const char* name, const float* x, const float* w, const float* bias, const float* gamma,
                 const float* beta, const float* mean, const float* var, float eps, const float* res, int act,
                 float* out, int N, int Cin, int H, int W, int Cout, int KH, int KW, int stride, int pad);
+
+// gW[co][(ci*KH+kh)*KW+kw] = sum over images and output pixels of
+// gradOutput[n][co][oh][ow] * x[n][ci][oh*stride-pad+kh][ow*stride-pad+kw]
+// (overwrites gW). `name` prefixes error messages. 0 or -1.
+int conv2dWeightGrad(const char* name, const float* x, const float* gO, float* gW, int N, int Cin, int H, int W,
+                     int Cout, int KH, int KW, int stride, int pad);
 
 // col[n][(c*KH+kh)*KW+kw][oh*Wo+ow] for every image of x (zero outside the image).
 int im2colBatched(const float* x, float* col, int N, int Cin, int H, int W, int KH, int KW, int pad, int strd,

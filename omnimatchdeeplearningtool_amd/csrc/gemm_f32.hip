@@ -97,27 +97,18 @@ __global__ __launch_bounds__(Cfg::NT) void gemm_f32_kernel(GemmF32Params p) {
     }
 }
 
-// Sums the partials of every split (and, when reduceBatch, every batch item)
-// in a fixed order and writes C. Thread per element, columns fastest.
+// Sums the partials of every split in split order and writes C. Thread per element, columns fastest.
 __global__ void gemm_splitk_finish(const float* ws, float* C, int splits, int batch, int M, int N, long long ldc,
-                                   long long sC, int reduceBatch, int accumulate) {
+                                   long long sC) {
     const long long plane = (long long)M * N;
-    const int outBatch = reduceBatch ? 1 : batch;
-    const long long total = plane * outBatch;
+    const long long total = plane * batch;
     for (long long i = blockIdx.x * (long long)blockDim.x + threadIdx.x; i < total;
          i += (long long)gridDim.x * blockDim.x) {
         const long long b = i / plane, e = i - b * plane;
         const long long r = e / N, c = e - r * N;
-        float* out = C + b * sC + r * ldc + c;
-        float v = accumulate ? *out : 0.f;
-        for (int s = 0; s < splits; ++s) {
-            if (reduceBatch) {
-                for (int bb = 0; bb < batch; ++bb) v += ws[((long long)s * batch + bb) * plane + e];
-            } else {
-                v += ws[((long long)s * batch + b) * plane + e];
-            }
-        }
-        *out = v;
+        float v = 0.f;
+        for (int s = 0; s < splits; ++s) v += ws[((long long)s * batch + b) * plane + e];
+        C[b * sC + r * ldc + c] = v;
     }
 }
 
@@ -198,11 +189,11 @@ static int launchCfg(const GemmF32Params& prm, int batch, int splits, int cfg, b
 
 static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
-// Launches the GEMM (partials to ws when splits > 1 or the batch is reduced)
-// and, if needed, the finishing sum.
+// Launches the GEMM (partials to ws when splits > 1) and, if needed, the
+// finishing sum.
 static int gemmF32Run(bool ta, bool tb, int batch, int M, int N, int K, const float* A, long long lda, long long sA,
                       const float* B, long long ldb, long long sB, float* C, long long ldc, long long sC,
-                      GemmPlan plan, bool reduceBatch, bool accumulate = false) {
+                      GemmPlan plan) {
     GemmF32Params prm{};
     prm.A = A; prm.B = B; prm.C = C;
     prm.M = M; prm.N = N; prm.K = K;
@@ -212,7 +203,7 @@ static int gemmF32Run(bool ta, bool tb, int batch, int M, int N, int K, const fl
     int splits = plan.splits;
     prm.kChunk = ((K + splits - 1) / splits + bk - 1) / bk * bk;
     splits = (K + prm.kChunk - 1) / prm.kChunk;
-    const bool partial = splits > 1 || reduceBatch;
+    const bool partial = splits > 1;
     if (partial) {
         prm.ws = static_cast<float*>(workspace((size_t)splits * batch * M * N * sizeof(float)));
         if (!prm.ws) return fail("gemm: no workspace for %d x %d partial products", splits * batch, M * N);
@@ -226,10 +217,10 @@ static int gemmF32Run(bool ta, bool tb, int batch, int M, int N, int K, const fl
     else if (ta && !tb) rc = launchCfg<true, false>(prm, batch, splits, plan.cfg, va, vb);
     else rc = launchCfg<true, true>(prm, batch, splits, plan.cfg, va, vb);
     if (rc || !partial) return rc;
-    const long long total = (long long)M * N * (reduceBatch ? 1 : batch);
+    const long long total = (long long)M * N * batch;
     const int blocks = (int)std::min<long long>((total + 255) / 256, (long long)cuCount() * 16);
     hipLaunchKernelGGL(gemm_splitk_finish, dim3(blocks), dim3(256), 0, stream(), prm.ws, C, splits, batch, M, N, ldc,
-                       sC, reduceBatch ? 1 : 0, accumulate ? 1 : 0);
+                       sC);
     OMHIP_CHECK_LAUNCH();
     return 0;
 }
@@ -243,22 +234,7 @@ int gemmF32(bool ta, bool tb, int batch, int M, int N, int K,
             float* C, long long ldc, long long sC) {
     const bool wsOk = (size_t)64 * batch * M * N * sizeof(float) <= kMaxSplitWorkspace;
     const GemmPlan plan = planGemm(M, N, K, batch, wsOk);
-    return gemmF32Run(ta, tb, batch, M, N, K, A, lda, sA, B, ldb, sB, C, ldc, sC, plan, false);
-}
-
-int gemmF32BatchReduce(bool ta, bool tb, int batch, int M, int N, int K,
-                       const float* A, long long lda, long long sA,
-                       const float* B, long long ldb, long long sB,
-                       float* C, long long ldc, bool accumulate) {
-    // Each batch item is one more partial; split K only while the partials stay small.
-    const long long cus = cuCount();
-    GemmPlan plan{2, 1};
-    auto tiles = [&](int bm, int bn) { return (long long)((M + bm - 1) / bm) * ((N + bn - 1) / bn) * batch; };
-    if (tiles(256, 256) >= cus) plan.cfg = 0;
-    else if (tiles(128, 128) >= cus) plan.cfg = 1;
-    if ((size_t)batch * M * N * sizeof(float) > kMaxSplitWorkspace)
-        return fail("gemm: batch-reduce partials (%d x %d x %d floats) exceed the workspace limit", batch, M, N);
-    return gemmF32Run(ta, tb, batch, M, N, K, A, lda, sA, B, ldb, sB, C, ldc, 0, plan, true, accumulate);
+    return gemmF32Run(ta, tb, batch, M, N, K, A, lda, sA, B, ldb, sB, C, ldc, sC, plan);
 }
 
 __global__ void zero_rows_kernel(float* C, int rows, int cols, long long ldc, long long sC) {

@@ -23,19 +23,6 @@ int gemmF32(bool ta, bool tb, int batch, int M, int N, int K,
             const float* B, long long ldb, long long sB,
             float* C, long long ldc, long long sC);
 
-// C (+)= sum over b of op(A[b]) * op(B[b]) (a batch-reduce GEMM: the batch
-// is one more reduction axis). Partial products go to the library workspace
-// and are summed in batch order onto 0 (or onto C's current value when
-// accumulate is set), so the result is deterministic. Fails when the partials
-// (batch x M x N floats) exceed 256 MiB: callers chunk the batch.
-int gemmF32BatchReduce(bool ta, bool tb, int batch, int M, int N, int K,
-                       const float* A, long long lda, long long sA,
-                       const float* B, long long ldb, long long sB,
-                       float* C, long long ldc, bool accumulate);
-
-// Largest partial-product buffer gemmF32BatchReduce accepts, in bytes.
-constexpr size_t kBatchReduceMaxBytes = (size_t)256 << 20;
-
 // Zeroes C (batch x M x N, row stride ldc, batch stride sC) on the stream.
 int zeroOutput(float* C, int batch, int M, int N, long long ldc, long long sC);
 

@@ -182,15 +182,19 @@ __device__ __forceinline__ void mma_slice(const float* __restrict__ sA, const fl
 // ids, and the grouped ordering turns a contiguous range into a compact 2-D
 // patch (GROUP_M tile rows wide), so tiles sharing A rows / B columns share an L2.
 // ---------------------------------------------------------------------------
+// Logical id of block `bid` among `total` blocks: XCD x (= bid % 8) gets the
+// contiguous logical range x*q .. (spread evenly when total % 8 != 0).
+__device__ __forceinline__ int xcd_remap(int bid, int total) {
+    constexpr int XCDS = 8;
+    if (total < XCDS) return bid;
+    const int q = total / XCDS, rem = total % XCDS;
+    const int xcd = bid % XCDS, idx = bid / XCDS;
+    return (xcd < rem) ? xcd * (q + 1) + idx : rem * (q + 1) + (xcd - rem) * q + idx;
+}
+
 __device__ __forceinline__ void tile_coords(int bid, int total, int tilesM, int tilesN, int groupM,
                                             int& tm, int& tn) {
-    constexpr int XCDS = 8;
-    int t = bid;
-    if (total >= XCDS) {
-        const int q = total / XCDS, rem = total % XCDS;
-        const int xcd = bid % XCDS, idx = bid / XCDS;
-        t = (xcd < rem) ? xcd * (q + 1) + idx : rem * (q + 1) + (xcd - rem) * q + idx;
-    }
+    const int t = xcd_remap(bid, total);
     const int perGroup = groupM * tilesN;
     const int g = t / perGroup;
     const int firstM = g * groupM;

@@ -15,9 +15,8 @@
 // a column buffer, then a gather col2im in which every input element sums its
 // (kh, kw) contributions in the reference's order (no atomics).
 //
-// Weight gradient: im2col of a chunk of images, then one batch-reduce GEMM
-// gradW = sum_n gradOutput[n] x col[n]^T (partials per image, summed in image
-// order). Bias gradient and the BatchNorm reductions are per-channel sums over
+// Weight gradient: an implicit GEMM over every output pixel of the batch
+// (conv_wgrad.hip), no column matrix. Bias gradient and the BatchNorm reductions are per-channel sums over
 // N x H x W: each (channel, part) workgroup sums a contiguous range of images
 // in a fixed order, a second kernel adds the parts in order — deterministic.
 #include "omhip_internal.hpp"
@@ -336,30 +335,10 @@ int omHipConv2dBackwardWeight(const float* pInput, const float* pGradOutput, flo
     int Ho, Wo;
     if (validateConvGrad(name, nBatch, nCin, nH, nW, nCout, nKH, nKW, nStride, nPad, Ho, Wo)) return -1;
     if (!pInput || !pGradOutput || !pGradWeight) return fail("%s: null pointer", name);
-    const long long Kc = (long long)nCin * nKH * nKW;
+    if (conv2dWeightGrad(name, pInput, pGradOutput, pGradWeight, nBatch, nCin, nH, nW, nCout, nKH, nKW, nStride,
+                         nPad))
+        return -1;
     const long long HWo = (long long)Ho * Wo;
-    if (Kc > (1LL << 30) || HWo > (1LL << 30)) return fail("%s: tensor too large", name);
-    // images per chunk: the column buffer and the per-image partials both fit
-    int chunk = std::min(nBatch, colChunk(Kc * HWo));
-    chunk = std::min<long long>(chunk, std::max<long long>(1, (long long)(kBatchReduceMaxBytes / sizeof(float)) /
-                                                                   std::max(1LL, (long long)nCout * Kc)));
-    if ((long long)nCout * Kc * (long long)sizeof(float) > (long long)kBatchReduceMaxBytes)
-        return fail("%s: weight gradient of %lld floats exceeds the partial-sum workspace", name,
-                    (long long)nCout * Kc);
-    float* col = nullptr;
-    if (omHipMalloc(reinterpret_cast<void**>(&col), (size_t)chunk * Kc * HWo * sizeof(float))) return -1;
-    int rc = 0;
-    for (int n0 = 0; n0 < nBatch && !rc; n0 += chunk) {
-        const int nb = std::min(chunk, nBatch - n0);
-        rc = im2colBatched(pInput + (long long)n0 * nCin * nH * nW, col, nb, nCin, nH, nW, nKH, nKW, nPad, nStride,
-                           Ho, Wo);
-        if (!rc)
-            rc = gemmF32BatchReduce(false, true, nb, nCout, (int)Kc, (int)HWo,
-                                    pGradOutput + (long long)n0 * nCout * HWo, HWo, (long long)nCout * HWo, col, HWo,
-                                    Kc * HWo, pGradWeight, Kc, n0 > 0);
-    }
-    (void)omHipFree(col);
-    if (rc) return rc;
     if (pGradBias) return channelSums<0>(pGradOutput, nullptr, nullptr, nullptr, pGradBias, nullptr, nBatch, nCout,
                                          (int)HWo, 1.0f, false);
     return 0;

@@ -110,6 +110,8 @@ ODD = [
     (1, 1, 8, 8, 4, 3, 1, 1), (1, 1, 8, 8, 4, 3, 1, 0), (2, 3, 9, 9, 4, 3, 2, 1),
     (3, 5, 13, 11, 7, 3, 1, 1), (2, 7, 17, 19, 100, 5, 2, 2), (1, 16, 7, 7, 300, 1, 1, 0),
     (4, 3, 31, 29, 33, 7, 3, 3), (2, 64, 10, 10, 65, 3, 1, 1), (1, 2, 5, 5, 3, 5, 1, 0),
+    # large kernels: 36 taps (64-bit tap mask), 81 taps (coordinate compares), both with K % 16 != 0
+    (1, 2, 9, 9, 3, 6, 2, 2), (1, 1, 12, 12, 3, 9, 1, 4),
 ]
 
 

@@ -21,8 +21,9 @@ from conftest import empty_dev, to_dev
 pytestmark = pytest.mark.gpu
 TOL = O.TOL_FP32
 
-# (N, Cin, H, W, Cout, KH, KW, stride, pad): stride-1 shapes take the flipped-weight
-# convolution, the others the GEMM + col2im gather.
+# (N, Cin, H, W, Cout, KH, KW, stride, pad): for the input gradient, stride-1 square
+# kernels take the flipped-weight convolution, the others the GEMM + col2im gather;
+# the tap counts cover every gather mode (32-bit mask, 64-bit mask, coordinate compares).
 GRAD_SHAPES = [
     (2, 16, 14, 14, 32, 3, 3, 1, 1),    # ResNet 3x3 s1
     (2, 16, 15, 15, 32, 3, 3, 2, 1),    # 3x3 s2, odd input
@@ -31,7 +32,13 @@ GRAD_SHAPES = [
     (2, 8, 11, 11, 8, 5, 5, 1, 1),      # 5x5 s1 pad 1 (flipped pad 3)
     (2, 8, 12, 10, 16, 3, 1, 1, 0),     # KH != KW
     (2, 8, 9, 9, 8, 1, 1, 1, 1),        # pad > K-1
+    (2, 16, 8, 8, 24, 1, 1, 1, 0),      # 1x1 s1: x read as a plane, 4-pixel vectors
+    (2, 16, 7, 7, 24, 1, 1, 1, 0),      # 1x1 s1, 49 pixels per image: scalar plane reads
     (3, 5, 7, 9, 6, 3, 3, 3, 2),        # stride 3, ragged
+    (1, 3, 10, 12, 5, 4, 8, 1, 2),      # 32 taps: 64-bit tap mask
+    (1, 2, 12, 12, 3, 7, 9, 1, 3),      # 63 taps: last 64-bit mask mode
+    (1, 2, 10, 10, 3, 8, 8, 1, 3),      # 64 taps: coordinate compares
+    (2, 2, 13, 13, 4, 9, 9, 2, 4),      # 81 taps, stride 2
 ]
 
 
@@ -104,9 +111,59 @@ def _f64_rect(x, w, g, s, p):
     return (dXp[sl], dXpb[sl]), (dW, dWb), (g64.sum(axis=(0, 2, 3)), np.abs(g64).sum(axis=(0, 2, 3)))
 
 
+def _wgrad_rows(x, g, rows, K, s, p):
+    """float64 weight-gradient rows and their |.| budget: sum_n g[n, rows] im2col(x[n])^T."""
+    cols, _, _ = O._im2col64(np.asarray(x, np.float64), K, K, s, p)     # N x Kc x HW
+    g64 = np.asarray(g, np.float64).reshape(g.shape[0], g.shape[1], -1)[:, rows]
+    ref = np.einsum("nop,nkp->ok", g64, cols, optimize=True)
+    bound = np.einsum("nop,nkp->ok", np.abs(g64), np.abs(cols), optimize=True)
+    return ref, bound
+
+
+# ResNet shapes at batch 8 (long pixel axes: hundreds of pixel splits, summed in order)
+WGRAD_LARGE = [
+    (8, 3, 224, 224, 64, 7, 2, 3),      # stem, 49 taps, 100k pixels
+    (8, 64, 56, 56, 64, 3, 1, 1),       # layer 1
+    (8, 128, 28, 28, 256, 1, 2, 0),     # downsample 1x1 s2
+    (8, 256, 14, 14, 256, 3, 1, 1),     # layer 3 (196 pixels per image: 4-pixel vectors)
+    (8, 256, 56, 56, 64, 1, 1, 0),      # ResNet-50 bottleneck 1x1 reduce
+]
+
+
+@pytest.mark.parametrize("shape", WGRAD_LARGE, ids=lambda s: "N{}C{}H{}W{}o{}k{}s{}p{}".format(*s))
+def test_conv_backward_weight_large(hip, shape):
+    N, Cin, H, W, Cout, K, s, p = shape
+    Ho, Wo = O.out_hw(H, W, K, K, s, p)
+    x = O.randn((N, Cin, H, W), 61 + Cin)
+    g = O.randn((N, Cout, Ho, Wo), 62 + Cout)
+    dW = empty_dev(hip, (Cout, Cin, K, K))
+    hip.HIPBackend.conv2dBackwardWeight(to_dev(hip, x), to_dev(hip, g), dW, None, N, Cin, H, W, Cout, K, K, s, p)
+    got = dW.numpy().reshape(Cout, -1)
+    rows = np.array([0, 1, Cout // 2 - 1, Cout - 1])
+    ref, bound = _wgrad_rows(x, g, rows, K, s, p)
+    assert O.normalized_error(got[rows], ref, bound) <= TOL
+    assert np.all(np.isfinite(got))
+
+
+def test_conv_backward_weight_batch_chunks(hip):
+    """A 1x1 conv whose output gradient (289 MiB) exceeds one 256 MiB buffer view:
+    the batch is walked in two chunks, the second adding onto the first."""
+    N, Cin, H, W, Cout = 90, 64, 56, 56, 256
+    x = O.randn((N, Cin, H, W), 73)
+    g = O.randn((N, Cout, H, W), 74)
+    dW = empty_dev(hip, (Cout, Cin, 1, 1))
+    hip.HIPBackend.conv2dBackwardWeight(to_dev(hip, x), to_dev(hip, g), dW, None, N, Cin, H, W, Cout, 1, 1, 1, 0)
+    got = dW.numpy().reshape(Cout, Cin)
+    rows = np.array([0, 77, 255])
+    x64 = np.asarray(x, np.float64).reshape(N, Cin, -1)
+    g64 = np.asarray(g, np.float64).reshape(N, Cout, -1)[:, rows]
+    ref = np.einsum("nop,nkp->ok", g64, x64, optimize=True)
+    bound = np.einsum("nop,nkp->ok", np.abs(g64), np.abs(x64), optimize=True)
+    assert O.normalized_error(got[rows], ref, bound) <= TOL
+
+
 def test_conv_backward_weight_chunked(hip):
-    """ResNet-18 layer-4 conv at batch 32: the per-image partial products exceed one
-    workspace, so the batch is reduced in two chunks (the second accumulates)."""
+    """ResNet-18 layer-4 conv at batch 32 (49 pixels per image: no 4-pixel vectors)."""
     N, Cin, H, W, Cout, K, s, p = 32, 512, 7, 7, 512, 3, 1, 1
     x = O.randn((N, Cin, H, W), 71)
     g = O.randn((N, Cout, H, W), 72)
@@ -114,10 +171,7 @@ def test_conv_backward_weight_chunked(hip):
     hip.HIPBackend.conv2dBackwardWeight(to_dev(hip, x), to_dev(hip, g), dW, None, N, Cin, H, W, Cout, K, K, s, p)
     got = dW.numpy().reshape(Cout, -1)
     rows = np.array([0, 1, 255, 511])
-    cols, _, _ = O._im2col64(np.asarray(x, np.float64), K, K, s, p)     # N x Kc x HW
-    g64 = np.asarray(g, np.float64).reshape(N, Cout, H * W)[:, rows]
-    ref = np.einsum("nop,nkp->ok", g64, cols)
-    bound = np.einsum("nop,nkp->ok", np.abs(g64), np.abs(cols))
+    ref, bound = _wgrad_rows(x, g, rows, K, s, p)
     assert O.normalized_error(got[rows], ref, bound) <= TOL
 
 
