@@ -34,6 +34,7 @@
 
 #include <algorithm>
 #include <cmath>
+#include <cstdlib>
 #include <map>
 #include <mutex>
 #include <tuple>
@@ -54,12 +55,21 @@ struct ConvParams {
     float* out;          // [N][Cout][Ho][Wo]
     float* ws;           // split-K partials [splits][Cout][Nq]
     const uint2* tab;    // per K row: (byte offset of tap (ci,kh,kw), tap code); "outside" code past K
-    int N, Cin, H, W, Cout, KH, KW, stride, pad, Ho, Wo;
+    int N, Cin, H, W, Cout, KH, KW, stride;
+    int padH, padW;      // top / left padding; negative crops (the window starts inside the image)
+    int Ho, Wo;          // output pixel grid of the GEMM
+    // Output image: grid pixel (oh, ow) is written at (oh*oStride + oOffH, ow*oStride + oOffW) of an
+    // oH x oW image (the plain conv: oStride 1, offsets 0, oH x oW = Ho x Wo).
+    int oH, oW, oStride, oOffH, oOffW;
     int K;               // Cin*KH*KW
     int Nq;              // N*Ho*Wo
     int tilesM, tilesN;
     int splits, kChunk;  // split-K: k range [s*kChunk, min(K,(s+1)*kChunk))
-    int padOff;          // pad*W + pad: the x buffer view starts this many floats before x
+    // splits == 1: tiles [0, fullTiles) of the grouped order run whole; the rest
+    // run as remPieces K pieces of remChunk, partials in rws [piece][tile - fullTiles][BM][BN].
+    int fullTiles, remPieces, remChunk;
+    float* rws;
+    int padOff;          // max(padH,0)*W + max(padW,0): the x buffer view starts this many floats before x
     uint32_t xBytes;     // range of the x buffer view
 };
 
@@ -180,8 +190,8 @@ struct GatherLoader {
         const int n = qq / HoWo;
         const int pix = qq - n * HoWo;
         const int oh = pix / p.Wo, ow = pix - (pix / p.Wo) * p.Wo;
-        ih0 = colValid ? oh * p.stride - p.pad : -(1 << 29);   // a padding column matches no tap
-        iw0 = ow * p.stride - p.pad;
+        ih0 = colValid ? oh * p.stride - p.padH : -(1 << 29);   // a padding column matches no tap
+        iw0 = ow * p.stride - p.padW;
         voffPix = (uint32_t)(n * p.Cin * p.H * p.W + (colValid ? ih0 : 0) * W + iw0 + p.padOff) * 4u;
         uint64_t inside = 0;
         if constexpr (MODE != 2) {
@@ -224,6 +234,13 @@ struct GatherLoader {
     }
 };
 
+// Index within the output image of grid pixel pix = oh*Wo + ow.
+__device__ __forceinline__ int outPixel(const ConvParams& p, int pix) {
+    if (p.oStride == 1 && p.oOffH == 0 && p.oOffW == 0 && p.oW == p.Wo) return pix;
+    const int oh = pix / p.Wo, ow = pix - (pix / p.Wo) * p.Wo;
+    return (oh * p.oStride + p.oOffH) * p.oW + ow * p.oStride + p.oOffW;
+}
+
 template <class Cfg, bool VA, int MODE>
 __global__ __launch_bounds__(Cfg::NT) void conv_igemm_kernel(ConvParams p) {
     extern __shared__ float smem[];
@@ -238,20 +255,39 @@ __global__ __launch_bounds__(Cfg::NT) void conv_igemm_kernel(ConvParams p) {
     const int wm = wave / Cfg::WAVES_N;
     const int wn = wave % Cfg::WAVES_N;
 
-    int tm, tn;
-    tile_coords(blockIdx.x, p.tilesM * p.tilesN, p.tilesM, p.tilesN, 4, tm, tn);
+    // Block -> (tile, k range). Split-K: blockIdx.y is the split. Otherwise the
+    // first fullTiles blocks take whole tiles and the rest take K pieces of the
+    // remaining tiles, which evens out the work per CU when the tile count is
+    // not a multiple of the CU count.
+    const int tiles = p.tilesM * p.tilesN;
+    const int split = blockIdx.y;
+    int tm, tn, kBeg, kEnd;
+    int piece = -1, rtile = 0;
+    if (p.splits > 1) {
+        tile_coords(blockIdx.x, tiles, p.tilesM, p.tilesN, 4, tm, tn);
+        kBeg = split * p.kChunk;
+        kEnd = min(p.K, kBeg + p.kChunk);
+    } else if ((int)blockIdx.x < p.fullTiles) {
+        tile_coords(blockIdx.x, p.fullTiles, p.tilesM, p.tilesN, 4, tm, tn);
+        kBeg = 0;
+        kEnd = p.K;
+    } else {
+        const int b = blockIdx.x - p.fullTiles;
+        rtile = b / p.remPieces;
+        piece = b - rtile * p.remPieces;
+        grouped_tile(p.fullTiles + rtile, p.tilesM, p.tilesN, 4, tm, tn);
+        kBeg = piece * p.remChunk;
+        kEnd = min(p.K, kBeg + p.remChunk);
+    }
     const int m0 = tm * Cfg::BM;
     const int n0 = tn * Cfg::BN;
-    const int split = blockIdx.y;
-    const int kBeg = split * p.kChunk;
-    const int kEnd = min(p.K, kBeg + p.kChunk);
 
     WeightLoader<Cfg::BM, Cfg::BK, Cfg::NT, VA> la;
     la.init(p, m0, tid);
     GatherLoader<Cfg::BN, Cfg::BK, Cfg::NT, MODE> lb;
     lb.init(p, n0 + tid % Cfg::BN);
 
-    const bool direct = p.splits == 1;
+    const bool direct = p.splits == 1 && piece < 0;
     if (direct && tid < Cfg::BM) {
         const int co = min(m0 + tid, p.Cout - 1);
         sEpi[tid] = p.bias ? p.bias[co] : 0.f;
@@ -309,6 +345,21 @@ __global__ __launch_bounds__(Cfg::NT) void conv_igemm_kernel(ConvParams p) {
 
     const int li = lane & 31, h = lane >> 5;
     const int HoWo = p.Ho * p.Wo;
+    const int oHW = p.oH * p.oW;
+    if (piece >= 0) {
+        // compact partial tile; the finishing kernel checks the tile edges
+        float* rp = p.rws + ((long long)piece * (tiles - p.fullTiles) + rtile) * (Cfg::BM * Cfg::BN);
+#pragma unroll
+        for (int fn = 0; fn < Cfg::FN; ++fn)
+#pragma unroll
+            for (int fm = 0; fm < Cfg::FM; ++fm)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int row = wm * Cfg::WM + fm * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
+                    rp[row * Cfg::BN + wn * Cfg::WN + fn * 32 + li] = acc[fm][fn][r];
+                }
+        return;
+    }
     if (!direct) {
         float* ws = p.ws + (long long)split * p.Cout * p.Nq;
 #pragma unroll
@@ -331,7 +382,8 @@ __global__ __launch_bounds__(Cfg::NT) void conv_igemm_kernel(ConvParams p) {
         if (q >= p.Nq) continue;
         const int n = q / HoWo;
         const int pix = q - n * HoWo;
-        float* o = p.out + (long long)n * p.Cout * HoWo + pix;
+        const int opix = outPixel(p, pix);
+        float* o = p.out + (long long)n * p.Cout * oHW + opix;
 #pragma unroll
         for (int fm = 0; fm < Cfg::FM; ++fm)
 #pragma unroll
@@ -343,35 +395,60 @@ __global__ __launch_bounds__(Cfg::NT) void conv_igemm_kernel(ConvParams p) {
                 if (p.gamma)
                     v = __builtin_fmaf(sEpi[3 * Cfg::BM + rl], (v - sEpi[Cfg::BM + rl]) * sEpi[2 * Cfg::BM + rl],
                                        sEpi[4 * Cfg::BM + rl]);
-                if (p.res) v += p.res[(long long)n * p.Cout * HoWo + (long long)co * HoWo + pix];
+                if (p.res) v += p.res[(long long)n * p.Cout * oHW + (long long)co * oHW + opix];
                 if (p.act == 1) v = v > 0.f ? v : 0.f;
-                o[(long long)co * HoWo] = v;
+                o[(long long)co * oHW] = v;
             }
     }
+}
+
+// Epilogue of one output element (co, grid pixel q) from its finished sum.
+__device__ __forceinline__ void finishOne(const ConvParams& p, int co, int q, float v) {
+    const int HoWo = p.Ho * p.Wo;
+    if (p.bias) v += p.bias[co];
+    if (p.gamma) {
+        const float inv = 1.0f / sqrtf(p.var[co] + p.eps);
+        v = __builtin_fmaf(p.gamma[co], (v - p.mean[co]) * inv, p.beta[co]);
+    }
+    const int n = q / HoWo;
+    const int pix = q - n * HoWo;
+    const long long o = ((long long)n * p.Cout + co) * (p.oH * p.oW) + outPixel(p, pix);
+    if (p.res) v += p.res[o];
+    if (p.act == 1) v = v > 0.f ? v : 0.f;
+    p.out[o] = v;
 }
 
 // Sums split-K partials in split order and applies the epilogue; one thread
 // per (co, q) with q fastest so reads and NCHW writes are both coalesced.
 __global__ void conv_splitk_finish(ConvParams p) {
     const long long total = (long long)p.Cout * p.Nq;
-    const int HoWo = p.Ho * p.Wo;
     const long long stride = (long long)gridDim.x * blockDim.x;
     for (long long i = blockIdx.x * (long long)blockDim.x + threadIdx.x; i < total; i += stride) {
         const int co = (int)(i / p.Nq);
         const int q = (int)(i - (long long)co * p.Nq);
         float v = 0.f;
         for (int s = 0; s < p.splits; ++s) v += p.ws[(long long)s * total + i];
-        if (p.bias) v += p.bias[co];
-        if (p.gamma) {
-            const float inv = 1.0f / sqrtf(p.var[co] + p.eps);
-            v = __builtin_fmaf(p.gamma[co], (v - p.mean[co]) * inv, p.beta[co]);
-        }
-        const int n = q / HoWo;
-        const int pix = q - n * HoWo;
-        const long long o = ((long long)n * p.Cout + co) * HoWo + pix;
-        if (p.res) v += p.res[o];
-        if (p.act == 1) v = v > 0.f ? v : 0.f;
-        p.out[o] = v;
+        finishOne(p, co, q, v);
+    }
+}
+
+// Sums the K pieces of the remainder tiles in piece order and applies the epilogue.
+template <int BM, int BN>
+__global__ void conv_rem_finish(ConvParams p) {
+    const int remTiles = p.tilesM * p.tilesN - p.fullTiles;
+    const long long total = (long long)remTiles * BM * BN;
+    for (long long i = blockIdx.x * (long long)blockDim.x + threadIdx.x; i < total;
+         i += (long long)gridDim.x * blockDim.x) {
+        const int rt = (int)(i / (BM * BN));
+        const int e = (int)(i - (long long)rt * (BM * BN));
+        int tm, tn;
+        grouped_tile(p.fullTiles + rt, p.tilesM, p.tilesN, 4, tm, tn);
+        const int co = tm * BM + e / BN;
+        const int q = tn * BN + e % BN;
+        if (co >= p.Cout || q >= p.Nq) continue;
+        float v = 0.f;
+        for (int k = 0; k < p.remPieces; ++k) v += p.rws[((long long)k * remTiles + rt) * (BM * BN) + e];
+        finishOne(p, co, q, v);
     }
 }
 
@@ -399,7 +476,7 @@ static size_t convLds() {
 }
 
 template <class Cfg, bool VA, int MODE>
-static int launchConvT(ConvParams& p) {
+static int launchConvT(ConvParams& p, int gridX) {
     auto kern = conv_igemm_kernel<Cfg, VA, MODE>;
     const size_t lds = convLds<Cfg>();
     static bool s_attr = false;
@@ -408,49 +485,104 @@ static int launchConvT(ConvParams& p) {
                                         hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds)));
         s_attr = true;
     }
-    hipLaunchKernelGGL(kern, dim3(p.tilesM * p.tilesN, p.splits), dim3(Cfg::NT), lds, stream(), p);
+    hipLaunchKernelGGL(kern, dim3(gridX, p.splits), dim3(Cfg::NT), lds, stream(), p);
     OMHIP_CHECK_LAUNCH();
     return 0;
 }
 
-// Split-K factor: a layer with fewer than 2 tiles per CU (late ResNet stages:
-// few pixels, many channels) splits K by the smallest power of two that gives
-// at least 4 blocks per CU, keeping >= 256 taps per split; the partial sums
-// cost one extra fp32 write + read of the output. Measured best on the
-// ResNet-18 shapes (e.g. 512x1568x4608: 8 splits, 256x6272x2304: 4 splits).
-static int planSplits(const ConvParams& p, bool haveWs) {
+struct ConvPlan {
+    int splits;      // uniform split-K factor
+    int fullTiles;   // splits == 1: tiles run whole (the rest run as remPieces K pieces)
+    int remPieces;
+};
+
+// Work split, from a model of per-CU time: all blocks of these launches are
+// resident at once, so a layer takes as long as its busiest CU.
+//  * Fewer than 2 tiles per CU (late ResNet stages: few pixels, many
+//    channels): split K uniformly by the s in [1, 16] (>= 128 taps per split)
+//    that minimises ceil(tiles*s/CUs)/s tile-times per CU plus s extra fp32
+//    writes and reads of the output (e.g. 512x1568x4608: 5 splits).
+//  * Otherwise, when the tile count is not a multiple of the CU count and the
+//    CUs hold few tiles each: the tiles beyond the last whole round run as K
+//    pieces (one per idle CU, at most 16 per tile) summed by a small second
+//    kernel, e.g. 1568 tiles on 256 CUs: 1536 whole + 32 x 8 pieces, 6.125
+//    tile-times per CU instead of 7 (K >= 256 only: shorter tiles do not pay
+//    for the second launch).
+static ConvPlan planConv(const ConvParams& p, bool haveSplitWs) {
+    using Cfg = ConvCfg;
+    ConvPlan pl{1, p.tilesM * p.tilesN, 1};
     // TUNE-HOOK
-    const long long cus = cuCount();
-    const long long tiles = (long long)((p.Cout + ConvCfg::BM - 1) / ConvCfg::BM) * ((p.Nq + ConvCfg::BN - 1) / ConvCfg::BN);
-    if (!haveWs || tiles >= 2 * cus) return 1;
-    int s = 1;
-    while (s < 16 && tiles * s < 4 * cus && p.K / (2 * s) >= 256) s *= 2;
-    return s;
+    const long long U = cuCount();
+    const long long T = (long long)p.tilesM * p.tilesN;
+    const int nk = (p.K + Cfg::BK - 1) / Cfg::BK;
+    if (T < 2 * U) {
+        if (!haveSplitWs) return pl;
+        // seconds: one tile on one CU at 65 % of its share of peak; one split's partial
+        // write + read at an effective 6 TB/s (it partly overlaps the MFMA work)
+        const double tileT = 2.0 * Cfg::BM * Cfg::BN * p.K / (0.65 * 157.3e12 / 256.0);
+        const double partT = 8.0 * p.Cout * (double)p.Nq / 6.0e12;
+        double best = (double)((T + U - 1) / U) * tileT;
+        for (int s = 2; s <= 16 && p.K / s >= 128; ++s) {
+            const double c = (double)((T * s + U - 1) / U) / s * tileT + s * partT;
+            if (c < best) { best = c; pl.splits = s; }
+        }
+        return pl;
+    }
+    if (T >= 12 * U || nk < 16) return pl;   // many rounds, or tiles too short to pay a second launch
+    const long long R = T % U;
+    const int pieces = (int)std::min<long long>({16, R ? U / R : 0, (long long)nk});
+    if (R == 0 || pieces < 2) return pl;
+    pl.fullTiles = (int)(T - R);
+    pl.remPieces = pieces;
+    return pl;
 }
 
-static int launchConv(ConvParams& p, int splits, float* wsBuf) {
+static int launchConv(ConvParams& p, const ConvPlan& pl, float* wsBuf) {
     using Cfg = ConvCfg;
-    p.tilesM = (p.Cout + Cfg::BM - 1) / Cfg::BM;
-    p.tilesN = (p.Nq + Cfg::BN - 1) / Cfg::BN;
-    p.kChunk = (p.K + splits - 1) / splits;
-    p.kChunk = (p.kChunk + Cfg::BK - 1) / Cfg::BK * Cfg::BK;
-    p.splits = (p.K + p.kChunk - 1) / p.kChunk;
-    p.ws = wsBuf;
+    const int tiles = p.tilesM * p.tilesN;
+    int gridX = tiles;
+    p.splits = 1;
+    p.kChunk = p.K;
+    p.fullTiles = tiles;
+    p.remPieces = 1;
+    p.remChunk = p.K;
+    p.ws = nullptr;
+    p.rws = nullptr;
+    if (pl.splits > 1) {
+        p.kChunk = (p.K + pl.splits - 1) / pl.splits;
+        p.kChunk = (p.kChunk + Cfg::BK - 1) / Cfg::BK * Cfg::BK;
+        p.splits = (p.K + p.kChunk - 1) / p.kChunk;
+        p.ws = wsBuf;
+    } else if (pl.fullTiles < tiles) {
+        p.remChunk = (p.K + pl.remPieces - 1) / pl.remPieces;
+        p.remChunk = (p.remChunk + Cfg::BK - 1) / Cfg::BK * Cfg::BK;
+        p.remPieces = (p.K + p.remChunk - 1) / p.remChunk;
+        p.fullTiles = pl.fullTiles;
+        p.rws = wsBuf;
+        gridX = p.fullTiles + (tiles - p.fullTiles) * p.remPieces;
+    }
     const bool va = (p.K % 4 == 0) && ((reinterpret_cast<uintptr_t>(p.w) & 15u) == 0);
     const int khw = p.KH * p.KW;
     const int mode = gatherMode(khw);
     int rc;
     if (va)
-        rc = mode == 0 ? launchConvT<Cfg, true, 0>(p)
-                       : (mode == 1 ? launchConvT<Cfg, true, 1>(p) : launchConvT<Cfg, true, 2>(p));
+        rc = mode == 0 ? launchConvT<Cfg, true, 0>(p, gridX)
+                       : (mode == 1 ? launchConvT<Cfg, true, 1>(p, gridX) : launchConvT<Cfg, true, 2>(p, gridX));
     else
-        rc = mode == 0 ? launchConvT<Cfg, false, 0>(p)
-                       : (mode == 1 ? launchConvT<Cfg, false, 1>(p) : launchConvT<Cfg, false, 2>(p));
-    if (rc || p.splits == 1) return rc;
-    const long long total = (long long)p.Cout * p.Nq;
-    const int blocks = (int)std::min<long long>((total + 255) / 256, (long long)cuCount() * 16);
-    hipLaunchKernelGGL(conv_splitk_finish, dim3(blocks), dim3(256), 0, stream(), p);
-    OMHIP_CHECK_LAUNCH();
+        rc = mode == 0 ? launchConvT<Cfg, false, 0>(p, gridX)
+                       : (mode == 1 ? launchConvT<Cfg, false, 1>(p, gridX) : launchConvT<Cfg, false, 2>(p, gridX));
+    if (rc) return rc;
+    if (p.splits > 1) {
+        const long long total = (long long)p.Cout * p.Nq;
+        const int blocks = (int)std::min<long long>((total + 255) / 256, (long long)cuCount() * 16);
+        hipLaunchKernelGGL(conv_splitk_finish, dim3(blocks), dim3(256), 0, stream(), p);
+        OMHIP_CHECK_LAUNCH();
+    } else if (p.fullTiles < tiles) {
+        const long long total = (long long)(tiles - p.fullTiles) * Cfg::BM * Cfg::BN;
+        const int blocks = (int)std::min<long long>((total + 255) / 256, (long long)cuCount() * 16);
+        hipLaunchKernelGGL((conv_rem_finish<Cfg::BM, Cfg::BN>), dim3(blocks), dim3(256), 0, stream(), p);
+        OMHIP_CHECK_LAUNCH();
+    }
     return 0;
 }
 
@@ -485,6 +617,22 @@ static const uint2* tapTable(int Cin, int H, int W, int KH, int KW) {
     return tab;
 }
 
+// Buffer-view limits shared by every conv launch: one image with its border
+// margin and the weights fit a view (the batch is split into chunks that do),
+// pixel indices stay below 2^30, and KH, KW < 2^16 and H + pad, W + pad <
+// 65535 for the tap codes.
+static int checkConvLimits(const char* name, int Cin, int H, int W, int Cout, int KH, int KW, int padH, int padW,
+                           long long outPerImage) {
+    const long long K = (long long)Cin * KH * KW;
+    const long long margin = (long long)std::max(padH, 0) * W + std::max(padW, 0);
+    const long long imgBytes = (long long)Cin * H * W * 4 + 8LL * (margin + W + 1);
+    if (K > (1LL << 26) || imgBytes > (long long)kMaxBufferBytes / 2 || (long long)Cout * K * 4 > kMaxBufferBytes ||
+        outPerImage > (1LL << 30) || H + std::abs(padH) >= 65535 || W + std::abs(padW) >= 65535 || KH >= 65536 ||
+        KW >= 65536)
+        return fail("%s: tensor exceeds the 2^30-byte buffer range of this kernel", name);
+    return 0;
+}
+
 static int validateConv(const char* name, const float* x, const float* w, float* out, int N, int Cin, int H, int W,
                         int Cout, int KH, int KW, int stride, int pad, int& Ho, int& Wo) {
     if (N <= 0 || Cin <= 0 || H <= 0 || W <= 0 || Cout <= 0 || KH <= 0 || KW <= 0 || stride <= 0 || pad < 0)
@@ -493,35 +641,50 @@ static int validateConv(const char* name, const float* x, const float* w, float*
     Ho = (H + 2 * pad - KH) / stride + 1;
     Wo = (W + 2 * pad - KW) / stride + 1;
     if (Ho <= 0 || Wo <= 0) return fail("%s: kernel larger than the padded input", name);
-    const long long K = (long long)Cin * KH * KW;
-    // One image, its border margin and the weights must fit the buffer views
-    // (the batch is split into chunks that do); KH, KW < 2^16 for the tap codes.
-    const long long imgBytes = (long long)Cin * H * W * 4 + 8LL * ((long long)pad * W + pad + W + 1);
-    if (K > (1LL << 26) || imgBytes > (long long)kMaxBufferBytes / 2 || (long long)Cout * K * 4 > kMaxBufferBytes ||
-        (long long)Cout * Ho * Wo > (1LL << 30) || H + pad >= 65535 || W + pad >= 65535 || KH >= 65536 ||
-        KW >= 65536)
-        return fail("%s: tensor exceeds the 2^30-byte buffer range of this kernel", name);
-    return 0;
+    return checkConvLimits(name, Cin, H, W, Cout, KH, KW, pad, pad, (long long)Cout * Ho * Wo);
 }
 
 static int convChunk(ConvParams p, int n0, int nb) {
     // one batch chunk: x, out and the pixel axis restricted to images [n0, n0+nb)
     p.x = p.x + (long long)n0 * p.Cin * p.H * p.W;
-    p.out = p.out + (long long)n0 * p.Cout * p.Ho * p.Wo;
-    if (p.res) p.res = p.res + (long long)n0 * p.Cout * p.Ho * p.Wo;
+    p.out = p.out + (long long)n0 * p.Cout * p.oH * p.oW;
+    if (p.res) p.res = p.res + (long long)n0 * p.Cout * p.oH * p.oW;
     p.N = nb;
     p.Nq = nb * p.Ho * p.Wo;
-    p.padOff = p.pad * p.W + p.pad;
+    p.padOff = std::max(p.padH, 0) * p.W + std::max(p.padW, 0);
     p.xBytes = (uint32_t)(((long long)nb * p.Cin * p.H * p.W + p.padOff) * 4);
+    p.tilesM = (p.Cout + ConvCfg::BM - 1) / ConvCfg::BM;
+    p.tilesN = (p.Nq + ConvCfg::BN - 1) / ConvCfg::BN;
     // Split-K workspace only for outputs up to 64 MiB (late layers, where splitting pays).
     const bool wsOk = (size_t)p.Cout * p.Nq * sizeof(float) <= ((size_t)64 << 20);
-    int splits = planSplits(p, wsOk);
+    ConvPlan pl = planConv(p, wsOk);
     float* ws = nullptr;
-    if (splits > 1) {
-        ws = static_cast<float*>(workspace((size_t)splits * p.Cout * p.Nq * sizeof(float)));
-        if (!ws) splits = 1;
+    if (pl.splits > 1) {
+        ws = static_cast<float*>(workspace((size_t)pl.splits * p.Cout * p.Nq * sizeof(float)));
+        if (!ws) pl.splits = 1;
+    } else if (pl.fullTiles < p.tilesM * p.tilesN) {
+        const size_t remTiles = (size_t)(p.tilesM * p.tilesN - pl.fullTiles);
+        ws = static_cast<float*>(workspace(remTiles * pl.remPieces * ConvCfg::BM * ConvCfg::BN * sizeof(float)));
+        if (!ws) pl.fullTiles = p.tilesM * p.tilesN;
     }
-    return launchConv(p, splits, ws);
+    return launchConv(p, pl, ws);
+}
+
+// Walks the batch in chunks whose x view stays below 2^29 bytes and whose
+// pixel and output indices stay below 2^30.
+static int runConv(const char* name, ConvParams& p) {
+    p.K = p.Cin * p.KH * p.KW;
+    p.tab = tapTable(p.Cin, p.H, p.W, p.KH, p.KW);
+    if (!p.tab) return fail("%s: could not build the tap table", name);
+    const long long perImg = (long long)p.Cin * p.H * p.W * 4;
+    long long chunk = std::max<long long>(1, ((long long)kMaxBufferBytes / 2) / perImg);
+    chunk = std::min<long long>(chunk, std::max<long long>(1, (1LL << 30) / ((long long)p.Cout * p.Ho * p.Wo)));
+    chunk = std::min<long long>(chunk, std::max<long long>(1, (1LL << 30) / ((long long)p.Cout * p.oH * p.oW)));
+    for (int n0 = 0; n0 < p.N; n0 += (int)chunk) {
+        const int nb = (int)std::min<long long>(chunk, p.N - n0);
+        if (convChunk(p, n0, nb)) return -1;
+    }
+    return 0;
 }
 
 int conv2dFused(const char* name, const float* x, const float* w, const float* bias, const float* gamma,
@@ -538,19 +701,26 @@ int conv2dFused(const char* name, const float* x, const float* w, const float* b
     p.gamma = anyBn ? gamma : nullptr; p.beta = beta; p.mean = mean; p.var = var;
     p.eps = eps; p.act = act; p.res = res; p.out = out;
     p.N = N; p.Cin = Cin; p.H = H; p.W = W; p.Cout = Cout; p.KH = KH; p.KW = KW;
-    p.stride = stride; p.pad = pad; p.Ho = Ho; p.Wo = Wo;
-    p.K = Cin * KH * KW;
-    p.tab = tapTable(Cin, H, W, KH, KW);
-    if (!p.tab) return fail("%s: could not build the tap table", name);
-    // Images per chunk: the x view stays below 2^29 bytes, pixel indices below 2^30.
-    const long long perImg = (long long)Cin * H * W * 4;
-    long long chunk = std::max<long long>(1, ((long long)kMaxBufferBytes / 2) / perImg);
-    chunk = std::min<long long>(chunk, std::max<long long>(1, (1LL << 30) / ((long long)Cout * Ho * Wo)));
-    for (int n0 = 0; n0 < N; n0 += (int)chunk) {
-        const int nb = (int)std::min<long long>(chunk, N - n0);
-        if (convChunk(p, n0, nb)) return -1;
-    }
-    return 0;
+    p.stride = stride; p.padH = pad; p.padW = pad; p.Ho = Ho; p.Wo = Wo;
+    p.oH = Ho; p.oW = Wo; p.oStride = 1; p.oOffH = 0; p.oOffW = 0;
+    return runConv(name, p);
+}
+
+int conv2dToGrid(const char* name, const float* x, const float* w, float* out, int N, int Cin, int H, int W, int Cout,
+                 int KH, int KW, int padH, int padW, int Ho, int Wo, int oH, int oW, int oStride, int oOffH,
+                 int oOffW) {
+    if (N <= 0 || Cin <= 0 || H <= 0 || W <= 0 || Cout <= 0 || KH <= 0 || KW <= 0 || Ho <= 0 || Wo <= 0 ||
+        oStride <= 0 || oOffH < 0 || oOffW < 0 || (Ho - 1) * oStride + oOffH >= oH ||
+        (Wo - 1) * oStride + oOffW >= oW)
+        return fail("%s: invalid grid geometry", name);
+    if (!x || !w || !out) return fail("%s: null pointer", name);
+    if (checkConvLimits(name, Cin, H, W, Cout, KH, KW, padH, padW, (long long)Cout * oH * oW)) return -1;
+    ConvParams p{};
+    p.x = x; p.w = w; p.out = out;
+    p.N = N; p.Cin = Cin; p.H = H; p.W = W; p.Cout = Cout; p.KH = KH; p.KW = KW;
+    p.stride = 1; p.padH = padH; p.padW = padW; p.Ho = Ho; p.Wo = Wo;
+    p.oH = oH; p.oW = oW; p.oStride = oStride; p.oOffH = oOffH; p.oOffW = oOffW;
+    return runConv(name, p);
 }
 
 }  // namespace omhip

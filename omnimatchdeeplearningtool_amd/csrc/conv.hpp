@@ -18,6 +18,15 @@ int conv2dFused(const char* name, const float* x, const float* w, const float* b
                 const float* beta, const float* mean, const float* var, float eps, const float* res, int act,
                 float* out, int N, int Cin, int H, int W, int Cout, int KH, int KW, int stride, int pad);
 
+// Stride-1 convolution onto an output grid: grid pixel (oh, ow), oh < Ho,
+// ow < Wo, reads the window whose top-left tap is x[oh - padH][ow - padW]
+// (negative pads start inside the image) and is written at
+// (oh*oStride + oOffH, ow*oStride + oOffW) of an oH x oW output image; the
+// output pixels off the grid are left untouched. No bias, BN or activation.
+int conv2dToGrid(const char* name, const float* x, const float* w, float* out, int N, int Cin, int H, int W, int Cout,
+                 int KH, int KW, int padH, int padW, int Ho, int Wo, int oH, int oW, int oStride, int oOffH,
+                 int oOffW);
+
 // gW[co][(ci*KH+kh)*KW+kw] = sum over images and output pixels of
 // gradOutput[n][co][oh][ow] * x[n][ci][oh*stride-pad+kh][ow*stride-pad+kw]
 // (overwrites gW). `name` prefixes error messages. 0 or -1.

@@ -11,16 +11,17 @@
 // Input gradient. For stride 1 it is itself a stride-1 convolution of the
 // output gradient with the weights swapped over (Cout, Cin) and flipped in
 // (kh, kw), padded by K-1-pad: it runs on the forward implicit-GEMM kernel.
-// Other strides follow the reference's lowering — a GEMM W^T x gradOutput into
-// a column buffer, then a gather col2im in which every input element sums its
-// (kh, kw) contributions in the reference's order (no atomics).
+// A stride-s gradient splits into s*s output phases (ih mod s, iw mod s),
+// each again a stride-1 convolution of the output gradient with a flipped
+// sub-kernel, written straight to its pixels of the input gradient — no
+// column buffer, no col2im, no work on taps that cannot reach a pixel.
 //
 // Weight gradient: an implicit GEMM over every output pixel of the batch
-// (conv_wgrad.hip), no column matrix. Bias gradient and the BatchNorm reductions are per-channel sums over
-// N x H x W: each (channel, part) workgroup sums a contiguous range of images
-// in a fixed order, a second kernel adds the parts in order — deterministic.
+// (conv_wgrad.hip), no column matrix. Bias gradient and the BatchNorm
+// reductions are per-channel sums over N x H x W: each (channel, part)
+// workgroup sums a contiguous range of images in a fixed order, a second
+// kernel adds the parts in order — deterministic.
 #include "omhip_internal.hpp"
-#include "gemm_f32.hpp"
 #include "conv.hpp"
 #include "../../include/omhip.h"
 
@@ -29,12 +30,34 @@
 
 namespace omhip {
 
-// Column buffers are chunked to at most this many bytes.
-constexpr size_t kColChunkBytes = (size_t)512 << 20;
+// ---- input gradient by output phase -------------------------------------------------
+// For stride s, the input-gradient pixels with ih = a (mod s) receive only the
+// taps kh = (a + p) (mod s): kh = r + s*j, oh = i + floor((a+p)/s) - j for
+// ih = a + s*i. Over those pixels the gradient is a stride-1 correlation of
+// gradOutput with the sub-kernel flipped in j (top pad KHa - 1 - floor((a+p)/s),
+// possibly negative), and likewise in w. Stride 1 is the single phase (0, 0)
+// with the whole flipped kernel and pad K - 1 - p.
 
-// Wf[ci][co][KH-1-kh][KW-1-kw] = W[co][ci][kh][kw]
-__global__ void flip_weights_kernel(const float* __restrict__ w, float* __restrict__ wf, int Cout, int Cin, int KH,
-                                    int KW) {
+// Taps k in [0, K) of phase a: k = (a + p) (mod s).
+__host__ __device__ inline int phaseTaps(int K, int s, int p, int a) {
+    const int r = (a + p) % s;
+    return r < K ? (K - r + s - 1) / s : 0;
+}
+__host__ __device__ inline int phaseTapsBefore(int K, int s, int p, int a) {
+    int n = 0;
+    for (int b = 0; b < a; ++b) n += phaseTaps(K, s, p, b);
+    return n;
+}
+// Offset (floats) of phase (a, b)'s sub-kernel in the phase-major buffer.
+__host__ __device__ inline long long phaseOffset(int Cout, int Cin, int KH, int KW, int s, int p, int a, int b) {
+    return (long long)Cin * Cout *
+           ((long long)phaseTapsBefore(KH, s, p, a) * KW + (long long)phaseTaps(KH, s, p, a) * phaseTapsBefore(KW, s, p, b));
+}
+
+// Phase (a, b) sub-kernel: wf[ci][co][jf][lf] = W[co][ci][ra + s*(KHa-1-jf)][rb + s*(KWb-1-lf)].
+// Every tap belongs to exactly one phase, so the sub-kernels tile a buffer of W's size.
+__global__ void phase_flip_kernel(const float* __restrict__ w, float* __restrict__ wf, int Cout, int Cin, int KH,
+                                  int KW, int s, int p) {
     const long long total = (long long)Cout * Cin * KH * KW;
     for (long long i = blockIdx.x * (long long)blockDim.x + threadIdx.x; i < total;
          i += (long long)gridDim.x * blockDim.x) {
@@ -42,40 +65,17 @@ __global__ void flip_weights_kernel(const float* __restrict__ w, float* __restri
         const int kh = (int)((i / KW) % KH);
         const int ci = (int)((i / ((long long)KW * KH)) % Cin);
         const int co = (int)(i / ((long long)KW * KH * Cin));
-        wf[(((long long)ci * Cout + co) * KH + (KH - 1 - kh)) * KW + (KW - 1 - kw)] = w[i];
+        const int a = ((kh % s) - (p % s) + s) % s;
+        const int b = ((kw % s) - (p % s) + s) % s;
+        const int KHa = phaseTaps(KH, s, p, a), KWb = phaseTaps(KW, s, p, b);
+        const int jf = KHa - 1 - kh / s, lf = KWb - 1 - kw / s;
+        wf[phaseOffset(Cout, Cin, KH, KW, s, p, a, b) + (((long long)ci * Cout + co) * KHa + jf) * KWb + lf] = w[i];
     }
 }
 
-// gI[n][ci][ih][iw] = sum over (kh, kw) of col[n][(ci*KH+kh)*KW+kw][oh*Wo+ow]
-// where ih = oh*s - p + kh, iw = ow*s - p + kw (cpu_backend.ixx:581-607 as a gather).
-__global__ void col2im_gather_kernel(const float* __restrict__ col, float* __restrict__ gI, int N, int Cin, int H,
-                                     int W, int KH, int KW, int stride, int pad, int Ho, int Wo) {
-    const long long total = (long long)N * Cin * H * W;
-    const long long HWo = (long long)Ho * Wo;
-    for (long long i = blockIdx.x * (long long)blockDim.x + threadIdx.x; i < total;
-         i += (long long)gridDim.x * blockDim.x) {
-        const int iw = (int)(i % W);
-        const int ih = (int)((i / W) % H);
-        const long long nc = i / ((long long)W * H);   // n*Cin + ci
-        const int ci = (int)(nc % Cin);
-        const long long n = nc / Cin;
-        const float* c0 = col + (n * Cin * KH * KW + (long long)ci * KH * KW) * HWo;
-        float v = 0.f;
-        for (int kh = 0; kh < KH; ++kh) {
-            const int th = ih + pad - kh;
-            if (th < 0 || th % stride) continue;
-            const int oh = th / stride;
-            if (oh >= Ho) continue;
-            for (int kw = 0; kw < KW; ++kw) {
-                const int tw = iw + pad - kw;
-                if (tw < 0 || tw % stride) continue;
-                const int ow = tw / stride;
-                if (ow >= Wo) continue;
-                v += c0[(long long)(kh * KW + kw) * HWo + oh * Wo + ow];
-            }
-        }
-        gI[i] = v;
-    }
+__global__ void zero_fill_kernel(float* __restrict__ y, long long n) {
+    for (long long i = blockIdx.x * (long long)blockDim.x + threadIdx.x; i < n; i += (long long)gridDim.x * blockDim.x)
+        y[i] = 0.f;
 }
 
 static int gridFor(long long n) {
@@ -271,11 +271,6 @@ static int validateConvGrad(const char* name, int N, int Cin, int H, int W, int 
     return 0;
 }
 
-// Images per column-buffer chunk (at least one).
-static int colChunk(long long colFloatsPerImage) {
-    return (int)std::max<long long>(1, (long long)(kColChunkBytes / sizeof(float)) / std::max(1LL, colFloatsPerImage));
-}
-
 }  // namespace omhip
 
 using namespace omhip;
@@ -289,41 +284,37 @@ int omHipConv2dBackwardInput(const float* pGradOutput, const float* pWeight, flo
     int Ho, Wo;
     if (validateConvGrad(name, nBatch, nCin, nH, nW, nCout, nKH, nKW, nStride, nPad, Ho, Wo)) return -1;
     if (!pGradOutput || !pWeight || !pGradInput) return fail("%s: null pointer", name);
+    const int s = nStride, p = nPad;
     const long long wsz = (long long)nCout * nCin * nKH * nKW;
-    if (nStride == 1 && nKH == nKW && nPad <= nKH - 1) {
-        // stride 1: conv of gradOutput with the flipped, channel-swapped weights, pad K-1-p
-        float* wf = nullptr;
-        if (omHipMalloc(reinterpret_cast<void**>(&wf), (size_t)wsz * sizeof(float))) return -1;
-        hipLaunchKernelGGL(flip_weights_kernel, dim3(gridFor(wsz)), dim3(256), 0, stream(), pWeight, wf, nCout, nCin,
-                           nKH, nKW);
-        int rc = hipGetLastError() == hipSuccess ? 0 : fail("%s: flip launch failed", name);
-        if (!rc)
-            rc = conv2dFused(name, pGradOutput, wf, nullptr, nullptr, nullptr, nullptr, nullptr, 0.f, nullptr, 0,
-                             pGradInput, nBatch, nCout, Ho, Wo, nCin, nKH, nKW, 1, nKH - 1 - nPad);
-        (void)omHipFree(wf);   // stream-ordered reuse: later work on the stream runs after the conv
-        return rc;
+    // Pixels of a phase without taps (stride > kernel) get no contribution.
+    bool emptyPhase = false;
+    for (int a = 0; a < std::min(s, nH); ++a)
+        for (int b = 0; b < std::min(s, nW); ++b)
+            if (phaseTaps(nKH, s, p, a) == 0 || phaseTaps(nKW, s, p, b) == 0) emptyPhase = true;
+    if (emptyPhase) {
+        const long long n = (long long)nBatch * nCin * nH * nW;
+        hipLaunchKernelGGL(zero_fill_kernel, dim3(gridFor(n)), dim3(256), 0, stream(), pGradInput, n);
+        OMHIP_CHECK_LAUNCH();
     }
-    // general stride: col[n] = W^T x gradOutput[n], then the gather col2im
-    const long long Kc = (long long)nCin * nKH * nKW;
-    const long long HWo = (long long)Ho * Wo;
-    if (Kc > (1LL << 30) || HWo > (1LL << 30)) return fail("%s: tensor too large", name);
-    const int chunk = std::min(nBatch, colChunk(Kc * HWo));
-    float* col = nullptr;
-    if (omHipMalloc(reinterpret_cast<void**>(&col), (size_t)chunk * Kc * HWo * sizeof(float))) return -1;
-    int rc = 0;
-    for (int n0 = 0; n0 < nBatch && !rc; n0 += chunk) {
-        const int nb = std::min(chunk, nBatch - n0);
-        rc = gemmF32(true, false, nb, (int)Kc, (int)HWo, nCout, pWeight, Kc, 0,
-                     pGradOutput + (long long)n0 * nCout * HWo, HWo, (long long)nCout * HWo, col, HWo, Kc * HWo);
-        if (!rc) {
-            const long long total = (long long)nb * nCin * nH * nW;
-            hipLaunchKernelGGL(col2im_gather_kernel, dim3(gridFor(total)), dim3(256), 0, stream(), col,
-                               pGradInput + (long long)n0 * nCin * nH * nW, nb, nCin, nH, nW, nKH, nKW, nStride, nPad,
-                               Ho, Wo);
-            if (hipGetLastError() != hipSuccess) rc = fail("%s: col2im launch failed", name);
+    float* wf = nullptr;
+    if (omHipMalloc(reinterpret_cast<void**>(&wf), (size_t)wsz * sizeof(float))) return -1;
+    hipLaunchKernelGGL(phase_flip_kernel, dim3(gridFor(wsz)), dim3(256), 0, stream(), pWeight, wf, nCout, nCin, nKH,
+                       nKW, s, p);
+    int rc = hipGetLastError() == hipSuccess ? 0 : fail("%s: flip launch failed", name);
+    for (int a = 0; a < std::min(s, nH) && !rc; ++a) {
+        const int KHa = phaseTaps(nKH, s, p, a);
+        if (KHa == 0) continue;
+        const int Hp = (nH - a + s - 1) / s;
+        for (int b = 0; b < std::min(s, nW) && !rc; ++b) {
+            const int KWb = phaseTaps(nKW, s, p, b);
+            if (KWb == 0) continue;
+            const int Wp = (nW - b + s - 1) / s;
+            rc = conv2dToGrid(name, pGradOutput, wf + phaseOffset(nCout, nCin, nKH, nKW, s, p, a, b), pGradInput,
+                              nBatch, nCout, Ho, Wo, nCin, KHa, KWb, KHa - 1 - (a + p) / s, KWb - 1 - (b + p) / s, Hp,
+                              Wp, nH, nW, s, a, b);
         }
     }
-    (void)omHipFree(col);
+    (void)omHipFree(wf);   // stream-ordered reuse: later work on the stream runs after the convs
     return rc;
 }
 

@@ -91,6 +91,28 @@ def test_resnet18_layer_fused_b32_sampled(hip, shape):
     _check(out[idx], np.ascontiguousarray(x[idx]), wt, None, bn, 1, s, p)
 
 
+# Tile counts of 2-12 per CU that are not a multiple of the CU count: the tiles
+# past the last whole round run as K pieces summed by a second kernel (tile
+# edges exact, and ragged in Cout and pixels).
+BALANCE = [(12, 64, 56, 56, 64, 3, 1, 1), (9, 16, 45, 45, 100, 3, 1, 1)]
+
+
+@pytest.mark.parametrize("geom", BALANCE, ids=lambda g: "N{}C{}H{}W{}o{}k{}s{}p{}".format(*g))
+@pytest.mark.parametrize("variant", ["bias", "bn_relu"])
+def test_balanced_work_split(hip, geom, variant):
+    N, cin, h, w, cout, k, s, p = geom
+    x = O.randn((N, cin, h, w), 900 + cout)
+    wt = _kaiming_uniform((cout, cin, k, k), 901)
+    bias = O.randn((cout,), 902) if variant == "bias" else None
+    bn = _params(cout, 903) if variant == "bn_relu" else None
+    print(f"case balance {geom} {variant}", flush=True)
+    if variant == "bias":
+        out = _run_conv(hip, x, wt, bias, None, 0, s, p, entry="omHipConv2d")
+    else:
+        out = _run_conv(hip, x, wt, None, bn, 1, s, p)
+    _check(out, x, wt, bias, bn, 1 if bn is not None else 0, s, p)
+
+
 R50 = [c for c in resnet50_convs() if c[0].endswith((".0.conv1", ".0.conv2", ".0.conv3", ".0.ds", "stem"))]
 
 

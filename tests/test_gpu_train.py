@@ -21,8 +21,8 @@ from conftest import empty_dev, to_dev
 pytestmark = pytest.mark.gpu
 TOL = O.TOL_FP32
 
-# (N, Cin, H, W, Cout, KH, KW, stride, pad): for the input gradient, stride-1 square
-# kernels take the flipped-weight convolution, the others the GEMM + col2im gather;
+# (N, Cin, H, W, Cout, KH, KW, stride, pad): the input gradient runs one convolution per
+# output phase (s*s of them; stride > kernel leaves phases without taps, zero-filled);
 # the tap counts cover every gather mode (32-bit mask, 64-bit mask, coordinate compares).
 GRAD_SHAPES = [
     (2, 16, 14, 14, 32, 3, 3, 1, 1),    # ResNet 3x3 s1
@@ -39,6 +39,8 @@ GRAD_SHAPES = [
     (1, 2, 12, 12, 3, 7, 9, 1, 3),      # 63 taps: last 64-bit mask mode
     (1, 2, 10, 10, 3, 8, 8, 1, 3),      # 64 taps: coordinate compares
     (2, 2, 13, 13, 4, 9, 9, 2, 4),      # 81 taps, stride 2
+    (1, 2, 9, 9, 2, 3, 3, 4, 0),        # stride > kernel: phases without taps
+    (1, 2, 8, 8, 2, 2, 2, 2, 1),        # even kernel, stride 2, pad 1
 ]
 
 
