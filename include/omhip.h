@@ -177,6 +177,23 @@ int omHipBatchNorm2dBackward(const float* pGradOutput, const float* pInput,
                              const float* pMean, const float* pInvStd, const float* pGamma,
                              float* pGradInput, float* pGradGamma, float* pGradBeta,
                              int nBatch, int nChannels, int nH, int nW, float fEps);
+/* NEW: the training forward of a conv block tail in one pass: y = act(BN_train(x)
+ * [+ pResidual]) — the reference's batchNorm2d (training) then add then relu
+ * (cpu_backend.ixx:796-840, :147-160, :317-332; BasicBlock resnet.ixx:55-79), each
+ * rounded as there, so the result is bit-identical to the three calls. Statistics
+ * and running averages as omHipBatchNorm2d in training mode; pResidual may be NULL,
+ * nAct 0 identity / 1 ReLU. */
+int omHipBatchNorm2dTrainAct(const float* pInput, float* pOutput, const float* pGamma, const float* pBeta,
+                             float* pRunningMean, float* pRunningVar, float* pSavedMean, float* pSavedInvStd,
+                             int nBatch, int nChannels, int nH, int nW, float fEps, float fMomentum,
+                             const float* pResidual, int nAct);
+/* NEW: omHipBatchNorm2dBackward of the gradient gated by a ReLU,
+ * gradOut' = reluInput > 0 ? gradOut : 0 (cpu_backend.ixx:337-346) — bit-identical to
+ * omHipReLUBackward followed by omHipBatchNorm2dBackward, without the gated tensor. */
+int omHipBatchNorm2dBackwardRelu(const float* pGradOutput, const float* pReluInput, const float* pInput,
+                                 const float* pMean, const float* pInvStd, const float* pGamma,
+                                 float* pGradInput, float* pGradGamma, float* pGradBeta,
+                                 int nBatch, int nChannels, int nH, int nW, float fEps);
 
 /* ===== pooling and the residual sum (cuda_kernels.cuh:218-245, :74) ===== */
 
@@ -214,6 +231,10 @@ int omHipAdaptiveAvgPool2dBackward(const float* pGradOut, float* pGradIn, int nN
                                    int nOutH, int nOutW);
 /* replaces omCudaAdd (cuh:74); CPUBackend::add cpu_backend.ixx:147-160 */
 int omHipAdd(const float* pA, const float* pB, float* pC, int nCount);
+/* NEW: out = a + (x > 0 ? gradOut : 0) — CPUBackend::add of a and reluBackward(x, gradOut)
+ * (cpu_backend.ixx:147-160, :337-346) in one pass, bit-identical: the identity shortcut's
+ * share of a residual block's backward. */
+int omHipAddReluBackward(const float* pA, const float* pIn, const float* pGradOut, float* pOut, int nCount);
 /* NEW: omHipConv2dBiasBnAct with the residual added after BN and before the
  * activation: out = act(BN(conv(x) + bias) + residual). Reference composition: the
  * BasicBlock / Bottleneck tail bn2(conv2(.)) + shortcut -> relu (resnet.ixx:55-79,

@@ -104,6 +104,24 @@ public:
                                        pGradBeta, nBatch, nChannels, nH, nW, 1e-5f),
               "batchNorm2dBackward");
     }
+    // fused training passes (bit-identical to the separate reference ops)
+    static void batchNorm2dBackwardRelu(const float* pGradOutput, const float* pReluInput, const float* pInput,
+                                        const float* pSavedMean, const float* pSavedInvStd, const float* pGamma,
+                                        float* pGradInput, float* pGradGamma, float* pGradBeta, int nBatch,
+                                        int nChannels, int nH, int nW) {
+        check(omHipBatchNorm2dBackwardRelu(pGradOutput, pReluInput, pInput, pSavedMean, pSavedInvStd, pGamma,
+                                           pGradInput, pGradGamma, pGradBeta, nBatch, nChannels, nH, nW, 1e-5f),
+              "batchNorm2dBackwardRelu");
+    }
+    static void batchNorm2dTrainAct(const float* pInput, float* pOutput, const float* pGamma, const float* pBeta,
+                                    float* pRunningMean, float* pRunningVar, float* pSavedMean, float* pSavedInvStd,
+                                    int nBatch, int nChannels, int nH, int nW, float fEps, float fMomentum,
+                                    const float* pResidual, bool bRelu) {
+        check(omHipBatchNorm2dTrainAct(pInput, pOutput, pGamma, pBeta, pRunningMean, pRunningVar, pSavedMean,
+                                       pSavedInvStd, nBatch, nChannels, nH, nW, fEps, fMomentum, pResidual,
+                                       bRelu ? 1 : 0),
+              "batchNorm2dTrainAct");
+    }
 
     // ---- pooling and add (cpu_backend.ixx:897-1023, :1467-1510, :147-160) ----
     static void maxPool2d(const float* pInput, float* pOutput, int* pIndices, int nBatch, int nChannels, int nH,
@@ -139,6 +157,10 @@ public:
     }
     static void add(const float* pA, const float* pB, float* pOut, size_t nCount) {
         check(omHipAdd(pA, pB, pOut, toInt(nCount)), "add");
+    }
+    static void addReluBackward(const float* pA, const float* pInput, const float* pGradOutput, float* pOut,
+                                size_t nCount) {
+        check(omHipAddReluBackward(pA, pInput, pGradOutput, pOut, toInt(nCount)), "addReluBackward");
     }
 
     // ---- fused attention (vit.ixx:150-239): qkv [B*S, 3*H*D] half -> out [B*S, H*D] ----

@@ -91,6 +91,9 @@ _SIGS = {
     "omHipAdaptiveAvgPool2d": [_vp, _vp] + [_i] * 6,
     "omHipAdaptiveAvgPool2dBackward": [_vp, _vp] + [_i] * 6,
     "omHipAdd": [_vp, _vp, _vp, _i],
+    "omHipAddReluBackward": [_vp, _vp, _vp, _vp, _i],
+    "omHipBatchNorm2dTrainAct": [_vp] * 8 + [_i] * 4 + [_fl, _fl, _vp, _i],
+    "omHipBatchNorm2dBackwardRelu": [_vp] * 9 + [_i] * 4 + [_fl],
     "omHipConv2dBiasBnAddAct": [_vp] * 7 + [_fl, _vp, _i, _vp] + [_i] * 9,
     "omHipAttentionHalf": [_i, _vp, _vp, _i, _i, _i, _i, _i, _fl],
     "omHipConvertF32ToF16": [_vp, _vp, _i],
@@ -309,6 +312,22 @@ class HIPBackend:
              _ptr(pGamma), _ptr(pGradInput), _ptr(pGradGamma), _ptr(pGradBeta), nBatch, nChannels, nH, nW, fEps)
 
     @staticmethod
+    def batchNorm2dBackwardRelu(pGradOutput, pReluInput, pInput, pSavedMean, pSavedInvStd, pGamma, pGradInput,
+                                pGradGamma, pGradBeta, nBatch, nChannels, nH, nW, fEps: float = 1e-5) -> None:
+        """batchNorm2dBackward of reluBackward(pReluInput, pGradOutput), one pass, bit-identical."""
+        call("omHipBatchNorm2dBackwardRelu", _ptr(pGradOutput), _ptr(pReluInput), _ptr(pInput), _ptr(pSavedMean),
+             _ptr(pSavedInvStd), _ptr(pGamma), _ptr(pGradInput), _ptr(pGradGamma), _ptr(pGradBeta), nBatch,
+             nChannels, nH, nW, fEps)
+
+    @staticmethod
+    def batchNorm2dTrainAct(pInput, pOutput, pGamma, pBeta, pRunningMean, pRunningVar, pSavedMean, pSavedInvStd,
+                            nBatch, nChannels, nH, nW, fEps, fMomentum, pResidual, nAct) -> None:
+        """act(batchNorm2d(training) [+ residual]) in one pass, bit-identical to the separate calls."""
+        call("omHipBatchNorm2dTrainAct", _ptr(pInput), _ptr(pOutput), _ptr(pGamma), _ptr(pBeta), _ptr(pRunningMean),
+             _ptr(pRunningVar), _ptr(pSavedMean), _ptr(pSavedInvStd), nBatch, nChannels, nH, nW, fEps, fMomentum,
+             _ptr(pResidual), nAct)
+
+    @staticmethod
     def maxPool2d(pInput, pOutput, pIndices, nBatch, nChannels, nH, nW, nKH, nKW, nStride, nPad) -> None:
         """CPUBackend::maxPool2d (cpu_backend.ixx:897-934); pIndices (int32) may be None."""
         call("omHipMaxPool2d", _ptr(pInput), _ptr(pOutput), _ptr(pIndices), nBatch, nChannels, nH, nW, nKH, nKW,
@@ -355,6 +374,11 @@ class HIPBackend:
     def add(pA, pB, pOut, nCount) -> None:
         """CPUBackend::add (cpu_backend.ixx:147-160)."""
         call("omHipAdd", _ptr(pA), _ptr(pB), _ptr(pOut), nCount)
+
+    @staticmethod
+    def addReluBackward(pA, pInput, pGradOutput, pOut, nCount) -> None:
+        """add(pA, reluBackward(pInput, pGradOutput)) in one pass, bit-identical."""
+        call("omHipAddReluBackward", _ptr(pA), _ptr(pInput), _ptr(pGradOutput), _ptr(pOut), nCount)
 
     @staticmethod
     def conv2dBiasBnAddAct(pInput, pWeight, pBias, pGamma, pBeta, pMean, pVar, fEps, pResidual, nAct, pOutput,

@@ -69,6 +69,13 @@ __global__ void relu_bwd_kernel(const float* x, const float* g, float* gi, long 
         gi[i] = x[i] > 0.f ? g[i] : 0.f;
 }
 
+// out = a + (x > 0 ? g : 0): the reference's add(a, reluBackward(x, g)) in one pass.
+__global__ void add_relu_bwd_kernel(const float* a, const float* x, const float* g, float* o, long long n) {
+    const long long stride = (long long)gridDim.x * blockDim.x;
+    for (long long i = blockIdx.x * (long long)blockDim.x + threadIdx.x; i < n; i += stride)
+        o[i] = a[i] + (x[i] > 0.f ? g[i] : 0.f);
+}
+
 // ---- bias broadcast: out[n,c,hw] = data[n,c,hw] + bias[c] -------------------
 __global__ void add_bias_kernel(const float* __restrict__ d, const float* __restrict__ b, float* __restrict__ o,
                                 long long total, int C, int HW) {
@@ -240,6 +247,16 @@ int omHipReLUBackward(const float* pIn, const float* pGradOut, float* pGradIn, i
     if (nCount <= 0) return 0;
     if (!pIn || !pGradOut || !pGradIn) return fail("omHipReLUBackward: null pointer");
     hipLaunchKernelGGL(relu_bwd_kernel, dim3(gridFor(nCount)), dim3(256), 0, stream(), pIn, pGradOut, pGradIn,
+                       (long long)nCount);
+    OMHIP_CHECK_LAUNCH();
+    return 0;
+}
+
+int omHipAddReluBackward(const float* pA, const float* pIn, const float* pGradOut, float* pOut, int nCount) {
+    clearError();
+    if (nCount <= 0) return 0;
+    if (!pA || !pIn || !pGradOut || !pOut) return fail("omHipAddReluBackward: null pointer");
+    hipLaunchKernelGGL(add_relu_bwd_kernel, dim3(gridFor(nCount)), dim3(256), 0, stream(), pA, pIn, pGradOut, pOut,
                        (long long)nCount);
     OMHIP_CHECK_LAUNCH();
     return 0;

@@ -25,28 +25,64 @@ static int gridFor(long long n) {
     return (int)std::max<long long>(1, std::min<long long>((n + 255) / 256, (long long)cuCount() * 16));
 }
 
+// Grid over (64-column, 4-row) blocks of a plane and the planes: about 16 k
+// workgroups (64 per CU), blockIdx.z walking the further planes. One element
+// per thread over every plane at once left the launch bound by workgroup
+// dispatch (ResNet stem max-pool backward: 83 us with 115 k workgroups, 59 us
+// with 16 k).
+static dim3 planeGrid(long long planes, int rows, int cols) {
+    const long long bx = (cols + 63) / 64, by = (rows + 3) / 4;
+    long long zmax = std::max<long long>(1, 16384 / (bx * by));
+    // TUNE-HOOK-POOL
+    return dim3((unsigned)bx, (unsigned)by,
+                (unsigned)std::max<long long>(1, std::min<long long>({planes, zmax, 65535LL})));
+}
+
 struct PoolGeom {
     int N, C, H, W, KH, KW, SH, SW, PH, PW, Ho, Wo;
+    uint32_t mulH, shH, mulW, shW;   // x / SH == (x * mulH) >> shH for 0 <= x < 2^31 (likewise W)
 };
+
+// x / d == (x * mul) >> shift for 0 <= x < 2^31: l = ceil(log2 d), mul =
+// floor(2^(31+l) / d) + 1 < 2^32 (Granlund & Montgomery 1994, Thm 4.2).
+static void magicDivisor(uint32_t d, uint32_t& mul, uint32_t& shift) {
+    uint32_t l = 0;
+    while ((1ull << l) < d) ++l;
+    mul = (uint32_t)((1ull << (31 + l)) / d + 1);
+    shift = 31 + l;
+}
+
+__device__ __forceinline__ int divMagic(int x, uint32_t mul, uint32_t shift) {
+    return (int)(((uint64_t)(uint32_t)x * mul) >> shift);
+}
 
 // Window range of outputs covering input coordinate i along one axis:
 // o*s - p <= i <= o*s - p + K - 1  ->  o in [ceil((i+p-K+1)/s), floor((i+p)/s)] within [0, O).
-__device__ __forceinline__ void coverRange(int i, int K, int s, int p, int O, int& o0, int& o1) {
+__device__ __forceinline__ void coverRange(int i, int K, int s, int p, int O, uint32_t mul, uint32_t shift, int& o0,
+                                           int& o1) {
     const int hi = i + p;   // >= 0
     const int lo = hi - K + 1;
-    o0 = lo <= 0 ? 0 : (lo + s - 1) / s;
-    o1 = min(hi / s, O - 1);
+    o0 = lo <= 0 ? 0 : divMagic(lo + s - 1, mul, shift);
+    o1 = min(divMagic(hi, mul, shift), O - 1);
 }
+
+// Kernels run over (column, row, plane): blocks of 64 columns x 4 rows,
+// blockIdx.z walking the N*C planes. In-plane indices are 32-bit, the plane
+// base 64-bit; no division is needed to locate a pixel.
+#define OMHIP_FOR_PLANE_PIXELS(P, ROWS, COLS, r, c)                                          \
+    const int c = blockIdx.x * 64 + (int)threadIdx.x;                                        \
+    const int r = blockIdx.y * 4 + (int)threadIdx.y;                                         \
+    if (c < (COLS) && r < (ROWS))                                                            \
+        for (long long pl = blockIdx.z; pl < (P); pl += gridDim.z)
 
 // cpu_backend.ixx:897-934: strict '>' keeps the first maximum in (kh, kw) order;
 // index = flat input index, -1 (value -1e30) for a window wholly in the padding.
 __global__ void maxpool_kernel(const float* __restrict__ x, float* __restrict__ y, int* __restrict__ idx, PoolGeom g) {
-    const long long total = (long long)g.N * g.C * g.Ho * g.Wo;
-    for (long long o = blockIdx.x * (long long)blockDim.x + threadIdx.x; o < total;
-         o += (long long)gridDim.x * blockDim.x) {
-        const int ow = (int)(o % g.Wo);
-        const int oh = (int)((o / g.Wo) % g.Ho);
-        const long long nc = o / ((long long)g.Wo * g.Ho);
+    const long long planes = (long long)g.N * g.C;
+    const int S = g.Ho * g.Wo;
+    OMHIP_FOR_PLANE_PIXELS(planes, g.Ho, g.Wo, oh, ow) {
+        const int px = oh * g.Wo + ow;
+        const long long ib = pl * g.H * g.W;
         float best = -1e30f;
         int bi = -1;
         for (int kh = 0; kh < g.KH; ++kh) {
@@ -55,14 +91,14 @@ __global__ void maxpool_kernel(const float* __restrict__ x, float* __restrict__ 
             for (int kw = 0; kw < g.KW; ++kw) {
                 const int iw = ow * g.SW - g.PW + kw;
                 if (iw < 0 || iw >= g.W) continue;
-                const long long ii = (nc * g.H + ih) * g.W + iw;
-                const float v = x[ii];
+                const float v = x[ib + ih * g.W + iw];
                 if (v > best) {
                     best = v;
-                    bi = (int)ii;
+                    bi = (int)(ib + ih * g.W + iw);
                 }
             }
         }
+        const long long o = pl * S + px;
         y[o] = best;
         if (idx) idx[o] = bi;
     }
@@ -72,21 +108,38 @@ __global__ void maxpool_kernel(const float* __restrict__ x, float* __restrict__ 
 // (ascending) whose saved index is i.
 __global__ void maxpool_backward_kernel(const float* __restrict__ gO, const int* __restrict__ idx,
                                         float* __restrict__ gI, PoolGeom g) {
-    const long long total = (long long)g.N * g.C * g.H * g.W;
-    for (long long i = blockIdx.x * (long long)blockDim.x + threadIdx.x; i < total;
-         i += (long long)gridDim.x * blockDim.x) {
-        const int iw = (int)(i % g.W);
-        const int ih = (int)((i / g.W) % g.H);
-        const long long nc = i / ((long long)g.W * g.H);
+    const long long planes = (long long)g.N * g.C;
+    const int S = g.H * g.W;
+    OMHIP_FOR_PLANE_PIXELS(planes, g.H, g.W, ih, iw) {
+        const int px = ih * g.W + iw;
+        const long long i = pl * S + px;
+        const long long ob = pl * g.Ho * g.Wo;
         int oh0, oh1, ow0, ow1;
-        coverRange(ih, g.KH, g.SH, g.PH, g.Ho, oh0, oh1);
-        coverRange(iw, g.KW, g.SW, g.PW, g.Wo, ow0, ow1);
+        coverRange(ih, g.KH, g.SH, g.PH, g.Ho, g.mulH, g.shH, oh0, oh1);
+        coverRange(iw, g.KW, g.SW, g.PW, g.Wo, g.mulW, g.shW, ow0, ow1);
         float v = 0.f;
-        for (int oh = oh0; oh <= oh1; ++oh)
-            for (int ow = ow0; ow <= ow1; ++ow) {
-                const long long o = (nc * g.Ho + oh) * g.Wo + ow;
-                if (idx[o] == (int)i) v += gO[o];
-            }
+        if (oh1 - oh0 <= 1 && ow1 - ow0 <= 1) {
+            // at most 2 x 2 covering windows (K <= 2*stride): issue every load, then
+            // add the matching ones in ascending (oh, ow) order
+            const int oh1c = max(oh1, oh0), ow1c = max(ow1, ow0);
+            const long long o00 = ob + oh0 * g.Wo + ow0, o01 = ob + oh0 * g.Wo + ow1c;
+            const long long o10 = ob + oh1c * g.Wo + ow0, o11 = ob + oh1c * g.Wo + ow1c;
+            const bool r0 = oh0 <= oh1, r1 = oh1 > oh0, c0 = ow0 <= ow1, c1 = ow1 > ow0;
+            const int i00 = (r0 && c0) ? idx[o00] : -1, i01 = (r0 && c1) ? idx[o01] : -1;
+            const int i10 = (r1 && c0) ? idx[o10] : -1, i11 = (r1 && c1) ? idx[o11] : -1;
+            const float g00 = (r0 && c0) ? gO[o00] : 0.f, g01 = (r0 && c1) ? gO[o01] : 0.f;
+            const float g10 = (r1 && c0) ? gO[o10] : 0.f, g11 = (r1 && c1) ? gO[o11] : 0.f;
+            if (i00 == (int)i) v += g00;
+            if (i01 == (int)i) v += g01;
+            if (i10 == (int)i) v += g10;
+            if (i11 == (int)i) v += g11;
+        } else {
+            for (int oh = oh0; oh <= oh1; ++oh)
+                for (int ow = ow0; ow <= ow1; ++ow) {
+                    const long long o = ob + oh * g.Wo + ow;
+                    if (idx[o] == (int)i) v += gO[o];
+                }
+        }
         gI[i] = v;
     }
 }
@@ -112,13 +165,12 @@ __global__ void maxpool_scatter_kernel(const float* __restrict__ gO, const int* 
 
 // cpu_backend.ixx:958-990: sum over the valid taps divided by KH*KW.
 __global__ void avgpool_kernel(const float* __restrict__ x, float* __restrict__ y, PoolGeom g) {
-    const long long total = (long long)g.N * g.C * g.Ho * g.Wo;
+    const long long planes = (long long)g.N * g.C;
+    const int S = g.Ho * g.Wo;
     const float div = (float)(g.KH * g.KW);
-    for (long long o = blockIdx.x * (long long)blockDim.x + threadIdx.x; o < total;
-         o += (long long)gridDim.x * blockDim.x) {
-        const int ow = (int)(o % g.Wo);
-        const int oh = (int)((o / g.Wo) % g.Ho);
-        const long long nc = o / ((long long)g.Wo * g.Ho);
+    OMHIP_FOR_PLANE_PIXELS(planes, g.Ho, g.Wo, oh, ow) {
+        const int px = oh * g.Wo + ow;
+        const long long ib = pl * g.H * g.W;
         float sum = 0.f;
         for (int kh = 0; kh < g.KH; ++kh) {
             const int ih = oh * g.SH - g.PH + kh;
@@ -126,10 +178,10 @@ __global__ void avgpool_kernel(const float* __restrict__ x, float* __restrict__ 
             for (int kw = 0; kw < g.KW; ++kw) {
                 const int iw = ow * g.SW - g.PW + kw;
                 if (iw < 0 || iw >= g.W) continue;
-                sum += x[(nc * g.H + ih) * g.W + iw];
+                sum += x[ib + ih * g.W + iw];
             }
         }
-        y[o] = sum / div;
+        y[pl * S + px] = sum / div;
     }
 }
 
@@ -138,20 +190,19 @@ __global__ void avgpool_kernel(const float* __restrict__ x, float* __restrict__ 
 // the multiply must not be fused into the add here.
 __global__ void avgpool_backward_kernel(const float* __restrict__ gO, float* __restrict__ gI, PoolGeom g) {
 #pragma clang fp contract(off)
-    const long long total = (long long)g.N * g.C * g.H * g.W;
+    const long long planes = (long long)g.N * g.C;
+    const int S = g.H * g.W;
     const float scale = 1.0f / (float)(g.KH * g.KW);
-    for (long long i = blockIdx.x * (long long)blockDim.x + threadIdx.x; i < total;
-         i += (long long)gridDim.x * blockDim.x) {
-        const int iw = (int)(i % g.W);
-        const int ih = (int)((i / g.W) % g.H);
-        const long long nc = i / ((long long)g.W * g.H);
+    OMHIP_FOR_PLANE_PIXELS(planes, g.H, g.W, ih, iw) {
+        const int px = ih * g.W + iw;
+        const long long ob = pl * g.Ho * g.Wo;
         int oh0, oh1, ow0, ow1;
-        coverRange(ih, g.KH, g.SH, g.PH, g.Ho, oh0, oh1);
-        coverRange(iw, g.KW, g.SW, g.PW, g.Wo, ow0, ow1);
+        coverRange(ih, g.KH, g.SH, g.PH, g.Ho, g.mulH, g.shH, oh0, oh1);
+        coverRange(iw, g.KW, g.SW, g.PW, g.Wo, g.mulW, g.shW, ow0, ow1);
         float v = 0.f;
         for (int oh = oh0; oh <= oh1; ++oh)
-            for (int ow = ow0; ow <= ow1; ++ow) v += gO[(nc * g.Ho + oh) * g.Wo + ow] * scale;
-        gI[i] = v;
+            for (int ow = ow0; ow <= ow1; ++ow) v += gO[ob + oh * g.Wo + ow] * scale;
+        gI[pl * S + px] = v;
     }
 }
 
@@ -225,9 +276,12 @@ static int poolGeom(const char* name, int N, int C, int H, int W, int KH, int KW
                     PoolGeom& g) {
     if (N <= 0 || C <= 0 || H <= 0 || W <= 0 || KH <= 0 || KW <= 0 || SH <= 0 || SW <= 0 || PH < 0 || PW < 0)
         return fail("%s: invalid geometry", name);
-    g = {N, C, H, W, KH, KW, SH, SW, PH, PW, (H + 2 * PH - KH) / SH + 1, (W + 2 * PW - KW) / SW + 1};
+    g = {N, C, H, W, KH, KW, SH, SW, PH, PW, (H + 2 * PH - KH) / SH + 1, (W + 2 * PW - KW) / SW + 1, 0, 0, 0, 0};
+    magicDivisor((uint32_t)SH, g.mulH, g.shH);
+    magicDivisor((uint32_t)SW, g.mulW, g.shW);
     if (g.Ho <= 0 || g.Wo <= 0) return fail("%s: window larger than the padded input", name);
     if ((long long)N * C * H * W >= (1LL << 31)) return fail("%s: input exceeds 2^31 elements (int indices)", name);
+    if (H > 4 * 65535) return fail("%s: more than %d rows", name, 4 * 65535);
     return 0;
 }
 
@@ -243,7 +297,7 @@ int omHipMaxPool2d(const float* pIn, float* pOut, int* pIndices, int nN, int nC,
     PoolGeom g;
     if (poolGeom("omHipMaxPool2d", nN, nC, nH, nW, nKH, nKW, nSH, nSW, nPH, nPW, g)) return -1;
     if (!pIn || !pOut) return fail("omHipMaxPool2d: null pointer");
-    hipLaunchKernelGGL(maxpool_kernel, dim3(gridFor((long long)nN * nC * g.Ho * g.Wo)), dim3(256), 0, stream(), pIn,
+    hipLaunchKernelGGL(maxpool_kernel, planeGrid((long long)nN * nC, g.Ho, g.Wo), dim3(64, 4), 0, stream(), pIn,
                        pOut, pIndices, g);
     OMHIP_CHECK_LAUNCH();
     return 0;
@@ -271,7 +325,7 @@ int omHipMaxPool2dBackwardEx(const float* pGradOut, const int* pIndices, float* 
     PoolGeom g;
     if (poolGeom("omHipMaxPool2dBackwardEx", nN, nC, nH, nW, nKH, nKW, nSH, nSW, nPH, nPW, g)) return -1;
     if (!pGradOut || !pIndices || !pGradIn) return fail("omHipMaxPool2dBackwardEx: null pointer");
-    hipLaunchKernelGGL(maxpool_backward_kernel, dim3(gridFor((long long)nN * nC * nH * nW)), dim3(256), 0, stream(),
+    hipLaunchKernelGGL(maxpool_backward_kernel, planeGrid((long long)nN * nC, nH, nW), dim3(64, 4), 0, stream(),
                        pGradOut, pIndices, pGradIn, g);
     OMHIP_CHECK_LAUNCH();
     return 0;
@@ -283,7 +337,7 @@ int omHipAvgPool2d(const float* pIn, float* pOut, int nN, int nC, int nH, int nW
     PoolGeom g;
     if (poolGeom("omHipAvgPool2d", nN, nC, nH, nW, nKH, nKW, nSH, nSW, nPH, nPW, g)) return -1;
     if (!pIn || !pOut) return fail("omHipAvgPool2d: null pointer");
-    hipLaunchKernelGGL(avgpool_kernel, dim3(gridFor((long long)nN * nC * g.Ho * g.Wo)), dim3(256), 0, stream(), pIn,
+    hipLaunchKernelGGL(avgpool_kernel, planeGrid((long long)nN * nC, g.Ho, g.Wo), dim3(64, 4), 0, stream(), pIn,
                        pOut, g);
     OMHIP_CHECK_LAUNCH();
     return 0;
@@ -295,7 +349,7 @@ int omHipAvgPool2dBackward(const float* pGradOut, float* pGradIn, int nN, int nC
     PoolGeom g;
     if (poolGeom("omHipAvgPool2dBackward", nN, nC, nH, nW, nKH, nKW, nSH, nSW, nPH, nPW, g)) return -1;
     if (!pGradOut || !pGradIn) return fail("omHipAvgPool2dBackward: null pointer");
-    hipLaunchKernelGGL(avgpool_backward_kernel, dim3(gridFor((long long)nN * nC * nH * nW)), dim3(256), 0, stream(),
+    hipLaunchKernelGGL(avgpool_backward_kernel, planeGrid((long long)nN * nC, nH, nW), dim3(64, 4), 0, stream(),
                        pGradOut, pGradIn, g);
     OMHIP_CHECK_LAUNCH();
     return 0;

@@ -104,17 +104,46 @@ __device__ __forceinline__ void blockSum(float (&v)[NV], float* red) {
     for (int k = 0; k < NV; ++k) v[k] = red[k * 256];
 }
 
-// MODE 0: sum x.  MODE 1: sum (x - mean)^2.  MODE 2: sum dy*xhat and sum dy,
-// xhat = (x - mean) * invStd. part[(c*P + p)*2 + k].
+// Sum over the P parts of channel c, in part order, of part[..][k] — the
+// reference's sequential sum split into P ordered pieces (one thread).
+__device__ __forceinline__ float partSumSerial(const float* __restrict__ part, int c, int P, int k) {
+    float a = 0.f;
+    for (int p = 0; p < P; ++p) a += part[((long long)c * P + p) * 2 + k];
+    return a;
+}
+
+// The same sum for a channel that is uniform across the wave, every lane
+// active: lane l of each wave loads part l (all loads in flight at once),
+// then every lane adds the lanes' values in part order from registers — the
+// same rounding as the sequential loop without its chain of dependent loads.
+__device__ __forceinline__ float partSum(const float* __restrict__ part, int c, int P, int k) {
+    const int lane = threadIdx.x & 63;
+    float a = 0.f;
+    for (int p0 = 0; p0 < P; p0 += 64) {
+        const int p = p0 + lane;
+        const float v = p < P ? part[((long long)c * P + p) * 2 + k] : 0.f;
+        const int n = min(64, P - p0);
+        for (int j = 0; j < n; ++j)
+            a += __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), j));
+    }
+    return a;
+}
+
+// MODE 0: sum x.  MODE 1: sum (x - mean)^2, mean = (sum of prev's parts) / cnt
+// (bit-identical to the reference's sum / count).  MODE 2: sum dy*xhat and
+// sum dy, xhat = (x - mean) * invStd, dy gated by mask > 0 when mask is given
+// (the reference's reluBackward folded in). part[(c*P + p)*2 + k].
 template <int MODE>
 __global__ __launch_bounds__(256) void chan_partial_kernel(const float* __restrict__ x, const float* __restrict__ dy,
+                                                           const float* __restrict__ mask,
                                                            const float* __restrict__ mean,
-                                                           const float* __restrict__ invStd, float* __restrict__ part,
-                                                           int N, int C, int HW, int P) {
+                                                           const float* __restrict__ invStd,
+                                                           const float* __restrict__ prev, float* __restrict__ part,
+                                                           int N, int C, int HW, int P, float cnt) {
     __shared__ float red[2 * 256];
     const int c = blockIdx.x, p = blockIdx.y;
     const int n0 = (int)((long long)p * N / P), n1 = (int)((long long)(p + 1) * N / P);
-    const float m = MODE ? mean[c] : 0.f;
+    const float m = MODE == 1 ? partSum(prev, c, P, 0) / cnt : (MODE == 2 ? mean[c] : 0.f);
     const float is = MODE == 2 ? invStd[c] : 0.f;
     float v[2] = {0.f, 0.f};
     for (int n = n0; n < n1; ++n) {
@@ -126,7 +155,7 @@ __global__ __launch_bounds__(256) void chan_partial_kernel(const float* __restri
                 const float d = x[base + s] - m;
                 v[0] = __builtin_fmaf(d, d, v[0]);
             } else {
-                const float g = dy[base + s];
+                const float g = (mask && !(mask[base + s] > 0.f)) ? 0.f : dy[base + s];
                 const float xh = (x[base + s] - m) * is;
                 v[0] = __builtin_fmaf(g, xh, v[0]);
                 v[1] += g;
@@ -147,57 +176,69 @@ __global__ void chan_finish_kernel(const float* __restrict__ part, float* out0, 
                                    float divisor, int accumulate) {
     const int c = blockIdx.x * blockDim.x + threadIdx.x;
     if (c >= C) return;
-    float a = 0.f, b = 0.f;
-    for (int p = 0; p < P; ++p) {
-        a += part[((long long)c * P + p) * 2];
-        b += part[((long long)c * P + p) * 2 + 1];
-    }
+    const float a = partSumSerial(part, c, P, 0), b = partSumSerial(part, c, P, 1);
     if (out0) out0[c] = accumulate ? out0[c] + a / divisor : a / divisor;
     if (out1) out1[c] = accumulate ? out1[c] + b / divisor : b / divisor;
 }
 
-// Training statistics (cpu_backend.ixx:796-822): batch mean and biased
-// variance are already in mean / var; saved stats and the running averages.
-__global__ void bn_train_stats_kernel(const float* mean, const float* var, float* savedMean, float* savedInvStd,
-                                      float* runMean, float* runVar, int C, float eps, float momentum) {
-    const int c = blockIdx.x * blockDim.x + threadIdx.x;
-    if (c >= C) return;
-    if (savedMean) savedMean[c] = mean[c];
-    if (savedInvStd) savedInvStd[c] = 1.0f / sqrtf(var[c] + eps);
-    runMean[c] = __builtin_fmaf(1.0f - momentum, runMean[c], momentum * mean[c]);
-    runVar[c] = __builtin_fmaf(1.0f - momentum, runVar[c], momentum * var[c]);
-}
-
-// y = gamma*((x-mean)*invStd)+beta, invStd = 1/sqrt(var+eps) (cpu_backend.ixx:832-840).
-__global__ void bn_apply_kernel(const float* __restrict__ x, float* __restrict__ y, const float* __restrict__ gamma,
-                                const float* __restrict__ beta, const float* __restrict__ mean,
-                                const float* __restrict__ var, int C, int HW, float eps, int plane0) {
+// BatchNorm training forward, second half (cpu_backend.ixx:796-840): batch
+// mean = sum(x)/cnt and biased variance = sum((x-mean)^2)/cnt from the two
+// passes' parts, invStd = 1/sqrt(var+eps), then
+//   y = act(gamma*((x-mean)*invStd) + beta [+ res])
+// (the reference's batchNorm2d, add and relu, each rounded as there). The
+// n = 0 plane of each channel also writes the saved statistics and the
+// running averages fma(1-m, run, m*batch).
+__global__ void bn_train_apply_kernel(const float* __restrict__ x, float* __restrict__ y,
+                                      const float* __restrict__ gamma, const float* __restrict__ beta,
+                                      const float* __restrict__ part0, const float* __restrict__ part1, int P,
+                                      float cnt, float eps, float momentum, const float* __restrict__ res, int act,
+                                      float* savedMean, float* savedInvStd, float* runMean, float* runVar, int C,
+                                      int HW, int plane0) {
+#pragma clang fp contract(off)
     const int plane = plane0 + blockIdx.y;
     const int c = plane % C;
-    const float mu = mean[c];
-    const float inv = 1.0f / sqrtf(var[c] + eps);
+    const float mu = partSum(part0, c, P, 0) / cnt;
+    const float var = partSum(part1, c, P, 0) / cnt;
+    const float inv = 1.0f / sqrtf(var + eps);
+    if (plane < C && blockIdx.x == 0 && threadIdx.x == 0) {
+        if (savedMean) savedMean[c] = mu;
+        if (savedInvStd) savedInvStd[c] = inv;
+        runMean[c] = __builtin_fmaf(1.0f - momentum, runMean[c], momentum * mu);
+        runVar[c] = __builtin_fmaf(1.0f - momentum, runVar[c], momentum * var);
+    }
     const float g = gamma[c], b = beta[c];
     const long long base = (long long)plane * HW;
-    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < HW; i += gridDim.x * blockDim.x)
-        y[base + i] = __builtin_fmaf(g, (x[base + i] - mu) * inv, b);
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < HW; i += gridDim.x * blockDim.x) {
+        float v = __builtin_fmaf(g, (x[base + i] - mu) * inv, b);
+        if (res) v = v + res[base + i];
+        if (act == 1) v = v > 0.f ? v : 0.f;
+        y[base + i] = v;
+    }
 }
 
 // dx = gamma*invStd*(1/cnt) * (cnt*dy - sum(dy) - xhat*sum(dy*xhat)) (cpu_backend.ixx:883-886),
-// with the multiply-adds fused as the reference compiled by clang fuses them.
-__global__ void bn_backward_apply_kernel(const float* __restrict__ dy, const float* __restrict__ x,
-                                         const float* __restrict__ mean, const float* __restrict__ invStd,
-                                         const float* __restrict__ gamma, const float* __restrict__ sumDyXh,
-                                         const float* __restrict__ sumDy, float* __restrict__ dx, int C, int HW,
-                                         float cnt, float invCnt, int plane0) {
+// with the multiply-adds fused as the reference compiled by clang fuses them;
+// dy gated by mask > 0 when mask is given. The sums come from the parts; the
+// n = 0 plane of each channel writes gradGamma = sum(dy*xhat), gradBeta = sum(dy).
+__global__ void bn_backward_apply_kernel(const float* __restrict__ dy, const float* __restrict__ mask,
+                                         const float* __restrict__ x, const float* __restrict__ mean,
+                                         const float* __restrict__ invStd, const float* __restrict__ gamma,
+                                         const float* __restrict__ part, int P, float* gradGamma, float* gradBeta,
+                                         float* __restrict__ dx, int C, int HW, float cnt, float invCnt, int plane0) {
     const int plane = plane0 + blockIdx.y;
     const int c = plane % C;
     const float m = mean[c], is = invStd[c], g = gamma[c];
-    const float sg = sumDyXh[c], sb = sumDy[c];
+    const float sg = partSum(part, c, P, 0), sb = partSum(part, c, P, 1);
+    if (plane < C && blockIdx.x == 0 && threadIdx.x == 0) {
+        if (gradGamma) gradGamma[c] = sg;
+        if (gradBeta) gradBeta[c] = sb;
+    }
     const float k = g * is * invCnt;
     const long long base = (long long)plane * HW;
     for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < HW; i += gridDim.x * blockDim.x) {
+        const float d = (mask && !(mask[base + i] > 0.f)) ? 0.f : dy[base + i];
         const float xh = (x[base + i] - m) * is;
-        dx[base + i] = k * __builtin_fmaf(-xh, sg, __builtin_fmaf(cnt, dy[base + i], -sb));
+        dx[base + i] = k * __builtin_fmaf(-xh, sg, __builtin_fmaf(cnt, d, -sb));
     }
 }
 
@@ -220,8 +261,8 @@ static int channelSums(const float* x, const float* dy, const float* mean, const
     const int P = channelParts(N, C);
     float* part = static_cast<float*>(workspace((size_t)C * P * 2 * sizeof(float)));
     if (!part) return fail("channel reduction: no workspace");
-    hipLaunchKernelGGL(chan_partial_kernel<MODE>, dim3(C, P), dim3(256), 0, stream(), x, dy, mean, invStd, part, N, C,
-                       HW, P);
+    hipLaunchKernelGGL(chan_partial_kernel<MODE>, dim3(C, P), dim3(256), 0, stream(), x, dy, nullptr, mean, invStd,
+                       nullptr, part, N, C, HW, P, 1.0f);
     OMHIP_CHECK_LAUNCH();
     hipLaunchKernelGGL(chan_finish_kernel, dim3((C + 255) / 256), dim3(256), 0, stream(), part, out0, out1, C, P,
                        divisor, accumulate ? 1 : 0);
@@ -229,35 +270,54 @@ static int channelSums(const float* x, const float* dy, const float* mean, const
     return 0;
 }
 
-// Device scratch for a few per-channel vectors, freed by the caller.
-struct ChannelScratch {
-    float* p = nullptr;
-    ~ChannelScratch() {
-        if (p) (void)omHipFree(p);
-    }
-    float* get(int C, int k) {
-        if (!p && omHipMalloc(reinterpret_cast<void**>(&p), (size_t)C * k * sizeof(float)) != 0) return nullptr;
-        return p;
-    }
-};
+int batchNorm2dTrainAct(const float* x, float* y, const float* gamma, const float* beta, float* runMean,
+                        float* runVar, float* savedMean, float* savedInvStd, int N, int C, int H, int W, float eps,
+                        float momentum, const float* res, int act) {
+    const int HW = H * W;
+    const float cnt = (float)((long long)N * HW);
+    const int P = channelParts(N, C);
+    float* part = static_cast<float*>(workspace((size_t)C * P * 4 * sizeof(float)));
+    if (!part) return fail("batchNorm2d: no workspace");
+    float* part0 = part;
+    float* part1 = part + (size_t)C * P * 2;
+    // two passes, as the reference: sum(x), then sum((x-mean)^2) with the first pass's mean
+    hipLaunchKernelGGL(chan_partial_kernel<0>, dim3(C, P), dim3(256), 0, stream(), x, nullptr, nullptr, nullptr,
+                       nullptr, nullptr, part0, N, C, HW, P, cnt);
+    OMHIP_CHECK_LAUNCH();
+    hipLaunchKernelGGL(chan_partial_kernel<1>, dim3(C, P), dim3(256), 0, stream(), x, nullptr, nullptr, nullptr,
+                       nullptr, part0, part1, N, C, HW, P, cnt);
+    OMHIP_CHECK_LAUNCH();
+    return forPlanes(N * C, HW, [&](dim3 g, int p0) {
+        hipLaunchKernelGGL(bn_train_apply_kernel, g, dim3(256), 0, stream(), x, y, gamma, beta, part0, part1, P, cnt,
+                           eps, momentum, res, act, savedMean, savedInvStd, runMean, runVar, C, HW, p0);
+    });
+}
 
 int batchNorm2dTrain(const float* x, float* y, const float* gamma, const float* beta, float* runMean, float* runVar,
                      float* savedMean, float* savedInvStd, int N, int C, int H, int W, float eps, float momentum) {
+    return batchNorm2dTrainAct(x, y, gamma, beta, runMean, runVar, savedMean, savedInvStd, N, C, H, W, eps, momentum,
+                               nullptr, 0);
+}
+
+// BatchNorm2d backward with an optional ReLU mask on the incoming gradient.
+static int batchNorm2dBackwardMasked(const char* name, const float* gO, const float* mask, const float* x,
+                                     const float* mean, const float* invStd, const float* gamma, float* gI,
+                                     float* gGamma, float* gBeta, int N, int C, int H, int W) {
+    if (N <= 0 || C <= 0 || H <= 0 || W <= 0) return 0;
+    if (!gO || !x || !mean || !invStd || !gamma || !gI) return fail("%s: null pointer", name);
     const int HW = H * W;
-    const float cnt = (float)((long long)N * HW);
-    ChannelScratch scratch;
-    float* st = scratch.get(C, 2);
-    if (!st) return -1;
-    float* mean = st;
-    float* var = st + C;
-    // two passes, as the reference: mean = sum(x)/cnt, var = sum((x-mean)^2)/cnt
-    if (channelSums<0>(x, nullptr, nullptr, nullptr, mean, nullptr, N, C, HW, cnt, false)) return -1;
-    if (channelSums<1>(x, nullptr, mean, nullptr, var, nullptr, N, C, HW, cnt, false)) return -1;
-    hipLaunchKernelGGL(bn_train_stats_kernel, dim3((C + 255) / 256), dim3(256), 0, stream(), mean, var, savedMean,
-                       savedInvStd, runMean, runVar, C, eps, momentum);
+    const int P = channelParts(N, C);
+    float* part = static_cast<float*>(workspace((size_t)C * P * 2 * sizeof(float)));
+    if (!part) return fail("%s: no workspace", name);
+    hipLaunchKernelGGL(chan_partial_kernel<2>, dim3(C, P), dim3(256), 0, stream(), x, gO, mask, mean, invStd, nullptr,
+                       part, N, C, HW, P, 1.0f);
     OMHIP_CHECK_LAUNCH();
+    const long long cntL = (long long)N * HW;
+    const float fcnt = (float)cntL;
+    const float invCnt = 1.0f / fcnt;
     return forPlanes(N * C, HW, [&](dim3 g, int p0) {
-        hipLaunchKernelGGL(bn_apply_kernel, g, dim3(256), 0, stream(), x, y, gamma, beta, mean, var, C, HW, eps, p0);
+        hipLaunchKernelGGL(bn_backward_apply_kernel, g, dim3(256), 0, stream(), gO, mask, x, mean, invStd, gamma, part,
+                           P, gGamma, gBeta, gI, C, HW, fcnt, invCnt, p0);
     });
 }
 
@@ -340,28 +400,32 @@ int omHipBatchNorm2dBackward(const float* pGradOutput, const float* pInput, cons
                              int nChannels, int nH, int nW, float fEps) {
     clearError();
     (void)fEps;   // the saved inverse standard deviation already carries eps
+    return batchNorm2dBackwardMasked("omHipBatchNorm2dBackward", pGradOutput, nullptr, pInput, pMean, pInvStd, pGamma,
+                                     pGradInput, pGradGamma, pGradBeta, nBatch, nChannels, nH, nW);
+}
+
+int omHipBatchNorm2dBackwardRelu(const float* pGradOutput, const float* pReluInput, const float* pInput,
+                                 const float* pMean, const float* pInvStd, const float* pGamma, float* pGradInput,
+                                 float* pGradGamma, float* pGradBeta, int nBatch, int nChannels, int nH, int nW,
+                                 float fEps) {
+    clearError();
+    (void)fEps;
+    if (!pReluInput) return fail("omHipBatchNorm2dBackwardRelu: null ReLU input");
+    return batchNorm2dBackwardMasked("omHipBatchNorm2dBackwardRelu", pGradOutput, pReluInput, pInput, pMean, pInvStd,
+                                     pGamma, pGradInput, pGradGamma, pGradBeta, nBatch, nChannels, nH, nW);
+}
+
+int omHipBatchNorm2dTrainAct(const float* pInput, float* pOutput, const float* pGamma, const float* pBeta,
+                             float* pRunningMean, float* pRunningVar, float* pSavedMean, float* pSavedInvStd,
+                             int nBatch, int nChannels, int nH, int nW, float fEps, float fMomentum,
+                             const float* pResidual, int nAct) {
+    clearError();
     if (nBatch <= 0 || nChannels <= 0 || nH <= 0 || nW <= 0) return 0;
-    if (!pGradOutput || !pInput || !pMean || !pInvStd || !pGamma || !pGradInput)
-        return fail("omHipBatchNorm2dBackward: null pointer");
-    const int C = nChannels, HW = nH * nW;
-    ChannelScratch scratch;
-    float* st = nullptr;
-    float* sg = pGradGamma;
-    float* sb = pGradBeta;
-    if (!sg || !sb) {
-        st = scratch.get(C, 2);
-        if (!st) return -1;
-        if (!sg) sg = st;
-        if (!sb) sb = st + C;
-    }
-    if (channelSums<2>(pInput, pGradOutput, pMean, pInvStd, sg, sb, nBatch, C, HW, 1.0f, false)) return -1;
-    const long long cnt = (long long)nBatch * HW;
-    const float fcnt = (float)cnt;
-    const float invCnt = 1.0f / fcnt;
-    return forPlanes(nBatch * C, HW, [&](dim3 g, int p0) {
-        hipLaunchKernelGGL(bn_backward_apply_kernel, g, dim3(256), 0, stream(), pGradOutput, pInput, pMean, pInvStd,
-                           pGamma, sg, sb, pGradInput, C, HW, fcnt, invCnt, p0);
-    });
+    if (!pInput || !pOutput || !pGamma || !pBeta || !pRunningMean || !pRunningVar)
+        return fail("omHipBatchNorm2dTrainAct: null pointer");
+    if (nAct != 0 && nAct != 1) return fail("omHipBatchNorm2dTrainAct: unknown activation %d", nAct);
+    return batchNorm2dTrainAct(pInput, pOutput, pGamma, pBeta, pRunningMean, pRunningVar, pSavedMean, pSavedInvStd,
+                               nBatch, nChannels, nH, nW, fEps, fMomentum, pResidual, nAct);
 }
 
 }  // extern "C"

@@ -97,9 +97,10 @@ def forward_flops(batch: int) -> float:
 
 
 class GpuResNet18:
-    def __init__(self, om, P: dict, batch: int, train: bool = False):
+    def __init__(self, om, P: dict, batch: int, train: bool = False, fused: bool = True):
         self.om, self.H, self.B = om, om.HIPBackend, batch
         self.train = train
+        self.fused = fused   # training step on the fused BN / ReLU / add entries
         self.d = {k: om.DeviceBuffer.from_numpy(np.ascontiguousarray(v)) for k, v in P.items()}
         self.nc = P["fc.w"].shape[1]
         self.buf = {}
@@ -147,16 +148,21 @@ class GpuResNet18:
         return logits
 
     # ---------------------------------------------------------------- training
-    def _conv_bn_train(self, x, name, cin, h, cout, k, s, p, key):
-        """z = conv(x); y = BN_train(z) (saved stats); returns (y, o)."""
+    def _conv_bn_train(self, x, name, cin, h, cout, k, s, p, key, out_key=None, act=0, res=None):
+        """z = conv(x); y = BN_train(z) (saved stats); returns (y, o). With out_key the
+        BN pass also adds res and applies the activation (the fused entry)."""
         H, d, B = self.H, self.d, self.B
         o = (h + 2 * p - k) // s + 1
         z = self._b(key + ".z", (B, cout, o, o))
         H.conv2d(x, d[name + ".w"], None, z, B, cin, h, h, cout, k, k, s, p)
-        y = self._b(key + ".y", (B, cout, o, o))
+        y = self._b(out_key or key + ".y", (B, cout, o, o))
         sm, si = self._b(key + ".sm", (cout,)), self._b(key + ".si", (cout,))
-        H.batchNorm2d(z, y, d[name + ".gamma"], d[name + ".beta"], d[name + ".mean"], d[name + ".var"], sm, si,
-                      B, cout, o, o, EPS, MOMENTUM, True)
+        if out_key is None:
+            H.batchNorm2d(z, y, d[name + ".gamma"], d[name + ".beta"], d[name + ".mean"], d[name + ".var"], sm, si,
+                          B, cout, o, o, EPS, MOMENTUM, True)
+        else:
+            H.batchNorm2dTrainAct(z, y, d[name + ".gamma"], d[name + ".beta"], d[name + ".mean"], d[name + ".var"],
+                                  sm, si, B, cout, o, o, EPS, MOMENTUM, res, act)
         return y, o
 
     def _relu(self, x, key, n):
@@ -165,6 +171,8 @@ class GpuResNet18:
         return a
 
     def forward_train(self, img):
+        if self.fused:
+            return self._forward_train_fused(img)
         H, B = self.H, self.B
         self.img = img
         y0, _ = self._conv_bn_train(img, "stem", 3, 224, 64, 7, 2, 3, "stem")
@@ -187,14 +195,42 @@ class GpuResNet18:
         self.last = x
         return self._head(x, c)
 
-    def _bn_conv_backward(self, g_y, name, x_in, cin, h, cout, k, s, p, key, need_dx=True):
-        """Backward through y = BN(conv(x_in)): returns dx (or None); weight / BN grads stored."""
+    def _forward_train_fused(self, img):
+        """The training forward on the fused entries: BN statistics, residual add and
+        ReLU in one pass per conv; the pre-activation tensors are never written."""
+        H, B = self.H, self.B
+        self.img = img
+        a0, _ = self._conv_bn_train(img, "stem", 3, 224, 64, 7, 2, 3, "stem", out_key="stem.a", act=1)
+        x = self._b("pool", (B, 64, 56, 56))
+        idx = self._b("pool.idx", (B, 64, 56, 56), np.int32)
+        H.maxPool2d(a0, x, idx, B, 64, 112, 112, 3, 3, 2, 1)
+        self.block_in = []
+        c = 64
+        for pre, ci, co, s, ds, hw in blocks():
+            self.block_in.append(x)
+            a1, o = self._conv_bn_train(x, pre + ".conv1", ci, hw, co, 3, s, 1, pre + ".c1", out_key=pre + ".a1",
+                                        act=1)
+            sc = self._conv_bn_train(x, pre + ".ds", ci, hw, co, 1, s, 0, pre + ".ds")[0] if ds else x
+            x, _ = self._conv_bn_train(a1, pre + ".conv2", co, o, co, 3, 1, 1, pre + ".c2", out_key=pre + ".out",
+                                       act=1, res=sc)
+            c = co
+        self.last = x
+        return self._head(x, c)
+
+    def _bn_conv_backward(self, g_y, name, x_in, cin, h, cout, k, s, p, key, need_dx=True, mask=None):
+        """Backward through y = BN(conv(x_in)): returns dx (or None); weight / BN grads stored.
+        With mask the incoming gradient is first gated by mask > 0 (a ReLU's backward)."""
         H, d, B = self.H, self.d, self.B
         o = (h + 2 * p - k) // s + 1
         g_z = self._b(key + ".gz", (B, cout, o, o))
-        H.batchNorm2dBackward(g_y, self.buf[key + ".z"], self.buf[key + ".sm"], self.buf[key + ".si"],
-                              d[name + ".gamma"], g_z, self._b(key + ".ggamma", (cout,)),
-                              self._b(key + ".gbeta", (cout,)), B, cout, o, o)
+        if mask is None:
+            H.batchNorm2dBackward(g_y, self.buf[key + ".z"], self.buf[key + ".sm"], self.buf[key + ".si"],
+                                  d[name + ".gamma"], g_z, self._b(key + ".ggamma", (cout,)),
+                                  self._b(key + ".gbeta", (cout,)), B, cout, o, o)
+        else:
+            H.batchNorm2dBackwardRelu(g_y, mask, self.buf[key + ".z"], self.buf[key + ".sm"], self.buf[key + ".si"],
+                                      d[name + ".gamma"], g_z, self._b(key + ".ggamma", (cout,)),
+                                      self._b(key + ".gbeta", (cout,)), B, cout, o, o)
         H.conv2dBackwardWeight(x_in, g_z, self._b(key + ".gw", (cout, cin, k, k)), None, B, cin, h, h, cout, k, k,
                                s, p)
         if not need_dx:
@@ -215,6 +251,8 @@ class GpuResNet18:
         H.matmulTransB(g_logits, d["fc.w"], g_p, B, nc, 512)
         g = self._b("g.last", (B, 512, 7, 7))
         H.adaptiveAvgPool2dBackward(g_p, g, B, 512, 7, 7, 1, 1)
+        if self.fused:
+            return self._backward_blocks_fused(g)
         bl = blocks()
         for bi in range(len(bl) - 1, -1, -1):
             pre, ci, co, s, ds, hw = bl[bi]
@@ -240,25 +278,55 @@ class GpuResNet18:
         H.reluBackward(self.buf["stem.y"], g_a0, g_y0, B * 64 * 112 * 112)
         self._bn_conv_backward(g_y0, "stem", self.img, 3, 224, 64, 7, 2, 3, "stem", need_dx=False)
 
+    def _backward_blocks_fused(self, g):
+        """Block backward on the fused entries. A ReLU's backward gates by its input > 0,
+        which is its output > 0: the saved post-activation tensors serve as the masks."""
+        H, B = self.H, self.B
+        bl = blocks()
+        for bi in range(len(bl) - 1, -1, -1):
+            pre, ci, co, s, ds, hw = bl[bi]
+            out = self.buf[pre + ".out"]
+            g_a1 = self._bn_conv_backward(g, pre + ".conv2", self.buf[pre + ".a1"], co, (hw + 2 - 3) // s + 1, co,
+                                          3, 1, 1, pre + ".c2", mask=out)
+            x_in = self.block_in[bi]
+            g_x = self._bn_conv_backward(g_a1, pre + ".conv1", x_in, ci, hw, co, 3, s, 1, pre + ".c1",
+                                         mask=self.buf[pre + ".a1"])
+            g_in = self._b(pre + ".gin", (B, ci, hw, hw))
+            if ds:
+                g_xd = self._bn_conv_backward(g, pre + ".ds", x_in, ci, hw, co, 1, s, 0, pre + ".ds", mask=out)
+                H.add(g_x, g_xd, g_in, B * ci * hw * hw)
+            else:
+                H.addReluBackward(g_x, out, g, g_in, B * ci * hw * hw)
+            g = g_in
+        g_a0 = self._b("g.a0", (B, 64, 112, 112))
+        H.maxPool2dBackwardEx(g, self.buf["pool.idx"], g_a0, B, 64, 112, 112, 3, 3, 2, 1)
+        self._bn_conv_backward(g_a0, "stem", self.img, 3, 224, 64, 7, 2, 3, "stem", need_dx=False,
+                               mask=self.buf["stem.a"])
+
     def forward_state(self, img: np.ndarray) -> dict:
         """Host copies of the training forward's intermediates (keys as cpu_forward_train)."""
         B = self.B
         f = {"img": img, "pool": self.buf["pool"].numpy(), "pool.idx": self.buf["pool.idx"].numpy(),
              "pooled": self.buf["pooled"].numpy()}
-        def conv_keys(key, shape):
+        fused = self.fused
+
+        def conv_keys(key, shape, with_y):
             f[key + ".z"] = self.buf[key + ".z"].numpy().reshape(shape)
-            f[key + ".y"] = self.buf[key + ".y"].numpy().reshape(shape)
+            if with_y:
+                f[key + ".y"] = self.buf[key + ".y"].numpy().reshape(shape)
             f[key + ".sm"] = self.buf[key + ".sm"].numpy()
             f[key + ".si"] = self.buf[key + ".si"].numpy()
-        conv_keys("stem", (B, 64, 112, 112))
+        conv_keys("stem", (B, 64, 112, 112), not fused)
+        if fused:
+            f["stem.a"] = self.buf["stem.a"].numpy().reshape(B, 64, 112, 112)
         for pre, ci, co, s, ds, hw in blocks():
             o = (hw + 2 - 3) // s + 1
             shp = (B, co, o, o)
-            conv_keys(pre + ".c1", shp)
-            conv_keys(pre + ".c2", shp)
+            conv_keys(pre + ".c1", shp, not fused)
+            conv_keys(pre + ".c2", shp, not fused)
             if ds:
-                conv_keys(pre + ".ds", shp)
-            for k in (".a1", ".sum", ".out"):
+                conv_keys(pre + ".ds", shp, True)
+            for k in (".a1", ".out") if fused else (".a1", ".sum", ".out"):
                 f[pre + k] = self.buf[pre + k].numpy().reshape(shp)
         return f
 
@@ -308,7 +376,7 @@ def cpu_forward_train(P: dict, img: np.ndarray, backend: str = "oracle") -> dict
         return y
 
     y0 = conv_bn(img, "stem", 2, 3, "stem")
-    a0 = O.relu(y0, backend=backend)
+    f["stem.a"] = a0 = O.relu(y0, backend=backend)
     x, f["pool.idx"] = O.maxpool2d(a0, 3, 2, 1, backend=backend)
     f["pool"] = x
     for pre, ci, co, s, ds, hw in blocks():
@@ -352,16 +420,20 @@ def cpu_backward(P: dict, f: dict, g_logits: np.ndarray, backend: str = "oracle"
             return O.conv2d_backward_input(g_z, w, x_in.shape[2], x_in.shape[3], s, p, backend=backend)
         return None
 
+    def relu_in(pre_key, post_key):
+        # reluBackward gates by input > 0, i.e. output > 0: either tensor serves
+        return f[pre_key] if pre_key in f else f[post_key]
+
     bl = blocks()
     for bi in range(len(bl) - 1, -1, -1):
         pre, ci, co, s, ds, hw = bl[bi]
-        g_s = O.relu_backward(f[pre + ".sum"], g, backend=backend)
+        g_s = O.relu_backward(relu_in(pre + ".sum", pre + ".out"), g, backend=backend)
         g_a1 = bn_conv_bwd(g_s, pre + ".conv2", pre + ".c2", f[pre + ".a1"], 1, 1)
-        g_y1 = O.relu_backward(f[pre + ".c1.y"], g_a1, backend=backend)
+        g_y1 = O.relu_backward(relu_in(pre + ".c1.y", pre + ".a1"), g_a1, backend=backend)
         g_x = bn_conv_bwd(g_y1, pre + ".conv1", pre + ".c1", ins[bi], s, 1)
         g = O.add(g_x, bn_conv_bwd(g_s, pre + ".ds", pre + ".ds", ins[bi], s, 0) if ds else g_s, backend=backend)
     g_a0 = O.maxpool2d_backward(g, f["pool.idx"], 112, 112, backend=backend)
-    g_y0 = O.relu_backward(f["stem.y"], g_a0, backend=backend)
+    g_y0 = O.relu_backward(relu_in("stem.y", "stem.a"), g_a0, backend=backend)
     bn_conv_bwd(g_y0, "stem", "stem", f["img"], 2, 3, need_dx=False)
     return grads
 

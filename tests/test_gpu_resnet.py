@@ -43,20 +43,22 @@ def test_resnet18_inference(hip, params):
     assert np.array_equal(np.argsort(logits, axis=1)[:, -5:], np.argsort(ref, axis=1)[:, -5:])
 
 
-def test_resnet18_train_step(hip, params):
+@pytest.mark.parametrize("fused", [True, False], ids=["fused", "reference_ops"])
+def test_resnet18_train_step(hip, params, fused):
     img = O.randn((2, 3, 224, 224), 42)
     g_logits = O.randn((2, 1000), 43, 0.01)
-    net = GpuResNet18(hip, params, 2, train=True)
+    net = GpuResNet18(hip, params, 2, train=True, fused=fused)
     net.forward_train(to_dev(hip, img))
     net.backward(to_dev(hip, g_logits))
     got = net.grads()
     fwd_gpu = net.forward_state(img)
     fwd_cpu = cpu_forward_train(params, img)
     worst_f = 0.0
-    for k, v in fwd_cpu.items():
+    for k, g in fwd_gpu.items():
         if k in ("img", "pool.idx"):
             continue
-        e = O.frobenius_rel(fwd_gpu[k].reshape(v.shape), v)
+        v = fwd_cpu[k]
+        e = O.frobenius_rel(g.reshape(v.shape), v)
         worst_f = max(worst_f, e)
         assert e <= 1e-4, k
     ref = cpu_backward(params, fwd_gpu, g_logits)

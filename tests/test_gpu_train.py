@@ -233,3 +233,87 @@ def test_batchnorm_backward(hip, shape):
     assert O.normalized_error(gi, ri, bound) <= TOL
     assert O.normalized_error(gg, rg, absGX) <= TOL
     assert O.normalized_error(gb, rb, absG) <= TOL
+
+
+# Fused training passes: each must equal the separate reference ops bit for bit.
+FUSE_SHAPES = [(4, 8, 7, 9), (8, 64, 28, 28), (2, 300, 5, 5)]
+
+
+@pytest.mark.parametrize("shape", FUSE_SHAPES, ids=lambda s: "N{}C{}H{}W{}".format(*s))
+@pytest.mark.parametrize("res,act", [(False, 0), (False, 1), (True, 1)], ids=["bn", "bn_relu", "bn_add_relu"])
+def test_batchnorm_train_act(hip, shape, res, act):
+    N, C, H, W = shape
+    x = O.randn(shape, 101 + C) * 1.5 + 0.25
+    r = O.randn(shape, 102 + C) if res else None
+    gamma, beta = O.uniform((C,), 103, 0.5, 1.5), O.randn((C,), 104, 0.1)
+    rm0, rv0 = O.randn((C,), 105, 0.1), O.uniform((C,), 106, 0.5, 1.5)
+    dx, dr = to_dev(hip, x), (to_dev(hip, r) if res else None)
+    dgam, dbet = to_dev(hip, gamma), to_dev(hip, beta)
+    # fused
+    dy, drm, drv, dsm, dsi = empty_dev(hip, shape), to_dev(hip, rm0), to_dev(hip, rv0), empty_dev(hip, (C,)), \
+        empty_dev(hip, (C,))
+    hip.HIPBackend.batchNorm2dTrainAct(dx, dy, dgam, dbet, drm, drv, dsm, dsi, N, C, H, W, 1e-5, 0.1, dr, act)
+    # separate reference ops
+    ey, erm, erv, esm, esi = empty_dev(hip, shape), to_dev(hip, rm0), to_dev(hip, rv0), empty_dev(hip, (C,)), \
+        empty_dev(hip, (C,))
+    hip.HIPBackend.batchNorm2d(dx, ey, dgam, dbet, erm, erv, esm, esi, N, C, H, W, 1e-5, 0.1, True)
+    n = N * C * H * W
+    if res:
+        hip.HIPBackend.add(ey, dr, ey, n)
+    if act:
+        hip.HIPBackend.relu(ey, ey, n)
+    for a, b in ((dy, ey), (drm, erm), (drv, erv), (dsm, esm), (dsi, esi)):
+        assert np.array_equal(a.numpy().view(np.uint32), b.numpy().view(np.uint32))
+    # and against the oracle chain (sums in the reference's order: within the BN bar)
+    ry, _, _, _, _ = O.batchnorm2d_train(x, gamma, beta, rm0, rv0)
+    if res:
+        ry = O.add(ry, r)
+    if act:
+        ry = O.relu(ry)
+    y64, mean64, var64, inv64 = O.bn_train_f64(x, gamma, beta)
+    absmean = np.abs(np.asarray(x, np.float64)).mean(axis=(0, 2, 3))
+    bound = (np.abs(gamma)[None, :, None, None] * inv64[None, :, None, None] *
+             (np.abs(np.asarray(x, np.float64)) + np.abs(mean64)[None, :, None, None] + absmean[None, :, None, None])
+             + np.abs(beta)[None, :, None, None] + (np.abs(r) if res else 0.0))
+    assert O.normalized_error(dy.numpy(), ry, bound) <= TOL
+
+
+@pytest.mark.parametrize("shape", FUSE_SHAPES, ids=lambda s: "N{}C{}H{}W{}".format(*s))
+def test_batchnorm_backward_relu(hip, shape):
+    N, C, H, W = shape
+    x = O.randn(shape, 111 + C)
+    gy = O.randn(shape, 112 + C)
+    m = O.randn(shape, 113 + C)
+    m.reshape(-1)[:4] = [np.nan, 0.0, -0.0, 1e-45]      # gate edge cases: only > 0 passes
+    gamma = O.uniform((C,), 114, 0.5, 1.5)
+    _, _, _, sm, si = O.batchnorm2d_train(x, gamma, np.zeros(C, np.float32), np.zeros(C, np.float32),
+                                          np.ones(C, np.float32))
+    dgy, dm, dx = to_dev(hip, gy), to_dev(hip, m), to_dev(hip, x)
+    dsm, dsi, dgam = to_dev(hip, sm), to_dev(hip, si), to_dev(hip, gamma)
+    fi, fg, fb = empty_dev(hip, shape), empty_dev(hip, (C,)), empty_dev(hip, (C,))
+    hip.HIPBackend.batchNorm2dBackwardRelu(dgy, dm, dx, dsm, dsi, dgam, fi, fg, fb, N, C, H, W)
+    t = empty_dev(hip, shape)
+    hip.HIPBackend.reluBackward(dm, dgy, t, N * C * H * W)
+    si_, sg_, sb_ = empty_dev(hip, shape), empty_dev(hip, (C,)), empty_dev(hip, (C,))
+    hip.HIPBackend.batchNorm2dBackward(t, dx, dsm, dsi, dgam, si_, sg_, sb_, N, C, H, W)
+    for a, b in ((fi, si_), (fg, sg_), (fb, sb_)):
+        assert np.array_equal(a.numpy().view(np.uint32), b.numpy().view(np.uint32))
+    gated = O.relu_backward(m, gy)
+    dX, dG, dB, bound, absGX, absG = O.bn_backward_f64(gated, x, sm, si, gamma)
+    assert O.normalized_error(fi.numpy(), dX, bound) <= TOL
+    assert O.normalized_error(fg.numpy(), dG, absGX) <= TOL
+    assert O.normalized_error(fb.numpy(), dB, absG) <= TOL
+    # gradient outputs optional
+    hip.HIPBackend.batchNorm2dBackwardRelu(dgy, dm, dx, dsm, dsi, dgam, fi, None, None, N, C, H, W)
+    assert np.array_equal(fi.numpy().view(np.uint32), si_.numpy().view(np.uint32))
+
+
+@pytest.mark.parametrize("n", [1, 7, 4096, 1000003])
+def test_add_relu_backward(hip, n):
+    a, x, g = O.randn((n,), n), O.randn((n,), n + 1), O.randn((n,), n + 2)
+    if n >= 4:
+        x[:4] = [np.nan, 0.0, -0.0, 1e-45]
+    do = empty_dev(hip, (n,))
+    hip.HIPBackend.addReluBackward(to_dev(hip, a), to_dev(hip, x), to_dev(hip, g), do, n)
+    ref = O.add(a, O.relu_backward(x, g))
+    assert np.array_equal(do.numpy().view(np.uint32), ref.view(np.uint32))
