@@ -228,6 +228,53 @@ def bench_resnet18_net(om, steps: int, warmup: int, batch: int = 32):
     return fwd_ms, fl, err, train_ms, train_fl
 
 
+def bench_infer_pipeline(om, n_img: int = 512, batch: int = 32, reps: int = 3):
+    """EngineBridge::inferBatch on this backend: n_img host images (pageable, float32 in
+    [0, 1]) -> ImageNet normalisation, ResNet-18 forward, softmax / argmax per image, in
+    batches of 32 with the upload of each batch overlapping the previous batch's compute.
+    Also the device-resident forward alone, eager and replayed from a captured graph."""
+    from omnimatchdeeplearningtool_amd.hiptime import StreamTimer
+    from resnet_net import make_params, pack_params
+    import oracle as O
+    P = make_params(seed=1)
+    net = om.ResNet18Infer(pack_params(P), 1000, batch)
+    imgs = O.uniform((n_img, 3, 224, 224), 905, 0.0, 1.0)
+    net.infer_batch(imgs[:2 * batch], batch)        # warm-up: tables, workspaces, staging
+    wall = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        cls, conf, _ = net.infer_batch(imgs, batch, with_probs=False)
+        wall.append(time.perf_counter() - t0)
+    pipe_s = float(np.median(wall))
+    # device-resident forward of one batch: eager, then a captured graph
+    d_in = om.DeviceBuffer.from_numpy(O.randn((batch, 3, 224, 224), 906))
+    d_log = om.DeviceBuffer.empty((batch, 1000))
+    timer = StreamTimer(om.stream_handle())
+    steps = 20
+    net.forward(d_in, d_log, batch)
+    om.synchronize()
+    timer.start()
+    for _ in range(steps):
+        net.forward(d_in, d_log, batch)
+    timer.stop()
+    eager_ms = timer.ms() / steps
+    graph = om.Graph(lambda: net.forward(d_in, d_log, batch))
+    graph.launch()
+    om.synchronize()
+    timer.start()
+    for _ in range(steps):
+        graph.launch()
+    timer.stop()
+    graph_ms = timer.ms() / steps
+    return {"images": n_img, "batch": batch, "img_s": round(n_img / pipe_s, 1),
+            "ms_per_batch": round(pipe_s / (n_img / batch) * 1e3, 4),
+            "scope": "host float32 images (pageable) -> page-locked staging -> transfer stream -> ImageNet "
+                     "normalisation -> ResNet-18 forward -> logits to the host -> softmax / argmax per image",
+            "resident_forward": {"ms": round(eager_ms, 4), "img_s": round(batch / eager_ms * 1e3, 1)},
+            "resident_forward_graph": {"ms": round(graph_ms, 4), "img_s": round(batch / graph_ms * 1e3, 1)},
+            "host_link_bytes_per_batch": batch * 3 * 224 * 224 * 4}
+
+
 def cpu_baseline_resnet18_net(n_img: int = 2, reps: int = 3):
     from resnet_net import cpu_forward, cpu_train_step, make_params
     import oracle as O
@@ -636,6 +683,11 @@ def main():
     log(f"resnet18 net forward {n_fwd_ms:.3f} ms  {32 / n_fwd_ms * 1e3:.0f} img/s  logits err {n_err:.1e}; "
         f"train step {n_train_ms:.3f} ms  {32 / n_train_ms * 1e3:.0f} img/s")
 
+    log("resnet18 inferBatch pipeline (host images -> classes)")
+    infer = bench_infer_pipeline(om)
+    log(f"inferBatch {infer['img_s']:.0f} img/s end to end; resident forward {infer['resident_forward']['ms']:.3f} ms, "
+        f"graph replay {infer['resident_forward_graph']['ms']:.3f} ms")
+
     log("resnet50 conv stack b64")
     r50_ms, r50_flops, r50_roof = bench_resnet50(om, max(3, args.steps // 10), 1)
     log(f"resnet50 {r50_ms:.3f} ms/batch  {64 / r50_ms * 1e3:.0f} img/s  roof frac {r50_roof / r50_ms:.3f}")
@@ -725,6 +777,7 @@ def main():
                                             "scope": "forward with batch statistics + backward to every weight; "
                                                      "no optimizer update"},
                              "cpu_baseline": cpu_extra.get("resnet18_net")},
+        "resnet18_infer_pipeline": infer,
         "resnet50_conv": {"value": round(64 / r50_ms * 1e3, 1), "unit": "img/s", "batch": 64, "ms_per_batch": round(r50_ms, 4),
                           "tflops": round(r50_flops / r50_ms / 1e9, 2),
                           "roofline": {"roof_ms": round(r50_roof, 4), "frac": round(r50_roof / r50_ms, 4)},

@@ -65,12 +65,47 @@ int omHipCopyH2D(void* pDst, const void* pSrc, size_t nBytes);
 int omHipCopyD2H(void* pDst, const void* pSrc, size_t nBytes);
 /* replaces omCudaCopyD2D (cuda_kernels.cuh:51): stream-ordered */
 int omHipCopyD2D(void* pDst, const void* pSrc, size_t nBytes);
-/* replaces omCudaMemset (cuda_kernels.cuh:54): stream-ordered */
+/* replaces omCudaMemset (cuda_kernels.cuh:54): stream-ordered (a fill kernel, so it may
+ * sit inside a captured graph) */
 int omHipMemset(void* pDev, int nValue, size_t nBytes);
 /* NEW: pool statistics: bytes held by the pool, bytes currently handed out */
 int omHipPoolStats(size_t* pHeldBytes, size_t* pUsedBytes);
 /* NEW: release every cached (free) block back to the driver */
 int omHipPoolTrim(void);
+
+/* ===== transfer stream and pinned host memory (cuda_kernels.cuh:56-66, :497-505) ===== */
+
+/* replaces omCudaMallocHost (cuh:501): page-locked host memory (hipHostMalloc), so the
+ * asynchronous copies below are true DMA transfers */
+int omHipMallocHost(void** ppPtr, size_t nBytes);
+/* replaces omCudaFreeHost (cuh:504) */
+int omHipFreeHost(void* pPtr);
+/* replaces omCudaAsyncCopyH2D (cuh:57): enqueued on the library transfer stream (a second
+ * stream, default priority), returns at once; the host buffer must stay valid until the
+ * transfer stream is synchronised */
+int omHipAsyncCopyH2D(void* pDst, const void* pSrc, size_t nBytes);
+/* replaces omCudaAsyncCopyD2H (cuh:60): as above, device to host */
+int omHipAsyncCopyD2H(void* pDst, const void* pSrc, size_t nBytes);
+/* replaces omCudaSyncTransferStream (cuh:63) */
+int omHipSyncTransferStream(void);
+/* NEW: work enqueued on the compute stream after this call waits for every transfer
+ * enqueued before it (an event, no host wait) */
+int omHipComputeWaitTransfer(void);
+/* NEW: transfers enqueued after this call wait for the compute work enqueued before it */
+int omHipTransferWaitCompute(void);
+
+/* ===== graphs (cuda_kernels.cuh:507-532: omCudaGraph*) ===== */
+
+/* replaces omCudaGraphBeginCapture (cuh:513): records the library calls that follow on the
+ * compute stream instead of running them. Capture a sequence after running it once
+ * eagerly, so that its workspaces, tables and pool blocks already exist. */
+int omHipGraphBeginCapture(void);
+/* replaces omCudaGraphEndCapture (cuh:519): ends the recording, returns an executable graph */
+int omHipGraphEndCapture(void** ppGraphExec);
+/* replaces omCudaGraphLaunch (cuh:524): replays the graph on the compute stream */
+int omHipGraphLaunch(void* pGraphExec);
+/* replaces omCudaGraphDestroy (cuh:528) */
+int omHipGraphDestroy(void* pGraphExec);
 
 /* ===== fills / copy (src/cuda/cuda_kernels.cuh:257-266; CPUBackend cpu_backend.ixx:65-77, :444-446) ===== */
 
@@ -280,6 +315,31 @@ int omHipGemmStridedBatchedHalf(int nDtype, int bTransA, int bTransB, int nBatch
  * nSeq <= 384. P is rounded to nDtype before P x V (fp32 accumulate). */
 int omHipAttentionHalf(int nDtype, const uint16_t* pQKV, void* pOut, int nOutHalf,
                        int nBatch, int nSeq, int nHeads, int nHeadDim, float fScale);
+
+/* ===== device-resident inference (EngineBridge::inferBatch, EngineBridge.cpp:3525-3772) ===== */
+
+/* NEW: a ResNet-18 classifier (torchvision layout, 3x224x224 input) resident on the device,
+ * every conv with its BatchNorm (running statistics) and ReLU fused, the shortcut fused into
+ * the second conv of each block. pParams (host) holds nParamFloats floats: for each conv in
+ * network order — stem 7x7/2, then per BasicBlock conv1, conv2 and (first block of stages
+ * 2-4) the 1x1/2 downsample — weight [Cout][Cin][K][K], BN gamma, beta, running mean,
+ * running var [Cout]; then the FC weight [512][nClasses] and bias [nClasses]. Buffers are
+ * sized for nMaxBatch images (at most 32, the reference's batch limit). */
+int omHipResNet18Create(const float* pParams, long long nParamFloats, int nClasses, int nMaxBatch, void** ppNet);
+/* NEW: waits for the net's work and frees it */
+int omHipResNet18Destroy(void* pNet);
+/* NEW: logits [nBatch, nClasses] (device) of nBatch normalised images (device) */
+int omHipResNet18Forward(void* pNet, const float* pInput, float* pLogits, int nBatch);
+/* NEW: the inferBatch pipeline: pImages (host) [nImages][nC][nH][nW] in batches of
+ * nBatchSize (clamped to [1, 32]); each batch is staged in page-locked memory and uploaded
+ * on the transfer stream while the previous batch computes; nNormPreset 1 applies the
+ * ImageNet normalisation of normalizeImage (data_pipeline.ixx:744-803) on the device (0:
+ * none). Per image, as the reference's classification branch: softmax of the logits,
+ * pClasses = argmax (-1 when the top probability is below fConfThreshold), pConfidences =
+ * top probability, pProbs [nImages][nClasses] (may be NULL). */
+int omHipResNet18InferBatch(void* pNet, const float* pImages, int nImages, int nC, int nH, int nW, int nBatchSize,
+                            int nNormPreset, float fConfThreshold, int* pClasses, float* pConfidences,
+                            float* pProbs);
 
 #ifdef __cplusplus
 }

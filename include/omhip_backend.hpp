@@ -17,6 +17,7 @@
 #include <cstdint>
 #include <stdexcept>
 #include <string>
+#include <vector>
 
 #include "omhip.h"
 
@@ -27,6 +28,21 @@ public:
     // ---- device ----
     static void init(int nDevice = 0) { check(omHipInit(nDevice), "omHipInit"); }
     static void synchronize() { check(omHipSynchronize(), "omHipSynchronize"); }
+    // ---- transfer stream and pinned host memory (cuda_kernels.cuh:56-66, :497-505) ----
+    static void* mallocHost(size_t nBytes) {
+        void* p = nullptr;
+        check(omHipMallocHost(&p, nBytes), "mallocHost");
+        return p;
+    }
+    static void freeHost(void* p) { check(omHipFreeHost(p), "freeHost"); }
+    static void asyncCopyH2D(void* pDst, const void* pSrc, size_t nBytes) {
+        check(omHipAsyncCopyH2D(pDst, pSrc, nBytes), "asyncCopyH2D");
+    }
+    static void asyncCopyD2H(void* pDst, const void* pSrc, size_t nBytes) {
+        check(omHipAsyncCopyD2H(pDst, pSrc, nBytes), "asyncCopyD2H");
+    }
+    static void syncTransferStream() { check(omHipSyncTransferStream(), "syncTransferStream"); }
+    static void computeWaitTransfer() { check(omHipComputeWaitTransfer(), "computeWaitTransfer"); }
     static void* malloc(size_t nBytes) {
         void* p = nullptr;
         check(omHipMalloc(&p, nBytes), "omHipMalloc");
@@ -216,6 +232,45 @@ private:
     static void check(int rc, const char* what) {
         if (rc != 0) throw std::runtime_error(std::string("HIPBackend::") + what + ": " + omHipGetLastError());
     }
+};
+
+// Device-resident ResNet-18 classifier and its batch inference pipeline
+// (EngineBridge::inferBatch, EngineBridge.cpp:3525-3772, classification branch).
+class ResNet18Infer {
+public:
+    struct Result {
+        std::vector<int> classes;        // -1 below the confidence threshold
+        std::vector<float> confidences;  // top probability
+        std::vector<float> probs;        // [images][classes]
+    };
+    ResNet18Infer(const std::vector<float>& params, int nClasses, int nMaxBatch = 32) : m_nc(nClasses) {
+        check(omHipResNet18Create(params.data(), static_cast<long long>(params.size()), nClasses, nMaxBatch,
+                                  &m_net),
+              "ResNet18Infer");
+    }
+    ~ResNet18Infer() { (void)omHipResNet18Destroy(m_net); }
+    ResNet18Infer(const ResNet18Infer&) = delete;
+    ResNet18Infer& operator=(const ResNet18Infer&) = delete;
+
+    // images: nImages x 3 x 224 x 224 floats in [0, 1], contiguous
+    Result inferBatch(const std::vector<float>& images, int nImages, int nBatchSize = 32, bool bImageNetNorm = true,
+                      float fConfThreshold = 0.0f) const {
+        Result r;
+        r.classes.resize(nImages);
+        r.confidences.resize(nImages);
+        r.probs.resize(static_cast<size_t>(nImages) * m_nc);
+        check(omHipResNet18InferBatch(m_net, images.data(), nImages, 3, 224, 224, nBatchSize, bImageNetNorm ? 1 : 0,
+                                      fConfThreshold, r.classes.data(), r.confidences.data(), r.probs.data()),
+              "inferBatch");
+        return r;
+    }
+
+private:
+    static void check(int rc, const char* what) {
+        if (rc != 0) throw std::runtime_error(std::string("ResNet18Infer::") + what + ": " + omHipGetLastError());
+    }
+    void* m_net = nullptr;
+    int m_nc;
 };
 
 }  // namespace om

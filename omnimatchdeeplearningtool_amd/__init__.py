@@ -60,6 +60,21 @@ _SIGS = {
     "omHipCopyD2D": [_vp, _vp, _sz],
     "omHipMemset": [_vp, _i, _sz],
     "omHipPoolStats": [ctypes.POINTER(_sz), ctypes.POINTER(_sz)],
+    "omHipMallocHost": [ctypes.POINTER(_vp), _sz],
+    "omHipFreeHost": [_vp],
+    "omHipAsyncCopyH2D": [_vp, _vp, _sz],
+    "omHipAsyncCopyD2H": [_vp, _vp, _sz],
+    "omHipSyncTransferStream": [],
+    "omHipComputeWaitTransfer": [],
+    "omHipTransferWaitCompute": [],
+    "omHipGraphBeginCapture": [],
+    "omHipGraphEndCapture": [ctypes.POINTER(_vp)],
+    "omHipGraphLaunch": [_vp],
+    "omHipGraphDestroy": [_vp],
+    "omHipResNet18Create": [_vp, _ll, _i, _i, ctypes.POINTER(_vp)],
+    "omHipResNet18Destroy": [_vp],
+    "omHipResNet18Forward": [_vp, _vp, _vp, _i],
+    "omHipResNet18InferBatch": [_vp, _vp, _i, _i, _i, _i, _i, _i, _fl, _vp, _vp, _vp],
     "omHipPoolTrim": [],
     "omHipFillZeros": [_vp, _i],
     "omHipFillOnes": [_vp, _i],
@@ -159,6 +174,61 @@ def stream_handle() -> int:
     s = _vp()
     call("omHipGetStream", ctypes.byref(s))
     return s.value or 0
+
+
+class Graph:
+    """A captured sequence of library calls (omHipGraphBeginCapture ... EndCapture), replayed
+    on the compute stream. Capture a sequence after one eager run of it."""
+
+    def __init__(self, fn):
+        call("omHipGraphBeginCapture")
+        try:
+            fn()
+        finally:
+            g = _vp()
+            call("omHipGraphEndCapture", ctypes.byref(g))
+        self.handle = g.value
+
+    def launch(self) -> None:
+        call("omHipGraphLaunch", self.handle)
+
+    def __del__(self):
+        if getattr(self, "handle", None) and _LIB is not None:
+            lib().omHipGraphDestroy(self.handle)
+            self.handle = None
+
+
+class ResNet18Infer:
+    """Device-resident ResNet-18 classifier and its batch inference pipeline
+    (EngineBridge::inferBatch, EngineBridge.cpp:3525-3772, classification branch).
+    params: the flat float32 array of omHipResNet18Create's layout."""
+
+    def __init__(self, params: np.ndarray, num_classes: int, max_batch: int = 32):
+        params = np.ascontiguousarray(params, np.float32)
+        h = _vp()
+        call("omHipResNet18Create", params.ctypes.data, params.size, num_classes, max_batch, ctypes.byref(h))
+        self.handle, self.nc = h.value, num_classes
+
+    def forward(self, d_input, d_logits, batch: int) -> None:
+        call("omHipResNet18Forward", self.handle, d_input.ptr, d_logits.ptr, batch)
+
+    def infer_batch(self, images: np.ndarray, batch_size: int = 32, imagenet_norm: bool = True,
+                    conf_threshold: float = 0.0, with_probs: bool = True):
+        """images [n, 3, 224, 224] float32 (host) -> (classes int32 [n], confidences [n], probs [n, nc])."""
+        images = np.ascontiguousarray(images, np.float32)
+        n = images.shape[0]
+        cls = np.empty(n, np.int32)
+        conf = np.empty(n, np.float32)
+        probs = np.empty((n, self.nc), np.float32) if with_probs else None
+        call("omHipResNet18InferBatch", self.handle, images.ctypes.data, n, images.shape[1], images.shape[2],
+             images.shape[3], batch_size, 1 if imagenet_norm else 0, conf_threshold, cls.ctypes.data,
+             conf.ctypes.data, probs.ctypes.data if probs is not None else None)
+        return cls, conf, probs
+
+    def __del__(self):
+        if getattr(self, "handle", None) and _LIB is not None:
+            lib().omHipResNet18Destroy(self.handle)
+            self.handle = None
 
 
 class DeviceBuffer:

@@ -47,6 +47,29 @@ int fillValue(float* p, long long n, float v) {
     return 0;
 }
 
+// Byte fill (omHipMemset): 16-byte stores over the aligned body, bytes at the ends.
+__global__ void byte_fill_kernel(unsigned char* p, long long n, unsigned int word) {
+    const long long stride = (long long)gridDim.x * blockDim.x;
+    const long long head = (long long)((16 - (reinterpret_cast<uintptr_t>(p) & 15u)) & 15u);
+    const long long h = head < n ? head : n;
+    const long long body = (n - h) / 16;
+    const uint4 w = {word, word, word, word};
+    uint4* q = reinterpret_cast<uint4*>(p + h);
+    for (long long i = blockIdx.x * (long long)blockDim.x + threadIdx.x; i < body; i += stride) q[i] = w;
+    const unsigned char b = (unsigned char)(word & 0xffu);
+    for (long long i = blockIdx.x * (long long)blockDim.x + threadIdx.x; i < h; i += stride) p[i] = b;
+    for (long long i = h + body * 16 + blockIdx.x * (long long)blockDim.x + threadIdx.x; i < n; i += stride) p[i] = b;
+}
+
+int byteFill(void* p, unsigned char value, size_t nBytes) {
+    if (nBytes == 0) return 0;
+    const unsigned int word = 0x01010101u * value;
+    hipLaunchKernelGGL(byte_fill_kernel, dim3(gridFor((long long)(nBytes / 16) + 1)), dim3(256), 0, stream(),
+                       static_cast<unsigned char*>(p), (long long)nBytes, word);
+    OMHIP_CHECK_LAUNCH();
+    return 0;
+}
+
 // ---- ReLU ------------------------------------------------------------------
 __global__ void relu_kernel4(const float* __restrict__ in, float* __restrict__ out, long long n) {
     const long long n4 = n / 4;

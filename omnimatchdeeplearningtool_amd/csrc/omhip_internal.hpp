@@ -16,6 +16,14 @@ namespace omhip {
 // called, so a forgotten init degrades to the reference's default device.
 hipStream_t stream();
 
+// Library transfer stream for the asynchronous host copies (created on
+// first use); nullptr with the error recorded on failure.
+hipStream_t transferStream();
+
+// Sets nBytes bytes at p to value with a kernel on the library stream (safe
+// inside a captured graph). 0 or -1.
+int byteFill(void* p, unsigned char value, size_t nBytes);
+
 // Records a message for omHipGetLastError (thread-local) and returns -1.
 int fail(const char* fmt, ...);
 

@@ -24,6 +24,10 @@ std::atomic<bool> g_inited{false};
 int g_device = 0;
 hipStream_t g_ownStream = nullptr;
 std::atomic<hipStream_t> g_userStream{nullptr};
+// Transfer stream and the two ordering events (created on first use).
+hipStream_t g_xferStream = nullptr;
+hipEvent_t g_evXfer = nullptr, g_evCompute = nullptr;
+std::mutex g_xferMutex;
 int g_cuCount = 0;
 int g_maxShared = 65536;
 std::unique_ptr<CachingPool> g_pool;
@@ -71,6 +75,21 @@ int ensureInit(int nDev, bool bExplicit) {
 }
 
 }  // namespace
+
+hipStream_t transferStream() {
+    if (ensureInit(0, false)) return nullptr;
+    std::lock_guard<std::mutex> lock(g_xferMutex);
+    if (!g_xferStream) {
+        // default priority, like the compute stream
+        if (hipStreamCreateWithFlags(&g_xferStream, hipStreamNonBlocking) != hipSuccess ||
+            hipEventCreateWithFlags(&g_evXfer, hipEventDisableTiming) != hipSuccess ||
+            hipEventCreateWithFlags(&g_evCompute, hipEventDisableTiming) != hipSuccess) {
+            (void)fail("transfer stream: %s", hipGetErrorString(hipGetLastError()));
+            return nullptr;
+        }
+    }
+    return g_xferStream;
+}
 
 hipStream_t stream() {
     hipStream_t s = g_userStream.load(std::memory_order_acquire);
@@ -190,6 +209,17 @@ int omHipCleanup(void) {
     for (auto fn : hooks) fn();
     if (g_pool) g_pool->clear();
     g_pool.reset();
+    {
+        std::lock_guard<std::mutex> xl(g_xferMutex);
+        if (g_xferStream) {
+            (void)hipStreamSynchronize(g_xferStream);
+            (void)hipStreamDestroy(g_xferStream);
+        }
+        if (g_evXfer) (void)hipEventDestroy(g_evXfer);
+        if (g_evCompute) (void)hipEventDestroy(g_evCompute);
+        g_xferStream = nullptr;
+        g_evXfer = g_evCompute = nullptr;
+    }
     (void)hipStreamDestroy(g_ownStream);
     g_ownStream = nullptr;
     g_userStream.store(nullptr, std::memory_order_release);
@@ -284,7 +314,109 @@ int omHipMemset(void* pDev, int nValue, size_t nBytes) {
     clearError();
     if (nBytes == 0) return 0;
     if (!pDev) return fail("omHipMemset: null pointer");
-    OMHIP_CHECK(hipMemsetAsync(pDev, nValue, nBytes, stream()));
+    // a kernel, not hipMemsetAsync, so the call may sit inside a captured graph
+    return byteFill(pDev, (unsigned char)nValue, nBytes);
+}
+
+// ---- transfer stream, pinned host memory (cuda_kernels.cu:388-417, :4887-4900) ----
+
+int omHipMallocHost(void** ppPtr, size_t nBytes) {
+    clearError();
+    if (!ppPtr) return fail("omHipMallocHost: null output");
+    *ppPtr = nullptr;
+    if (ensureInit(0, false)) return -1;
+    OMHIP_CHECK(hipHostMalloc(ppPtr, nBytes, hipHostMallocDefault));
+    return 0;
+}
+
+int omHipFreeHost(void* pPtr) {
+    clearError();
+    if (!pPtr) return 0;
+    OMHIP_CHECK(hipHostFree(pPtr));
+    return 0;
+}
+
+int omHipAsyncCopyH2D(void* pDst, const void* pSrc, size_t nBytes) {
+    clearError();
+    if (nBytes == 0) return 0;
+    if (!pDst || !pSrc) return fail("omHipAsyncCopyH2D: null pointer");
+    hipStream_t x = transferStream();
+    if (!x) return -1;
+    OMHIP_CHECK(hipMemcpyAsync(pDst, pSrc, nBytes, hipMemcpyHostToDevice, x));
+    return 0;
+}
+
+int omHipAsyncCopyD2H(void* pDst, const void* pSrc, size_t nBytes) {
+    clearError();
+    if (nBytes == 0) return 0;
+    if (!pDst || !pSrc) return fail("omHipAsyncCopyD2H: null pointer");
+    hipStream_t x = transferStream();
+    if (!x) return -1;
+    OMHIP_CHECK(hipMemcpyAsync(pDst, pSrc, nBytes, hipMemcpyDeviceToHost, x));
+    return 0;
+}
+
+int omHipSyncTransferStream(void) {
+    clearError();
+    hipStream_t x = transferStream();
+    if (!x) return -1;
+    OMHIP_CHECK(hipStreamSynchronize(x));
+    return 0;
+}
+
+int omHipComputeWaitTransfer(void) {
+    clearError();
+    hipStream_t x = transferStream();
+    if (!x) return -1;
+    OMHIP_CHECK(hipEventRecord(g_evXfer, x));
+    OMHIP_CHECK(hipStreamWaitEvent(stream(), g_evXfer, 0));
+    return 0;
+}
+
+int omHipTransferWaitCompute(void) {
+    clearError();
+    hipStream_t x = transferStream();
+    if (!x) return -1;
+    OMHIP_CHECK(hipEventRecord(g_evCompute, stream()));
+    OMHIP_CHECK(hipStreamWaitEvent(x, g_evCompute, 0));
+    return 0;
+}
+
+// ---- graphs on the compute stream (cuda_kernels.cu OPT-3.5: omCudaGraph*) ----
+
+int omHipGraphBeginCapture(void) {
+    clearError();
+    if (ensureInit(0, false)) return -1;
+    // relaxed: the pool may still call hipMalloc while a graph is recorded
+    OMHIP_CHECK(hipStreamBeginCapture(stream(), hipStreamCaptureModeRelaxed));
+    return 0;
+}
+
+int omHipGraphEndCapture(void** ppGraphExec) {
+    clearError();
+    if (!ppGraphExec) return fail("omHipGraphEndCapture: null output");
+    *ppGraphExec = nullptr;
+    hipGraph_t g = nullptr;
+    OMHIP_CHECK(hipStreamEndCapture(stream(), &g));
+    hipGraphExec_t exec = nullptr;
+    const hipError_t e = hipGraphInstantiate(&exec, g, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(g);
+    if (e != hipSuccess) return fail("hipGraphInstantiate: %s", hipGetErrorString(e));
+    *ppGraphExec = static_cast<void*>(exec);
+    return 0;
+}
+
+int omHipGraphLaunch(void* pGraphExec) {
+    clearError();
+    if (!pGraphExec) return fail("omHipGraphLaunch: null graph");
+    OMHIP_CHECK(hipGraphLaunch(static_cast<hipGraphExec_t>(pGraphExec), stream()));
+    return 0;
+}
+
+int omHipGraphDestroy(void* pGraphExec) {
+    clearError();
+    if (!pGraphExec) return 0;
+    OMHIP_CHECK(hipGraphExecDestroy(static_cast<hipGraphExec_t>(pGraphExec)));
     return 0;
 }
 

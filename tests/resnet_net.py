@@ -87,6 +87,17 @@ def conv_list():
     return L
 
 
+def pack_params(P: dict) -> np.ndarray:
+    """The flat parameter array of omHipResNet18Create: per conv in network order its
+    weight, BN gamma, beta, running mean and running var; then fc weight and bias."""
+    parts = []
+    for name, *_ in conv_list():
+        parts += [P[name + ".w"].ravel(), P[name + ".gamma"], P[name + ".beta"], P[name + ".mean"],
+                  P[name + ".var"]]
+    parts += [P["fc.w"].ravel(), P["fc.b"]]
+    return np.ascontiguousarray(np.concatenate(parts), np.float32)
+
+
 def forward_flops(batch: int) -> float:
     """Conv + FC multiply-adds x 2 of one inference forward."""
     f = 0.0
