@@ -30,5 +30,9 @@ __device__ __forceinline__ float bufLoad1(__amdgpu_buffer_rsrc_t r, uint32_t vof
 __device__ __forceinline__ f32x4 bufLoad4(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
     return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
 }
+// Vector-memory store; a lane whose voffset is out of range writes nothing.
+__device__ __forceinline__ void bufStore1(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff, float v) {
+    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), r, voff, soff, 0);
+}
 
 }  // namespace omhip

@@ -241,6 +241,71 @@ __device__ __forceinline__ int outPixel(const ConvParams& p, int pix) {
     return (oh * p.oStride + p.oOffH) * p.oW + ow * p.oStride + p.oOffW;
 }
 
+// Direct epilogue of one block's tile: bias, BN (inference), residual and
+// ReLU applied to the finished sums and written to the NCHW output. The lane
+// holding acc[fm][fn][r] owns tile row wm*WM + fm*32 + 8*(r/4) + 4*(lane/32) +
+// r%4 and column wn*WN + fn*32 + lane%32, so rows r = 4j..4j+3 are four
+// consecutive channels (one 16-byte read of each epilogue vector) and a row's
+// byte offset past the lane's first row is the wave-uniform (8j + r%4) * row
+// stride, carried in soffset. Columns past Nq and rows past Cout get an
+// out-of-range voffset and store nothing. The output view (chunk images x
+// Cout x oH x oW floats) is at most 2^30 bytes.
+template <class Cfg, bool BN, bool RES, bool RELU>
+__device__ __forceinline__ void storeTile(const ConvParams& p, const f32x16 (&acc)[Cfg::FM][Cfg::FN],
+                                          const float* sEpi, int m0, int n0, int wm, int wn, int lane) {
+    const int li = lane & 31, h = lane >> 5;
+    const int HoWo = p.Ho * p.Wo;
+    const uint32_t oHW = (uint32_t)(p.oH * p.oW);
+    const uint32_t viewBytes = (uint32_t)p.N * (uint32_t)p.Cout * oHW * 4u;
+    const auto ro = bufferRsrc(p.out, viewBytes);
+    const auto rr = bufferRsrc(RES ? p.res : p.out, viewBytes);   // read only when RES
+    const bool fullM = m0 + Cfg::BM <= p.Cout;
+#pragma unroll
+    for (int fn = 0; fn < Cfg::FN; ++fn) {
+        const int q = n0 + wn * Cfg::WN + fn * 32 + li;
+        const bool colOk = q < p.Nq;
+        const int qq = colOk ? q : 0;
+        const int n = qq / HoWo;
+        const int opix = outPixel(p, qq - n * HoWo);
+#pragma unroll
+        for (int fm = 0; fm < Cfg::FM; ++fm) {
+            const int rl0 = wm * Cfg::WM + fm * 32 + 4 * h;
+            const uint32_t vbase = colOk ? ((uint32_t)(n * p.Cout + m0 + rl0) * oHW + (uint32_t)opix) * 4u : kOOB;
+            const int rowsLeft = p.Cout - m0 - rl0;   // rows of this lane's column still inside Cout
+            // one group of four channels at a time: its residuals, epilogue
+            // vectors and results stay within a few registers
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int rl = rl0 + 8 * j;
+                uint32_t vo[4];
+                float rv[4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    vo[i] = (fullM || 8 * j + i < rowsLeft) ? vbase : kOOB;
+                    if constexpr (RES) rv[i] = bufLoad1(rr, vo[i], (8 * j + i) * oHW * 4u);
+                }
+                const f32x4 b = *reinterpret_cast<const f32x4*>(sEpi + rl);
+                f32x4 mu, is, g, be;
+                if constexpr (BN) {
+                    mu = *reinterpret_cast<const f32x4*>(sEpi + Cfg::BM + rl);
+                    is = *reinterpret_cast<const f32x4*>(sEpi + 2 * Cfg::BM + rl);
+                    g = *reinterpret_cast<const f32x4*>(sEpi + 3 * Cfg::BM + rl);
+                    be = *reinterpret_cast<const f32x4*>(sEpi + 4 * Cfg::BM + rl);
+                }
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    float v = acc[fm][fn][4 * j + i] + b[i];
+                    if constexpr (BN) v = __builtin_fmaf(g[i], (v - mu[i]) * is[i], be[i]);
+                    if constexpr (RES) v += rv[i];
+                    if constexpr (RELU) v = v > 0.f ? v : 0.f;
+                    bufStore1(ro, vo[i], (8 * j + i) * oHW * 4u, v);
+                }
+                __builtin_amdgcn_sched_barrier(0);   // keeps one group's registers live at a time
+            }
+        }
+    }
+}
+
 template <class Cfg, bool VA, int MODE>
 __global__ __launch_bounds__(Cfg::NT) void conv_igemm_kernel(ConvParams p) {
     extern __shared__ float smem[];
@@ -344,8 +409,6 @@ __global__ __launch_bounds__(Cfg::NT) void conv_igemm_kernel(ConvParams p) {
     }
 
     const int li = lane & 31, h = lane >> 5;
-    const int HoWo = p.Ho * p.Wo;
-    const int oHW = p.oH * p.oW;
     if (piece >= 0) {
         // compact partial tile; the finishing kernel checks the tile edges
         float* rp = p.rws + ((long long)piece * (tiles - p.fullTiles) + rtile) * (Cfg::BM * Cfg::BN);
@@ -361,44 +424,36 @@ __global__ __launch_bounds__(Cfg::NT) void conv_igemm_kernel(ConvParams p) {
         return;
     }
     if (!direct) {
-        float* ws = p.ws + (long long)split * p.Cout * p.Nq;
+        // this split's [Cout][Nq] partials (at most 64 MiB); same row / column
+        // ownership and out-of-range handling as storeTile
+        const uint32_t nq = (uint32_t)p.Nq;
+        const auto rw = bufferRsrc(p.ws + (long long)split * p.Cout * p.Nq, (uint32_t)p.Cout * nq * 4u);
 #pragma unroll
         for (int fn = 0; fn < Cfg::FN; ++fn) {
             const int q = n0 + wn * Cfg::WN + fn * 32 + li;
-            if (q >= p.Nq) continue;
 #pragma unroll
-            for (int fm = 0; fm < Cfg::FM; ++fm)
+            for (int fm = 0; fm < Cfg::FM; ++fm) {
+                const int rl0 = wm * Cfg::WM + fm * 32 + 4 * h;
+                const uint32_t vbase = q < p.Nq ? ((uint32_t)(m0 + rl0) * nq + (uint32_t)q) * 4u : kOOB;
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
-                    const int co = m0 + wm * Cfg::WM + fm * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
-                    if (co < p.Cout) ws[(long long)co * p.Nq + q] = acc[fm][fn][r];
+                    const int rowOff = 8 * (r >> 2) + (r & 3);
+                    const uint32_t vo = m0 + rl0 + rowOff < p.Cout ? vbase : kOOB;
+                    bufStore1(rw, vo, (uint32_t)rowOff * nq * 4u, acc[fm][fn][r]);
                 }
+            }
         }
         return;
     }
-#pragma unroll
-    for (int fn = 0; fn < Cfg::FN; ++fn) {
-        const int q = n0 + wn * Cfg::WN + fn * 32 + li;
-        if (q >= p.Nq) continue;
-        const int n = q / HoWo;
-        const int pix = q - n * HoWo;
-        const int opix = outPixel(p, pix);
-        float* o = p.out + (long long)n * p.Cout * oHW + opix;
-#pragma unroll
-        for (int fm = 0; fm < Cfg::FM; ++fm)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int rl = wm * Cfg::WM + fm * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
-                const int co = m0 + rl;
-                if (co >= p.Cout) continue;
-                float v = acc[fm][fn][r] + sEpi[rl];
-                if (p.gamma)
-                    v = __builtin_fmaf(sEpi[3 * Cfg::BM + rl], (v - sEpi[Cfg::BM + rl]) * sEpi[2 * Cfg::BM + rl],
-                                       sEpi[4 * Cfg::BM + rl]);
-                if (p.res) v += p.res[(long long)n * p.Cout * oHW + (long long)co * oHW + opix];
-                if (p.act == 1) v = v > 0.f ? v : 0.f;
-                o[(long long)co * oHW] = v;
-            }
+    switch ((p.gamma ? 1 : 0) | (p.res ? 2 : 0) | (p.act == 1 ? 4 : 0)) {
+        case 0: storeTile<Cfg, false, false, false>(p, acc, sEpi, m0, n0, wm, wn, lane); break;
+        case 1: storeTile<Cfg, true, false, false>(p, acc, sEpi, m0, n0, wm, wn, lane); break;
+        case 2: storeTile<Cfg, false, true, false>(p, acc, sEpi, m0, n0, wm, wn, lane); break;
+        case 3: storeTile<Cfg, true, true, false>(p, acc, sEpi, m0, n0, wm, wn, lane); break;
+        case 4: storeTile<Cfg, false, false, true>(p, acc, sEpi, m0, n0, wm, wn, lane); break;
+        case 5: storeTile<Cfg, true, false, true>(p, acc, sEpi, m0, n0, wm, wn, lane); break;
+        case 6: storeTile<Cfg, false, true, true>(p, acc, sEpi, m0, n0, wm, wn, lane); break;
+        default: storeTile<Cfg, true, true, true>(p, acc, sEpi, m0, n0, wm, wn, lane); break;
     }
 }
 
@@ -618,16 +673,16 @@ static const uint2* tapTable(int Cin, int H, int W, int KH, int KW) {
 }
 
 // Buffer-view limits shared by every conv launch: one image with its border
-// margin and the weights fit a view (the batch is split into chunks that do),
-// pixel indices stay below 2^30, and KH, KW < 2^16 and H + pad, W + pad <
-// 65535 for the tap codes.
+// margin, one image's output and the weights fit a view (the batch is split
+// into chunks that do), pixel indices stay below 2^30, and KH, KW < 2^16 and
+// H + pad, W + pad < 65535 for the tap codes.
 static int checkConvLimits(const char* name, int Cin, int H, int W, int Cout, int KH, int KW, int padH, int padW,
                            long long outPerImage) {
     const long long K = (long long)Cin * KH * KW;
     const long long margin = (long long)std::max(padH, 0) * W + std::max(padW, 0);
     const long long imgBytes = (long long)Cin * H * W * 4 + 8LL * (margin + W + 1);
     if (K > (1LL << 26) || imgBytes > (long long)kMaxBufferBytes / 2 || (long long)Cout * K * 4 > kMaxBufferBytes ||
-        outPerImage > (1LL << 30) || H + std::abs(padH) >= 65535 || W + std::abs(padW) >= 65535 || KH >= 65536 ||
+        outPerImage > (long long)kMaxBufferBytes / 4 || H + std::abs(padH) >= 65535 || W + std::abs(padW) >= 65535 || KH >= 65536 ||
         KW >= 65536)
         return fail("%s: tensor exceeds the 2^30-byte buffer range of this kernel", name);
     return 0;
@@ -670,8 +725,9 @@ static int convChunk(ConvParams p, int n0, int nb) {
     return launchConv(p, pl, ws);
 }
 
-// Walks the batch in chunks whose x view stays below 2^29 bytes and whose
-// pixel and output indices stay below 2^30.
+// Walks the batch in chunks whose x view stays below 2^29 bytes, whose pixel
+// indices stay below 2^30 and whose output (and residual) view is at most 2^30
+// bytes.
 static int runConv(const char* name, ConvParams& p) {
     p.K = p.Cin * p.KH * p.KW;
     p.tab = tapTable(p.Cin, p.H, p.W, p.KH, p.KW);
@@ -679,7 +735,8 @@ static int runConv(const char* name, ConvParams& p) {
     const long long perImg = (long long)p.Cin * p.H * p.W * 4;
     long long chunk = std::max<long long>(1, ((long long)kMaxBufferBytes / 2) / perImg);
     chunk = std::min<long long>(chunk, std::max<long long>(1, (1LL << 30) / ((long long)p.Cout * p.Ho * p.Wo)));
-    chunk = std::min<long long>(chunk, std::max<long long>(1, (1LL << 30) / ((long long)p.Cout * p.oH * p.oW)));
+    chunk = std::min<long long>(chunk,
+                              std::max<long long>(1, ((long long)kMaxBufferBytes / 4) / ((long long)p.Cout * p.oH * p.oW)));
     for (int n0 = 0; n0 < p.N; n0 += (int)chunk) {
         const int nb = (int)std::min<long long>(chunk, p.N - n0);
         if (convChunk(p, n0, nb)) return -1;
