@@ -19,6 +19,9 @@
 //    before the LDS store. The MFMA takes the B fragment as its first operand,
 //    so each lane ends up holding 4 consecutive output columns and the fp32
 //    tile leaves in 128-bit stores.
+//    K-major operands whose rows are only 2-byte aligned (odd K or leading
+//    dimension) are fetched 16 bytes at a time from the dword boundary below
+//    and funnel-shifted into place.
 //  * gemm_half_generic: any other layout (element loads with bounds checks).
 //
 // Within a 16-deep MFMA step the two 32-lane halves supply k = 0..7 and
@@ -28,6 +31,7 @@
 #include "../../include/omhip.h"
 
 #include <algorithm>
+#include <cmath>
 #include <type_traits>
 
 namespace omhip {
@@ -335,6 +339,76 @@ struct KMajorSlice {
     }
 };
 
+// K-major operand whose rows start at any half (an odd leading dimension,
+// base or batch stride, e.g. P of P x V with 197 keys). Chunks are laid out as
+// in KMajorSlice; a chunk that starts at half h is fetched as the 16 bytes at
+// the dword boundary below it plus the next dword, and shifted down by 16 bits
+// when h is odd. The view starts at the dword holding the tile's first element
+// and ends at the dword holding row rowsValid-1's K-th element (the 2 bytes
+// after it, inside that same dword, are read but belong to no output that is
+// kept: they fall past K, where the last slice zeroes every half, or in a row
+// past the matrix). K-contiguous halves past K are zeroed explicitly on the
+// last slice: there the next row's data lies, not the end of the view.
+template <int R, int BK, int NT>
+struct KMajorRaggedSlice {
+    static constexpr int CH = BK / 8;
+    static constexpr int PER_T = R * CH / NT;
+    static_assert(R * CH % NT == 0, "slice must split evenly");
+    static constexpr int NLOADS = 2 * PER_T, NSTORES = PER_T;   // per thread and slice
+    struct Regs {
+        u32x4 v[PER_T];
+    };
+    __amdgpu_buffer_rsrc_t r;
+    uint32_t voff[PER_T];   // byte offset of the dword holding the chunk's first half
+    uint32_t sh[PER_T];     // 16 when that half is the dword's upper one, else 0
+
+    __device__ void init(const uint16_t* base, int ld, int rowsValid, int K, int tid) {
+        const int rv = rowsValid < R ? rowsValid : R;
+        const uint32_t lead = (uint32_t)(reinterpret_cast<uintptr_t>(base) & 2u) >> 1;   // halves below base in its dword
+        const uint16_t* b4 = base - lead;
+        const uint32_t endHalves = (uint32_t)(rv - 1) * (uint32_t)ld + (uint32_t)K + lead;
+        r = halfRsrc(b4, ((endHalves * 2u) + 3u) & ~3u);
+#pragma unroll
+        for (int i = 0; i < PER_T; ++i) {
+            const int e = tid + i * NT;
+            const uint32_t h = (uint32_t)(e / CH) * (uint32_t)ld + (uint32_t)(e % CH) * 8u + lead;
+            voff[i] = (h * 2u) & ~3u;
+            sh[i] = (h & 1u) * 16u;
+        }
+    }
+    // FULL: the slice lies inside K. The slice start k0 is a multiple of BK, so
+    // the scalar offset 2*k0 keeps the dword alignment.
+    template <bool FULL>
+    __device__ void load(int k0, int K, int tid, Regs& g) const {
+        const uint32_t soff = (uint32_t)k0 * 2u;
+#pragma unroll
+        for (int i = 0; i < PER_T; ++i) {
+            const u32x4 lo = ld128(r, voff[i], soff);
+            const uint32_t hi = __builtin_amdgcn_raw_buffer_load_b32(r, voff[i] + 16u, soff, 0);
+            u32x4 v = {__builtin_amdgcn_alignbit(lo[1], lo[0], sh[i]), __builtin_amdgcn_alignbit(lo[2], lo[1], sh[i]),
+                       __builtin_amdgcn_alignbit(lo[3], lo[2], sh[i]), __builtin_amdgcn_alignbit(hi, lo[3], sh[i])};
+            if (!FULL && k0 + BK > K) {
+                const int n = K - (k0 + ((tid + i * NT) % CH) * 8);   // halves of this chunk inside K
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    v[j] &= (2 * j < n ? 0x0000ffffu : 0u) | (2 * j + 1 < n ? 0xffff0000u : 0u);
+            }
+            g.v[i] = v;
+        }
+    }
+    template <int LD>
+    __device__ void store(uint16_t* s, int tid, const Regs& g) const {
+#pragma unroll
+        for (int i = 0; i < PER_T; ++i) {
+            const int e = tid + i * NT;
+            *reinterpret_cast<u32x4*>(s + (e / CH) * LD + (e % CH) * 8) = g.v[i];
+        }
+    }
+};
+
+template <bool RAG, int R, int BK, int NT>
+using KMajorFor = std::conditional_t<RAG, KMajorRaggedSlice<R, BK, NT>, KMajorSlice<R, BK, NT>>;
+
 // R-major operand: element (r,k) at P[k*ld + r]. A slice is (R/8) x (BK/8)
 // blocks of 8 k x 8 r; block e is (rb = e / (BK/8), kb = e % (BK/8)). A thread
 // loads its block's 8 rows (one 16-byte load each; the row step rides in the
@@ -469,7 +543,8 @@ __device__ __forceinline__ void interleave() {
 // SWAP (C rows allow 128-bit stores: N, ldc, batch stride multiples of 4 and a
 // 16-byte aligned base) puts the B fragment first so each lane holds 4
 // consecutive columns; otherwise lanes run along n for coalesced 32-bit stores.
-template <class Cfg, bool BF16, bool TA, bool TB, bool SWAP>
+// RAG: the K-major operands' rows may start at any half (KMajorRaggedSlice).
+template <class Cfg, bool BF16, bool TA, bool TB, bool SWAP, bool RAG>
 __global__ __launch_bounds__(Cfg::NT) void gemm_half_fast(HalfFastParams p) {
     extern __shared__ uint16_t hsm[];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -483,8 +558,8 @@ __global__ __launch_bounds__(Cfg::NT) void gemm_half_fast(HalfFastParams p) {
     const uint16_t* Bb = p.B + batch * p.sB;
 
     // A's rows are m: K-major unless transposed. B's rows are n: K-major when transposed.
-    using LA = std::conditional_t<TA, RMajorSlice<Cfg::BM, Cfg::BK, Cfg::NT>, KMajorSlice<Cfg::BM, Cfg::BK, Cfg::NT>>;
-    using LB = std::conditional_t<TB, KMajorSlice<Cfg::BN, Cfg::BK, Cfg::NT>, RMajorSlice<Cfg::BN, Cfg::BK, Cfg::NT>>;
+    using LA = std::conditional_t<TA, RMajorSlice<Cfg::BM, Cfg::BK, Cfg::NT>, KMajorFor<RAG, Cfg::BM, Cfg::BK, Cfg::NT>>;
+    using LB = std::conditional_t<TB, KMajorFor<RAG, Cfg::BN, Cfg::BK, Cfg::NT>, RMajorSlice<Cfg::BN, Cfg::BK, Cfg::NT>>;
     LA la;
     LB lb;
     la.init(TA ? Ab + m0 : Ab + (long long)m0 * p.lda, p.lda, p.M - m0, p.K, tid);
@@ -603,9 +678,9 @@ using FCfgL = FCfg<OMHIP_HALF_L>;
 using FCfgM = FCfg<128, 128, 64, 64, 64>;
 using FCfgS = FCfg<64, 64, 64, 32, 32>;
 
-template <class Cfg, bool BF16, bool TA, bool TB, bool SWAP>
+template <class Cfg, bool BF16, bool TA, bool TB, bool SWAP, bool RAG>
 static int launchFast(HalfFastParams prm, int batch) {
-    auto kern = gemm_half_fast<Cfg, BF16, TA, TB, SWAP>;
+    auto kern = gemm_half_fast<Cfg, BF16, TA, TB, SWAP, RAG>;
     static bool s_attr = false;
     if (!s_attr) {
         OMHIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
@@ -620,49 +695,80 @@ static int launchFast(HalfFastParams prm, int batch) {
     return 0;
 }
 
-// Tile choice: the large tile once it covers at least half the CUs (its
-// higher per-CU rate outweighs the idle half, e.g. 12608 x 768), then the
-// 128x128 tile once it gives every CU a workgroup, else the 64x64 tile.
+// Tile choice from a model of the time per CU. A CU receives n = ceil(tiles /
+// CUs) workgroups and runs up to `slots` of them at once (256x256: 1 per CU,
+// 128x128: 2, 64x64: 4, by LDS); its time is n x tile area / throughput,
+// where the throughput with j of the slots filled is rate x (j/slots)^0.6 (a
+// lone workgroup gets more than its share of the CU). Rates 1, 0.75, 0.45
+// were fitted to a sweep of all three tiles over the ViT-B/16 GEMMs, the
+// batched attention products and square / tall-skinny problems on MI355X,
+// where the model picks the fastest tile or one within 4 % of it: e.g.
+// 12608 x 2304 x 768 and 4096^3 take 256x256, 2048 x 4096 x 4096 128x128,
+// 768 x (197 x 64 x 197) and 1024^3 64x64.
 static int pickFastTile(int M, int N, int batch) {
     const long long cus = cuCount();
-    auto tiles = [&](int bm, int bn) { return (long long)((M + bm - 1) / bm) * ((N + bn - 1) / bn) * batch; };
+    struct T { int bm, bn, slots; double rate; };
+    const T cand[3] = {{256, 256, 1, 1.0}, {128, 128, 2, 0.75}, {64, 64, 4, 0.45}};
     // TILE-HOOK
-    if (2 * tiles(256, 256) >= cus) return 0;
-    if (tiles(128, 128) >= cus) return 1;
-    return 2;
+    int best = 0;
+    double bestCost = 0;
+    for (int c = 0; c < 3; ++c) {
+        const long long tiles = (long long)((M + cand[c].bm - 1) / cand[c].bm) * ((N + cand[c].bn - 1) / cand[c].bn) * batch;
+        const long long n = (tiles + cus - 1) / cus;
+        const double fill = (double)std::min<long long>(n, cand[c].slots) / cand[c].slots;
+        const double cost = (double)n * cand[c].bm * cand[c].bn / (cand[c].rate * std::pow(fill, 0.6));
+        if (c == 0 || cost < bestCost) { best = c; bestCost = cost; }
+    }
+    return best;
 }
 
-template <bool BF16, bool TA, bool TB, bool SWAP>
+template <bool BF16, bool TA, bool TB, bool SWAP, bool RAG>
 static int launchFastT(const HalfFastParams& prm, int batch) {
     switch (pickFastTile(prm.M, prm.N, batch)) {
-        case 0: return launchFast<FCfgL, BF16, TA, TB, SWAP>(prm, batch);
-        case 1: return launchFast<FCfgM, BF16, TA, TB, SWAP>(prm, batch);
-        default: return launchFast<FCfgS, BF16, TA, TB, SWAP>(prm, batch);
+        case 0: return launchFast<FCfgL, BF16, TA, TB, SWAP, RAG>(prm, batch);
+        case 1: return launchFast<FCfgM, BF16, TA, TB, SWAP, RAG>(prm, batch);
+        default: return launchFast<FCfgS, BF16, TA, TB, SWAP, RAG>(prm, batch);
     }
 }
 
-template <bool BF16, bool TA, bool TB>
+template <bool BF16, bool TA, bool TB, bool RAG>
 static int launchFastC(const HalfFastParams& prm, int batch, bool vecC) {
-    return vecC ? launchFastT<BF16, TA, TB, true>(prm, batch) : launchFastT<BF16, TA, TB, false>(prm, batch);
+    return vecC ? launchFastT<BF16, TA, TB, true, RAG>(prm, batch) : launchFastT<BF16, TA, TB, false, RAG>(prm, batch);
+}
+
+template <bool BF16, bool TA, bool TB>
+static int launchFastR(const HalfFastParams& prm, int batch, bool vecC, bool rag) {
+    if constexpr (TA && !TB) {
+        return launchFastC<BF16, TA, TB, false>(prm, batch, vecC);   // no K-major operand
+    } else {
+        return rag ? launchFastC<BF16, TA, TB, true>(prm, batch, vecC) : launchFastC<BF16, TA, TB, false>(prm, batch, vecC);
+    }
 }
 
 template <bool BF16>
 static int dispatchH(bool ta, bool tb, const GemmHalfParams& prm, int batch, bool va, bool vb) {
-    // The fast kernel needs 16-byte operand chunks and every buffer view
-    // (a 256-row K-major tile, or all K rows of an R-major operand) below 2^30 bytes.
+    // The fast kernel needs every buffer view (a 256-row K-major tile, or all K
+    // rows of an R-major operand) below 2^30 bytes and R-major operands in
+    // 16-byte chunks; K-major operands whose rows are not 16-byte aligned (odd
+    // K or leading dimension, e.g. P of P x V over 197 keys) take the ragged
+    // loader.
     const bool ldOk = prm.lda < (1LL << 21) && prm.ldb < (1LL << 21);
-    const long long viewA = ta ? (long long)prm.K * prm.lda * 2 : 256LL * prm.lda * 2;
-    const long long viewB = tb ? 256LL * prm.ldb * 2 : (long long)prm.K * prm.ldb * 2;
-    if (va && vb && ldOk && viewA < kMaxViewBytes && viewB < kMaxViewBytes) {
+    const long long viewA = ta ? (long long)prm.K * prm.lda * 2 : 256LL * prm.lda * 2 + 4;
+    const long long viewB = tb ? 256LL * prm.ldb * 2 + 4 : (long long)prm.K * prm.ldb * 2;
+    auto even = [](const void* q) { return (reinterpret_cast<uintptr_t>(q) & 1u) == 0; };
+    const bool aOk = ta ? va : (va || even(prm.A));
+    const bool bOk = tb ? (vb || even(prm.B)) : vb;
+    const bool rag = (!ta && !va) || (tb && !vb);
+    if (aOk && bOk && ldOk && viewA < kMaxViewBytes && viewB < kMaxViewBytes) {
         HalfFastParams f{};
         f.A = prm.A; f.B = prm.B; f.C = prm.C; f.M = prm.M; f.N = prm.N; f.K = prm.K;
         f.lda = (int)prm.lda; f.ldb = (int)prm.ldb; f.ldc = prm.ldc; f.sA = prm.sA; f.sB = prm.sB; f.sC = prm.sC;
         const bool vecC = (prm.N % 4 == 0) && (prm.ldc % 4 == 0) && (prm.sC % 4 == 0) &&
                           ((reinterpret_cast<uintptr_t>(prm.C) & 15u) == 0);
-        if (!ta && !tb) return launchFastC<BF16, false, false>(f, batch, vecC);
-        if (!ta && tb) return launchFastC<BF16, false, true>(f, batch, vecC);
-        if (ta && !tb) return launchFastC<BF16, true, false>(f, batch, vecC);
-        return launchFastC<BF16, true, true>(f, batch, vecC);
+        if (!ta && !tb) return launchFastR<BF16, false, false>(f, batch, vecC, rag);
+        if (!ta && tb) return launchFastR<BF16, false, true>(f, batch, vecC, rag);
+        if (ta && !tb) return launchFastR<BF16, true, false>(f, batch, vecC, rag);
+        return launchFastR<BF16, true, true>(f, batch, vecC, rag);
     }
     if (!ta && !tb) return launchGenericC<BF16, false, false>(prm, batch, va, vb);
     if (!ta && tb) return launchGenericC<BF16, false, true>(prm, batch, va, vb);

@@ -73,7 +73,7 @@ def test_attention_batched(hip, bf16):
 # the 128x128 tile (second) and the 64x64 tile (third); every one has ragged
 # M, N and a K that ends inside a 64-deep slice. The last shape has N % 4 != 0,
 # so C leaves through 32-bit stores.
-FAST_SHAPES = [(32, 296, 264, 136), (20, 392, 392, 72), (4, 296, 264, 136), (3, 104, 262, 200)]
+FAST_SHAPES = [(40, 392, 392, 136), (24, 392, 392, 72), (4, 296, 264, 136), (3, 104, 262, 200)]
 
 
 @pytest.mark.parametrize("bf16", [False, True], ids=["f16", "bf16"])
@@ -124,3 +124,55 @@ def test_half_known_answer(hip):
     dA, dB, dC = to_dev(hip, A), to_dev(hip, B), empty_dev(hip, (2, 2))
     hip.HIPBackend.matmulHalf(dA, dB, dC, 2, 2, 2)
     assert dC.numpy().tolist() == [[19, 22], [43, 50]]
+
+
+# K-major operands whose rows start at odd halves (odd K): the ragged loader.
+# (batch, M, N, K) chosen so the tile model picks, on a 256-CU MI355X, the
+# 256x256 tile (first), the 128x128 tile (second) and the 64x64 tile (third:
+# the ViT P.V shape, 197 keys). K ends 1, 13 and 5 halves into its last
+# 64-deep slice, so the zeroing of the halves past K (where the next row's
+# data lies) decides the result.
+RAGGED_SHAPES = [(16, 600, 1000, 65), (3, 1300, 1300, 77), (48, 197, 64, 197)]
+
+
+@pytest.mark.parametrize("bf16", [False, True], ids=["f16", "bf16"])
+@pytest.mark.parametrize("transB", [0, 1], ids=["NN", "NT"])
+@pytest.mark.parametrize("batch,M,N,K", RAGGED_SHAPES)
+def test_half_ragged_k(hip, bf16, transB, batch, M, N, K):
+    seed = batch + M + N + K + transB
+    A = O.randn((batch, M, K), seed)
+    B = O.randn((batch, N, K) if transB else (batch, K, N), seed + 1)
+    dA, dB = to_dev(hip, _bits(A, bf16)), to_dev(hip, _bits(B, bf16))
+    dC = empty_dev(hip, (batch, M, N))
+    ldb = K if transB else N
+    hip.HIPBackend.gemmStridedBatchedHalf(1 if bf16 else 0, 0, transB, batch, M, N, K, dA, K, M * K, dB, ldb, N * K,
+                                          dC, N, M * N)
+    C64, bound = O.gemm_f64(_round(A, bf16), _round(B, bf16), transB=bool(transB))
+    assert O.normalized_error(dC.numpy(), C64, bound) <= 1e-4
+
+
+@pytest.mark.parametrize("transB", [0, 1], ids=["NN", "NT"])
+@pytest.mark.parametrize("offA,offB", [(1, 3), (3, 1), (2, 0)])
+def test_half_ragged_views(hip, transB, offA, offB):
+    """Operands that start at odd halves (sub-buffer views), odd leading dimensions and
+    odd batch strides with an even K: only the alignment makes the K-major rows ragged."""
+    batch, M, N, K = 3, 70, 88, 96
+    lda = K + 3
+    ldb = (K + 5) if transB else N
+    sA, sB = M * lda + 7, (N * ldb + 9) if transB else K * ldb
+    A = O.randn((offA + batch * sA,), 21)
+    B = O.randn((offB + batch * sB,), 22)
+    dA, dB = to_dev(hip, _bits(A, False)), to_dev(hip, _bits(B, False))
+    dC = empty_dev(hip, (batch, M, N))
+    hip.HIPBackend.gemmStridedBatchedHalf(0, 0, transB, batch, M, N, K, int(dA) + 2 * offA, lda, sA,
+                                          int(dB) + 2 * offB, ldb, sB, dC, N, M * N)
+    Ar, Br = _round(A, False), _round(B, False)
+    C = dC.numpy()
+    for b in range(batch):
+        a = Ar[offA + b * sA:offA + b * sA + M * lda].reshape(M, lda)[:, :K]
+        if transB:
+            bm = Br[offB + b * sB:offB + b * sB + N * ldb].reshape(N, ldb)[:, :K]
+        else:
+            bm = Br[offB + b * sB:offB + b * sB + K * ldb].reshape(K, ldb)
+        C64, bound = O.gemm_f64(a, bm, transB=bool(transB))
+        assert O.normalized_error(C[b], C64, bound) <= 1e-4
