@@ -104,6 +104,111 @@ __global__ void maxpool_kernel(const float* __restrict__ x, float* __restrict__ 
     }
 }
 
+// The ResNet stem pooling (3x3, stride 2, pad 1; W a multiple of 4, H even):
+// one thread per pair of outputs (oh, 2j), (oh, 2j+1), whose windows cover
+// input columns 4j-1 .. 4j+3. Each window row is one 16-byte load of columns
+// 4j .. 4j+3 plus column 4j-1 from the neighbouring lane (a load of its own
+// for lane 0). The candidates are scanned in the same (kh, kw) order with the
+// same strict '>' as maxpool_kernel, so values and indices are identical.
+__global__ void maxpool_3s2_kernel(const float* __restrict__ x, float* __restrict__ y, int* __restrict__ idx,
+                                   long long planes, int H, int W) {
+    typedef float f4 __attribute__((ext_vector_type(4)));
+    const int Ho = H / 2, Wo = W / 2, J = W / 4;
+    const long long total = planes * Ho * J;
+    const int lane = threadIdx.x & 63;
+    // every lane of a wave runs the same trip count (the shuffle needs the whole wave)
+    const long long stride = (long long)gridDim.x * blockDim.x;
+    for (long long t0 = blockIdx.x * (long long)blockDim.x + (threadIdx.x & ~63); t0 < total; t0 += stride) {
+        const long long t = t0 + lane;
+        const bool active = t < total;
+        const long long tt = active ? t : total - 1;
+        const int j = (int)(tt % J);
+        const long long r = tt / J;
+        const int oh = (int)(r % Ho);
+        const long long pl = r / Ho;
+        const long long ib = pl * H * W;
+        float best0 = -1e30f, best1 = -1e30f;
+        int bi0 = -1, bi1 = -1;
+#pragma unroll
+        for (int kh = 0; kh < 3; ++kh) {
+            const int ih = 2 * oh - 1 + kh;
+            const bool rowOk = ih >= 0;   // ih <= H-1 always
+            const long long rb = ib + (long long)(rowOk ? ih : 0) * W;
+            const f4 q = rowOk ? *reinterpret_cast<const f4*>(x + rb + 4 * j) : f4{0.f, 0.f, 0.f, 0.f};
+            float left = __shfl_up(q[3], 1, 64);
+            if (lane == 0 && j > 0 && rowOk) left = x[rb + 4 * j - 1];
+            if (rowOk) {
+                const int c0 = (int)(rb - ib) + 4 * j;   // in-plane index of column 4j
+                // output 2j: columns 4j-1, 4j, 4j+1
+                if (j > 0 && left > best0) { best0 = left; bi0 = (int)(ib + c0 - 1); }
+                if (q[0] > best0) { best0 = q[0]; bi0 = (int)(ib + c0); }
+                if (q[1] > best0) { best0 = q[1]; bi0 = (int)(ib + c0 + 1); }
+                // output 2j+1: columns 4j+1, 4j+2, 4j+3
+                if (q[1] > best1) { best1 = q[1]; bi1 = (int)(ib + c0 + 1); }
+                if (q[2] > best1) { best1 = q[2]; bi1 = (int)(ib + c0 + 2); }
+                if (q[3] > best1) { best1 = q[3]; bi1 = (int)(ib + c0 + 3); }
+            }
+        }
+        if (active) {
+            const long long o = (pl * Ho + oh) * Wo + 2 * j;
+            typedef float f2 __attribute__((ext_vector_type(2)));
+            typedef int i2 __attribute__((ext_vector_type(2)));
+            *reinterpret_cast<f2*>(y + o) = f2{best0, best1};
+            if (idx) *reinterpret_cast<i2*>(idx + o) = i2{bi0, bi1};
+        }
+    }
+}
+
+// Backward of the stem pooling as a gather over 2x2 input blocks: input rows
+// 2a, 2a+1 and columns 2i, 2i+1 are covered only by outputs (a or a, a+1) x
+// (i or i, i+1), so a thread reads those four outputs once and adds, for each
+// of its four inputs, the gradients of the covering outputs whose saved index
+// is that input, in ascending (oh, ow) order as maxpool_backward_kernel does.
+__global__ void maxpool_3s2_backward_kernel(const float* __restrict__ gO, const int* __restrict__ idx,
+                                            float* __restrict__ gI, long long planes, int H, int W) {
+    typedef float f2 __attribute__((ext_vector_type(2)));
+    const int Ho = H / 2, Wo = W / 2;
+    const long long total = planes * Ho * Wo;   // one thread per 2x2 input block
+    for (long long t = blockIdx.x * (long long)blockDim.x + threadIdx.x; t < total;
+         t += (long long)gridDim.x * blockDim.x) {
+        const int i = (int)(t % Wo);
+        const long long r = t / Wo;
+        const int a = (int)(r % Ho);
+        const long long pl = r / Ho;
+        const long long ob = pl * Ho * Wo;
+        const bool a1 = a + 1 < Ho, i1 = i + 1 < Wo;
+        const long long o00 = ob + (long long)a * Wo + i;
+        const int x00 = idx[o00];
+        const int x01 = i1 ? idx[o00 + 1] : -1;
+        const int x10 = a1 ? idx[o00 + Wo] : -1;
+        const int x11 = (a1 && i1) ? idx[o00 + Wo + 1] : -1;
+        const float g00 = gO[o00];
+        const float g01 = i1 ? gO[o00 + 1] : 0.f;
+        const float g10 = a1 ? gO[o00 + Wo] : 0.f;
+        const float g11 = (a1 && i1) ? gO[o00 + Wo + 1] : 0.f;
+        const long long ib = pl * H * W;
+        const int f = (int)(ib + (long long)(2 * a) * W + 2 * i);   // flat index of input (2a, 2i)
+        // (2a, 2i): output (a, i) only
+        const float v00 = x00 == f ? 0.f + g00 : 0.f;   // 0 + g as the running sum would give (-0 -> +0)
+        // (2a, 2i+1): outputs (a, i), (a, i+1)
+        float v01 = 0.f;
+        if (x00 == f + 1) v01 += g00;
+        if (x01 == f + 1) v01 += g01;
+        // (2a+1, 2i): outputs (a, i), (a+1, i)
+        float v10 = 0.f;
+        if (x00 == f + W) v10 += g00;
+        if (x10 == f + W) v10 += g10;
+        // (2a+1, 2i+1): outputs (a, i), (a, i+1), (a+1, i), (a+1, i+1)
+        float v11 = 0.f;
+        if (x00 == f + W + 1) v11 += g00;
+        if (x01 == f + W + 1) v11 += g01;
+        if (x10 == f + W + 1) v11 += g10;
+        if (x11 == f + W + 1) v11 += g11;
+        *reinterpret_cast<f2*>(gI + f) = f2{v00, v01};
+        *reinterpret_cast<f2*>(gI + f + W) = f2{v10, v11};
+    }
+}
+
 // cpu_backend.ixx:937-955 as a gather: gI[i] = sum of gO[o] over the outputs o
 // (ascending) whose saved index is i.
 __global__ void maxpool_backward_kernel(const float* __restrict__ gO, const int* __restrict__ idx,
@@ -272,6 +377,15 @@ __global__ void add_kernel(const float* __restrict__ a, const float* __restrict_
     }
 }
 
+// 3x3 window, stride 2, pad 1 over an even H and W (the ResNet stem pooling):
+// Ho = H/2, Wo = W/2 and the outputs tile the input in 2x2 blocks.
+static bool stemPool(const PoolGeom& g) {
+    return g.KH == 3 && g.KW == 3 && g.SH == 2 && g.SW == 2 && g.PH == 1 && g.PW == 1 && g.H % 2 == 0 &&
+           g.W % 2 == 0;
+}
+static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+static bool aligned8(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 7u) == 0; }   // null passes
+
 static int poolGeom(const char* name, int N, int C, int H, int W, int KH, int KW, int SH, int SW, int PH, int PW,
                     PoolGeom& g) {
     if (N <= 0 || C <= 0 || H <= 0 || W <= 0 || KH <= 0 || KW <= 0 || SH <= 0 || SW <= 0 || PH < 0 || PW < 0)
@@ -297,6 +411,13 @@ int omHipMaxPool2d(const float* pIn, float* pOut, int* pIndices, int nN, int nC,
     PoolGeom g;
     if (poolGeom("omHipMaxPool2d", nN, nC, nH, nW, nKH, nKW, nSH, nSW, nPH, nPW, g)) return -1;
     if (!pIn || !pOut) return fail("omHipMaxPool2d: null pointer");
+    if (stemPool(g) && nW % 4 == 0 && aligned16(pIn) && aligned8(pOut) && aligned8(pIndices)) {
+        const long long planes = (long long)nN * nC;
+        hipLaunchKernelGGL(maxpool_3s2_kernel, dim3(gridFor(planes * g.Ho * (nW / 4))), dim3(256), 0, stream(), pIn,
+                           pOut, pIndices, planes, nH, nW);
+        OMHIP_CHECK_LAUNCH();
+        return 0;
+    }
     hipLaunchKernelGGL(maxpool_kernel, planeGrid((long long)nN * nC, g.Ho, g.Wo), dim3(64, 4), 0, stream(), pIn,
                        pOut, pIndices, g);
     OMHIP_CHECK_LAUNCH();
@@ -325,6 +446,13 @@ int omHipMaxPool2dBackwardEx(const float* pGradOut, const int* pIndices, float* 
     PoolGeom g;
     if (poolGeom("omHipMaxPool2dBackwardEx", nN, nC, nH, nW, nKH, nKW, nSH, nSW, nPH, nPW, g)) return -1;
     if (!pGradOut || !pIndices || !pGradIn) return fail("omHipMaxPool2dBackwardEx: null pointer");
+    if (stemPool(g) && aligned8(pGradIn)) {
+        const long long planes = (long long)nN * nC;
+        hipLaunchKernelGGL(maxpool_3s2_backward_kernel, dim3(gridFor(planes * g.Ho * g.Wo)), dim3(256), 0, stream(),
+                           pGradOut, pIndices, pGradIn, planes, nH, nW);
+        OMHIP_CHECK_LAUNCH();
+        return 0;
+    }
     hipLaunchKernelGGL(maxpool_backward_kernel, planeGrid((long long)nN * nC, nH, nW), dim3(64, 4), 0, stream(),
                        pGradOut, pIndices, pGradIn, g);
     OMHIP_CHECK_LAUNCH();

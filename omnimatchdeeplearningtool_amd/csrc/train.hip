@@ -22,6 +22,7 @@
 // workgroup sums a contiguous range of images in a fixed order, a second
 // kernel adds the parts in order — deterministic.
 #include "omhip_internal.hpp"
+#include "buffer_io.hpp"
 #include "conv.hpp"
 #include "../../include/omhip.h"
 
@@ -56,20 +57,22 @@ __host__ __device__ inline long long phaseOffset(int Cout, int Cin, int KH, int 
 
 // Phase (a, b) sub-kernel: wf[ci][co][jf][lf] = W[co][ci][ra + s*(KHa-1-jf)][rb + s*(KWb-1-lf)].
 // Every tap belongs to exactly one phase, so the sub-kernels tile a buffer of W's size.
+// One thread per weight (reads coalesced); all index arithmetic is 32-bit
+// (Cout*Cin*KH*KW < 2^28 by the conv limits).
 __global__ void phase_flip_kernel(const float* __restrict__ w, float* __restrict__ wf, int Cout, int Cin, int KH,
                                   int KW, int s, int p) {
-    const long long total = (long long)Cout * Cin * KH * KW;
-    for (long long i = blockIdx.x * (long long)blockDim.x + threadIdx.x; i < total;
-         i += (long long)gridDim.x * blockDim.x) {
-        const int kw = (int)(i % KW);
-        const int kh = (int)((i / KW) % KH);
-        const int ci = (int)((i / ((long long)KW * KH)) % Cin);
-        const int co = (int)(i / ((long long)KW * KH * Cin));
+    const int taps = KH * KW;
+    const int total = Cout * Cin * taps;
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < total; i += gridDim.x * blockDim.x) {
+        const int t = i / taps;
+        const int tap = i - t * taps;
+        const int kh = tap / KW, kw = tap - (tap / KW) * KW;
+        const int co = t / Cin, ci = t - (t / Cin) * Cin;
         const int a = ((kh % s) - (p % s) + s) % s;
         const int b = ((kw % s) - (p % s) + s) % s;
         const int KHa = phaseTaps(KH, s, p, a), KWb = phaseTaps(KW, s, p, b);
         const int jf = KHa - 1 - kh / s, lf = KWb - 1 - kw / s;
-        wf[phaseOffset(Cout, Cin, KH, KW, s, p, a, b) + (((long long)ci * Cout + co) * KHa + jf) * KWb + lf] = w[i];
+        wf[phaseOffset(Cout, Cin, KH, KW, s, p, a, b) + ((ci * Cout + co) * KHa + jf) * KWb + lf] = w[i];
     }
 }
 
@@ -346,6 +349,8 @@ int omHipConv2dBackwardInput(const float* pGradOutput, const float* pWeight, flo
     if (!pGradOutput || !pWeight || !pGradInput) return fail("%s: null pointer", name);
     const int s = nStride, p = nPad;
     const long long wsz = (long long)nCout * nCin * nKH * nKW;
+    if (wsz * 4 > (long long)kMaxBufferBytes)
+        return fail("%s: weights exceed the 2^30-byte buffer range of this kernel", name);
     // Pixels of a phase without taps (stride > kernel) get no contribution.
     bool emptyPhase = false;
     for (int a = 0; a < std::min(s, nH); ++a)

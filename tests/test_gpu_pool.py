@@ -55,6 +55,34 @@ def test_maxpool(hip, g):
     assert np.array_equal(bits(dy.numpy()), bits(y_ref))
 
 
+# The stem pooling (3x3, stride 2, pad 1, even H and W) has its own kernels:
+# a paired forward when W % 4 == 0 and a 2x2-block gather backward. Planes: a
+# constant plane (every window ties: the first candidate in (kh, kw) order
+# wins), a plane of large values at odd (row, col) (each the maximum of up to
+# four windows, so the backward adds several gradients into one input), and
+# random planes. W % 4 != 0 exercises the general forward with the fast backward.
+@pytest.mark.parametrize("shape", [(2, 4, 8, 12), (1, 3, 6, 10), (2, 3, 16, 16), (1, 2, 2, 4)],
+                         ids=lambda v: "N{}C{}H{}W{}".format(*v))
+def test_maxpool_stem_paths(hip, shape):
+    N, C, H, W = shape
+    x = O.randn((N, C, H, W), 100 + H + W)
+    x[0, 0] = 0.25
+    if C > 1:
+        x[0, 1] = -1.0
+        x[0, 1, 1::2, 1::2] = 5.0 + np.arange((H // 2) * (W // 2), dtype=np.float32).reshape(H // 2, W // 2) % 3
+    y_ref, i_ref = O.maxpool2d(x, 3, 2, 1)
+    dx, dy, di = to_dev(hip, x), empty_dev(hip, y_ref.shape), empty_dev(hip, y_ref.shape, np.int32)
+    hip.HIPBackend.maxPool2d(dx, dy, di, N, C, H, W, 3, 3, 2, 1)
+    assert np.array_equal(bits(dy.numpy()), bits(y_ref))
+    assert np.array_equal(di.numpy(), i_ref)
+    gO = O.randn(y_ref.shape, 200 + H)
+    gO[0, 0, 0, 0] = -0.0
+    gi_ref = O.maxpool2d_backward(gO, i_ref, H, W)
+    dg, dgi = to_dev(hip, gO), to_dev(hip, np.full(x.shape, 3.0, np.float32))
+    hip.HIPBackend.maxPool2dBackwardEx(dg, di, dgi, N, C, H, W, 3, 3, 2, 1)
+    assert np.array_equal(bits(dgi.numpy()), bits(gi_ref))
+
+
 @pytest.mark.parametrize("g", POOL, ids=_pid)
 def test_avgpool(hip, g):
     N, C, H, W, K, s, p = g
