@@ -149,20 +149,28 @@ __global__ __launch_bounds__(256) void chan_partial_kernel(const float* __restri
     const float m = MODE == 1 ? partSum(prev, c, P, 0) / cnt : (MODE == 2 ? mean[c] : 0.f);
     const float is = MODE == 2 ? invStd[c] : 0.f;
     float v[2] = {0.f, 0.f};
-    for (int n = n0; n < n1; ++n) {
-        const long long base = ((long long)n * C + c) * HW;
-        for (int s = threadIdx.x; s < HW; s += 256) {
-            if constexpr (MODE == 0) {
-                v[0] += x[base + s];
-            } else if constexpr (MODE == 1) {
-                const float d = x[base + s] - m;
-                v[0] = __builtin_fmaf(d, d, v[0]);
-            } else {
-                const float g = (mask && !(mask[base + s] > 0.f)) ? 0.f : dy[base + s];
-                const float xh = (x[base + s] - m) * is;
-                v[0] = __builtin_fmaf(g, xh, v[0]);
-                v[1] += g;
-            }
+    // The part's images n0..n1-1 as one sequence of (image, pixel) pairs, 256
+    // consecutive pairs per trip, so small planes keep every lane busy.
+    const int dn = 256 / HW, ds = 256 % HW;
+    int n = n0 + (int)threadIdx.x / HW, s = (int)threadIdx.x % HW;
+    while (n < n1) {
+        const long long e = ((long long)n * C + c) * HW + s;
+        if constexpr (MODE == 0) {
+            v[0] += x[e];
+        } else if constexpr (MODE == 1) {
+            const float d = x[e] - m;
+            v[0] = __builtin_fmaf(d, d, v[0]);
+        } else {
+            const float g = (mask && !(mask[e] > 0.f)) ? 0.f : dy[e];
+            const float xh = (x[e] - m) * is;
+            v[0] = __builtin_fmaf(g, xh, v[0]);
+            v[1] += g;
+        }
+        n += dn;
+        s += ds;
+        if (s >= HW) {
+            s -= HW;
+            ++n;
         }
     }
     blockSum<2>(v, red);
@@ -196,22 +204,57 @@ __global__ void bn_train_apply_kernel(const float* __restrict__ x, float* __rest
                                       const float* __restrict__ part0, const float* __restrict__ part1, int P,
                                       float cnt, float eps, float momentum, const float* __restrict__ res, int act,
                                       float* savedMean, float* savedInvStd, float* runMean, float* runVar, int C,
-                                      int HW, int plane0) {
+                                      int HW, int plane0, int G, int planes) {
 #pragma clang fp contract(off)
-    const int plane = plane0 + blockIdx.y;
+    // G == 1: workgroup (bx, y) covers plane plane0 + y (channel uniform across
+    // the workgroup). G > 1: planes of HW <= 128 pixels, G of them per workgroup,
+    // thread t on pixel t % HW of plane t / HW.
+    int plane, i0, di;
+    if (G == 1) {
+        plane = plane0 + blockIdx.y;
+        i0 = blockIdx.x * blockDim.x + threadIdx.x;
+        di = gridDim.x * blockDim.x;
+    } else {
+        plane = plane0 + blockIdx.y * G + (int)threadIdx.x / HW;
+        i0 = (int)threadIdx.x % HW;
+        di = HW;
+        if ((int)threadIdx.x >= G * HW || plane >= planes) return;
+    }
     const int c = plane % C;
-    const float mu = partSum(part0, c, P, 0) / cnt;
-    const float var = partSum(part1, c, P, 0) / cnt;
+    const long long base = (long long)plane * HW;
+    // the first (up to) four elements are loaded before the statistics so the
+    // two memory latencies overlap (planes of up to 1024 pixels need no more)
+    constexpr int PRE = 4;
+    float xv[PRE], rv[PRE];
+#pragma unroll
+    for (int k = 0; k < PRE; ++k) {
+        const int i = i0 + k * di;
+        xv[k] = i < HW ? x[base + i] : 0.f;
+        rv[k] = (res && i < HW) ? res[base + i] : 0.f;
+    }
+    const float sum0 = G == 1 ? partSum(part0, c, P, 0) : partSumSerial(part0, c, P, 0);
+    const float sum1 = G == 1 ? partSum(part1, c, P, 0) : partSumSerial(part1, c, P, 0);
+    const float mu = sum0 / cnt;
+    const float var = sum1 / cnt;
     const float inv = 1.0f / sqrtf(var + eps);
-    if (plane < C && blockIdx.x == 0 && threadIdx.x == 0) {
+    if (plane < C && (G == 1 ? blockIdx.x == 0 && threadIdx.x == 0 : i0 == 0)) {
         if (savedMean) savedMean[c] = mu;
         if (savedInvStd) savedInvStd[c] = inv;
         runMean[c] = __builtin_fmaf(1.0f - momentum, runMean[c], momentum * mu);
         runVar[c] = __builtin_fmaf(1.0f - momentum, runVar[c], momentum * var);
     }
     const float g = gamma[c], b = beta[c];
-    const long long base = (long long)plane * HW;
-    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < HW; i += gridDim.x * blockDim.x) {
+#pragma unroll
+    for (int k = 0; k < PRE; ++k) {
+        const int i = i0 + k * di;
+        if (i < HW) {
+            float v = __builtin_fmaf(g, (xv[k] - mu) * inv, b);
+            if (res) v = v + rv[k];
+            if (act == 1) v = v > 0.f ? v : 0.f;
+            y[base + i] = v;
+        }
+    }
+    for (int i = i0 + PRE * di; i < HW; i += di) {
         float v = __builtin_fmaf(g, (x[base + i] - mu) * inv, b);
         if (res) v = v + res[base + i];
         if (act == 1) v = v > 0.f ? v : 0.f;
@@ -227,31 +270,73 @@ __global__ void bn_backward_apply_kernel(const float* __restrict__ dy, const flo
                                          const float* __restrict__ x, const float* __restrict__ mean,
                                          const float* __restrict__ invStd, const float* __restrict__ gamma,
                                          const float* __restrict__ part, int P, float* gradGamma, float* gradBeta,
-                                         float* __restrict__ dx, int C, int HW, float cnt, float invCnt, int plane0) {
-    const int plane = plane0 + blockIdx.y;
+                                         float* __restrict__ dx, int C, int HW, float cnt, float invCnt, int plane0,
+                                         int G, int planes) {
+    // plane / pixel assignment as bn_train_apply_kernel
+    int plane, i0, di;
+    if (G == 1) {
+        plane = plane0 + blockIdx.y;
+        i0 = blockIdx.x * blockDim.x + threadIdx.x;
+        di = gridDim.x * blockDim.x;
+    } else {
+        plane = plane0 + blockIdx.y * G + (int)threadIdx.x / HW;
+        i0 = (int)threadIdx.x % HW;
+        di = HW;
+        if ((int)threadIdx.x >= G * HW || plane >= planes) return;
+    }
     const int c = plane % C;
+    const long long base = (long long)plane * HW;
+    // first elements loaded before the statistics, as in bn_train_apply_kernel
+    constexpr int PRE = 4;
+    float dv[PRE], xv[PRE];
+#pragma unroll
+    for (int k = 0; k < PRE; ++k) {
+        const int i = i0 + k * di;
+        dv[k] = (i < HW && !(mask && !(mask[base + i] > 0.f))) ? dy[base + i] : 0.f;
+        xv[k] = i < HW ? x[base + i] : 0.f;
+    }
     const float m = mean[c], is = invStd[c], g = gamma[c];
-    const float sg = partSum(part, c, P, 0), sb = partSum(part, c, P, 1);
-    if (plane < C && blockIdx.x == 0 && threadIdx.x == 0) {
+    const float sg = G == 1 ? partSum(part, c, P, 0) : partSumSerial(part, c, P, 0);
+    const float sb = G == 1 ? partSum(part, c, P, 1) : partSumSerial(part, c, P, 1);
+    if (plane < C && (G == 1 ? blockIdx.x == 0 && threadIdx.x == 0 : i0 == 0)) {
         if (gradGamma) gradGamma[c] = sg;
         if (gradBeta) gradBeta[c] = sb;
     }
     const float k = g * is * invCnt;
-    const long long base = (long long)plane * HW;
-    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < HW; i += gridDim.x * blockDim.x) {
+#pragma unroll
+    for (int j = 0; j < PRE; ++j) {
+        const int i = i0 + j * di;
+        if (i < HW) {
+            const float xh = (xv[j] - m) * is;
+            dx[base + i] = k * __builtin_fmaf(-xh, sg, __builtin_fmaf(cnt, dv[j], -sb));
+        }
+    }
+    for (int i = i0 + PRE * di; i < HW; i += di) {
         const float d = (mask && !(mask[base + i] > 0.f)) ? 0.f : dy[base + i];
         const float xh = (x[base + i] - m) * is;
         dx[base + i] = k * __builtin_fmaf(-xh, sg, __builtin_fmaf(cnt, d, -sb));
     }
 }
 
-// Launches a per-plane kernel over N*C planes (grid.y <= 65535 per launch).
+// Launches a per-plane kernel over N*C planes: one workgroup row per plane
+// (grid.y <= 65535 per launch), or, for planes of at most 128 pixels, G =
+// 256 / HW planes per workgroup. launch(grid, firstPlane, G).
 template <class F>
 static int forPlanes(int planes, int HW, F launch) {
+    const int G = HW <= 128 ? 256 / HW : 1;
+    if (G > 1) {
+        const long long groups = ((long long)planes + G - 1) / G;
+        for (long long g0 = 0; g0 < groups; g0 += 65535) {
+            const int cnt = (int)std::min<long long>(65535, groups - g0);
+            launch(dim3(1, cnt), (int)(g0 * G), G);
+            OMHIP_CHECK_LAUNCH();
+        }
+        return 0;
+    }
     const int bx = std::max(1, std::min((HW + 255) / 256, std::max(1, 4096 / std::max(1, planes))));
     for (int p0 = 0; p0 < planes; p0 += 65535) {
         const int cnt = std::min(65535, planes - p0);
-        launch(dim3(bx, cnt), p0);
+        launch(dim3(bx, cnt), p0, 1);
         OMHIP_CHECK_LAUNCH();
     }
     return 0;
@@ -290,9 +375,9 @@ int batchNorm2dTrainAct(const float* x, float* y, const float* gamma, const floa
     hipLaunchKernelGGL(chan_partial_kernel<1>, dim3(C, P), dim3(256), 0, stream(), x, nullptr, nullptr, nullptr,
                        nullptr, part0, part1, N, C, HW, P, cnt);
     OMHIP_CHECK_LAUNCH();
-    return forPlanes(N * C, HW, [&](dim3 g, int p0) {
+    return forPlanes(N * C, HW, [&](dim3 g, int p0, int G) {
         hipLaunchKernelGGL(bn_train_apply_kernel, g, dim3(256), 0, stream(), x, y, gamma, beta, part0, part1, P, cnt,
-                           eps, momentum, res, act, savedMean, savedInvStd, runMean, runVar, C, HW, p0);
+                           eps, momentum, res, act, savedMean, savedInvStd, runMean, runVar, C, HW, p0, G, N * C);
     });
 }
 
@@ -318,9 +403,9 @@ static int batchNorm2dBackwardMasked(const char* name, const float* gO, const fl
     const long long cntL = (long long)N * HW;
     const float fcnt = (float)cntL;
     const float invCnt = 1.0f / fcnt;
-    return forPlanes(N * C, HW, [&](dim3 g, int p0) {
+    return forPlanes(N * C, HW, [&](dim3 g, int p0, int G) {
         hipLaunchKernelGGL(bn_backward_apply_kernel, g, dim3(256), 0, stream(), gO, mask, x, mean, invStd, gamma, part,
-                           P, gGamma, gBeta, gI, C, HW, fcnt, invCnt, p0);
+                           P, gGamma, gBeta, gI, C, HW, fcnt, invCnt, p0, G, N * C);
     });
 }
 
