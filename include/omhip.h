@@ -152,7 +152,12 @@ int omHipGemmStridedBatched(int bTransA, int bTransB, int nBatch, int nM, int nN
 /* replaces omCudaTranspose (cuh:117): out[c,r] = in[r,c]; CPUBackend::transpose2d cpu_backend.ixx:1535-1539 */
 int omHipTranspose(const float* pIn, float* pOut, int nRows, int nCols);
 
-/* ===== conv2d / batchnorm (cuda_kernels.cuh:136-146, :165-170) ===== */
+/* ===== conv2d / batchnorm (cuda_kernels.cuh:136-146, :165-170) =====
+ * Size limits of the implicit-GEMM convolutions (forward, fused and gradient
+ * entries): one image's input with its padding margin below 2^29 bytes, one
+ * image's output at most 2^30 bytes, the weights at most 2^30 bytes,
+ * KH, KW < 65536 and H + pad, W + pad < 65535. Larger batches are processed in
+ * chunks internally; a call outside these limits returns -1 with a message. */
 
 /* replaces omCudaConv2d (cuh:136): NCHW conv, symmetric stride/pad, dilation 1,
  * groups 1; pBias may be NULL. CPUBackend::conv2d cpu_backend.ixx:619-658 */
