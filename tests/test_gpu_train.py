@@ -177,7 +177,9 @@ def test_conv_backward_weight_chunked(hip):
     assert O.normalized_error(got[rows], ref, bound) <= TOL
 
 
-BN_SHAPES = [(4, 8, 7, 9), (8, 64, 28, 28), (32, 16, 7, 7), (1, 3, 1, 1), (2, 300, 5, 5)]
+# planes of 49 and fewer pixels go several to a workgroup; 6400 pixels take
+# several workgroups per plane
+BN_SHAPES = [(4, 8, 7, 9), (8, 64, 28, 28), (32, 16, 7, 7), (1, 3, 1, 1), (2, 300, 5, 5), (2, 4, 80, 80)]
 
 
 @pytest.mark.parametrize("shape", BN_SHAPES, ids=lambda s: "N{}C{}H{}W{}".format(*s))
@@ -236,7 +238,7 @@ def test_batchnorm_backward(hip, shape):
 
 
 # Fused training passes: each must equal the separate reference ops bit for bit.
-FUSE_SHAPES = [(4, 8, 7, 9), (8, 64, 28, 28), (2, 300, 5, 5)]
+FUSE_SHAPES = [(4, 8, 7, 9), (8, 64, 28, 28), (2, 300, 5, 5), (2, 4, 80, 80)]
 
 
 @pytest.mark.parametrize("shape", FUSE_SHAPES, ids=lambda s: "N{}C{}H{}W{}".format(*s))
