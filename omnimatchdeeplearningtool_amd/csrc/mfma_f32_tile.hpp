@@ -140,44 +140,6 @@ __device__ __forceinline__ void mma_slice(const float* __restrict__ sA, const fl
     const int li = lane & 31;
     const int h = lane >> 5;
     const int kb = h * Cfg::KH;
-#ifdef OMHIP_MMA_PREFETCH
-    float a[Cfg::KH / 4][Cfg::FM][4], b[Cfg::KH / 4][Cfg::FN][4];
-#pragma unroll
-    for (int u = 0; u < Cfg::KH / 4; ++u) {
-#pragma unroll
-        for (int fm = 0; fm < Cfg::FM; ++fm) {
-            const int row = wm * Cfg::WM + fm * 32 + li;
-            if constexpr (A_KMAJOR) {
-                const f32x4 v = *reinterpret_cast<const f32x4*>(sA + row * SA::LD + kb + 4 * u);
-                a[u][fm][0] = v[0]; a[u][fm][1] = v[1]; a[u][fm][2] = v[2]; a[u][fm][3] = v[3];
-            } else {
-#pragma unroll
-                for (int s = 0; s < 4; ++s) a[u][fm][s] = sA[(kb + 4 * u + s) * SA::LD + row];
-            }
-        }
-#pragma unroll
-        for (int fn = 0; fn < Cfg::FN; ++fn) {
-            const int col = wn * Cfg::WN + fn * 32 + li;
-            if constexpr (B_KMAJOR) {
-                const f32x4 v = *reinterpret_cast<const f32x4*>(sB + col * SB::LD + kb + 4 * u);
-                b[u][fn][0] = v[0]; b[u][fn][1] = v[1]; b[u][fn][2] = v[2]; b[u][fn][3] = v[3];
-            } else {
-#pragma unroll
-                for (int s = 0; s < 4; ++s) b[u][fn][s] = sB[(kb + 4 * u + s) * SB::LD + col];
-            }
-        }
-    }
-#pragma unroll
-    for (int u = 0; u < Cfg::KH / 4; ++u)
-#pragma unroll
-        for (int s = 0; s < 4; ++s)
-#pragma unroll
-            for (int fm = 0; fm < Cfg::FM; ++fm)
-#pragma unroll
-                for (int fn = 0; fn < Cfg::FN; ++fn)
-                    acc[fm][fn] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[u][fm][s], b[u][fn][s], acc[fm][fn], 0, 0, 0);
-    return;
-#endif
 #pragma unroll
     for (int u = 0; u < Cfg::KH / 4; ++u) {
         float a[Cfg::FM][4], b[Cfg::FN][4];
