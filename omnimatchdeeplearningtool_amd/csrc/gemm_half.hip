@@ -7,21 +7,22 @@
 // halfToFloat(A), halfToFloat(B), matmul would, with fp32 accumulation.
 //
 // Two kernels:
-//  * gemm_half_fast: operands whose contiguous axis, leading dimension and base
-//    are multiples of 8 halves (every layout the networks produce). Slices are
-//    fetched with raw buffer loads whose per-lane offset is fixed for the whole
-//    K walk (the slice start rides in the scalar offset; rows past the matrix
-//    fall outside the buffer range and read 0), so the mainloop spends almost
-//    no VALU on addressing. Both operands sit K-contiguous in LDS ([R][BK+8]
-//    halves), so an MFMA fragment (8 consecutive k of one row) is one
-//    ds_read_b128. An operand that is R-contiguous in HBM (B of A*B, A of
-//    A^T*B) is loaded as 8x8 blocks and transposed in registers with v_perm
-//    before the LDS store. The MFMA takes the B fragment as its first operand,
-//    so each lane ends up holding 4 consecutive output columns and the fp32
-//    tile leaves in 128-bit stores.
-//    K-major operands whose rows are only 2-byte aligned (odd K or leading
-//    dimension) are fetched 16 bytes at a time from the dword boundary below
-//    and funnel-shifted into place.
+//  * gemm_half_fast: R-major operands whose contiguous axis, leading dimension
+//    and base are multiples of 8 halves, and K-major operands of any alignment
+//    (every layout the networks produce). Slices are fetched with raw buffer
+//    loads whose per-lane offset is fixed for the whole K walk (the slice
+//    start rides in the scalar offset; rows past the matrix fall outside the
+//    buffer range and read 0), so the mainloop spends almost no VALU on
+//    addressing. Both operands sit K-contiguous in LDS, so an MFMA fragment (8
+//    consecutive k of one row) is one ds_read_b128. A 16-byte-aligned K-major
+//    operand goes straight from the buffer into LDS (buffer_load ... lds, a
+//    swizzled unpadded layout); one that is only 2-byte aligned (odd K or
+//    leading dimension) is fetched 16 bytes at a time from the dword boundary
+//    below and funnel-shifted into place in registers. An operand that is
+//    R-contiguous in HBM (B of A*B, A of A^T*B) is loaded as 8x8 blocks and
+//    transposed in registers with v_perm before the LDS store. The MFMA takes
+//    the B fragment as its first operand, so each lane ends up holding 4
+//    consecutive output columns and the fp32 tile leaves in 128-bit stores.
 //  * gemm_half_generic: any other layout (element loads with bounds checks).
 //
 // Within a 16-deep MFMA step the two 32-lane halves supply k = 0..7 and
@@ -288,60 +289,11 @@ struct HalfFastParams {
     int tilesM, tilesN;
 };
 
-// K-major operand: element (r,k) at P[r*ld + k]. An R x BK slice is R*BK/8
-// 16-byte chunks; chunk e is (row e / (BK/8), k 8*(e % (BK/8))), so 8
-// consecutive lanes read one row's 128 contiguous bytes. The buffer view starts
-// at the tile's first row and ends after row rowsValid-1's K-th element, so
-// rows past the matrix read 0; chunks past K are masked on the last slice.
-template <int R, int BK, int NT>
-struct KMajorSlice {
-    static constexpr int CH = BK / 8;
-    static constexpr int PER_T = R * CH / NT;
-    static_assert(R * CH % NT == 0, "slice must split evenly");
-    static constexpr int NLOADS = PER_T, NSTORES = PER_T;   // per thread and slice
-    struct Regs {
-        u32x4 v[PER_T];
-    };
-    __amdgpu_buffer_rsrc_t r;
-    uint32_t voff[PER_T];
-
-    __device__ void init(const uint16_t* base, int ld, int rowsValid, int K, int tid) {
-        const int rv = rowsValid < R ? rowsValid : R;
-        r = halfRsrc(base, ((uint32_t)(rv - 1) * (uint32_t)ld + (uint32_t)K) * 2u);
-#pragma unroll
-        for (int i = 0; i < PER_T; ++i) {
-            const int e = tid + i * NT;
-            voff[i] = ((uint32_t)(e / CH) * (uint32_t)ld + (uint32_t)(e % CH) * 8u) * 2u;
-        }
-    }
-    // FULL: the slice lies inside K (no per-chunk test).
-    template <bool FULL>
-    __device__ void load(int k0, int K, int tid, Regs& g) const {
-        const uint32_t soff = (uint32_t)k0 * 2u;
-        if (FULL || k0 + BK <= K) {
-#pragma unroll
-            for (int i = 0; i < PER_T; ++i) g.v[i] = ld128(r, voff[i], soff);
-        } else {
-#pragma unroll
-            for (int i = 0; i < PER_T; ++i) {
-                const int kc = ((tid + i * NT) % CH) * 8;
-                g.v[i] = ld128(r, (k0 + kc < K) ? voff[i] : kOOBH, soff);   // K % 8 == 0: all-or-none
-            }
-        }
-    }
-    template <int LD>
-    __device__ void store(uint16_t* s, int tid, const Regs& g) const {
-#pragma unroll
-        for (int i = 0; i < PER_T; ++i) {
-            const int e = tid + i * NT;
-            *reinterpret_cast<u32x4*>(s + (e / CH) * LD + (e % CH) * 8) = g.v[i];
-        }
-    }
-};
-
 // K-major operand whose rows start at any half (an odd leading dimension,
-// base or batch stride, e.g. P of P x V with 197 keys). Chunks are laid out as
-// in KMajorSlice; a chunk that starts at half h is fetched as the 16 bytes at
+// base or batch stride, e.g. P of P x V with 197 keys), through registers into
+// padded LDS rows ([R][BK+8] halves). An R x BK slice is R*BK/8 chunks of 8
+// halves; chunk e is (row e / (BK/8), k 8*(e % (BK/8))), so 8 consecutive lanes
+// cover one row's 128 bytes. A chunk that starts at half h is fetched as the 16 bytes at
 // the dword boundary below it plus the next dword, and shifted down by 16 bits
 // when h is odd. The view starts at the dword holding the tile's first element
 // and ends at the dword holding row rowsValid-1's K-th element (the 2 bytes
@@ -351,6 +303,7 @@ struct KMajorSlice {
 // last slice: there the next row's data lies, not the end of the view.
 template <int R, int BK, int NT>
 struct KMajorRaggedSlice {
+    static constexpr bool DMA = false, SWZ = false;
     static constexpr int CH = BK / 8;
     static constexpr int PER_T = R * CH / NT;
     static_assert(R * CH % NT == 0, "slice must split evenly");
@@ -406,8 +359,73 @@ struct KMajorRaggedSlice {
     }
 };
 
+// K-major operand in 16-byte chunks, loaded straight into LDS
+// (buffer_load_dwordx4 ... lds): one instruction writes 64 lanes x 16 bytes
+// contiguously at the LDS address in m0, lane L at +16L, so 8 rows of 64 halves
+// per instruction, with no VGPR staging and no ds_write. The LDS rows are
+// unpadded (BK = 64 halves) and the 16-byte chunk c of row r sits in slot
+// c ^ ((r >> 1) & 7): the 16 lanes of a fragment read (rows r0 .. r0+15, one
+// chunk) then hit 16 distinct 16-byte bank groups. Lane L of the instruction
+// that fills rows 8j .. 8j+7 therefore fetches chunk (L % 8) ^ ((r >> 1) & 7) of
+// row r = 8j + L / 8. Lanes past the matrix rows or past K use an offset
+// outside the buffer view, for which the load writes zeros.
+typedef __attribute__((address_space(3))) void* LdsPtr;
+
+template <int R, int BK, int NT>
+struct KMajorDmaSlice {
+    static_assert(BK == 64, "8 chunks of 8 halves per row");
+    static constexpr bool DMA = true, SWZ = true;
+    static constexpr int NW = NT / 64;
+    static constexpr int INSTR = R / 8 / NW;   // instructions per wave and slice
+    static_assert(R % (8 * NW) == 0, "rows must split evenly over the waves");
+    static constexpr int NLOADS = INSTR, NSTORES = 0;
+    struct Regs {};
+    __amdgpu_buffer_rsrc_t r;
+    uint32_t voff[INSTR];
+    uint32_t kc[INSTR];   // k offset (halves) of the lane's chunk within the slice
+    int wave;
+
+    __device__ void init(const uint16_t* base, int ld, int rowsValid, int K, int tid) {
+        const int rv = rowsValid < R ? rowsValid : R;
+        r = halfRsrc(base, ((uint32_t)(rv - 1) * (uint32_t)ld + (uint32_t)K) * 2u);
+        wave = tid >> 6;
+        const int lane = tid & 63;
+#pragma unroll
+        for (int i = 0; i < INSTR; ++i) {
+            const int row = 8 * (wave + i * NW) + lane / 8;
+            const int c = (lane & 7) ^ ((row >> 1) & 7);
+            kc[i] = (uint32_t)c * 8u;
+            voff[i] = row < rv ? ((uint32_t)row * (uint32_t)ld + (uint32_t)c * 8u) * 2u : kOOBH;
+        }
+    }
+    // Writes the slice starting at k0 into dst (this operand's region of an LDS stage).
+    template <bool FULL>
+    __device__ void dma(int k0, int K, uint16_t* dst) const {
+        const uint32_t soff = (uint32_t)k0 * 2u;
+#pragma unroll
+        for (int i = 0; i < INSTR; ++i) {
+            const uint32_t vo = (FULL || k0 + (int)kc[i] < K) ? voff[i] : kOOBH;   // K % 8 == 0: whole chunks
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (LdsPtr)(dst + (wave + i * NW) * 8 * BK), 16, vo, soff, 0, 0);
+        }
+    }
+    template <bool FULL>
+    __device__ void load(int, int, int, Regs&) const {}
+    template <int LD>
+    __device__ void store(uint16_t*, int, const Regs&) const {}
+};
+
 template <bool RAG, int R, int BK, int NT>
-using KMajorFor = std::conditional_t<RAG, KMajorRaggedSlice<R, BK, NT>, KMajorSlice<R, BK, NT>>;
+using KMajorFor = std::conditional_t<RAG, KMajorRaggedSlice<R, BK, NT>, KMajorDmaSlice<R, BK, NT>>;
+
+// LDS layout of one operand's slice: padded rows (register path) or
+// unpadded swizzled rows (DMA path); offset (halves) of chunk c of row r.
+template <bool SWZ, int LDP, int BK>
+__device__ __forceinline__ int ldsChunk(int r, int c) {
+    if constexpr (SWZ)
+        return r * BK + ((c ^ ((r >> 1) & 7)) << 3);
+    else
+        return r * LDP + (c << 3);
+}
 
 // R-major operand: element (r,k) at P[k*ld + r]. A slice is (R/8) x (BK/8)
 // blocks of 8 k x 8 r; block e is (rb = e / (BK/8), kb = e % (BK/8)). A thread
@@ -418,6 +436,7 @@ using KMajorFor = std::conditional_t<RAG, KMajorRaggedSlice<R, BK, NT>, KMajorSl
 // columns are pointed outside the view.
 template <int R, int BK, int NT>
 struct RMajorSlice {
+    static constexpr bool DMA = false, SWZ = false;
     static constexpr int KB = BK / 8;
     static constexpr int BLKS = (R / 8) * KB;
     static constexpr bool PARTIAL = BLKS < NT;   // only threads < BLKS carry a block
@@ -503,17 +522,29 @@ __device__ __forceinline__ void staticFor(F&& f) {
 
 // Fragments of 16-deep MFMA step s: 8 consecutive k (lane half h: k = 16s+8h ..)
 // of rows li of each 32-row block of the wave's sub-tile.
-template <class Cfg>
+template <class Cfg, bool SWZA, bool SWZB>
 __device__ __forceinline__ void readFrags(const uint16_t* sA, const uint16_t* sB, int s, u32x4 (&a)[Cfg::FM],
                                           u32x4 (&b)[Cfg::FN], int wm, int wn, int li, int h) {
-    const int kc = s * 16 + h * 8;
+    const int c = s * 2 + h;   // chunk of 8 k
 #pragma unroll
     for (int fm = 0; fm < Cfg::FM; ++fm)
-        a[fm] = *reinterpret_cast<const u32x4*>(sA + (wm * Cfg::WM + fm * 32 + li) * Cfg::LD + kc);
+        a[fm] = *reinterpret_cast<const u32x4*>(sA + ldsChunk<SWZA, Cfg::LD, Cfg::BK>(wm * Cfg::WM + fm * 32 + li, c));
 #pragma unroll
     for (int fn = 0; fn < Cfg::FN; ++fn)
-        b[fn] = *reinterpret_cast<const u32x4*>(sB + (wn * Cfg::WN + fn * 32 + li) * Cfg::LD + kc);
+        b[fn] = *reinterpret_cast<const u32x4*>(sB + ldsChunk<SWZB, Cfg::LD, Cfg::BK>(wn * Cfg::WN + fn * 32 + li, c));
 }
+
+// Loader types and LDS footprint of the fast kernel for a layout.
+template <class Cfg, bool TA, bool TB, bool RAG>
+struct HalfOps {
+    using LA = std::conditional_t<TA, RMajorSlice<Cfg::BM, Cfg::BK, Cfg::NT>, KMajorFor<RAG, Cfg::BM, Cfg::BK, Cfg::NT>>;
+    using LB = std::conditional_t<TB, KMajorFor<RAG, Cfg::BN, Cfg::BK, Cfg::NT>, RMajorSlice<Cfg::BN, Cfg::BK, Cfg::NT>>;
+    static constexpr int SA = Cfg::BM * (LA::SWZ ? Cfg::BK : Cfg::LD);
+    static constexpr int SB = Cfg::BN * (LB::SWZ ? Cfg::BK : Cfg::LD);
+    static constexpr int STAGE = SA + SB;
+    static constexpr size_t LDS_BYTES = 2 * (size_t)STAGE * sizeof(uint16_t);
+    static constexpr bool ANY_DMA = LA::DMA || LB::DMA;
+};
 
 template <class Cfg, bool BF16, bool SWAP>
 __device__ __forceinline__ void mfmaStep(const u32x4 (&a)[Cfg::FM], const u32x4 (&b)[Cfg::FN],
@@ -558,8 +589,10 @@ __global__ __launch_bounds__(Cfg::NT) void gemm_half_fast(HalfFastParams p) {
     const uint16_t* Bb = p.B + batch * p.sB;
 
     // A's rows are m: K-major unless transposed. B's rows are n: K-major when transposed.
-    using LA = std::conditional_t<TA, RMajorSlice<Cfg::BM, Cfg::BK, Cfg::NT>, KMajorFor<RAG, Cfg::BM, Cfg::BK, Cfg::NT>>;
-    using LB = std::conditional_t<TB, KMajorFor<RAG, Cfg::BN, Cfg::BK, Cfg::NT>, RMajorSlice<Cfg::BN, Cfg::BK, Cfg::NT>>;
+    using Ops = HalfOps<Cfg, TA, TB, RAG>;
+    using LA = typename Ops::LA;
+    using LB = typename Ops::LB;
+    constexpr int SA = Ops::SA, STAGE = Ops::STAGE;
     LA la;
     LB lb;
     la.init(TA ? Ab + m0 : Ab + (long long)m0 * p.lda, p.lda, p.M - m0, p.K, tid);
@@ -577,10 +610,14 @@ __global__ __launch_bounds__(Cfg::NT) void gemm_half_fast(HalfFastParams p) {
 
     const int nk = (p.K + Cfg::BK - 1) / Cfg::BK;
     const int nFull = p.K / Cfg::BK;   // slices entirely inside K
-    la.template load<false>(0, p.K, tid, ra);
-    lb.template load<false>(0, p.K, tid, rb);
-    la.template store<Cfg::LD>(hsm, tid, ra);
-    lb.template store<Cfg::LD>(hsm + Cfg::SA, tid, rb);
+    // first slice into stage 0 (a DMA operand writes LDS itself)
+    if constexpr (LA::DMA) la.template dma<false>(0, p.K, hsm);
+    else la.template load<false>(0, p.K, tid, ra);
+    if constexpr (LB::DMA) lb.template dma<false>(0, p.K, hsm + SA);
+    else lb.template load<false>(0, p.K, tid, rb);
+    if constexpr (!LA::DMA) la.template store<Cfg::LD>(hsm, tid, ra);
+    if constexpr (!LB::DMA) lb.template store<Cfg::LD>(hsm + SA, tid, rb);
+    if constexpr (Ops::ANY_DMA) __builtin_amdgcn_s_waitcnt(0);   // LDS writes of the DMA loads done
     __syncthreads();
     // One slice per trip: fetch slice t+1 into registers, run slice t from LDS
     // stage t&1, park slice t+1 in the other stage. (Unrolling two slices to
@@ -593,22 +630,22 @@ __global__ __launch_bounds__(Cfg::NT) void gemm_half_fast(HalfFastParams p) {
     // registers (fetched at the top) are written to the other stage during the
     // last step. The group barriers pin that interleave.
     auto runSlice = [&](int t, bool more) {
-        const uint16_t* sA = hsm + (t & 1) * Cfg::STAGE;
-        const uint16_t* sB = sA + Cfg::SA;
-        uint16_t* nxt = hsm + ((t & 1) ^ 1) * Cfg::STAGE;
+        const uint16_t* sA = hsm + (t & 1) * STAGE;
+        const uint16_t* sB = sA + SA;
+        uint16_t* nxt = hsm + ((t & 1) ^ 1) * STAGE;
         u32x4 fa[2][Cfg::FM], fb[2][Cfg::FN];
-        readFrags<Cfg>(sA, sB, 0, fa[0], fb[0], wm, wn, li, h);
+        readFrags<Cfg, LA::SWZ, LB::SWZ>(sA, sB, 0, fa[0], fb[0], wm, wn, li, h);
         __builtin_amdgcn_sched_group_barrier(kSgDsRead, NFRAG, 0);
         staticFor<0, STEPS>([&](auto I) {
             constexpr int st = decltype(I)::value;
             if constexpr (st + 1 < STEPS) {
-                readFrags<Cfg>(sA, sB, st + 1, fa[(st + 1) & 1], fb[(st + 1) & 1], wm, wn, li, h);
+                readFrags<Cfg, LA::SWZ, LB::SWZ>(sA, sB, st + 1, fa[(st + 1) & 1], fb[(st + 1) & 1], wm, wn, li, h);
                 mfmaStep<Cfg, BF16, SWAP>(fa[st & 1], fb[st & 1], acc);
                 interleave<kSgDsRead, NFRAG, Cfg::FM * Cfg::FN>();
             } else {
                 if (more) {
-                    la.template store<Cfg::LD>(nxt, tid, ra);
-                    lb.template store<Cfg::LD>(nxt + Cfg::SA, tid, rb);
+                    if constexpr (!LA::DMA) la.template store<Cfg::LD>(nxt, tid, ra);
+                    if constexpr (!LB::DMA) lb.template store<Cfg::LD>(nxt + SA, tid, rb);
                 }
                 mfmaStep<Cfg, BF16, SWAP>(fa[st & 1], fb[st & 1], acc);
                 interleave<kSgDsWrite, LA::NSTORES + LB::NSTORES, Cfg::FM * Cfg::FN>();
@@ -617,10 +654,15 @@ __global__ __launch_bounds__(Cfg::NT) void gemm_half_fast(HalfFastParams p) {
     };
     auto step = [&](int t, auto fullTag) {
         constexpr bool FULL = decltype(fullTag)::value;
-        la.template load<FULL>((t + 1) * Cfg::BK, p.K, tid, ra);
-        lb.template load<FULL>((t + 1) * Cfg::BK, p.K, tid, rb);
+        // stage (t+1)&1 was last read in slice t-1, which every wave finished before the barrier
+        uint16_t* nxt = hsm + ((t & 1) ^ 1) * STAGE;
+        if constexpr (LA::DMA) la.template dma<FULL>((t + 1) * Cfg::BK, p.K, nxt);
+        else la.template load<FULL>((t + 1) * Cfg::BK, p.K, tid, ra);
+        if constexpr (LB::DMA) lb.template dma<FULL>((t + 1) * Cfg::BK, p.K, nxt + SA);
+        else lb.template load<FULL>((t + 1) * Cfg::BK, p.K, tid, rb);
         __builtin_amdgcn_sched_group_barrier(kSgVmemRead, LA::NLOADS + LB::NLOADS, 0);
         runSlice(t, true);
+        if constexpr (Ops::ANY_DMA) __builtin_amdgcn_s_waitcnt(0);   // this wave's DMA writes landed
         __syncthreads();
     };
     int t = 0;
@@ -681,16 +723,16 @@ using FCfgS = FCfg<64, 64, 64, 32, 32>;
 template <class Cfg, bool BF16, bool TA, bool TB, bool SWAP, bool RAG>
 static int launchFast(HalfFastParams prm, int batch) {
     auto kern = gemm_half_fast<Cfg, BF16, TA, TB, SWAP, RAG>;
+    constexpr size_t lds = HalfOps<Cfg, TA, TB, RAG>::LDS_BYTES;
     static bool s_attr = false;
     if (!s_attr) {
         OMHIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
-                                        hipFuncAttributeMaxDynamicSharedMemorySize,
-                                        static_cast<int>(Cfg::LDS_BYTES)));
+                                        hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds)));
         s_attr = true;
     }
     prm.tilesM = (prm.M + Cfg::BM - 1) / Cfg::BM;
     prm.tilesN = (prm.N + Cfg::BN - 1) / Cfg::BN;
-    hipLaunchKernelGGL(kern, dim3(prm.tilesM * prm.tilesN, 1, batch), dim3(Cfg::NT), Cfg::LDS_BYTES, stream(), prm);
+    hipLaunchKernelGGL(kern, dim3(prm.tilesM * prm.tilesN, 1, batch), dim3(Cfg::NT), lds, stream(), prm);
     OMHIP_CHECK_LAUNCH();
     return 0;
 }
@@ -699,16 +741,16 @@ static int launchFast(HalfFastParams prm, int batch) {
 // CUs) workgroups and runs up to `slots` of them at once (256x256: 1 per CU,
 // 128x128: 2, 64x64: 4, by LDS); its time is n x tile area / throughput,
 // where the throughput with j of the slots filled is rate x (j/slots)^0.6 (a
-// lone workgroup gets more than its share of the CU). Rates 1, 0.75, 0.45
+// lone workgroup gets more than its share of the CU). Rates 1, 0.75, 0.5
 // were fitted to a sweep of all three tiles over the ViT-B/16 GEMMs, the
 // batched attention products and square / tall-skinny problems on MI355X,
 // where the model picks the fastest tile or one within 4 % of it: e.g.
 // 12608 x 2304 x 768 and 4096^3 take 256x256, 2048 x 4096 x 4096 128x128,
-// 768 x (197 x 64 x 197) and 1024^3 64x64.
+// 768 x (197 x 64 x 197), 2048^3 and 1024^3 64x64.
 static int pickFastTile(int M, int N, int batch) {
     const long long cus = cuCount();
     struct T { int bm, bn, slots; double rate; };
-    const T cand[3] = {{256, 256, 1, 1.0}, {128, 128, 2, 0.75}, {64, 64, 4, 0.45}};
+    const T cand[3] = {{256, 256, 1, 1.0}, {128, 128, 2, 0.75}, {64, 64, 4, 0.5}};
     // TILE-HOOK
     int best = 0;
     double bestCost = 0;
