@@ -127,9 +127,11 @@ struct WeightLoader {
         }
     }
 
+    // FULL: the slice lies inside [k0, kEnd) (no per-element test).
+    template <bool FULL = false>
     __device__ void load(int k0, int kEnd, int tid) {
         const uint32_t soff = (uint32_t)k0 * 4u;
-        if (k0 + BK <= kEnd) {
+        if (FULL || k0 + BK <= kEnd) {
 #pragma unroll
             for (int i = 0; i < PER_T; ++i) {
                 if constexpr (VEC) v4[i] = bufLoad4(r, voff[i], soff);
@@ -177,10 +179,12 @@ struct GatherLoader {
     uint32_t voffPix;
     uint32_t invLo, invHi;
     int ih0, iw0, H, W;
+    int rowOff;   // (tid / BN) * RPT: wave-uniform, kept in a scalar register
     const uint2* tab;
     float v[RPT];
 
-    __device__ void init(const ConvParams& p, int q) {
+    __device__ void init(const ConvParams& p, int q, int tid) {
+        rowOff = __builtin_amdgcn_readfirstlane((tid / BN) * RPT);
         r = bufferRsrc(p.x - p.padOff, p.xBytes);
         tab = p.tab;
         H = p.H; W = p.W;
@@ -206,8 +210,8 @@ struct GatherLoader {
     }
 
     // Issues this thread's RPT loads of the slice starting at row kk0.
-    __device__ void load(int kk0, int tid) {
-        const int base = __builtin_amdgcn_readfirstlane(kk0 + (tid / BN) * RPT);
+    __device__ void load(int kk0, int /*tid*/) {
+        const int base = kk0 + rowOff;
 #pragma unroll
         for (int j = 0; j < RPT; ++j) {
             const uint2 e = tab[base + j];
@@ -350,7 +354,7 @@ __global__ __launch_bounds__(Cfg::NT) void conv_igemm_kernel(ConvParams p) {
     WeightLoader<Cfg::BM, Cfg::BK, Cfg::NT, VA> la;
     la.init(p, m0, tid);
     GatherLoader<Cfg::BN, Cfg::BK, Cfg::NT, MODE> lb;
-    lb.init(p, n0 + tid % Cfg::BN);
+    lb.init(p, n0 + tid % Cfg::BN, tid);
 
     const bool direct = p.splits == 1 && piece < 0;
     if (direct && tid < Cfg::BM) {
@@ -379,7 +383,33 @@ __global__ __launch_bounds__(Cfg::NT) void conv_igemm_kernel(ConvParams p) {
     lb.store(smem + SA::SIZE, tid);
     __syncthreads();
     // Two slices per trip so both LDS stage addresses are compile-time offsets.
-    for (int t = 0; t < nk; t += 2) {
+    // The main loop runs while both slices it fetches (t+1, t+2) lie wholly
+    // inside the K range, so it has no per-slice tests; the last slices run in
+    // the checked loop below (slice t is always in stage t & 1). The schedule
+    // barriers keep each half in the order global loads, MFMAs, LDS stores:
+    // left alone, the scheduler hoists the stores and the block barrier above
+    // most MFMAs and then waits on the loads it has just issued.
+    const int nFull = (kEnd - kBeg) / Cfg::BK;
+    int t = 0;
+    for (; t + 2 < nFull; t += 2) {
+        lb.load(kBeg + (t + 1) * Cfg::BK, tid);
+        la.template load<true>(kBeg + (t + 1) * Cfg::BK, kEnd, tid);
+        __builtin_amdgcn_sched_barrier(0);
+        mma_slice<Cfg, true, true>(smem, smem + SA::SIZE, acc, wm, wn, lane);
+        __builtin_amdgcn_sched_barrier(0);
+        la.store(smem + STAGE, tid);
+        lb.store(smem + STAGE + SA::SIZE, tid);
+        __syncthreads();
+        lb.load(kBeg + (t + 2) * Cfg::BK, tid);
+        la.template load<true>(kBeg + (t + 2) * Cfg::BK, kEnd, tid);
+        __builtin_amdgcn_sched_barrier(0);
+        mma_slice<Cfg, true, true>(smem + STAGE, smem + STAGE + SA::SIZE, acc, wm, wn, lane);
+        __builtin_amdgcn_sched_barrier(0);
+        la.store(smem, tid);
+        lb.store(smem + SA::SIZE, tid);
+        __syncthreads();
+    }
+    for (; t < nk; t += 2) {
         {
             const bool more = (t + 1) < nk;
             if (more) {
