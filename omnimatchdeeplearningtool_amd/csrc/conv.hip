@@ -28,6 +28,7 @@
 #include "omhip_internal.hpp"
 #include "mfma_f32_tile.hpp"
 #include "buffer_io.hpp"
+#include "fastdiv.hpp"
 #include "gemm_f32.hpp"
 #include "conv.hpp"
 #include "../../include/omhip.h"
@@ -71,6 +72,8 @@ struct ConvParams {
     float* rws;
     int padOff;          // max(padH,0)*W + max(padW,0): the x buffer view starts this many floats before x
     uint32_t xBytes;     // range of the x buffer view
+    FastDiv dHoWo, dWo;  // division by Ho*Wo and by Wo (grid pixel indices are below 2^30)
+    uint64_t rowRep;     // bit rr*KW set for rr < KH (mask modes: KH*KW <= 63)
 };
 
 // Tap table: entry kk = (4*(ci*H*W + kh*W + kw), code), code = kh*KW+kw for
@@ -191,19 +194,21 @@ struct GatherLoader {
         const bool colValid = q < p.Nq;
         const int qq = colValid ? q : 0;
         const int HoWo = p.Ho * p.Wo;
-        const int n = qq / HoWo;
+        const int n = (int)p.dHoWo.div((uint32_t)qq);
         const int pix = qq - n * HoWo;
-        const int oh = pix / p.Wo, ow = pix - (pix / p.Wo) * p.Wo;
+        const int oh = (int)p.dWo.div((uint32_t)pix), ow = pix - oh * p.Wo;
         ih0 = colValid ? oh * p.stride - p.padH : -(1 << 29);   // a padding column matches no tap
         iw0 = ow * p.stride - p.padW;
         voffPix = (uint32_t)(n * p.Cin * p.H * p.W + (colValid ? ih0 : 0) * W + iw0 + p.padOff) * 4u;
         uint64_t inside = 0;
         if constexpr (MODE != 2) {
-            uint64_t colBits = 0;
-            for (int c = 0; c < p.KW; ++c)
-                if ((unsigned)(iw0 + c) < (unsigned)W) colBits |= 1ull << c;
-            for (int rr = 0; rr < p.KH; ++rr)
-                if ((unsigned)(ih0 + rr) < (unsigned)H) inside |= colBits << (rr * p.KW);
+            // Taps (kh, kw) inside the image: kw in [cl, ch), kh in [rl, rh).
+            // colBits * rowRep repeats the column bits in every row's KW-bit
+            // field (no carries: colBits < 2^KW); the row mask keeps [rl, rh).
+            const int cl = min(max(-iw0, 0), p.KW), ch = max(min(p.KW, W - iw0), cl);
+            const int rl = min(max(-ih0, 0), p.KH), rh = max(min(p.KH, H - ih0), rl);
+            const uint64_t colBits = (1ull << ch) - (1ull << cl);
+            inside = (colBits * p.rowRep) & ((1ull << (rh * p.KW)) - (1ull << (rl * p.KW)));
         }
         invLo = ~(uint32_t)inside;
         invHi = ~(uint32_t)(inside >> 32);
@@ -241,7 +246,7 @@ struct GatherLoader {
 // Index within the output image of grid pixel pix = oh*Wo + ow.
 __device__ __forceinline__ int outPixel(const ConvParams& p, int pix) {
     if (p.oStride == 1 && p.oOffH == 0 && p.oOffW == 0 && p.oW == p.Wo) return pix;
-    const int oh = pix / p.Wo, ow = pix - (pix / p.Wo) * p.Wo;
+    const int oh = (int)p.dWo.div((uint32_t)pix), ow = pix - oh * p.Wo;
     return (oh * p.oStride + p.oOffH) * p.oW + ow * p.oStride + p.oOffW;
 }
 
@@ -269,7 +274,7 @@ __device__ __forceinline__ void storeTile(const ConvParams& p, const f32x16 (&ac
         const int q = n0 + wn * Cfg::WN + fn * 32 + li;
         const bool colOk = q < p.Nq;
         const int qq = colOk ? q : 0;
-        const int n = qq / HoWo;
+        const int n = (int)p.dHoWo.div((uint32_t)qq);
         const int opix = outPixel(p, qq - n * HoWo);
 #pragma unroll
         for (int fm = 0; fm < Cfg::FM; ++fm) {
@@ -495,7 +500,7 @@ __device__ __forceinline__ void finishOne(const ConvParams& p, int co, int q, fl
         const float inv = 1.0f / sqrtf(p.var[co] + p.eps);
         v = __builtin_fmaf(p.gamma[co], (v - p.mean[co]) * inv, p.beta[co]);
     }
-    const int n = q / HoWo;
+    const int n = (int)p.dHoWo.div((uint32_t)q);
     const int pix = q - n * HoWo;
     const long long o = ((long long)n * p.Cout + co) * (p.oH * p.oW) + outPixel(p, pix);
     if (p.res) v += p.res[o];
@@ -760,6 +765,11 @@ static int convChunk(ConvParams p, int n0, int nb) {
 // bytes.
 static int runConv(const char* name, ConvParams& p) {
     p.K = p.Cin * p.KH * p.KW;
+    p.dHoWo = FastDiv::make((uint32_t)(p.Ho * p.Wo));
+    p.dWo = FastDiv::make((uint32_t)p.Wo);
+    p.rowRep = 0;
+    if (p.KH * p.KW <= 63)
+        for (int rr = 0; rr < p.KH; ++rr) p.rowRep |= 1ull << (rr * p.KW);
     p.tab = tapTable(p.Cin, p.H, p.W, p.KH, p.KW);
     if (!p.tab) return fail("%s: could not build the tap table", name);
     const long long perImg = (long long)p.Cin * p.H * p.W * 4;
