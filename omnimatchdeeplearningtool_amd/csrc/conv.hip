@@ -492,14 +492,29 @@ __global__ __launch_bounds__(Cfg::NT) void conv_igemm_kernel(ConvParams p) {
     }
 }
 
-// Epilogue of one output element (co, grid pixel q) from its finished sum.
-__device__ __forceinline__ void finishOne(const ConvParams& p, int co, int q, float v) {
-    const int HoWo = p.Ho * p.Wo;
-    if (p.bias) v += p.bias[co];
+// Epilogue constants of output channel co (the BN scale is computed as in the
+// conv kernel's staging, so both paths round identically).
+struct ChanEpi {
+    float bias, mean, inv, gamma, beta;
+};
+
+__device__ __forceinline__ ChanEpi chanEpi(const ConvParams& p, int co) {
+    ChanEpi c{0.f, 0.f, 0.f, 0.f, 0.f};
+    if (p.bias) c.bias = p.bias[co];
     if (p.gamma) {
-        const float inv = 1.0f / sqrtf(p.var[co] + p.eps);
-        v = __builtin_fmaf(p.gamma[co], (v - p.mean[co]) * inv, p.beta[co]);
+        c.inv = 1.0f / sqrtf(p.var[co] + p.eps);
+        c.mean = p.mean[co];
+        c.gamma = p.gamma[co];
+        c.beta = p.beta[co];
     }
+    return c;
+}
+
+// Epilogue of one output element (co, grid pixel q) from its finished sum.
+__device__ __forceinline__ void finishOne(const ConvParams& p, const ChanEpi& c, int co, int q, float v) {
+    const int HoWo = p.Ho * p.Wo;
+    if (p.bias) v += c.bias;
+    if (p.gamma) v = __builtin_fmaf(c.gamma, (v - c.mean) * c.inv, c.beta);
     const int n = (int)p.dHoWo.div((uint32_t)q);
     const int pix = q - n * HoWo;
     const long long o = ((long long)n * p.Cout + co) * (p.oH * p.oW) + outPixel(p, pix);
@@ -508,38 +523,61 @@ __device__ __forceinline__ void finishOne(const ConvParams& p, int co, int q, fl
     p.out[o] = v;
 }
 
-// Sums split-K partials in split order and applies the epilogue; one thread
-// per (co, q) with q fastest so reads and NCHW writes are both coalesced.
-__global__ void conv_splitk_finish(ConvParams p) {
-    const long long total = (long long)p.Cout * p.Nq;
-    const long long stride = (long long)gridDim.x * blockDim.x;
-    for (long long i = blockIdx.x * (long long)blockDim.x + threadIdx.x; i < total; i += stride) {
-        const int co = (int)(i / p.Nq);
-        const int q = (int)(i - (long long)co * p.Nq);
-        float v = 0.f;
-        for (int s = 0; s < p.splits; ++s) v += p.ws[(long long)s * total + i];
-        finishOne(p, co, q, v);
+// Sums split-K partials in split order and applies the epilogue. Block
+// (x, y): channels y, y + gridDim.y, ...; four consecutive grid pixels per
+// thread. VEC (Nq % 4 == 0): the four partials of each split are one aligned
+// 16-byte load. The partial buffer holds splits x Cout x Nq < 2^31 floats.
+template <bool VEC>
+__global__ __launch_bounds__(256) void conv_splitk_finish(ConvParams p) {
+    const int q0 = (blockIdx.x * 256 + threadIdx.x) * 4;
+    if (q0 >= p.Nq) return;
+    const int total = p.Cout * p.Nq;
+    for (int co = blockIdx.y; co < p.Cout; co += gridDim.y) {
+        const float* src = p.ws + co * p.Nq + q0;
+        float v[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll 4
+        for (int s = 0; s < p.splits; ++s) {
+            if constexpr (VEC) {
+                const f32x4 t = *reinterpret_cast<const f32x4*>(src + s * total);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) v[i] += t[i];
+            } else {
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    if (q0 + i < p.Nq) v[i] += src[s * total + i];
+            }
+        }
+        const ChanEpi c = chanEpi(p, co);
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            if (q0 + i < p.Nq) finishOne(p, c, co, q0 + i, v[i]);
     }
 }
 
-// Sums the K pieces of the remainder tiles in piece order and applies the epilogue.
+// Sums the K pieces of the remainder tiles in piece order and applies the
+// epilogue. Block (x, y) of one wave: remainder tile x, column quads
+// [64y, 64y + 64) of it; a thread takes four consecutive columns of one tile
+// row (one aligned 16-byte load per piece).
 template <int BM, int BN>
-__global__ void conv_rem_finish(ConvParams p) {
+__global__ __launch_bounds__(64) void conv_rem_finish(ConvParams p) {
+    static_assert(BN % 4 == 0 && (BM * BN / 4) % 64 == 0, "column quads");
     const int remTiles = p.tilesM * p.tilesN - p.fullTiles;
-    const long long total = (long long)remTiles * BM * BN;
-    for (long long i = blockIdx.x * (long long)blockDim.x + threadIdx.x; i < total;
-         i += (long long)gridDim.x * blockDim.x) {
-        const int rt = (int)(i / (BM * BN));
-        const int e = (int)(i - (long long)rt * (BM * BN));
-        int tm, tn;
-        grouped_tile(p.fullTiles + rt, p.tilesM, p.tilesN, 4, tm, tn);
-        const int co = tm * BM + e / BN;
-        const int q = tn * BN + e % BN;
-        if (co >= p.Cout || q >= p.Nq) continue;
-        float v = 0.f;
-        for (int k = 0; k < p.remPieces; ++k) v += p.rws[((long long)k * remTiles + rt) * (BM * BN) + e];
-        finishOne(p, co, q, v);
-    }
+    const int rt = blockIdx.x;
+    int tm, tn;
+    grouped_tile(p.fullTiles + rt, p.tilesM, p.tilesN, 4, tm, tn);
+    const int e4 = blockIdx.y * 64 + threadIdx.x;
+    const int row = e4 / (BN / 4), q0 = tn * BN + (e4 % (BN / 4)) * 4;
+    const int co = tm * BM + row;
+    if (co >= p.Cout || q0 >= p.Nq) return;
+    const float* src = p.rws + (size_t)rt * (BM * BN) + e4 * 4;
+    const size_t pieceStride = (size_t)remTiles * (BM * BN);
+    f32x4 v = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll 4
+    for (int k = 0; k < p.remPieces; ++k) v += *reinterpret_cast<const f32x4*>(src + k * pieceStride);
+    const ChanEpi c = chanEpi(p, co);
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+        if (q0 + i < p.Nq) finishOne(p, c, co, q0 + i, v[i]);
 }
 
 // ---- tile configuration -------------------------------------------------------
@@ -663,14 +701,15 @@ static int launchConv(ConvParams& p, const ConvPlan& pl, float* wsBuf) {
                        : (mode == 1 ? launchConvT<Cfg, false, 1>(p, gridX) : launchConvT<Cfg, false, 2>(p, gridX));
     if (rc) return rc;
     if (p.splits > 1) {
-        const long long total = (long long)p.Cout * p.Nq;
-        const int blocks = (int)std::min<long long>((total + 255) / 256, (long long)cuCount() * 16);
-        hipLaunchKernelGGL(conv_splitk_finish, dim3(blocks), dim3(256), 0, stream(), p);
+        const dim3 grid((p.Nq + 1023) / 1024, std::min(p.Cout, 65535));
+        if (p.Nq % 4 == 0)
+            hipLaunchKernelGGL(conv_splitk_finish<true>, grid, dim3(256), 0, stream(), p);
+        else
+            hipLaunchKernelGGL(conv_splitk_finish<false>, grid, dim3(256), 0, stream(), p);
         OMHIP_CHECK_LAUNCH();
     } else if (p.fullTiles < tiles) {
-        const long long total = (long long)(tiles - p.fullTiles) * Cfg::BM * Cfg::BN;
-        const int blocks = (int)std::min<long long>((total + 255) / 256, (long long)cuCount() * 16);
-        hipLaunchKernelGGL((conv_rem_finish<Cfg::BM, Cfg::BN>), dim3(blocks), dim3(256), 0, stream(), p);
+        hipLaunchKernelGGL((conv_rem_finish<Cfg::BM, Cfg::BN>), dim3(tiles - p.fullTiles, Cfg::BM * Cfg::BN / 256),
+                           dim3(64), 0, stream(), p);
         OMHIP_CHECK_LAUNCH();
     }
     return 0;

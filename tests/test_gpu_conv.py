@@ -113,6 +113,28 @@ def test_balanced_work_split(hip, geom, variant):
     _check(out, x, wt, bias, bn, 1 if bn is not None else 0, s, p)
 
 
+# Few tiles and a long K: the K range is split, the partial sums are added by
+# a second kernel four pixels at a time (Nq = 49 and 75 leave ragged quads;
+# 392 takes the aligned 16-byte path).
+SPLITK = [(1, 256, 7, 7, 100, 3, 1, 1), (3, 128, 9, 9, 70, 3, 2, 1), (2, 256, 14, 14, 64, 3, 1, 1)]
+
+
+@pytest.mark.parametrize("geom", SPLITK, ids=lambda g: "N{}C{}H{}W{}o{}k{}s{}p{}".format(*g))
+@pytest.mark.parametrize("variant", ["bias", "bn_relu"])
+def test_split_k_finish(hip, geom, variant):
+    N, cin, h, w, cout, k, s, p = geom
+    x = O.randn((N, cin, h, w), 700 + cout)
+    wt = _kaiming_uniform((cout, cin, k, k), 701)
+    bias = O.randn((cout,), 702) if variant == "bias" else None
+    bn = _params(cout, 703) if variant == "bn_relu" else None
+    print(f"case splitk {geom} {variant}", flush=True)
+    if variant == "bias":
+        out = _run_conv(hip, x, wt, bias, None, 0, s, p, entry="omHipConv2d")
+    else:
+        out = _run_conv(hip, x, wt, None, bn, 1, s, p)
+    _check(out, x, wt, bias, bn, 1 if bn is not None else 0, s, p)
+
+
 R50 = [c for c in resnet50_convs() if c[0].endswith((".0.conv1", ".0.conv2", ".0.conv3", ".0.ds", "stem"))]
 
 
