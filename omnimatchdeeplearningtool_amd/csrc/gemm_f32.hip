@@ -9,14 +9,101 @@
 // (src/engine/om.engine.autograd.ixx:261-286).
 #include "omhip_internal.hpp"
 #include "mfma_f32_tile.hpp"
+#include "buffer_io.hpp"
 #include "gemm_f32.hpp"
 #include "../../include/omhip.h"
 
 #include <algorithm>
+#include <type_traits>
 
 namespace omhip {
 
-template <class Cfg, bool TA, bool TB, bool VA, bool VB>
+// Dense operand loader through range-checked buffer loads, 16-byte vectors
+// along the contiguous axis (element (r,k) at P[r*ld + k] when KMAJOR, at
+// P[k*ld + r] otherwise). A thread's byte offsets inside the tile are fixed
+// at init, rows past the matrix get kOOB (read as zeros), and each slice
+// re-bases the buffer view at the slice's first element with scalar
+// arithmetic: a whole slice is PER_T buffer loads and no vector ALU work.
+// Only the last, partial slice of a K range tests k per vector.
+// Host conditions (bufVecOk): the vector layout of DenseLoader (contiguous
+// axis, ld and base multiples of 4 floats) and every in-tile offset below
+// 2^30 bytes.
+template <bool KMAJOR, int R, int BK, int NT>
+struct BufVecLoader {
+    static constexpr int PER_T = R * BK / 4 / NT;
+    static_assert(R * BK % (NT * 4) == 0, "tile must split evenly over threads");
+    using Shape = LdsShape<KMAJOR, R, BK>;
+
+    const float* tile;   // element (r0, k = 0) of the operand
+    long long ld;
+    uint32_t voff[PER_T];
+    f32x4 v4[PER_T];
+
+    static __device__ __forceinline__ void coords(int e, int& r, int& k) {
+        if constexpr (KMAJOR) { r = e / (BK / 4); k = (e % (BK / 4)) * 4; }
+        else { k = e / (R / 4); r = (e % (R / 4)) * 4; }
+    }
+
+    __device__ void init(const float* p, long long ld_, int rows, int r0, int tid) {
+        ld = ld_;
+        tile = KMAJOR ? p + (long long)r0 * ld : p + r0;
+#pragma unroll
+        for (int i = 0; i < PER_T; ++i) {
+            int r, k;
+            coords(tid + i * NT, r, k);
+            voff[i] = (r0 + r < rows) ? (uint32_t)((KMAJOR ? r * ld + k : k * ld + r) * 4) : kOOB;
+        }
+    }
+
+    // FULL: the slice [k0, k0 + BK) lies inside [0, kEnd).
+    template <bool FULL>
+    __device__ void load(int k0, int kEnd, int tid) {
+        const auto rs = bufferRsrc(tile + (KMAJOR ? (long long)k0 : (long long)k0 * ld), kMaxBufferBytes);
+#pragma unroll
+        for (int i = 0; i < PER_T; ++i) {
+            uint32_t o = voff[i];
+            if constexpr (!FULL) {
+                int r, k;
+                coords(tid + i * NT, r, k);
+                if (k0 + k >= kEnd) o = kOOB;
+            }
+            v4[i] = bufLoad4(rs, o, 0);
+        }
+    }
+
+    __device__ void store(float* s, int tid) const {
+#pragma unroll
+        for (int i = 0; i < PER_T; ++i) {
+            int r, k;
+            coords(tid + i * NT, r, k);
+            float* dst = KMAJOR ? s + r * Shape::LD + k : s + k * Shape::LD + r;
+            *reinterpret_cast<f32x4*>(dst) = v4[i];
+        }
+    }
+};
+
+// The generic loader behind the same interface (any alignment, 64-bit
+// addressing, per-element bounds tests on every slice).
+template <bool KMAJOR, bool VEC, int R, int BK, int NT>
+struct DenseLoaderAdapter : DenseLoader<KMAJOR, VEC, R, BK, NT> {
+    using Base = DenseLoader<KMAJOR, VEC, R, BK, NT>;
+    __device__ void init(const float* p, long long ld, int rows, int r0, int) {
+        this->p = p; this->ld = ld; this->rows = rows; this->r0 = r0;
+    }
+    template <bool FULL>
+    __device__ void load(int k0, int kEnd, int tid) {
+        this->K = kEnd;
+        Base::load(k0, tid);
+    }
+};
+
+// Operand loader kinds: 0 generic scalar, 1 generic 16-byte vectors,
+// 2 buffer-view 16-byte vectors.
+template <bool KMAJOR, int LK, int R, int BK, int NT>
+using GemmLoader = std::conditional_t<LK == 2, BufVecLoader<KMAJOR, R, BK, NT>,
+                                      DenseLoaderAdapter<KMAJOR, LK == 1, R, BK, NT>>;
+
+template <class Cfg, bool TA, bool TB, int LA, int LB>
 __global__ __launch_bounds__(Cfg::NT) void gemm_f32_kernel(GemmF32Params p) {
     extern __shared__ float smem[];
     constexpr bool A_KMAJOR = !TA;
@@ -41,10 +128,10 @@ __global__ __launch_bounds__(Cfg::NT) void gemm_f32_kernel(GemmF32Params p) {
     const int kBeg = split * p.kChunk;
     const int kEnd = min(p.K, kBeg + p.kChunk);
 
-    DenseLoader<A_KMAJOR, VA, Cfg::BM, Cfg::BK, Cfg::NT> la;
-    la.p = p.A + batch * p.sA; la.ld = p.lda; la.rows = p.M; la.K = kEnd; la.r0 = m0;
-    DenseLoader<B_KMAJOR, VB, Cfg::BN, Cfg::BK, Cfg::NT> lb;
-    lb.p = p.B + batch * p.sB; lb.ld = p.ldb; lb.rows = p.N; lb.K = kEnd; lb.r0 = n0;
+    GemmLoader<A_KMAJOR, LA, Cfg::BM, Cfg::BK, Cfg::NT> la;
+    la.init(p.A + batch * p.sA, p.lda, p.M, m0, tid);
+    GemmLoader<B_KMAJOR, LB, Cfg::BN, Cfg::BK, Cfg::NT> lb;
+    lb.init(p.B + batch * p.sB, p.ldb, p.N, n0, tid);
 
     f32x16 acc[Cfg::FM][Cfg::FN];
 #pragma unroll
@@ -55,26 +142,64 @@ __global__ __launch_bounds__(Cfg::NT) void gemm_f32_kernel(GemmF32Params p) {
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
     const int nk = (kEnd - kBeg + Cfg::BK - 1) / Cfg::BK;
-    la.load(kBeg, tid);
-    lb.load(kBeg, tid);
+    la.template load<false>(kBeg, kEnd, tid);
+    lb.template load<false>(kBeg, kEnd, tid);
     la.store(smem, tid);
     lb.store(smem + SA::SIZE, tid);
     __syncthreads();
-    for (int t = 0; t < nk; ++t) {
-        const int cur = t & 1;
-        const bool more = (t + 1) < nk;
-        if (more) {
-            la.load(kBeg + (t + 1) * Cfg::BK, tid);
-            lb.load(kBeg + (t + 1) * Cfg::BK, tid);
-        }
-        float* sCur = smem + cur * STAGE;
-        float* sNxt = smem + (cur ^ 1) * STAGE;
-        mma_slice<Cfg, A_KMAJOR, B_KMAJOR>(sCur, sCur + SA::SIZE, acc, wm, wn, lane);
-        if (more) {
-            la.store(sNxt, tid);
-            lb.store(sNxt + SA::SIZE, tid);
-        }
+    // Two slices per trip so both LDS stage addresses are compile-time
+    // offsets. The main loop runs while both slices it fetches (t+1, t+2) lie
+    // wholly inside the K range, so its loads test nothing; the last slices
+    // run in the checked loop below (slice t is always in stage t & 1). The
+    // schedule barriers keep each half in the order global loads, MFMAs, LDS
+    // stores, block barrier.
+    const int nFull = (kEnd - kBeg) / Cfg::BK;
+    int t = 0;
+    for (; t + 2 < nFull; t += 2) {
+        la.template load<true>(kBeg + (t + 1) * Cfg::BK, kEnd, tid);
+        lb.template load<true>(kBeg + (t + 1) * Cfg::BK, kEnd, tid);
+        __builtin_amdgcn_sched_barrier(0);
+        mma_slice<Cfg, A_KMAJOR, B_KMAJOR>(smem, smem + SA::SIZE, acc, wm, wn, lane);
+        __builtin_amdgcn_sched_barrier(0);
+        la.store(smem + STAGE, tid);
+        lb.store(smem + STAGE + SA::SIZE, tid);
         __syncthreads();
+        la.template load<true>(kBeg + (t + 2) * Cfg::BK, kEnd, tid);
+        lb.template load<true>(kBeg + (t + 2) * Cfg::BK, kEnd, tid);
+        __builtin_amdgcn_sched_barrier(0);
+        mma_slice<Cfg, A_KMAJOR, B_KMAJOR>(smem + STAGE, smem + STAGE + SA::SIZE, acc, wm, wn, lane);
+        __builtin_amdgcn_sched_barrier(0);
+        la.store(smem, tid);
+        lb.store(smem + SA::SIZE, tid);
+        __syncthreads();
+    }
+    for (; t < nk; t += 2) {
+        {
+            const bool more = (t + 1) < nk;
+            if (more) {
+                la.template load<false>(kBeg + (t + 1) * Cfg::BK, kEnd, tid);
+                lb.template load<false>(kBeg + (t + 1) * Cfg::BK, kEnd, tid);
+            }
+            mma_slice<Cfg, A_KMAJOR, B_KMAJOR>(smem, smem + SA::SIZE, acc, wm, wn, lane);
+            if (more) {
+                la.store(smem + STAGE, tid);
+                lb.store(smem + STAGE + SA::SIZE, tid);
+            }
+            __syncthreads();
+        }
+        if (t + 1 < nk) {
+            const bool more = (t + 2) < nk;
+            if (more) {
+                la.template load<false>(kBeg + (t + 2) * Cfg::BK, kEnd, tid);
+                lb.template load<false>(kBeg + (t + 2) * Cfg::BK, kEnd, tid);
+            }
+            mma_slice<Cfg, A_KMAJOR, B_KMAJOR>(smem + STAGE, smem + STAGE + SA::SIZE, acc, wm, wn, lane);
+            if (more) {
+                la.store(smem, tid);
+                lb.store(smem + SA::SIZE, tid);
+            }
+            __syncthreads();
+        }
     }
 
     // Split-K / batch-reduce partials go densely to [split][batch][M][N].
@@ -119,9 +244,9 @@ static size_t ldsBytesFor() {
     return 2 * (SA::SIZE + SB::SIZE) * sizeof(float);
 }
 
-template <class Cfg, bool TA, bool TB, bool VA, bool VB>
+template <class Cfg, bool TA, bool TB, int LA, int LB>
 static int launchOne(const GemmF32Params& prm, int batch, int splits) {
-    auto kern = gemm_f32_kernel<Cfg, TA, TB, VA, VB>;
+    auto kern = gemm_f32_kernel<Cfg, TA, TB, LA, LB>;
     const size_t lds = ldsBytesFor<Cfg, TA, TB>();
     static bool s_attr = false;
     if (!s_attr) {
@@ -135,14 +260,24 @@ static int launchOne(const GemmF32Params& prm, int batch, int splits) {
     return 0;
 }
 
+// In-tile byte offsets of the buffer-view loader stay below 2^30.
+template <bool KMAJOR, int R, int BK>
+static bool bufVecOk(bool vec, long long ld) {
+    const long long maxOff = KMAJOR ? ((long long)(R - 1) * ld + BK) * 4 : ((long long)(BK - 1) * ld + R) * 4;
+    return vec && maxOff < (long long)kMaxBufferBytes;
+}
+
 template <class Cfg, bool TA, bool TB>
 static int launchVec(GemmF32Params prm, int batch, int splits, bool va, bool vb) {
     prm.tilesM = (prm.M + Cfg::BM - 1) / Cfg::BM;
     prm.tilesN = (prm.N + Cfg::BN - 1) / Cfg::BN;
-    if (va && vb) return launchOne<Cfg, TA, TB, true, true>(prm, batch, splits);
-    if (va) return launchOne<Cfg, TA, TB, true, false>(prm, batch, splits);
-    if (vb) return launchOne<Cfg, TA, TB, false, true>(prm, batch, splits);
-    return launchOne<Cfg, TA, TB, false, false>(prm, batch, splits);
+    const bool ba = bufVecOk<!TA, Cfg::BM, Cfg::BK>(va, prm.lda);
+    const bool bb = bufVecOk<TB, Cfg::BN, Cfg::BK>(vb, prm.ldb);
+    if (ba && bb) return launchOne<Cfg, TA, TB, 2, 2>(prm, batch, splits);
+    if (va && vb) return launchOne<Cfg, TA, TB, 1, 1>(prm, batch, splits);
+    if (va) return launchOne<Cfg, TA, TB, 1, 0>(prm, batch, splits);
+    if (vb) return launchOne<Cfg, TA, TB, 0, 1>(prm, batch, splits);
+    return launchOne<Cfg, TA, TB, 0, 0>(prm, batch, splits);
 }
 
 // Slice depth of the large tile is a build-time constant (LDS: 2 x (256x(BK+4) + BKx260) floats).
