@@ -159,18 +159,18 @@ __global__ __launch_bounds__(Cfg::NT) void gemm_f32_kernel(GemmF32Params p) {
         la.template load<true>(kBeg + (t + 1) * Cfg::BK, kEnd, tid);
         lb.template load<true>(kBeg + (t + 1) * Cfg::BK, kEnd, tid);
         __builtin_amdgcn_sched_barrier(0);
-        mma_slice<Cfg, A_KMAJOR, B_KMAJOR>(smem, smem + SA::SIZE, acc, wm, wn, lane);
-        __builtin_amdgcn_sched_barrier(0);
-        la.store(smem + STAGE, tid);
-        lb.store(smem + STAGE + SA::SIZE, tid);
+        mma_slice_split<Cfg, A_KMAJOR, B_KMAJOR>(smem, smem + SA::SIZE, acc, wm, wn, lane, [&] {
+            la.store(smem + STAGE, tid);
+            lb.store(smem + STAGE + SA::SIZE, tid);
+        });
         __syncthreads();
         la.template load<true>(kBeg + (t + 2) * Cfg::BK, kEnd, tid);
         lb.template load<true>(kBeg + (t + 2) * Cfg::BK, kEnd, tid);
         __builtin_amdgcn_sched_barrier(0);
-        mma_slice<Cfg, A_KMAJOR, B_KMAJOR>(smem + STAGE, smem + STAGE + SA::SIZE, acc, wm, wn, lane);
-        __builtin_amdgcn_sched_barrier(0);
-        la.store(smem, tid);
-        lb.store(smem + SA::SIZE, tid);
+        mma_slice_split<Cfg, A_KMAJOR, B_KMAJOR>(smem + STAGE, smem + STAGE + SA::SIZE, acc, wm, wn, lane, [&] {
+            la.store(smem, tid);
+            lb.store(smem + SA::SIZE, tid);
+        });
         __syncthreads();
     }
     for (; t < nk; t += 2) {

@@ -175,6 +175,73 @@ __device__ __forceinline__ void mma_slice(const float* __restrict__ sA, const fl
     }
 }
 
+// The MFMAs of one LDS slice with `mid` run between its first and second
+// halves: every fragment of the slice is read first, then the first half of
+// the k steps, mid() (the next slice's LDS stores), the second half. The
+// schedule barriers keep that order, so the stores' LDS traffic overlaps the
+// second half's MFMAs instead of sitting between the last MFMA and the block
+// barrier.
+template <class Cfg, bool A_KMAJOR, bool B_KMAJOR, class Mid>
+__device__ __forceinline__ void mma_slice_split(const float* __restrict__ sA, const float* __restrict__ sB,
+                                                f32x16 (&acc)[Cfg::FM][Cfg::FN], int wm, int wn, int lane,
+                                                Mid&& mid) {
+    using SA = LdsShape<A_KMAJOR, Cfg::BM, Cfg::BK>;
+    using SB = LdsShape<B_KMAJOR, Cfg::BN, Cfg::BK>;
+    constexpr int U = Cfg::KH / 4;
+    static_assert(U % 2 == 0, "two halves of k steps");
+    const int li = lane & 31;
+    const int h = lane >> 5;
+    const int kb = h * Cfg::KH;
+    float a[U][Cfg::FM][4], b[U][Cfg::FN][4];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+#pragma unroll
+        for (int fm = 0; fm < Cfg::FM; ++fm) {
+            const int row = wm * Cfg::WM + fm * 32 + li;
+            if constexpr (A_KMAJOR) {
+                const f32x4 v = *reinterpret_cast<const f32x4*>(sA + row * SA::LD + kb + 4 * u);
+                a[u][fm][0] = v[0]; a[u][fm][1] = v[1]; a[u][fm][2] = v[2]; a[u][fm][3] = v[3];
+            } else {
+#pragma unroll
+                for (int s = 0; s < 4; ++s) a[u][fm][s] = sA[(kb + 4 * u + s) * SA::LD + row];
+            }
+        }
+#pragma unroll
+        for (int fn = 0; fn < Cfg::FN; ++fn) {
+            const int col = wn * Cfg::WN + fn * 32 + li;
+            if constexpr (B_KMAJOR) {
+                const f32x4 v = *reinterpret_cast<const f32x4*>(sB + col * SB::LD + kb + 4 * u);
+                b[u][fn][0] = v[0]; b[u][fn][1] = v[1]; b[u][fn][2] = v[2]; b[u][fn][3] = v[3];
+            } else {
+#pragma unroll
+                for (int s = 0; s < 4; ++s) b[u][fn][s] = sB[(kb + 4 * u + s) * SB::LD + col];
+            }
+        }
+    }
+#pragma unroll
+    for (int u = 0; u < U / 2; ++u)
+#pragma unroll
+        for (int s = 0; s < 4; ++s)
+#pragma unroll
+            for (int fm = 0; fm < Cfg::FM; ++fm)
+#pragma unroll
+                for (int fn = 0; fn < Cfg::FN; ++fn)
+                    acc[fm][fn] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[u][fm][s], b[u][fn][s], acc[fm][fn], 0, 0, 0);
+    __builtin_amdgcn_sched_barrier(0);
+    mid();
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int u = U / 2; u < U; ++u)
+#pragma unroll
+        for (int s = 0; s < 4; ++s)
+#pragma unroll
+            for (int fm = 0; fm < Cfg::FM; ++fm)
+#pragma unroll
+                for (int fn = 0; fn < Cfg::FN; ++fn)
+                    acc[fm][fn] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[u][fm][s], b[u][fn][s], acc[fm][fn], 0, 0, 0);
+    __builtin_amdgcn_sched_barrier(0);
+}
+
 // ---------------------------------------------------------------------------
 // Block-tile -> (tm, tn) mapping. Workgroups are dispatched round-robin over
 // the 8 XCDs (each with its own L2), so consecutive block ids land on
