@@ -35,6 +35,8 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 sys.path.insert(0, os.path.join(ROOT, "tests"))
 
+from omnimatchdeeplearningtool_amd import synthetic as syn   # noqa: E402  (seeded inputs)
+
 PEAK_FP32 = 157.3e12      # MI355X dense fp32 MFMA, FLOP/s
 PEAK_HBM = 8.0e12         # bytes/s
 M = N = K = 4096
@@ -55,11 +57,13 @@ def _traffic(name: str):
         return None
 
 
+GEMM_ROWS = np.r_[0:4, 2046:2050, 4092:4096]   # rows of the 4096^3 product checked on the CPU
+
+
 def bench_gemm(om, steps: int, warmup: int):
     from omnimatchdeeplearningtool_amd.hiptime import StreamTimer
-    import oracle as O
-    A = O.randn((M, K), 11)
-    B = O.randn((K, N), 12)
+    A = syn.randn((M, K), 11)
+    B = syn.randn((K, N), 12)
     dA, dB = om.DeviceBuffer.from_numpy(A), om.DeviceBuffer.from_numpy(B)
     dC = om.DeviceBuffer.empty((M, N))
     H = om.HIPBackend
@@ -77,12 +81,7 @@ def bench_gemm(om, steps: int, warmup: int):
     wall = time.perf_counter() - t0
     ms = ms_total / steps
     flops = 2.0 * M * N * K
-    # parity on sampled rows (float64 brute force, K-scaled bound)
-    C = dC.numpy()
-    rows = np.r_[0:4, 2046:2050, 4092:4096]
-    C64, bound = O.gemm_f64(A[rows], B)
-    err = O.normalized_error(C[rows], C64, bound)
-    return ms, flops, wall, err
+    return ms, flops, wall, dC.numpy()[GEMM_ROWS]
 
 
 GEMM_SWEEP = [(512, 512, 512), (1024, 1024, 1024), (2048, 2048, 2048), (4096, 4096, 4096), (8192, 8192, 8192),
@@ -92,17 +91,16 @@ GEMM_SWEEP = [(512, 512, 512), (1024, 1024, 1024), (2048, 2048, 2048), (4096, 40
 def bench_gemm_sweep(om, steps: int, warmup: int):
     """The fp32 GEMM sweep in both layouts: row-major A x B and A x B^T (Linear weight)."""
     from omnimatchdeeplearningtool_amd.hiptime import StreamTimer
-    import oracle as O
     H = om.HIPBackend
     timer = StreamTimer(om.stream_handle())
-    out = []
+    out, samples = [], []
     for (m, n, k) in GEMM_SWEEP:
-        A = O.randn((m, k), 21 + m)
+        A = syn.randn((m, k), 21 + m)
         dA = om.DeviceBuffer.from_numpy(A)
         dC = om.DeviceBuffer.empty((m, n))
         reps = max(3, min(steps, int(2e12 / (2.0 * m * n * k))))   # about 2 TFLOP of work per shape
         for layout in ("NN", "NT"):
-            B = O.randn((k, n) if layout == "NN" else (n, k), 22 + n)
+            B = syn.randn((k, n) if layout == "NN" else (n, k), 22 + n)
             dB = om.DeviceBuffer.from_numpy(B)
             f = (lambda: H.matmul(dA, dB, dC, m, k, n)) if layout == "NN" else (lambda: H.matmulTransB(dA, dB, dC, m, k, n))
             for _ in range(warmup):
@@ -114,30 +112,38 @@ def bench_gemm_sweep(om, steps: int, warmup: int):
             timer.stop()
             ms = timer.ms() / reps
             rows = np.unique(np.r_[0, m // 2, m - 1])
-            C64, bound = O.gemm_f64(A[rows], B, transB=(layout == "NT"))
-            err = O.normalized_error(dC.numpy()[rows], C64, bound)
+            samples.append(((m, n, k, layout), rows, dC.numpy()[rows]))
             tf = 2.0 * m * n * k / ms / 1e9
             out.append({"M": m, "N": n, "K": k, "layout": layout, "ms": round(ms, 4), "tflops": round(tf, 1),
-                        "frac_of_157_3": round(tf / 157.3, 3), "parity": err})
-            log(f"gemm sweep {m}x{n}x{k} {layout}: {ms:.4f} ms  {tf:.1f} TFLOP/s  parity {err:.1e}")
+                        "frac_of_157_3": round(tf / 157.3, 3), "parity": None})
+            log(f"gemm sweep {m}x{n}x{k} {layout}: {ms:.4f} ms  {tf:.1f} TFLOP/s")
             dB.free()
         dA.free(); dC.free()
-    return out
+    return out, samples
+
+
+RESNET18_CHECKED = (0, 9, 19)   # layers whose outputs (two images) are checked on the CPU
+
+
+def resnet18_layer_inputs(li: int, batch: int):
+    """Seeded input, Kaiming-uniform weight and BN vectors of ResNet-18 conv layer li."""
+    from resnet_shapes import resnet18_convs
+    name, cin, h, w, cout, k, s, p = resnet18_convs()[li]
+    bnd = np.sqrt(6.0 / (cin * k * k))
+    x = syn.randn((batch, cin, h, w), 100 + li)
+    wt = syn.uniform((cout, cin, k, k), 200 + li, -bnd, bnd)
+    g, b = syn.uniform((cout,), 300 + li, 0.5, 1.5), syn.randn((cout,), 400 + li, 0.1)
+    m, v = syn.randn((cout,), 500 + li, 0.1), syn.uniform((cout,), 600 + li, 0.5, 1.5)
+    return x, wt, g, b, m, v
 
 
 def bench_resnet18(om, steps: int, warmup: int, batch: int = 32):
     from omnimatchdeeplearningtool_amd.hiptime import StreamTimer
     from resnet_shapes import conv_bytes, conv_flops, out_hw, resnet18_convs
-    import oracle as O
     H = om.HIPBackend
     layers = []
     for li, (name, cin, h, w, cout, k, s, p) in enumerate(resnet18_convs()):
-        fan_in = cin * k * k
-        bnd = np.sqrt(6.0 / fan_in)
-        x = O.randn((batch, cin, h, w), 100 + li)
-        wt = O.uniform((cout, cin, k, k), 200 + li, -bnd, bnd)
-        g, b = O.uniform((cout,), 300 + li, 0.5, 1.5), O.randn((cout,), 400 + li, 0.1)
-        m, v = O.randn((cout,), 500 + li, 0.1), O.uniform((cout,), 600 + li, 0.5, 1.5)
+        x, wt, g, b, m, v = resnet18_layer_inputs(li, batch)
         ho, wo = out_hw(h, k, s, p), out_hw(w, k, s, p)
         dev = dict(x=om.DeviceBuffer.from_numpy(x), w=om.DeviceBuffer.from_numpy(wt),
                    g=om.DeviceBuffer.from_numpy(g), b=om.DeviceBuffer.from_numpy(b),
@@ -177,24 +183,18 @@ def bench_resnet18(om, steps: int, warmup: int, batch: int = 32):
                     "roof_frac": round(roof / lms, 3)})
     flops = sum(conv_flops(sh, batch) for sh, _, _ in layers)
     roof_ms = sum(max(conv_flops(sh, batch) / PEAK_FP32, conv_bytes(sh, batch) / PEAK_HBM) for sh, _, _ in layers) * 1e3
-    # parity: two images of three layers against float64
-    errs = []
-    for idx in (0, 9, 19):
-        (name, cin, h, w, cout, k, s, p), d, (x, wt, g, b, m, v) = layers[idx]
-        y = d["y"].numpy()[[0, batch - 1]]
-        o64, bound = O.conv_f64(x[[0, batch - 1]], wt, None, s, p, gamma=g, beta=b, mean=m, var=v, act=1)
-        errs.append(O.normalized_error(y, o64, bound))
-    return ms, flops, roof_ms, per, max(errs)
+    # outputs of two images of three layers, checked on the CPU
+    samples = [(idx, layers[idx][1]["y"].numpy()[[0, batch - 1]]) for idx in RESNET18_CHECKED]
+    return ms, flops, roof_ms, per, samples
 
 
 def bench_resnet18_net(om, steps: int, warmup: int, batch: int = 32):
     """The whole ResNet-18 at batch 32: fused inference forward, and one training
     step (forward with batch statistics + backward to every weight)."""
     from omnimatchdeeplearningtool_amd.hiptime import StreamTimer
-    from resnet_net import GpuResNet18, conv_list, cpu_forward, forward_flops, make_params
-    import oracle as O
+    from resnet_net import GpuResNet18, forward_flops, make_params
     P = make_params(seed=1)
-    img = O.randn((batch, 3, 224, 224), 900)
+    img = syn.randn((batch, 3, 224, 224), 900)
     d_img = om.DeviceBuffer.from_numpy(img)
     timer = StreamTimer(om.stream_handle())
     net = GpuResNet18(om, P, batch)
@@ -207,10 +207,9 @@ def bench_resnet18_net(om, steps: int, warmup: int, batch: int = 32):
     timer.stop()
     fwd_ms = timer.ms() / steps
     got = logits.numpy()[:2]
-    err = O.frobenius_rel(got, cpu_forward(P, img[:2]))
     # training step
     tnet = GpuResNet18(om, P, batch, train=True)
-    g_logits = om.DeviceBuffer.from_numpy(O.randn((batch, 1000), 901, 0.01))
+    g_logits = om.DeviceBuffer.from_numpy(syn.randn((batch, 1000), 901, 0.01))
     for _ in range(max(1, warmup // 2)):
         tnet.forward_train(d_img)
         tnet.backward(g_logits)
@@ -225,7 +224,7 @@ def bench_resnet18_net(om, steps: int, warmup: int, batch: int = 32):
     fl = forward_flops(batch)
     stem = 2.0 * batch * 64 * 112 * 112 * 3 * 49
     train_fl = 3.0 * fl - stem        # forward + input gradients (none for the image) + weight gradients
-    return fwd_ms, fl, err, train_ms, train_fl
+    return fwd_ms, fl, got, train_ms, train_fl
 
 
 def bench_infer_pipeline(om, n_img: int = 512, batch: int = 32, reps: int = 3):
@@ -235,10 +234,9 @@ def bench_infer_pipeline(om, n_img: int = 512, batch: int = 32, reps: int = 3):
     Also the device-resident forward alone, eager and replayed from a captured graph."""
     from omnimatchdeeplearningtool_amd.hiptime import StreamTimer
     from resnet_net import make_params, pack_params
-    import oracle as O
     P = make_params(seed=1)
     net = om.ResNet18Infer(pack_params(P), 1000, batch)
-    imgs = O.uniform((n_img, 3, 224, 224), 905, 0.0, 1.0)
+    imgs = syn.uniform((n_img, 3, 224, 224), 905, 0.0, 1.0)
     net.infer_batch(imgs[:2 * batch], batch)        # warm-up: tables, workspaces, staging
     wall = []
     for _ in range(reps):
@@ -247,7 +245,7 @@ def bench_infer_pipeline(om, n_img: int = 512, batch: int = 32, reps: int = 3):
         wall.append(time.perf_counter() - t0)
     pipe_s = float(np.median(wall))
     # device-resident forward of one batch: eager, then a captured graph
-    d_in = om.DeviceBuffer.from_numpy(O.randn((batch, 3, 224, 224), 906))
+    d_in = om.DeviceBuffer.from_numpy(syn.randn((batch, 3, 224, 224), 906))
     d_log = om.DeviceBuffer.empty((batch, 1000))
     timer = StreamTimer(om.stream_handle())
     steps = 20
@@ -298,16 +296,15 @@ def bench_resnet50(om, steps: int, warmup: int, batch: int = 64):
     """ResNet-50 conv stack forward (53 convs, fused conv+BN+ReLU) at batch 64."""
     from omnimatchdeeplearningtool_amd.hiptime import StreamTimer
     from resnet_shapes import conv_bytes, conv_flops, out_hw, resnet50_convs
-    import oracle as O
     H = om.HIPBackend
     layers = []
     for li, (name, cin, h, w, cout, k, s, p) in enumerate(resnet50_convs()):
         bnd = np.sqrt(6.0 / (cin * k * k))
         ho, wo = out_hw(h, k, s, p), out_hw(w, k, s, p)
-        x = om.DeviceBuffer.from_numpy(O.randn((batch, cin, h, w), 700 + li))
-        wt = om.DeviceBuffer.from_numpy(O.uniform((cout, cin, k, k), 800 + li, -bnd, bnd))
-        bn = [om.DeviceBuffer.from_numpy(a) for a in (O.uniform((cout,), 900 + li, 0.5, 1.5), O.randn((cout,), 1000 + li, 0.1),
-                                                       O.randn((cout,), 1100 + li, 0.1), O.uniform((cout,), 1200 + li, 0.5, 1.5))]
+        x = om.DeviceBuffer.from_numpy(syn.randn((batch, cin, h, w), 700 + li))
+        wt = om.DeviceBuffer.from_numpy(syn.uniform((cout, cin, k, k), 800 + li, -bnd, bnd))
+        bn = [om.DeviceBuffer.from_numpy(a) for a in (syn.uniform((cout,), 900 + li, 0.5, 1.5), syn.randn((cout,), 1000 + li, 0.1),
+                                                       syn.randn((cout,), 1100 + li, 0.1), syn.uniform((cout,), 1200 + li, 0.5, 1.5))]
         y = om.DeviceBuffer.empty((batch, cout, ho, wo))
         layers.append(((name, cin, h, w, cout, k, s, p), x, wt, bn, y))
 
@@ -407,11 +404,10 @@ def bench_vit_half(om, steps: int, warmup: int, bf16: bool):
 def bench_mlp(om, steps: int, warmup: int, batch: int = 128):
     """MLP 784-256-128-10 (ReLU) forward + backward through the HAL entries, fp32, batch 128."""
     from omnimatchdeeplearningtool_amd.hiptime import StreamTimer
-    import oracle as O
     H = om.HIPBackend
     dims = [784, 256, 128, 10]
-    x = om.DeviceBuffer.from_numpy(O.uniform((batch, 784), 1))
-    Ws = [om.DeviceBuffer.from_numpy(O.uniform((i, o), 10 + j, -np.sqrt(6 / i), np.sqrt(6 / i)))
+    x = om.DeviceBuffer.from_numpy(syn.uniform((batch, 784), 1))
+    Ws = [om.DeviceBuffer.from_numpy(syn.uniform((i, o), 10 + j, -np.sqrt(6 / i), np.sqrt(6 / i)))
           for j, (i, o) in enumerate(zip(dims[:-1], dims[1:]))]
     bs = [om.DeviceBuffer.from_numpy(np.zeros(o, np.float32)) for o in dims[1:]]
     z = [om.DeviceBuffer.empty((batch, o)) for o in dims[1:]]
@@ -444,8 +440,60 @@ def bench_mlp(om, steps: int, warmup: int, batch: int = 128):
         step()
     t.stop()
     ms = t.ms() / steps
+    # The same step replayed from a captured graph (its kernels unchanged; the
+    # per-launch host cost is gone). Every output is overwritten per step, so
+    # the replay's results must equal the eager step's bit for bit.
+    eager_out = [d.numpy().copy() for d in gW + gA]
+    graph = om.Graph(step)
+    graph.launch()
+    om.synchronize()
+    same = all(np.array_equal(d.numpy(), e) for d, e in zip(gW + gA, eager_out))
+    t.start()
+    for _ in range(steps):
+        graph.launch()
+    t.stop()
+    graph_ms = t.ms() / steps
     flops = sum(3 * 2.0 * batch * i * o for i, o in zip(dims[:-1], dims[1:]))
-    return ms, flops
+    return ms, flops, graph_ms, same
+
+
+# ---- CPU checks of the GPU legs' results (run with the CPU baseline leg) ----
+# Each regenerates its leg's seeded inputs and compares the sampled GPU outputs
+# with the oracle's float64 result under the K-scaled bound.
+
+def cpu_check_gemm(c_rows) -> float:
+    import oracle as O
+    A, B = syn.randn((M, K), 11), syn.randn((K, N), 12)
+    C64, bound = O.gemm_f64(A[GEMM_ROWS], B)
+    return O.normalized_error(c_rows, C64, bound)
+
+
+def cpu_check_sweep(sweep: list, samples: list) -> None:
+    import oracle as O
+    for entry, ((m, n, k, layout), rows, c_rows) in zip(sweep, samples):
+        A = syn.randn((m, k), 21 + m)
+        B = syn.randn((k, n) if layout == "NN" else (n, k), 22 + n)
+        C64, bound = O.gemm_f64(A[rows], B, transB=(layout == "NT"))
+        entry["parity"] = O.normalized_error(c_rows, C64, bound)
+
+
+def cpu_check_resnet18(samples: list, batch: int = 32) -> float:
+    import oracle as O
+    from resnet_shapes import resnet18_convs
+    errs = []
+    for li, y in samples:
+        name, cin, h, w, cout, k, s, p = resnet18_convs()[li]
+        x, wt, g, b, m, v = resnet18_layer_inputs(li, batch)
+        o64, bound = O.conv_f64(x[[0, batch - 1]], wt, None, s, p, gamma=g, beta=b, mean=m, var=v, act=1)
+        errs.append(O.normalized_error(y, o64, bound))
+    return max(errs)
+
+
+def cpu_check_resnet18_net(logits2) -> float:
+    import oracle as O
+    from resnet_net import cpu_forward, make_params
+    img2 = syn.randn((32, 3, 224, 224), 900)[:2]
+    return O.frobenius_rel(logits2, cpu_forward(make_params(seed=1), img2))
 
 
 def cpu_baseline_gemm(budget_s: float = 10.0):
@@ -605,20 +653,19 @@ def workload_probe(name: str):
     resnet18_train — three ResNet-18 b32 training steps; vit_attention — ten fused
     attentions (ViT-B/16 b64, fp16) after the ten Q.K^T / P.V batched products they replace."""
     import omnimatchdeeplearningtool_amd as om
-    import oracle as O
     om.init(0)
     H = om.HIPBackend
     if name == "resnet18_train":
         from resnet_net import GpuResNet18, make_params
-        img = om.DeviceBuffer.from_numpy(O.randn((32, 3, 224, 224), 900))
-        g = om.DeviceBuffer.from_numpy(O.randn((32, 1000), 901, 0.01))
+        img = om.DeviceBuffer.from_numpy(syn.randn((32, 3, 224, 224), 900))
+        g = om.DeviceBuffer.from_numpy(syn.randn((32, 1000), 901, 0.01))
         net = GpuResNet18(om, make_params(seed=1), 32, train=True)
         for _ in range(3):
             net.forward_train(img)
             net.backward(g)
     elif name == "vit_attention":
         T, S, heads, dh, b = 64 * 197, 197, 12, 64, 64
-        src = om.DeviceBuffer.from_numpy(O.randn((T * 3 * heads * dh,), 5, 0.5))
+        src = om.DeviceBuffer.from_numpy(syn.randn((T * 3 * heads * dh,), 5, 0.5))
         qkv = om.DeviceBuffer.empty((T * 3 * heads * dh,), np.uint16)
         H.convertToHalf(src, qkv, T * 3 * heads * dh)
         ctx = om.DeviceBuffer.empty((T * heads * dh,), np.uint16)
@@ -666,21 +713,21 @@ def main():
     log(f"device {dev}")
 
     log(f"gemm 4096^3 NN: warmup {args.warmup}, steps {args.steps}")
-    ms, flops, wall, gemm_err = bench_gemm(om, args.steps, args.warmup)
+    ms, flops, wall, gemm_rows = bench_gemm(om, args.steps, args.warmup)
     tflops = flops / ms / 1e9
-    log(f"gemm {ms:.4f} ms/step  {tflops:.1f} TFLOP/s  parity {gemm_err:.2e}")
+    log(f"gemm {ms:.4f} ms/step  {tflops:.1f} TFLOP/s")
 
-    sweep = bench_gemm_sweep(om, args.steps, 2)
+    sweep, sweep_samples = bench_gemm_sweep(om, args.steps, 2)
 
     log("resnet18 conv stack b32")
     r_steps = max(5, args.steps // 2)
-    r_ms, r_flops, r_roof_ms, per, conv_err = bench_resnet18(om, r_steps, max(2, args.warmup))
+    r_ms, r_flops, r_roof_ms, per, conv_samples = bench_resnet18(om, r_steps, max(2, args.warmup))
     img_s = 32.0 / (r_ms / 1e3)
-    log(f"resnet18 {r_ms:.3f} ms/batch  {img_s:.0f} img/s  roof frac {r_roof_ms / r_ms:.3f}  parity {conv_err:.2e}")
+    log(f"resnet18 {r_ms:.3f} ms/batch  {img_s:.0f} img/s  roof frac {r_roof_ms / r_ms:.3f}")
 
     log("resnet18 network b32 (inference forward, training step)")
-    n_fwd_ms, n_fl, n_err, n_train_ms, n_train_fl = bench_resnet18_net(om, max(5, args.steps // 5), 2)
-    log(f"resnet18 net forward {n_fwd_ms:.3f} ms  {32 / n_fwd_ms * 1e3:.0f} img/s  logits err {n_err:.1e}; "
+    n_fwd_ms, n_fl, n_logits2, n_train_ms, n_train_fl = bench_resnet18_net(om, max(5, args.steps // 5), 2)
+    log(f"resnet18 net forward {n_fwd_ms:.3f} ms  {32 / n_fwd_ms * 1e3:.0f} img/s; "
         f"train step {n_train_ms:.3f} ms  {32 / n_train_ms * 1e3:.0f} img/s")
 
     log("resnet18 inferBatch pipeline (host images -> classes)")
@@ -702,13 +749,21 @@ def main():
         log(f"vit {'bf16' if bf else 'fp16'} {v_ms:.3f} ms  {v_flops / v_ms / 1e9:.1f} TFLOP/s; fused attention "
             f"{v_fused['ms'] * 1e3:.1f} us ({v_fused['hbm_gb_s']:.0f} GB/s) replaces {v_fused['replaces_ms'] * 1e3:.1f} us "
             f"of Q.K^T + P.V")
-    mlp_ms, mlp_flops = bench_mlp(om, max(20, args.steps), 5)
-    log(f"mlp step {mlp_ms * 1e3:.1f} us")
+    mlp_ms, mlp_flops, mlp_graph_ms, mlp_graph_same = bench_mlp(om, max(20, args.steps), 5)
+    log(f"mlp step {mlp_ms * 1e3:.1f} us (graph replay {mlp_graph_ms * 1e3:.1f} us, bit-identical {mlp_graph_same})")
 
     cpu = None
     cpu_r18 = None
     cpu_extra = {}
+    gemm_err = conv_err = n_err = None
     if rank == 0 and not args.no_cpu:
+        log("cpu checks of the sampled GPU results (oracle, float64)")
+        gemm_err = cpu_check_gemm(gemm_rows)
+        cpu_check_sweep(sweep, sweep_samples)
+        conv_err = cpu_check_resnet18(conv_samples)
+        n_err = cpu_check_resnet18_net(n_logits2)
+        log(f"parity: gemm {gemm_err:.2e}, sweep max {max(e['parity'] for e in sweep):.2e}, conv {conv_err:.2e}, "
+            f"network logits {n_err:.1e}")
         threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
         log(f"cpu baseline (reference CPUBackend, {threads} threads)")
         kind, cpu_tf, cpu_dt, n1 = cpu_baseline_gemm()
@@ -785,7 +840,10 @@ def main():
         "vit_b16_gemms": {"batch": 64, "tokens": 197, "hidden": 768, "heads": 12, **vit,
                           "cpu_baseline": cpu_extra.get("vit")},
         "mlp_784_256_128_10": {"batch": 128, "us_per_step": round(mlp_ms * 1e3, 2),
-                               "gflops": round(mlp_flops / mlp_ms / 1e6, 1), "cpu_baseline": cpu_extra.get("mlp")},
+                               "gflops": round(mlp_flops / mlp_ms / 1e6, 1),
+                               "graph_replay": {"us_per_step": round(mlp_graph_ms * 1e3, 2),
+                                                "bit_identical_to_eager": bool(mlp_graph_same)},
+                               "cpu_baseline": cpu_extra.get("mlp")},
     }
     print(json.dumps(line), flush=True)
 

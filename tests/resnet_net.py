@@ -20,7 +20,7 @@ from __future__ import annotations
 
 import numpy as np
 
-import oracle as O
+from omnimatchdeeplearningtool_amd import synthetic as S
 
 STAGES = [("l1", 64, 64, 1), ("l2", 64, 128, 2), ("l3", 128, 256, 2), ("l4", 256, 512, 2)]
 EPS = 1e-5
@@ -51,13 +51,13 @@ def make_params(seed: int = 0, num_classes: int = 1000) -> dict:
 
     def conv(name, cout, cin, ks):
         b = np.sqrt(6.0 / (cin * ks * ks))
-        P[name + ".w"] = O.uniform((cout, cin, ks, ks), nxt(), -b, b)
+        P[name + ".w"] = S.uniform((cout, cin, ks, ks), nxt(), -b, b)
 
     def bn(name, c):
-        P[name + ".gamma"] = O.uniform((c,), nxt(), 0.5, 1.5)
-        P[name + ".beta"] = O.randn((c,), nxt(), 0.1)
-        P[name + ".mean"] = O.randn((c,), nxt(), 0.1)
-        P[name + ".var"] = O.uniform((c,), nxt(), 0.5, 1.5)
+        P[name + ".gamma"] = S.uniform((c,), nxt(), 0.5, 1.5)
+        P[name + ".beta"] = S.randn((c,), nxt(), 0.1)
+        P[name + ".mean"] = S.randn((c,), nxt(), 0.1)
+        P[name + ".var"] = S.uniform((c,), nxt(), 0.5, 1.5)
 
     conv("stem", 64, 3, 7)
     bn("stem", 64)
@@ -70,8 +70,8 @@ def make_params(seed: int = 0, num_classes: int = 1000) -> dict:
             conv(pre + ".ds", co, ci, 1)
             bn(pre + ".ds", co)
     b = np.sqrt(6.0 / 512)
-    P["fc.w"] = O.uniform((512, num_classes), nxt(), -b, b)     # Linear weight [in, out] (linear.ixx:50-58)
-    P["fc.b"] = O.uniform((num_classes,), nxt(), -0.01, 0.01)
+    P["fc.w"] = S.uniform((512, num_classes), nxt(), -b, b)     # Linear weight [in, out] (linear.ixx:50-58)
+    P["fc.b"] = S.uniform((num_classes,), nxt(), -0.01, 0.01)
     return P
 
 
@@ -354,6 +354,7 @@ class GpuResNet18:
 def cpu_forward(P: dict, img: np.ndarray, backend: str = "oracle") -> np.ndarray:
     """The reference's unfused inference chain: conv2d -> batchNorm2d(eval) -> relu,
     add, maxPool2d, adaptiveAvgPool2d, matmul + addBias."""
+    import oracle as O
     def cbr(x, name, s, p, act=True):
         z = O.conv2d(x, P[name + ".w"], None, s, p, backend=backend)
         y, _, _ = O.batchnorm2d_eval(z, P[name + ".gamma"], P[name + ".beta"], P[name + ".mean"], P[name + ".var"],
@@ -375,6 +376,7 @@ def cpu_forward(P: dict, img: np.ndarray, backend: str = "oracle") -> np.ndarray
 def cpu_forward_train(P: dict, img: np.ndarray, backend: str = "oracle") -> dict:
     """Training forward with the reference's CPU functions. Returns every
     intermediate the backward needs (keys as GpuResNet18.forward_state)."""
+    import oracle as O
     Pm = {k: v.copy() for k, v in P.items()}   # running stats are updated in place
     f = {"img": img}
 
@@ -413,6 +415,7 @@ def cpu_backward(P: dict, f: dict, g_logits: np.ndarray, backend: str = "oracle"
     """Backward of the training step from the forward state f (from
     cpu_forward_train, or GpuResNet18.forward_state to replay the GPU's own
     forward decisions); returns the weight gradients (as GpuResNet18.grads)."""
+    import oracle as O
     B = g_logits.shape[0]
     pooled = np.ascontiguousarray(f["pooled"].reshape(B, -1))
     grads = {"fc.w": O.matmul(np.ascontiguousarray(pooled.T), g_logits, backend=backend),
