@@ -181,3 +181,36 @@ def test_strided_batched_shared_operand(hip):
         C64, bound = O.gemm_f64(A, B[i])
         assert O.normalized_error(C[i, :, :N], C64, bound) <= TOL
         assert np.all(C[i, :, N:] == 0)
+
+
+def _padded(X, ld):
+    """X [rows, cols] stored in rows x ld floats; the padding columns hold NaN."""
+    S = np.full((X.shape[0], ld), np.nan, np.float32)
+    S[:, :X.shape[1]] = X
+    return S
+
+
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
+@pytest.mark.parametrize("M,N,K", [(72, 88, 36), (64, 64, 4132)])
+def test_padded_leading_dims(hip, ta, tb, M, N, K):
+    """Leading dimensions past the logical width, batch strides, every
+    transposition, a last K slice that is partial (K % 16 = 4) and, for
+    K = 4132, split K. The padding holds NaN, so a load outside the logical
+    matrix shows up in C."""
+    b = 2
+    A = O.randn((b, M, K), 41)
+    B = O.randn((b, K, N), 42)
+    As = [A[i].T if ta else A[i] for i in range(b)]          # stored operand, rows x cols
+    Bs = [B[i].T if tb else B[i] for i in range(b)]
+    lda, ldb, ldc = As[0].shape[1] + 8, Bs[0].shape[1] + 12, N + 4
+    sA, sB, sC = As[0].shape[0] * lda, Bs[0].shape[0] * ldb, M * ldc
+    dA = to_dev(hip, np.stack([_padded(a, lda) for a in As]))
+    dB = to_dev(hip, np.stack([_padded(x, ldb) for x in Bs]))
+    dC = to_dev(hip, np.zeros((b, M, ldc), np.float32))
+    print(f"case padded ta={ta} tb={tb} M={M} N={N} K={K}", flush=True)
+    hip.call("omHipGemmStridedBatched", ta, tb, b, M, N, K, dA.ptr, lda, sA, dB.ptr, ldb, sB, dC.ptr, ldc, sC)
+    C = dC.numpy()
+    for i in range(b):
+        C64, bound = O.gemm_f64(A[i], B[i])
+        assert O.normalized_error(C[i, :, :N], C64, bound) <= TOL
+        assert np.all(C[i, :, N:] == 0)
