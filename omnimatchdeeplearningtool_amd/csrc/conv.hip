@@ -639,7 +639,6 @@ struct ConvPlan {
 static ConvPlan planConv(const ConvParams& p, bool haveSplitWs) {
     using Cfg = ConvCfg;
     ConvPlan pl{1, p.tilesM * p.tilesN, 1};
-    // TUNE-HOOK
     const long long U = cuCount();
     const long long T = (long long)p.tilesM * p.tilesN;
     const int nk = (p.K + Cfg::BK - 1) / Cfg::BK;

@@ -476,7 +476,6 @@ static int launchWgrad(const WgradParams& p, int splits, int xk) {
 // when Ho*Wo % 4 == 0 and x is 16-byte aligned); other 1x1 kernels read along
 // pixels; larger kernels read along taps with the gather mode of their size.
 static int xLoaderKind(int KH, int KW, int stride, int pad, long long HWo, const float* x) {
-    // TUNE-HOOK-WGRAD-X
     if (KH == 1 && KW == 1 && stride == 1 && pad == 0)
         return (HWo % 4 == 0 && (reinterpret_cast<uintptr_t>(x) & 15u) == 0) ? kXDenseVec : kXDense;
     if (KH * KW == 1) return kXPixels;
@@ -499,7 +498,6 @@ static void magicDivisor(uint32_t d, uint32_t& mul, uint32_t& shift) {
 // partials. Measured on MI355X over the ResNet-18/50 weight gradients at batch
 // 32 (e.g. 64x576x100352: 228 splits, 128x256x100352 1x1: 128 splits).
 static int planWgradSplits(long long tiles, long long Nq, long long Cout, long long Kc, int taps) {
-    // TUNE-HOOK-WGRAD
     const long long cus = cuCount();
     const long long target = (taps > 1 ? 8 : 4) * cus;
     long long s = (target + tiles - 1) / tiles;

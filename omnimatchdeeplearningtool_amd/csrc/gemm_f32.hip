@@ -304,7 +304,6 @@ struct GemmPlan {
 static GemmPlan planGemm(int M, int N, int K, int batch, bool wsOk) {
     const long long cus = cuCount();
     auto tiles = [&](int bm, int bn) { return (long long)((M + bm - 1) / bm) * ((N + bn - 1) / bn) * batch; };
-    // TUNE-HOOK-GEMM
     if (tiles(256, 256) >= cus) return {0, 1};
     if (tiles(128, 128) >= cus) return {1, 1};
     if (tiles(64, 64) >= cus || !wsOk || K < 1024) return {2, 1};

@@ -33,7 +33,6 @@ static int gridFor(long long n) {
 static dim3 planeGrid(long long planes, int rows, int cols) {
     const long long bx = (cols + 63) / 64, by = (rows + 3) / 4;
     long long zmax = std::max<long long>(1, 16384 / (bx * by));
-    // TUNE-HOOK-POOL
     return dim3((unsigned)bx, (unsigned)by,
                 (unsigned)std::max<long long>(1, std::min<long long>({planes, zmax, 65535LL})));
 }
