@@ -631,7 +631,7 @@ def frobenius_rel(C, Cref) -> float:
     return float(np.linalg.norm(C - R) / n) if n > 0 else float(np.linalg.norm(C))
 
 
-# Tolerances (north star): fp32 inputs 1e-4; fp16/bf16 inputs with fp32 accumulate 1e-2.
+# Tolerances: fp32 inputs 1e-4; fp16/bf16 inputs with fp32 accumulate 1e-2.
 TOL_FP32 = 1e-4
 TOL_HALF = 1e-2
 

@@ -4,7 +4,7 @@ Two bars, both K-scaled (|C - C_ref| <= tol * sum_k |a_ik||b_kj|):
   * against the oracle CPUBackend matmul on the SAME rounded inputs
     (halfToFloat(A), halfToFloat(B), matmul): tol 1e-4 (only accumulation
     order differs: every fp16/bf16 product is exact in fp32);
-  * against CPUBackend on the ORIGINAL fp32 inputs: tol 1e-2 (north star).
+  * against CPUBackend on the ORIGINAL fp32 inputs: tol 1e-2.
 Inputs are rounded to nearest-even (the reference's own FP16Converter
 truncates, fp16.ixx:92; the rounding rule is stated, not reproduced).
 Shapes: the ViT-B/16 projections (tokens 12608 = 64 x 197) on a token subset,
