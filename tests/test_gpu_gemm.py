@@ -4,9 +4,10 @@ Tolerance (K-scaled): for every output
     |C_hip - C_ref| <= 1e-4 * sum_k |a_ik| |b_kj|
 where C_ref is the oracle (bit-identical to the reference CPUBackend); the
 same bound is checked against float64 brute force. Shapes cover the fp32
-GEMM sweep (512^3 ... 8192^3, 128x4096x4096, 8192x256x2048; NN and NT), the MLP layers, the ViT Q.K^T / P.V shapes and ragged
-edges; the 4096^3 and 8192-row cases are checked on sampled rows against
-float64 so the oracle stays within seconds.
+GEMM sweep (512^3 ... 8192^3, 128x4096x4096, 8192x256x2048; NN and NT), the
+MLP layers, the ViT Q.K^T / P.V shapes and ragged edges; the 4096^3 and
+8192-row cases are checked on sampled rows against float64 so the oracle
+stays within seconds.
 """
 import numpy as np
 import pytest
