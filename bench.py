@@ -402,7 +402,8 @@ def bench_vit_half(om, steps: int, warmup: int, bf16: bool):
 
 
 def bench_mlp(om, steps: int, warmup: int, batch: int = 128):
-    """MLP 784-256-128-10 (ReLU) forward + backward through the HAL entries, fp32, batch 128."""
+    """MLP 784-256-128-10 (ReLU) forward + backward, fp32, batch 128: each Linear (+ ReLU) is one
+    fused launch, the backward the reference's NT / TN products and ReLU gates."""
     from omnimatchdeeplearningtool_amd.hiptime import StreamTimer
     H = om.HIPBackend
     dims = [784, 256, 128, 10]
@@ -418,18 +419,17 @@ def bench_mlp(om, steps: int, warmup: int, batch: int = 128):
     H.fillValue(g[-1], batch * 10, 0.01)
 
     def step():
+        # forward: one fused launch per layer, act(x W + b); the hidden layers
+        # keep only the activation, whose sign is the ReLU gate of the backward
         for j in range(3):
             i, o = dims[j], dims[j + 1]
-            H.matmul(a[j], Ws[j], z[j], batch, i, o)
-            H.addBias(z[j], bs[j], z[j], batch, o)
-            if j < 2:
-                H.relu(z[j], a[j + 1], batch * o)
+            H.linearBiasAct(a[j], Ws[j], bs[j], a[j + 1] if j < 2 else z[j], batch, i, o, 1 if j < 2 else 0)
         for j in reversed(range(3)):
             i, o = dims[j], dims[j + 1]
             H.matmulTransA(a[j], g[j], gW[j], i, batch, o)        # dW = A^T G
             H.matmulTransB(g[j], Ws[j], gA[j], batch, o, i)        # dA = G W^T (as the reference, every layer)
             if j > 0:
-                H.reluBackward(z[j - 1], gA[j], g[j - 1], batch * i)
+                H.reluBackward(a[j], gA[j], g[j - 1], batch * i)   # a > 0 exactly where x W + b > 0
 
     for _ in range(warmup):
         step()

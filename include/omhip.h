@@ -136,6 +136,13 @@ int omHipMatmulTransB(const float* pA, const float* pB, float* pC, int nM, int n
 /* NEW: C[M,N] = A[K,M]^T * B[K,N]. Reference composition: transpose2d(A, At, K, M);
  * matmul(At, B, C, M, K, N)  (the dB half of MatMulBackward autograd.ixx:276-286) */
 int omHipMatmulTransA(const float* pA, const float* pB, float* pC, int nM, int nK, int nN);
+/* NEW: out[M,N] = act(A[M,K] * W[K,N] + bias[N]) in one pass (bias nullable; nAct 0
+ * identity, 1 ReLU). Reference composition: Linear::forward's tensorMatmul +
+ * tensorAddBias (linear.ixx:50-58, tensor_ops.ixx:305-349, :542-576) followed by
+ * tensorReLU (tensor_ops.ixx:511-536); each element is the unfused chain's value:
+ * the same sum, then + bias, then x > 0 ? x : 0. */
+int omHipLinearBiasAct(const float* pA, const float* pW, const float* pBias, float* pOut, int nM, int nK, int nN,
+                       int nAct);
 /* replaces omCudaBatchedMatmul (cuh:112): C[b] = A[b] * B[b], strides M*K, K*N, M*N
  * (CPUBackend::batchedMatmul cpu_backend.ixx:1520-1532) */
 int omHipBatchedMatmul(const float* pA, const float* pB, float* pC, int nBatch, int nM, int nK, int nN);

@@ -195,6 +195,11 @@ public:
     static void matmulTransA(const float* pA, const float* pB, float* pC, int nM, int nK, int nN) {
         check(omHipMatmulTransA(pA, pB, pC, nM, nK, nN), "matmulTransA");
     }
+    // Linear + bias (+ ReLU when nAct = 1) in one pass: act(A * W + bias), W [K, N].
+    static void linearBiasAct(const float* pA, const float* pW, const float* pBias, float* pOut, int nM, int nK,
+                              int nN, int nAct) {
+        check(omHipLinearBiasAct(pA, pW, pBias, pOut, nM, nK, nN, nAct), "linearBiasAct");
+    }
     static void batchedMatmulTransB(const float* pA, const float* pB, float* pC, int nBatch, int nM, int nK, int nN) {
         check(omHipBatchedMatmulTransB(pA, pB, pC, nBatch, nM, nK, nN), "batchedMatmulTransB");
     }

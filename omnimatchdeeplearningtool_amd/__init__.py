@@ -86,6 +86,7 @@ _SIGS = {
     "omHipMatmul": [_vp, _vp, _vp, _i, _i, _i],
     "omHipMatmulTransB": [_vp, _vp, _vp, _i, _i, _i],
     "omHipMatmulTransA": [_vp, _vp, _vp, _i, _i, _i],
+    "omHipLinearBiasAct": [_vp, _vp, _vp, _vp, _i, _i, _i, _i],
     "omHipBatchedMatmul": [_vp, _vp, _vp, _i, _i, _i, _i],
     "omHipBatchedMatmulTransB": [_vp, _vp, _vp, _i, _i, _i, _i],
     "omHipGemmStridedBatched": [_i, _i, _i, _i, _i, _i, _vp, _ll, _ll, _vp, _ll, _ll, _vp, _ll, _ll],
@@ -475,6 +476,11 @@ class HIPBackend:
     def matmulTransA(pA, pB, pC, nM: int, nK: int, nN: int) -> None:
         """C = A[K,M]^T x B[K,N] (reference: transpose2d + matmul, autograd.ixx:276-286)."""
         call("omHipMatmulTransA", _ptr(pA), _ptr(pB), _ptr(pC), nM, nK, nN)
+
+    @staticmethod
+    def linearBiasAct(pA, pW, pBias, pOut, nM: int, nK: int, nN: int, nAct: int) -> None:
+        """act(A[M,K] * W[K,N] + bias[N]) in one pass (bias may be None; nAct 0 / 1 = ReLU)."""
+        call("omHipLinearBiasAct", _ptr(pA), _ptr(pW), _ptr(pBias), _ptr(pOut), nM, nK, nN, nAct)
 
     @staticmethod
     def batchedMatmulTransB(pA, pB, pC, nBatch: int, nM: int, nK: int, nN: int) -> None:

@@ -207,16 +207,24 @@ __global__ __launch_bounds__(Cfg::NT) void gemm_f32_kernel(GemmF32Params p) {
     float* C = partial ? p.ws + ((long long)split * gridDim.z + batch) * p.M * p.N : p.C + batch * p.sC;
     const long long ldc = partial ? p.N : p.ldc;
     const int li = lane & 31, h = lane >> 5;
+    // Bias and activation apply to the finished sums only (the split-K
+    // finish applies them to partial products' sum).
+    const bool bias = !partial && p.bias != nullptr;
+    const bool relu = !partial && p.act == 1;
 #pragma unroll
     for (int fm = 0; fm < Cfg::FM; ++fm) {
 #pragma unroll
         for (int fn = 0; fn < Cfg::FN; ++fn) {
             const int col = n0 + wn * Cfg::WN + fn * 32 + li;
             if (col >= p.N) continue;
+            const float b = bias ? p.bias[col] : 0.f;
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const int row = m0 + wm * Cfg::WM + fm * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
-                if (row < p.M) C[(long long)row * ldc + col] = acc[fm][fn][r];
+                float v = acc[fm][fn][r];
+                if (bias) v += b;
+                if (relu) v = v > 0.f ? v : 0.f;
+                if (row < p.M) C[(long long)row * ldc + col] = v;
             }
         }
     }
@@ -224,7 +232,7 @@ __global__ __launch_bounds__(Cfg::NT) void gemm_f32_kernel(GemmF32Params p) {
 
 // Sums the partials of every split in split order and writes C. Thread per element, columns fastest.
 __global__ void gemm_splitk_finish(const float* ws, float* C, int splits, int batch, int M, int N, long long ldc,
-                                   long long sC) {
+                                   long long sC, const float* bias, int act) {
     const long long plane = (long long)M * N;
     const long long total = plane * batch;
     for (long long i = blockIdx.x * (long long)blockDim.x + threadIdx.x; i < total;
@@ -233,6 +241,8 @@ __global__ void gemm_splitk_finish(const float* ws, float* C, int splits, int ba
         const long long r = e / N, c = e - r * N;
         float v = 0.f;
         for (int s = 0; s < splits; ++s) v += ws[((long long)s * batch + b) * plane + e];
+        if (bias) v += bias[c];
+        if (act == 1) v = v > 0.f ? v : 0.f;
         C[b * sC + r * ldc + c] = v;
     }
 }
@@ -327,9 +337,10 @@ static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 
 // finishing sum.
 static int gemmF32Run(bool ta, bool tb, int batch, int M, int N, int K, const float* A, long long lda, long long sA,
                       const float* B, long long ldb, long long sB, float* C, long long ldc, long long sC,
-                      GemmPlan plan) {
+                      GemmPlan plan, const float* bias, int act) {
     GemmF32Params prm{};
     prm.A = A; prm.B = B; prm.C = C;
+    prm.bias = bias; prm.act = act;
     prm.M = M; prm.N = N; prm.K = K;
     prm.lda = lda; prm.ldb = ldb; prm.ldc = ldc;
     prm.sA = sA; prm.sB = sB; prm.sC = sC;
@@ -354,7 +365,7 @@ static int gemmF32Run(bool ta, bool tb, int batch, int M, int N, int K, const fl
     const long long total = (long long)M * N * batch;
     const int blocks = (int)std::min<long long>((total + 255) / 256, (long long)cuCount() * 16);
     hipLaunchKernelGGL(gemm_splitk_finish, dim3(blocks), dim3(256), 0, stream(), prm.ws, C, splits, batch, M, N, ldc,
-                       sC);
+                       sC, prm.bias, prm.act);
     OMHIP_CHECK_LAUNCH();
     return 0;
 }
@@ -365,10 +376,10 @@ constexpr size_t kMaxSplitWorkspace = (size_t)256 << 20;
 int gemmF32(bool ta, bool tb, int batch, int M, int N, int K,
             const float* A, long long lda, long long sA,
             const float* B, long long ldb, long long sB,
-            float* C, long long ldc, long long sC) {
+            float* C, long long ldc, long long sC, const float* bias, int act) {
     const bool wsOk = (size_t)64 * batch * M * N * sizeof(float) <= kMaxSplitWorkspace;
     const GemmPlan plan = planGemm(M, N, K, batch, wsOk);
-    return gemmF32Run(ta, tb, batch, M, N, K, A, lda, sA, B, ldb, sB, C, ldc, sC, plan);
+    return gemmF32Run(ta, tb, batch, M, N, K, A, lda, sA, B, ldb, sB, C, ldc, sC, plan, bias, act);
 }
 
 __global__ void zero_rows_kernel(float* C, int rows, int cols, long long ldc, long long sC) {
@@ -419,6 +430,21 @@ int omHipMatmulTransB(const float* pA, const float* pB, float* pC, int nM, int n
 
 int omHipMatmulTransA(const float* pA, const float* pB, float* pC, int nM, int nK, int nN) {
     return gemmF32Checked("omHipMatmulTransA", true, false, 1, nM, nN, nK, pA, nM, 0, pB, nN, 0, pC, nN, 0);
+}
+
+int omHipLinearBiasAct(const float* pA, const float* pW, const float* pBias, float* pOut, int nM, int nK, int nN,
+                       int nAct) {
+    clearError();
+    if (nAct != 0 && nAct != 1) return fail("omHipLinearBiasAct: unknown activation %d", nAct);
+    if (nM <= 0 || nN <= 0) return 0;
+    if (!pOut) return fail("omHipLinearBiasAct: null output");
+    if (!pA || !pW || nK <= 0) {
+        // a product with no terms: act(0 + bias), as the unfused chain computes it
+        if (zeroOutput(pOut, 1, nM, nN, nN, 0)) return -1;
+        if (pBias && omHipAddBias(pOut, pBias, pOut, nM, nN, 1)) return -1;
+        return nAct == 1 ? omHipReLU(pOut, pOut, nM * nN) : 0;
+    }
+    return gemmF32(false, false, 1, nM, nN, nK, pA, nK, 0, pW, nN, 0, pOut, nN, 0, pBias, nAct);
 }
 
 int omHipBatchedMatmul(const float* pA, const float* pB, float* pC, int nBatch, int nM, int nK, int nN) {

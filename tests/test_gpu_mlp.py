@@ -87,3 +87,35 @@ def test_mlp_step(hip):
         assert np.array_equal(dGprev.numpy(), O.relu_backward(pre[k - 1], dAg.numpy()))
         G = dGprev.numpy()
         dG = dGprev
+
+
+@pytest.mark.parametrize("M,K,N", [(128, 784, 256), (128, 128, 10), (37, 29, 53), (64, 4096, 96)])
+@pytest.mark.parametrize("act", [0, 1])
+@pytest.mark.parametrize("with_bias", [True, False])
+def test_linear_bias_act(hip, M, K, N, act, with_bias):
+    """The fused Linear entry equals the unfused HAL chain (matmul -> addBias ->
+    ReLU) bit for bit, and the oracle chain under the K-scaled bound. 64 x 4096
+    x 96 takes the split-K path (bias and ReLU applied by the finishing sum)."""
+    H = hip.HIPBackend
+    A = O.randn((M, K), 51)
+    W = O.randn((K, N), 52, 0.05)
+    b = O.randn((N,), 53, 0.5) if with_bias else None
+    dA, dW = to_dev(hip, A), to_dev(hip, W)
+    db = to_dev(hip, b) if with_bias else None
+    fused, ref = empty_dev(hip, (M, N)), empty_dev(hip, (M, N))
+    print(f"case linear M={M} K={K} N={N} act={act} bias={with_bias}", flush=True)
+    H.linearBiasAct(dA, dW, db, fused, M, K, N, act)
+    H.matmul(dA, dW, ref, M, K, N)
+    if with_bias:
+        H.addBias(ref, db, ref, M, N)
+    if act:
+        H.relu(ref, ref, M * N)
+    got, want = fused.numpy(), ref.numpy()
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    y = O.matmul(A, W)
+    if with_bias:
+        y = O.add_bias(y, b)
+    if act:
+        y = O.relu(y)
+    C64, bound = O.gemm_f64(A, W)
+    assert O.normalized_error(got, y, bound + (np.abs(b)[None, :] if with_bias else 0)) <= TOL
