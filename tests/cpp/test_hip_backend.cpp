@@ -152,6 +152,19 @@ static void testTrainingPieces() {
     std::printf("TrainingPieces done\n");
 }
 
+static void testLinearBiasAct() {
+    // relu([1 2 3; -4 -5 -6] @ W + b) with W = [[1, 0], [0, 1], [1, 1]] (in = 3, out = 2), b = [0.5, -10]
+    Dev x(std::vector<float>{1, 2, 3, -4, -5, -6}), w(std::vector<float>{1, 0, 0, 1, 1, 1});
+    Dev b(std::vector<float>{0.5f, -10.f}), y(4), z(4);
+    HIPBackend::linearBiasAct(x.p, w.p, b.p, y.p, 2, 3, 2, 1);
+    auto h = y.host();
+    EXPECT_NEAR(h[0], 4.5, 0); EXPECT_NEAR(h[1], 0, 0); EXPECT_NEAR(h[2], 0, 0); EXPECT_NEAR(h[3], 0, 0);
+    HIPBackend::linearBiasAct(x.p, w.p, b.p, z.p, 2, 3, 2, 0);   // no activation
+    auto g = z.host();
+    EXPECT_NEAR(g[0], 4.5, 0); EXPECT_NEAR(g[1], -5, 0); EXPECT_NEAR(g[2], -9.5, 0); EXPECT_NEAR(g[3], -21, 0);
+    std::printf("LinearBiasAct done\n");
+}
+
 int main() {
     try {
         HIPBackend::init(0);
@@ -159,6 +172,7 @@ int main() {
         testMatmulNonSquare();
         testBatchedMatmulForward();
         testLinearZeroInput();
+        testLinearBiasAct();
         testConvAllOnes();
         testReluAndErrors();
         testTrainingPieces();
