@@ -230,20 +230,44 @@ __global__ __launch_bounds__(Cfg::NT) void gemm_f32_kernel(GemmF32Params p) {
     }
 }
 
-// Sums the partials of every split in split order and writes C. Thread per element, columns fastest.
-__global__ void gemm_splitk_finish(const float* ws, float* C, int splits, int batch, int M, int N, long long ldc,
-                                   long long sC, const float* bias, int act) {
+// Sums the partials of every split in split order and writes C (+ bias, act).
+// Block (x, y, z): columns [4 * 256x, ...) of rows y, y + gridDim.y, ... of
+// batch z; a thread takes four consecutive columns. VEC (N % 4 == 0, ldc and
+// the buffers 16-byte aligned): one 16-byte load per split and one store.
+template <bool VEC>
+__global__ __launch_bounds__(256) void gemm_splitk_finish(const float* ws, float* C, int splits, int batch, int M,
+                                                          int N, long long ldc, long long sC, const float* bias,
+                                                          int act) {
+    const int c0 = (blockIdx.x * 256 + threadIdx.x) * 4;
+    if (c0 >= N) return;
+    const long long b = blockIdx.z;
     const long long plane = (long long)M * N;
-    const long long total = plane * batch;
-    for (long long i = blockIdx.x * (long long)blockDim.x + threadIdx.x; i < total;
-         i += (long long)gridDim.x * blockDim.x) {
-        const long long b = i / plane, e = i - b * plane;
-        const long long r = e / N, c = e - r * N;
-        float v = 0.f;
-        for (int s = 0; s < splits; ++s) v += ws[((long long)s * batch + b) * plane + e];
-        if (bias) v += bias[c];
-        if (act == 1) v = v > 0.f ? v : 0.f;
-        C[b * sC + r * ldc + c] = v;
+    const long long sStride = plane * batch;
+    for (int r = blockIdx.y; r < M; r += gridDim.y) {
+        const float* src = ws + b * plane + (long long)r * N + c0;
+        f32x4 v = {0.f, 0.f, 0.f, 0.f};
+        for (int s = 0; s < splits; ++s) {
+            if constexpr (VEC) {
+                v += *reinterpret_cast<const f32x4*>(src + s * sStride);
+            } else {
+#pragma unroll
+                for (int w = 0; w < 4; ++w)
+                    if (c0 + w < N) v[w] += src[s * sStride + w];
+            }
+        }
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+            if (bias && c0 + w < N) v[w] += bias[c0 + w];
+            if (act == 1) v[w] = v[w] > 0.f ? v[w] : 0.f;
+        }
+        float* dst = C + b * sC + (long long)r * ldc + c0;
+        if constexpr (VEC) {
+            *reinterpret_cast<f32x4*>(dst) = v;
+        } else {
+#pragma unroll
+            for (int w = 0; w < 4; ++w)
+                if (c0 + w < N) dst[w] = v[w];
+        }
     }
 }
 
@@ -362,10 +386,14 @@ static int gemmF32Run(bool ta, bool tb, int batch, int M, int N, int K, const fl
     else if (ta && !tb) rc = launchCfg<true, false>(prm, batch, splits, plan.cfg, va, vb);
     else rc = launchCfg<true, true>(prm, batch, splits, plan.cfg, va, vb);
     if (rc || !partial) return rc;
-    const long long total = (long long)M * N * batch;
-    const int blocks = (int)std::min<long long>((total + 255) / 256, (long long)cuCount() * 16);
-    hipLaunchKernelGGL(gemm_splitk_finish, dim3(blocks), dim3(256), 0, stream(), prm.ws, C, splits, batch, M, N, ldc,
-                       sC, prm.bias, prm.act);
+    const dim3 grid((N + 1023) / 1024, std::min(M, 65535), batch);
+    const bool vec = N % 4 == 0 && ldc % 4 == 0 && sC % 4 == 0 && aligned16(C) && aligned16(prm.ws);
+    if (vec)
+        hipLaunchKernelGGL(gemm_splitk_finish<true>, grid, dim3(256), 0, stream(), prm.ws, C, splits, batch, M, N,
+                           ldc, sC, prm.bias, prm.act);
+    else
+        hipLaunchKernelGGL(gemm_splitk_finish<false>, grid, dim3(256), 0, stream(), prm.ws, C, splits, batch, M, N,
+                           ldc, sC, prm.bias, prm.act);
     OMHIP_CHECK_LAUNCH();
     return 0;
 }

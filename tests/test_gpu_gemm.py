@@ -42,6 +42,7 @@ SHAPES = [
     (197, 64, 197), (197, 197, 64),                       # ViT attention per head
     (512, 512, 512), (1024, 1024, 1024), (130, 257, 300),
     (128, 4096, 4096), (8192, 2048, 256), (2048, 2048, 2048),
+    (64, 2048, 30),                                       # split K with N % 4 != 0 (scalar finish)
 ]
 
 
