@@ -48,8 +48,13 @@ int omHipCleanup(void);
 /* NEW: the library stream as a hipStream_t (for event timing / interop) */
 int omHipGetStream(void** ppStream);
 /* NEW: route subsequent work to a caller-owned hipStream_t (NULL restores the
- * library stream). The caller keeps ownership of the stream. */
+ * library stream). The caller keeps ownership of the stream. Each stream gets its own
+ * split-K workspace (kept until omHipCleanup), so work on different streams may overlap. */
 int omHipSetStream(void* pStream);
+/* NEW: the caller is done with a stream it passed to omHipSetStream (call before destroying
+ * it): waits for the stream, returns its workspace to the pool (held back while any executable
+ * graph exists) and, if it is the current stream, restores the library stream. */
+int omHipReleaseStream(void* pStream);
 /* NEW: message of the last failing call on this thread ("" if none) */
 const char* omHipGetLastError(void);
 
@@ -97,14 +102,18 @@ int omHipTransferWaitCompute(void);
 /* ===== graphs (cuda_kernels.cuh:507-532: omCudaGraph*) ===== */
 
 /* replaces omCudaGraphBeginCapture (cuh:513): records the library calls that follow on the
- * compute stream instead of running them. Capture a sequence after running it once
- * eagerly, so that its workspaces, tables and pool blocks already exist. */
+ * compute stream (the library stream, or the caller stream set by omHipSetStream) instead of
+ * running them. Capture a sequence after running it once eagerly on that stream, so that its
+ * workspace, lookup tables and pool blocks already exist: a call that would need a larger
+ * workspace or a new table during the recording fails (-1, "records a graph"). */
 int omHipGraphBeginCapture(void);
 /* replaces omCudaGraphEndCapture (cuh:519): ends the recording, returns an executable graph */
 int omHipGraphEndCapture(void** ppGraphExec);
-/* replaces omCudaGraphLaunch (cuh:524): replays the graph on the compute stream */
+/* replaces omCudaGraphLaunch (cuh:524): replays the graph on the stream it was captured on
+ * (its nodes use that stream's workspace). While any executable graph exists, workspaces
+ * the library outgrows are kept allocated, so a replay never touches reused memory. */
 int omHipGraphLaunch(void* pGraphExec);
-/* replaces omCudaGraphDestroy (cuh:528) */
+/* replaces omCudaGraphDestroy (cuh:528): waits for the graph's stream, then frees the graph */
 int omHipGraphDestroy(void* pGraphExec);
 
 /* ===== fills / copy (src/cuda/cuda_kernels.cuh:257-266; CPUBackend cpu_backend.ixx:65-77, :444-446) ===== */
@@ -124,6 +133,33 @@ int omHipReLUBackward(const float* pIn, const float* pGradOut, float* pGradIn, i
  * CPUBackend::addBias(A, bias, out, batch, cols) (cpu_backend.ixx:433-440) is
  * the case nN=batch, nC=cols, nHW=1. */
 int omHipAddBias(const float* pData, const float* pBias, float* pOut, int nN, int nC, int nHW);
+
+/* ===== softmax, cross-entropy, bias gradient (cuda_kernels.cuh:122, :288, :348, :399) ===== */
+
+/* replaces omCudaSoftmax (cuh:122); CPUBackend::softmax cpu_backend.ixx:352-370: per row of
+ * [nBatch, nClasses], exp(x - max) / sum. The row maximum is the reference's scan (NaN
+ * elements skipped, a NaN first element kept); exp is the device expf and the sum's order is
+ * fixed but not sequential, so elements agree with CPUBackend to a few ulp, not bitwise. */
+int omHipSoftmax(const float* pIn, float* pOut, int nBatch, int nClasses);
+/* replaces omCudaCrossEntropy (cuh:399) with CPUBackend::crossEntropy's rule
+ * (cpu_backend.ixx:375-388; omCudaCrossEntropy's log(p + eps) differs): pResult[0] (device) =
+ * -sum of log(max(p, 1e-7)) over the elements whose target exceeds 0.5, divided by nBatch */
+int omHipCrossEntropy(const float* pSoftmax, const float* pTarget, float* pResult, int nBatch, int nClasses);
+/* replaces omCudaSoftmaxCrossEntropyBackward (cuh:288); CPUBackend::crossEntropySoftmaxBackward
+ * cpu_backend.ixx:393-410: grad = (softmax - target) * (1 / nBatch), bit-identical */
+int omHipSoftmaxCrossEntropyBackward(const float* pSoftmax, const float* pTarget, float* pGradLogits,
+                                     int nBatch, int nClasses);
+/* NEW: omHipSoftmax -> omHipCrossEntropy -> omHipSoftmaxCrossEntropyBackward in one launch, each
+ * output bit-identical to those calls' (tensorSoftmaxCrossEntropy tensor_ops.ixx:583-633 and
+ * SoftmaxCrossEntropyBackward autograd.ixx:440-488 with a loss gradient of 1). pSoftmax, pLoss
+ * and pGradLogits may each be NULL (not written). One workgroup: meant for class scores. */
+int omHipSoftmaxCrossEntropy(const float* pLogits, const float* pTarget, float* pSoftmax, float* pLoss,
+                             float* pGradLogits, int nBatch, int nClasses);
+/* replaces omCudaAddBiasBackward (cuh:348): gradBias[c] = sum over n and hw of gradOut[n,c,hw].
+ * AddBiasBackward (autograd.ixx:399-433) is the case nN = batch, nC = cols, nHW = 1; for it the
+ * rows are added in order from 0, bit-identical to the reference loop, up to 4096 rows (more
+ * rows: 16 ordered parts). nHW > 1: a fixed-order reduction per channel. */
+int omHipAddBiasBackward(const float* pGradOut, float* pGradBias, int nN, int nC, int nHW);
 
 /* ===== fp32 GEMM (cuda_kernels.cuh:109-117) ===== */
 

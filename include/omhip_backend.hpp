@@ -79,6 +79,38 @@ public:
     static void addBias(const float* pA, const float* pBias, float* pOut, int nBatch, int nCols) {
         check(omHipAddBias(pA, pBias, pOut, nBatch, nCols, 1), "addBias");
     }
+    // AddBiasBackward's reduction (autograd.ixx:399-433), CUDABackend::addBiasBackward's
+    // signature (cuda_backend.ixx:747): gradBias[c] = sum over n, hw of gradOut[n,c,hw].
+    static void addBiasBackward(const float* pGradOut, float* pGradBias, int nN, int nC, int nHW) {
+        check(omHipAddBiasBackward(pGradOut, pGradBias, nN, nC, nHW), "addBiasBackward");
+    }
+
+    // ---- softmax / cross-entropy (cpu_backend.ixx:352-410) ----
+    static void softmax(const float* pIn, float* pOut, int nBatch, int nClasses) {
+        check(omHipSoftmax(pIn, pOut, nBatch, nClasses), "softmax");
+    }
+    // CPUBackend::crossEntropy returns the loss: computed on the device, then copied back
+    // (waits for the stream).
+    static float crossEntropy(const float* pPred, const float* pTarget, int nBatch, int nClasses) {
+        float* d = nullptr;
+        check(omHipMalloc(reinterpret_cast<void**>(&d), sizeof(float)), "crossEntropy");
+        float v = 0.f;
+        const int rc = omHipCrossEntropy(pPred, pTarget, d, nBatch, nClasses);
+        const int rc2 = rc ? rc : omHipCopyD2H(&v, d, sizeof(float));
+        omHipFree(d);
+        check(rc2, "crossEntropy");
+        return v;
+    }
+    // CUDABackend::crossEntropyForward (cuda_backend.ixx:823): the loss stays on the device.
+    static void crossEntropyForward(const float* pSoftmax, const float* pTarget, float* pResult, int nBatch,
+                                    int nClasses) {
+        check(omHipCrossEntropy(pSoftmax, pTarget, pResult, nBatch, nClasses), "crossEntropyForward");
+    }
+    static void crossEntropySoftmaxBackward(const float* pSoftmax, const float* pTarget, float* pGradInput,
+                                            int nBatch, int nClasses) {
+        check(omHipSoftmaxCrossEntropyBackward(pSoftmax, pTarget, pGradInput, nBatch, nClasses),
+              "crossEntropySoftmaxBackward");
+    }
 
     // ---- conv / BN (cpu_backend.ixx:544-575, :619-658, :781-842) ----
     static void im2col(const float* pInput, int nCin, int nH, int nW, int nKH, int nKW, int nPadH, int nPadW,

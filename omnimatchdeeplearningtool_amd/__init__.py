@@ -21,7 +21,7 @@ from typing import Optional
 
 import numpy as np
 
-__all__ = ["lib", "lib_path", "DeviceBuffer", "HIPBackend", "OmHipError", "init", "synchronize"]
+__all__ = ["lib", "lib_path", "DeviceBuffer", "HIPBackend", "OmHipError", "init", "synchronize", "set_stream", "release_stream"]
 
 _PKG = os.path.dirname(os.path.abspath(__file__))
 _LIB: Optional[ctypes.CDLL] = None
@@ -52,7 +52,13 @@ _SIGS = {
     "omHipSyncComputeStream": [],
     "omHipCleanup": [],
     "omHipGetStream": [ctypes.POINTER(_vp)],
+    "omHipSoftmax": [_vp, _vp, _i, _i],
+    "omHipCrossEntropy": [_vp, _vp, _vp, _i, _i],
+    "omHipSoftmaxCrossEntropyBackward": [_vp, _vp, _vp, _i, _i],
+    "omHipSoftmaxCrossEntropy": [_vp, _vp, _vp, _vp, _vp, _i, _i],
+    "omHipAddBiasBackward": [_vp, _vp, _i, _i, _i],
     "omHipSetStream": [_vp],
+    "omHipReleaseStream": [_vp],
     "omHipMalloc": [ctypes.POINTER(_vp), _sz],
     "omHipFree": [_vp],
     "omHipCopyH2D": [_vp, _vp, _sz],
@@ -182,21 +188,41 @@ class Graph:
     on the compute stream. Capture a sequence after one eager run of it."""
 
     def __init__(self, fn):
+        self.handle = None
         call("omHipGraphBeginCapture")
+        g = _vp()
         try:
             fn()
-        finally:
-            g = _vp()
-            call("omHipGraphEndCapture", ctypes.byref(g))
+        except BaseException:
+            # end the recording and drop what was recorded, then report the failure
+            if lib().omHipGraphEndCapture(ctypes.byref(g)) == 0 and g.value:
+                lib().omHipGraphDestroy(g.value)
+            raise
+        call("omHipGraphEndCapture", ctypes.byref(g))
         self.handle = g.value
 
     def launch(self) -> None:
         call("omHipGraphLaunch", self.handle)
 
+    def destroy(self) -> None:
+        if getattr(self, "handle", None) and _LIB is not None:
+            call("omHipGraphDestroy", self.handle)
+        self.handle = None
+
     def __del__(self):
         if getattr(self, "handle", None) and _LIB is not None:
             lib().omHipGraphDestroy(self.handle)
             self.handle = None
+
+
+def set_stream(handle: Optional[int]) -> None:
+    """Routes later library calls to a caller-owned hipStream_t (None: the library stream)."""
+    call("omHipSetStream", handle)
+
+
+def release_stream(handle: int) -> None:
+    """Hands a caller stream's workspace back (call before destroying the stream)."""
+    call("omHipReleaseStream", handle)
 
 
 class ResNet18Infer:
@@ -343,6 +369,32 @@ class HIPBackend:
     @staticmethod
     def addBias(pA, pBias, pOut, nBatch: int, nCols: int) -> None:
         call("omHipAddBias", _ptr(pA), _ptr(pBias), _ptr(pOut), nBatch, nCols, 1)
+
+    @staticmethod
+    def addBiasBackward(pGradOut, pGradBias, nN: int, nC: int, nHW: int = 1) -> None:
+        """AddBiasBackward's column sum (autograd.ixx:399-433; cuda_backend.ixx:747)."""
+        call("omHipAddBiasBackward", _ptr(pGradOut), _ptr(pGradBias), nN, nC, nHW)
+
+    # ---- softmax / cross-entropy (cpu_backend.ixx:352-410) ----
+    @staticmethod
+    def softmax(pIn, pOut, nBatch: int, nClasses: int) -> None:
+        call("omHipSoftmax", _ptr(pIn), _ptr(pOut), nBatch, nClasses)
+
+    @staticmethod
+    def crossEntropyForward(pSoftmax, pTarget, pResult, nBatch: int, nClasses: int) -> None:
+        """CUDABackend::crossEntropyForward (cuda_backend.ixx:823) with CPUBackend::crossEntropy's
+        rule (cpu_backend.ixx:375-388): the loss is written to the device scalar pResult."""
+        call("omHipCrossEntropy", _ptr(pSoftmax), _ptr(pTarget), _ptr(pResult), nBatch, nClasses)
+
+    @staticmethod
+    def crossEntropySoftmaxBackward(pSoftmax, pTarget, pGradInput, nBatch: int, nClasses: int) -> None:
+        call("omHipSoftmaxCrossEntropyBackward", _ptr(pSoftmax), _ptr(pTarget), _ptr(pGradInput), nBatch, nClasses)
+
+    @staticmethod
+    def softmaxCrossEntropy(pLogits, pTarget, pSoftmax, pLoss, pGradLogits, nBatch: int, nClasses: int) -> None:
+        """softmax -> crossEntropy -> crossEntropySoftmaxBackward in one launch (any output may be None)."""
+        call("omHipSoftmaxCrossEntropy", _ptr(pLogits), _ptr(pTarget), _ptr(pSoftmax), _ptr(pLoss),
+             _ptr(pGradLogits), nBatch, nClasses)
 
     # ---- conv / BN (cpu_backend.ixx:544-575, :619-658, :781-842) ----
     @staticmethod

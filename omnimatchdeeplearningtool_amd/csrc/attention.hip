@@ -263,12 +263,7 @@ int launchAttnT(const AttnParams& prm) {
     constexpr int SP = NT * 16;
     constexpr size_t lds = (size_t)(SP * kLdK + kD * (SP + 8)) * sizeof(uint16_t);   // K, V^T
     static_assert(lds <= 160 * 1024, "attention tile exceeds LDS");
-    static bool s_attr = false;
-    if (!s_attr) {
-        OMHIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
-                                        hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds)));
-        s_attr = true;
-    }
+    OMHIP_CHECK(OMHIP_SET_MAX_DYNAMIC_LDS_ONCE(kern, lds));
     const int nq = OMHIP_ATTN_SPLIT ? std::min(NIT, (prm.S + NW * 16 - 1) / (NW * 16)) : 1;
     hipLaunchKernelGGL(kern, dim3(prm.B * prm.H, nq), dim3(NW * 64), lds, stream(), prm);
     OMHIP_CHECK_LAUNCH();

@@ -607,12 +607,7 @@ template <class Cfg, bool VA, int MODE>
 static int launchConvT(ConvParams& p, int gridX) {
     auto kern = conv_igemm_kernel<Cfg, VA, MODE>;
     const size_t lds = convLds<Cfg>();
-    static bool s_attr = false;
-    if (!s_attr) {
-        OMHIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
-                                        hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds)));
-        s_attr = true;
-    }
+    OMHIP_CHECK(OMHIP_SET_MAX_DYNAMIC_LDS_ONCE(kern, lds));
     hipLaunchKernelGGL(kern, dim3(gridX, p.splits), dim3(Cfg::NT), lds, stream(), p);
     OMHIP_CHECK_LAUNCH();
     return 0;
@@ -738,9 +733,18 @@ static const uint2* tapTable(int Cin, int H, int W, int KH, int KW) {
     void* mem = nullptr;
     if (omHipMalloc(&mem, (size_t)Kpad * sizeof(uint2)) != 0) return nullptr;
     uint2* tab = static_cast<uint2*>(mem);
+    if (capturing(stream())) {
+        (void)omHipFree(mem);
+        (void)publish(stream(), "conv tap table");
+        return nullptr;
+    }
     hipLaunchKernelGGL(build_tap_table, dim3((Kpad + 255) / 256), dim3(256), 0, stream(), tab, K, Kpad, KH, KW, H, W,
                        gatherMode(KH * KW));
-    if (hipGetLastError() != hipSuccess) return nullptr;
+    // complete before any stream reads it
+    if (hipGetLastError() != hipSuccess || publish(stream(), "conv tap table")) {
+        (void)omHipFree(mem);
+        return nullptr;
+    }
     g_tabs.emplace(key, tab);
     return tab;
 }
@@ -789,10 +793,12 @@ static int convChunk(ConvParams p, int n0, int nb) {
     float* ws = nullptr;
     if (pl.splits > 1) {
         ws = static_cast<float*>(workspace((size_t)pl.splits * p.Cout * p.Nq * sizeof(float)));
-        if (!ws) pl.splits = 1;
+        if (!ws && capturing(stream())) return -1;
+        if (!ws) pl.splits = 1;   // out of memory: one pass without partials
     } else if (pl.fullTiles < p.tilesM * p.tilesN) {
         const size_t remTiles = (size_t)(p.tilesM * p.tilesN - pl.fullTiles);
         ws = static_cast<float*>(workspace(remTiles * pl.remPieces * ConvCfg::BM * ConvCfg::BN * sizeof(float)));
+        if (!ws && capturing(stream())) return -1;
         if (!ws) pl.fullTiles = p.tilesM * p.tilesN;
     }
     return launchConv(p, pl, ws);
@@ -809,7 +815,10 @@ static int runConv(const char* name, ConvParams& p) {
     if (p.KH * p.KW <= 63)
         for (int rr = 0; rr < p.KH; ++rr) p.rowRep |= 1ull << (rr * p.KW);
     p.tab = tapTable(p.Cin, p.H, p.W, p.KH, p.KW);
-    if (!p.tab) return fail("%s: could not build the tap table", name);
+    if (!p.tab) {
+        if (capturing(stream())) return -1;   // tapTable recorded why
+        return fail("%s: could not build the tap table", name);
+    }
     const long long perImg = (long long)p.Cin * p.H * p.W * 4;
     long long chunk = std::max<long long>(1, ((long long)kMaxBufferBytes / 2) / perImg);
     chunk = std::min<long long>(chunk, std::max<long long>(1, (1LL << 30) / ((long long)p.Cout * p.Ho * p.Wo)));
@@ -909,14 +918,13 @@ int omHipConv2dIm2col(const float* pInput, const float* pWeight, const float* pB
     const long long K = (long long)nCin * nKH * nKW;
     const long long HWo = (long long)Ho * Wo;
     if (K > (1LL << 30) || HWo > (1LL << 30)) return fail("omHipConv2dIm2col: tensor too large");
-    void* col = nullptr;
-    if (omHipMalloc(&col, (size_t)(nBatch * K * HWo) * sizeof(float))) return -1;
+    void* col = workspace((size_t)nBatch * K * HWo * sizeof(float), kWsOperand);
+    if (!col) return -1;   // workspace() recorded the cause
     int rc = im2colBatched(pInput, static_cast<float*>(col), nBatch, nCin, nH, nW, nKH, nKW, nPad, nStride, Ho, Wo);
     if (!rc)
         rc = gemmF32(false, false, nBatch, nCout, (int)HWo, (int)K, pWeight, K, 0, static_cast<const float*>(col), HWo,
                      K * HWo, pOutput, HWo, (long long)nCout * HWo);
     if (!rc && pBias) rc = omHipAddBias(pOutput, pBias, pOutput, nBatch, nCout, (int)HWo);
-    (void)omHipFree(col);
     return rc;
 }
 

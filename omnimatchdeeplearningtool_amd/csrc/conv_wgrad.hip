@@ -542,9 +542,18 @@ static const uint4* pixelTable(int nb, int Cin, int H, int W, int KH, int KW, in
     void* mem = nullptr;
     if (omHipMalloc(&mem, (size_t)Nqpad * sizeof(uint4)) != 0) return nullptr;
     uint4* tab = static_cast<uint4*>(mem);
+    if (capturing(stream())) {
+        (void)omHipFree(mem);
+        (void)publish(stream(), "weight-gradient pixel table");
+        return nullptr;
+    }
     hipLaunchKernelGGL(build_pixel_table, dim3((Nqpad + 255) / 256), dim3(256), 0, stream(), tab, Nq, Nqpad, Cin, H,
                        W, KH, KW, stride, pad, Ho, Wo, gatherMode(KH * KW));
-    if (hipGetLastError() != hipSuccess) return nullptr;
+    // complete before any stream reads it
+    if (hipGetLastError() != hipSuccess || publish(stream(), "weight-gradient pixel table")) {
+        (void)omHipFree(mem);
+        return nullptr;
+    }
     g_ptabs.emplace(key, tab);
     return tab;
 }
@@ -591,13 +600,17 @@ int conv2dWeightGrad(const char* name, const float* x, const float* gO, float* g
         p.gBytes = (uint32_t)((long long)nb * imgG);
         if (xk != kXDense && xk != kXDenseVec) {
             p.ptab = pixelTable(nb, Cin, H, W, KH, KW, stride, pad, Ho, Wo);
-            if (!p.ptab) return fail("%s: could not build the pixel table", name);
+            if (!p.ptab) {
+                if (capturing(stream())) return -1;   // pixelTable recorded why
+                return fail("%s: could not build the pixel table", name);
+            }
         }
         int splits = planWgradSplits((long long)p.tilesM * p.tilesN, p.Nq, Cout, Kc, KH * KW);
         float* ws = nullptr;
         if (splits > 1) {
             ws = static_cast<float*>(workspace((size_t)splits * total * sizeof(float)));
-            if (!ws) splits = 1;
+            if (!ws && capturing(stream())) return -1;
+            if (!ws) splits = 1;   // out of memory: one pass without partials
         }
         p.qChunk = (p.Nq + splits - 1) / splits;
         p.qChunk = (p.qChunk + Cfg::BK - 1) / Cfg::BK * Cfg::BK;

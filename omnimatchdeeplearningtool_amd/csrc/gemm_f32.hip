@@ -282,12 +282,7 @@ template <class Cfg, bool TA, bool TB, int LA, int LB>
 static int launchOne(const GemmF32Params& prm, int batch, int splits) {
     auto kern = gemm_f32_kernel<Cfg, TA, TB, LA, LB>;
     const size_t lds = ldsBytesFor<Cfg, TA, TB>();
-    static bool s_attr = false;
-    if (!s_attr) {
-        OMHIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
-                                        hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds)));
-        s_attr = true;
-    }
+    OMHIP_CHECK(OMHIP_SET_MAX_DYNAMIC_LDS_ONCE(kern, lds));
     dim3 grid(prm.tilesM * prm.tilesN, splits, batch);
     hipLaunchKernelGGL(kern, grid, dim3(Cfg::NT), lds, stream(), prm);
     OMHIP_CHECK_LAUNCH();
@@ -375,7 +370,7 @@ static int gemmF32Run(bool ta, bool tb, int batch, int M, int N, int K, const fl
     const bool partial = splits > 1;
     if (partial) {
         prm.ws = static_cast<float*>(workspace((size_t)splits * batch * M * N * sizeof(float)));
-        if (!prm.ws) return fail("gemm: no workspace for %d x %d partial products", splits * batch, M * N);
+        if (!prm.ws) return -1;   // workspace() recorded the cause
     }
     // A is K-contiguous unless transposed; the vector axis is K (A) or M (A^T).
     const bool va = aligned16(A) && lda % 4 == 0 && sA % 4 == 0 && (ta ? M % 4 == 0 : K % 4 == 0);
@@ -470,7 +465,13 @@ int omHipLinearBiasAct(const float* pA, const float* pW, const float* pBias, flo
         // a product with no terms: act(0 + bias), as the unfused chain computes it
         if (zeroOutput(pOut, 1, nM, nN, nN, 0)) return -1;
         if (pBias && omHipAddBias(pOut, pBias, pOut, nM, nN, 1)) return -1;
-        return nAct == 1 ? omHipReLU(pOut, pOut, nM * nN) : 0;
+        if (nAct == 1) {
+            // omHipReLU takes an int count: walk M*N (up to 2^62 elements) in 2^30 pieces
+            const long long total = (long long)nM * nN;
+            for (long long off = 0; off < total; off += 1LL << 30)
+                if (omHipReLU(pOut + off, pOut + off, (int)std::min(total - off, 1LL << 30))) return -1;
+        }
+        return 0;
     }
     return gemmF32(false, false, 1, nM, nN, nK, pA, nK, 0, pW, nN, 0, pOut, nN, 0, pBias, nAct);
 }

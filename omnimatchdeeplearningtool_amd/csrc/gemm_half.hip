@@ -236,12 +236,7 @@ template <class Cfg, bool BF16, bool TA, bool TB, bool VA, bool VB>
 static int launchGeneric(GemmHalfParams prm, int batch) {
     auto kern = gemm_half_generic<Cfg, BF16, TA, TB, VA, VB>;
     const size_t lds = 2 * (size_t)(Cfg::BM + Cfg::BN) * Cfg::LD * sizeof(uint16_t);
-    static bool s_attr = false;
-    if (!s_attr) {
-        OMHIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
-                                        hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds)));
-        s_attr = true;
-    }
+    OMHIP_CHECK(OMHIP_SET_MAX_DYNAMIC_LDS_ONCE(kern, lds));
     prm.tilesM = (prm.M + Cfg::BM - 1) / Cfg::BM;
     prm.tilesN = (prm.N + Cfg::BN - 1) / Cfg::BN;
     hipLaunchKernelGGL(kern, dim3(prm.tilesM * prm.tilesN, 1, batch), dim3(Cfg::NT), lds, stream(), prm);
@@ -724,12 +719,7 @@ template <class Cfg, bool BF16, bool TA, bool TB, bool SWAP, bool RAG>
 static int launchFast(HalfFastParams prm, int batch) {
     auto kern = gemm_half_fast<Cfg, BF16, TA, TB, SWAP, RAG>;
     constexpr size_t lds = HalfOps<Cfg, TA, TB, RAG>::LDS_BYTES;
-    static bool s_attr = false;
-    if (!s_attr) {
-        OMHIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
-                                        hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds)));
-        s_attr = true;
-    }
+    OMHIP_CHECK(OMHIP_SET_MAX_DYNAMIC_LDS_ONCE(kern, lds));
     prm.tilesM = (prm.M + Cfg::BM - 1) / Cfg::BM;
     prm.tilesN = (prm.N + Cfg::BN - 1) / Cfg::BN;
     hipLaunchKernelGGL(kern, dim3(prm.tilesM * prm.tilesN, 1, batch), dim3(Cfg::NT), lds, stream(), prm);

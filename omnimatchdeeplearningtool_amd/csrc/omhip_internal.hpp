@@ -8,6 +8,7 @@
 #include <cstddef>
 #include <cstdint>
 #include <cstdio>
+#include <mutex>
 
 namespace omhip {
 
@@ -30,16 +31,44 @@ int fail(const char* fmt, ...);
 // Clears the thread-local error message (called at the top of every entry).
 void clearError();
 
-// Library-owned device workspace of at least `bytes` (grown on demand, kept
-// until omHipCleanup). Reuse is ordered by the single stream; nullptr on OOM.
-void* workspace(size_t bytes);
+// Device workspace of at least `bytes` for the current stream (one block per
+// stream and slot, grown on demand; an outgrown block stays allocated until its
+// last use has finished and no executable graph exists). Reuse is ordered by
+// the stream. Slot 0 holds split-K partial sums, slot 1 a call's temporary
+// operand (flipped weights, an im2col buffer) that slot-0 users read. nullptr
+// with the error recorded on OOM, or when the block must grow while the stream
+// records a graph.
+enum WsSlot { kWsPartials = 0, kWsOperand = 1 };
+void* workspace(size_t bytes, int slot = kWsPartials);
+
+// Whether stream s is recording a graph.
+bool capturing(hipStream_t s);
+
+// Makes a lookup table that a kernel just built on stream s visible to every
+// stream: waits for s. Fails (-1, naming `what`) while s records a graph.
+int publish(hipStream_t s, const char* what);
+
+// Sets a kernel's dynamic-LDS limit once per call site (each template
+// instantiation of the enclosing function has its own), thread-safely;
+// evaluates to the status of that single hipFuncSetAttribute call.
+#define OMHIP_SET_MAX_DYNAMIC_LDS_ONCE(kernel, bytes)                                          \
+    ([&]() -> hipError_t {                                                                      \
+        static std::once_flag omhip_once_;                                                      \
+        static hipError_t omhip_status_ = hipSuccess;                                           \
+        std::call_once(omhip_once_, [&] {                                                       \
+            omhip_status_ = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),          \
+                                                hipFuncAttributeMaxDynamicSharedMemorySize,     \
+                                                static_cast<int>(bytes));                       \
+        });                                                                                     \
+        return omhip_status_;                                                                   \
+    }())
 
 // Registers a function that omHipCleanup runs before the pool is released
 // (for caches of pool-owned device buffers).
 void onCleanup(void (*fn)());
 
 // Device properties cached at init.
-int cuCount();          // compute units of the current device
+int cuCount();           // compute units of the current device
 int maxSharedPerBlock(); // bytes
 
 }  // namespace omhip

@@ -10,6 +10,7 @@
 #include "../../include/omhip.h"
 
 #include <atomic>
+#include <map>
 #include <cstdarg>
 #include <cstring>
 #include <memory>
@@ -33,8 +34,33 @@ int g_maxShared = 65536;
 std::unique_ptr<CachingPool> g_pool;
 std::mutex g_wsMutex;
 std::vector<void (*)()> g_cleanupHooks;
-void* g_ws = nullptr;
-size_t g_wsBytes = 0;
+
+// Library workspace: one block per (stream, slot), so partials written on one
+// stream are never overwritten by work enqueued on another, and the two users
+// of one call (split-K partials, slot 0; a call's own temporary such as
+// flipped weights or an im2col buffer, slot 1) never share memory. A block that is
+// outgrown is retired, not freed: it goes back to the pool only once the event
+// recorded after its last use has completed and no executable graph exists
+// (a graph captured earlier may hold its address in its nodes).
+struct WsBlock {
+    void* p = nullptr;
+    size_t bytes = 0;
+};
+struct RetiredWs {
+    void* p;
+    hipEvent_t done;
+};
+std::map<std::pair<hipStream_t, int>, WsBlock> g_ws;   // (stream, slot)
+std::vector<RetiredWs> g_wsRetired;
+int g_liveGraphs = 0;   // executable graphs not yet destroyed (guarded by g_wsMutex)
+
+// Graph handle: the executable graph and the stream it was captured on (its
+// nodes use that stream's workspace, so replays are ordered on that stream).
+struct GraphHandle {
+    hipGraphExec_t exec;
+    hipStream_t stream;
+};
+thread_local hipStream_t t_captureStream = nullptr;
 
 thread_local char t_err[512] = {0};
 
@@ -120,22 +146,71 @@ void onCleanup(void (*fn)()) {
     g_cleanupHooks.push_back(fn);
 }
 
-void* workspace(size_t bytes) {
-    std::lock_guard<std::mutex> lock(g_wsMutex);
-    if (bytes <= g_wsBytes) return g_ws;
-    if (!g_inited.load(std::memory_order_acquire) && ensureInit(0, false)) return nullptr;
-    if (g_ws) {
-        // the old buffer may still be read by enqueued kernels: wait before handing it back
-        (void)hipStreamSynchronize(stream());
-        g_pool->release(g_ws);
-        g_ws = nullptr;
-        g_wsBytes = 0;
+bool capturing(hipStream_t s) {
+    hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(s, &st) != hipSuccess) {
+        (void)hipGetLastError();
+        return true;   // unknown: treat as recording, the caller then refuses to allocate
     }
-    void* p = g_pool->allocate(bytes);
-    if (!p) return nullptr;
-    g_ws = p;
-    g_wsBytes = bytes;
-    return g_ws;
+    return st != hipStreamCaptureStatusNone;
+}
+
+int publish(hipStream_t s, const char* what) {
+    if (capturing(s))
+        return fail("%s: not built yet while the stream records a graph; run the sequence once before capture", what);
+    OMHIP_CHECK(hipStreamSynchronize(s));
+    return 0;
+}
+
+namespace {
+// Returns retired blocks whose last use has finished to the pool (g_wsMutex held).
+void reapRetiredLocked() {
+    if (g_liveGraphs > 0) return;
+    for (size_t i = 0; i < g_wsRetired.size();) {
+        if (hipEventQuery(g_wsRetired[i].done) == hipSuccess) {
+            (void)hipEventDestroy(g_wsRetired[i].done);
+            g_pool->release(g_wsRetired[i].p);
+            g_wsRetired[i] = g_wsRetired.back();
+            g_wsRetired.pop_back();
+        } else {
+            (void)hipGetLastError();   // hipErrorNotReady
+            ++i;
+        }
+    }
+}
+}  // namespace
+
+void* workspace(size_t bytes, int slot) {
+    if (!g_inited.load(std::memory_order_acquire) && ensureInit(0, false)) return nullptr;
+    const hipStream_t s = stream();
+    std::lock_guard<std::mutex> lock(g_wsMutex);
+    WsBlock& w = g_ws[{s, slot}];
+    if (bytes <= w.bytes) return w.p;
+    if (capturing(s)) {
+        (void)fail("workspace of %zu bytes needed while the stream records a graph (it holds %zu); "
+                   "run the sequence once before capture", bytes, w.bytes);
+        return nullptr;
+    }
+    reapRetiredLocked();
+    if (w.p) {
+        hipEvent_t ev = nullptr;
+        if (hipEventCreateWithFlags(&ev, hipEventDisableTiming) != hipSuccess || hipEventRecord(ev, s) != hipSuccess) {
+            (void)fail("workspace: event: %s", hipGetErrorString(hipGetLastError()));
+            if (ev) (void)hipEventDestroy(ev);
+            return nullptr;
+        }
+        g_wsRetired.push_back({w.p, ev});
+        w = WsBlock{};
+    }
+    const size_t want = (bytes + (1u << 20) - 1) / (1u << 20) * (1u << 20);   // 1 MiB steps
+    void* p = g_pool->allocate(want);
+    if (!p) {
+        (void)fail("workspace: out of device memory (%zu bytes)", want);
+        return nullptr;
+    }
+    w.p = p;
+    w.bytes = want;
+    return p;
 }
 
 }  // namespace omhip
@@ -198,12 +273,13 @@ int omHipCleanup(void) {
     clearError();
     std::lock_guard<std::mutex> lock(g_initMutex);
     if (!g_inited.load(std::memory_order_acquire)) return 0;
-    (void)hipStreamSynchronize(g_ownStream);
+    (void)hipDeviceSynchronize();   // every stream that used a workspace or a table
     std::vector<void (*)()> hooks;
     {
         std::lock_guard<std::mutex> wsLock(g_wsMutex);
-        g_ws = nullptr;
-        g_wsBytes = 0;
+        g_ws.clear();
+        for (auto& r : g_wsRetired) (void)hipEventDestroy(r.done);
+        g_wsRetired.clear();   // their memory goes with the pool below
         hooks = g_cleanupHooks;
     }
     for (auto fn : hooks) fn();
@@ -224,6 +300,35 @@ int omHipCleanup(void) {
     g_ownStream = nullptr;
     g_userStream.store(nullptr, std::memory_order_release);
     g_inited.store(false, std::memory_order_release);
+    return 0;
+}
+
+int omHipReleaseStream(void* pStream) {
+    clearError();
+    if (!pStream || !g_inited.load(std::memory_order_acquire)) return 0;
+    const hipStream_t s = static_cast<hipStream_t>(pStream);
+    if (capturing(s)) return fail("omHipReleaseStream: the stream records a graph");
+    OMHIP_CHECK(hipStreamSynchronize(s));
+    std::lock_guard<std::mutex> lock(g_wsMutex);
+    for (auto it = g_ws.begin(); it != g_ws.end();) {
+        if (it->first.first != s) {
+            ++it;
+            continue;
+        }
+        if (it->second.p) {
+            if (g_liveGraphs > 0) {
+                // a graph captured on this stream may still replay: keep the block until it is gone
+                hipEvent_t ev = nullptr;
+                OMHIP_CHECK(hipEventCreateWithFlags(&ev, hipEventDisableTiming));
+                OMHIP_CHECK(hipEventRecord(ev, s));
+                g_wsRetired.push_back({it->second.p, ev});
+            } else {
+                g_pool->release(it->second.p);
+            }
+        }
+        it = g_ws.erase(it);
+    }
+    if (g_userStream.load(std::memory_order_acquire) == s) g_userStream.store(nullptr, std::memory_order_release);
     return 0;
 }
 
@@ -387,8 +492,10 @@ int omHipTransferWaitCompute(void) {
 int omHipGraphBeginCapture(void) {
     clearError();
     if (ensureInit(0, false)) return -1;
+    const hipStream_t s = stream();
     // relaxed: the pool may still call hipMalloc while a graph is recorded
-    OMHIP_CHECK(hipStreamBeginCapture(stream(), hipStreamCaptureModeRelaxed));
+    OMHIP_CHECK(hipStreamBeginCapture(s, hipStreamCaptureModeRelaxed));
+    t_captureStream = s;
     return 0;
 }
 
@@ -396,27 +503,44 @@ int omHipGraphEndCapture(void** ppGraphExec) {
     clearError();
     if (!ppGraphExec) return fail("omHipGraphEndCapture: null output");
     *ppGraphExec = nullptr;
+    const hipStream_t s = t_captureStream ? t_captureStream : stream();
+    t_captureStream = nullptr;
     hipGraph_t g = nullptr;
-    OMHIP_CHECK(hipStreamEndCapture(stream(), &g));
+    OMHIP_CHECK(hipStreamEndCapture(s, &g));
     hipGraphExec_t exec = nullptr;
     const hipError_t e = hipGraphInstantiate(&exec, g, nullptr, nullptr, 0);
     (void)hipGraphDestroy(g);
     if (e != hipSuccess) return fail("hipGraphInstantiate: %s", hipGetErrorString(e));
-    *ppGraphExec = static_cast<void*>(exec);
+    {
+        std::lock_guard<std::mutex> lock(g_wsMutex);
+        ++g_liveGraphs;
+    }
+    *ppGraphExec = static_cast<void*>(new GraphHandle{exec, s});
     return 0;
 }
 
 int omHipGraphLaunch(void* pGraphExec) {
     clearError();
     if (!pGraphExec) return fail("omHipGraphLaunch: null graph");
-    OMHIP_CHECK(hipGraphLaunch(static_cast<hipGraphExec_t>(pGraphExec), stream()));
+    const GraphHandle* h = static_cast<const GraphHandle*>(pGraphExec);
+    OMHIP_CHECK(hipGraphLaunch(h->exec, h->stream));
     return 0;
 }
 
 int omHipGraphDestroy(void* pGraphExec) {
     clearError();
     if (!pGraphExec) return 0;
-    OMHIP_CHECK(hipGraphExecDestroy(static_cast<hipGraphExec_t>(pGraphExec)));
+    GraphHandle* h = static_cast<GraphHandle*>(pGraphExec);
+    // replays still running may use retired workspaces: let them finish first
+    const hipError_t es = hipStreamSynchronize(h->stream);
+    const hipError_t ed = hipGraphExecDestroy(h->exec);
+    delete h;
+    {
+        std::lock_guard<std::mutex> lock(g_wsMutex);
+        --g_liveGraphs;
+    }
+    OMHIP_CHECK(es);
+    OMHIP_CHECK(ed);
     return 0;
 }
 

@@ -348,7 +348,7 @@ static int channelSums(const float* x, const float* dy, const float* mean, const
                        float* out1, int N, int C, int HW, float divisor, bool accumulate) {
     const int P = channelParts(N, C);
     float* part = static_cast<float*>(workspace((size_t)C * P * 2 * sizeof(float)));
-    if (!part) return fail("channel reduction: no workspace");
+    if (!part) return -1;   // workspace() recorded the cause
     hipLaunchKernelGGL(chan_partial_kernel<MODE>, dim3(C, P), dim3(256), 0, stream(), x, dy, nullptr, mean, invStd,
                        nullptr, part, N, C, HW, P, 1.0f);
     OMHIP_CHECK_LAUNCH();
@@ -365,7 +365,7 @@ int batchNorm2dTrainAct(const float* x, float* y, const float* gamma, const floa
     const float cnt = (float)((long long)N * HW);
     const int P = channelParts(N, C);
     float* part = static_cast<float*>(workspace((size_t)C * P * 4 * sizeof(float)));
-    if (!part) return fail("batchNorm2d: no workspace");
+    if (!part) return -1;
     float* part0 = part;
     float* part1 = part + (size_t)C * P * 2;
     // two passes, as the reference: sum(x), then sum((x-mean)^2) with the first pass's mean
@@ -396,7 +396,7 @@ static int batchNorm2dBackwardMasked(const char* name, const float* gO, const fl
     const int HW = H * W;
     const int P = channelParts(N, C);
     float* part = static_cast<float*>(workspace((size_t)C * P * 2 * sizeof(float)));
-    if (!part) return fail("%s: no workspace", name);
+    if (!part) return -1;
     hipLaunchKernelGGL(chan_partial_kernel<2>, dim3(C, P), dim3(256), 0, stream(), x, gO, mask, mean, invStd, nullptr,
                        part, N, C, HW, P, 1.0f);
     OMHIP_CHECK_LAUNCH();
@@ -446,8 +446,8 @@ int omHipConv2dBackwardInput(const float* pGradOutput, const float* pWeight, flo
         hipLaunchKernelGGL(zero_fill_kernel, dim3(gridFor(n)), dim3(256), 0, stream(), pGradInput, n);
         OMHIP_CHECK_LAUNCH();
     }
-    float* wf = nullptr;
-    if (omHipMalloc(reinterpret_cast<void**>(&wf), (size_t)wsz * sizeof(float))) return -1;
+    float* wf = static_cast<float*>(workspace((size_t)wsz * sizeof(float), kWsOperand));
+    if (!wf) return -1;   // workspace() recorded the cause
     hipLaunchKernelGGL(phase_flip_kernel, dim3(gridFor(wsz)), dim3(256), 0, stream(), pWeight, wf, nCout, nCin, nKH,
                        nKW, s, p);
     int rc = hipGetLastError() == hipSuccess ? 0 : fail("%s: flip launch failed", name);
@@ -464,7 +464,6 @@ int omHipConv2dBackwardInput(const float* pGradOutput, const float* pWeight, flo
                               Wp, nH, nW, s, a, b);
         }
     }
-    (void)omHipFree(wf);   // stream-ordered reuse: later work on the stream runs after the convs
     return rc;
 }
 

@@ -97,11 +97,15 @@ def lib() -> ctypes.CDLL:
             "omrefAdd": [_f, _f, _f, _sz],
             "omrefSoftmax": [_f, _f, _i, _i],
             "omrefAttention": [_f, _f, _i, _i, _i, _i, ctypes.c_float],
+            "omrefCrossEntropySoftmaxBackward": [_f, _f, _f, _i, _i],
+            "omrefAddBiasBackward": [_f, _f, _i, _i, _i],
         }
         for name, args in sig.items():
             fn = getattr(L, name)
             fn.argtypes = args
             fn.restype = None
+        L.omrefCrossEntropy.argtypes = [_f, _f, _i, _i]
+        L.omrefCrossEntropy.restype = ctypes.c_float
         L.omrefHasAvx2.restype = ctypes.c_int
         L.omrefMaxThreads.restype = ctypes.c_int
         _LIB = L
@@ -138,11 +142,14 @@ def ref_lib() -> Optional[ctypes.CDLL]:
                 "refAdaptiveAvgPool2dBackward": [_f, _f] + [_i] * 6,
                 "refAdd": [_f, _f, _f, _sz],
                 "refSoftmax": [_f, _f, _i, _i],
+                "refCrossEntropySoftmaxBackward": [_f, _f, _f, _i, _i],
             }
             for name, args in sig.items():
                 fn = getattr(R, name)
                 fn.argtypes = args
                 fn.restype = None
+            R.refCrossEntropy.argtypes = [_f, _f, _i, _i]
+            R.refCrossEntropy.restype = ctypes.c_float
             _REF = R
     return _REF
 
@@ -451,6 +458,36 @@ def softmax(x, backend: str = "oracle") -> np.ndarray:
     x = _f32(x)
     out = np.empty_like(x)
     _fn("Softmax", backend)(_p(x), _p(out), x.size // x.shape[-1], x.shape[-1])
+    return out
+
+
+def cross_entropy(pred, target, backend: str = "oracle") -> float:
+    """CPUBackend::crossEntropy (cpu_backend.ixx:375-388): -sum log(max(p, 1e-7)) over the
+    elements whose target exceeds 0.5, divided by the batch (float32)."""
+    pred, target = _f32(pred), _f32(target)
+    rows, cols = pred.size // pred.shape[-1], pred.shape[-1]
+    if backend == "reference":
+        R = ref_lib()
+        if R is None:
+            raise RuntimeError("the compiled reference (oracle/_ref) is not built")
+        return float(np.float32(R.refCrossEntropy(_p(pred), _p(target), rows, cols)))
+    return float(np.float32(lib().omrefCrossEntropy(_p(pred), _p(target), rows, cols)))
+
+
+def cross_entropy_softmax_backward(s, target, backend: str = "oracle") -> np.ndarray:
+    """CPUBackend::crossEntropySoftmaxBackward (cpu_backend.ixx:393-410): (s - t) * (1 / batch)."""
+    s, target = _f32(s), _f32(target)
+    out = np.empty_like(s)
+    _fn("CrossEntropySoftmaxBackward", backend)(_p(s), _p(target), _p(out), s.size // s.shape[-1], s.shape[-1])
+    return out
+
+
+def add_bias_backward(g, N, C, HW=1) -> np.ndarray:
+    """AddBiasBackward's bias gradient (autograd.ixx:428-433): per channel, the zeroed
+    gradient adds every (n, hw) element in order."""
+    g = _f32(g)
+    out = np.empty(C, np.float32)
+    lib().omrefAddBiasBackward(_p(g), _p(out), N, C, HW)
     return out
 
 

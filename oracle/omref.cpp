@@ -461,6 +461,37 @@ void omrefSoftmax(const float* in, float* out, int rows, int cols) {
     }
 }
 
+// cpu_backend.ixx:375-388 — loss -= log(max(p, 1e-7)) over the elements whose target
+// exceeds 0.5, in (row, class) order; divided by the batch.
+float omrefCrossEntropy(const float* pred, const float* tgt, int rows, int cols) {
+    float loss = 0.f;
+    for (int b = 0; b < rows; ++b)
+        for (int j = 0; j < cols; ++j)
+            if (tgt[(size_t)b * cols + j] > 0.5f) {
+                float p = pred[(size_t)b * cols + j];
+                if (p < 1e-7f) p = 1e-7f;
+                loss -= std::log(p);
+            }
+    return loss / (float)rows;
+}
+
+// cpu_backend.ixx:393-410 — grad = (softmax - target) * (1 / batch).
+void omrefCrossEntropySoftmaxBackward(const float* s, const float* t, float* g, int rows, int cols) {
+    const float scale = 1.0f / (float)rows;
+    const size_t n = (size_t)rows * cols;
+    for (size_t i = 0; i < n; ++i) g[i] = (s[i] - t[i]) * scale;
+}
+
+// autograd.ixx:428-433 (AddBiasBackward, CPU path) — bias gradient: the zeroed
+// gradient accumulates every row in order; for an [N, C, HW] gradient the
+// rows are the (n, hw) pairs in that order.
+void omrefAddBiasBackward(const float* g, float* gb, int N, int C, int HW) {
+    for (int c = 0; c < C; ++c) gb[c] = 0.f;
+    for (int n = 0; n < N; ++n)
+        for (int c = 0; c < C; ++c)
+            for (int hw = 0; hw < HW; ++hw) gb[c] += g[((size_t)n * C + c) * HW + hw];
+}
+
 // om.engine.vit.ixx:193-236 (MultiHeadAttention::forward, CPU path, after the QKV
 // projection): split heads with Q scaled, scores = Q x K^T (transpose2d +
 // batchedMatmul), softmax over the last dim, context = P x V, merge heads.

@@ -62,4 +62,10 @@ void refAdaptiveAvgPool2dBackward(const float* gO, float* gI, int n, int c, int 
 }
 void refAdd(const float* a, const float* b, float* out, size_t n) { om::CPUBackend::add(a, b, out, n); }
 void refSoftmax(const float* in, float* out, int rows, int cols) { om::CPUBackend::softmax(in, out, rows, cols); }
+float refCrossEntropy(const float* p, const float* t, int rows, int cols) {
+    return om::CPUBackend::crossEntropy(p, t, rows, cols);
+}
+void refCrossEntropySoftmaxBackward(const float* s, const float* t, float* g, int rows, int cols) {
+    om::CPUBackend::crossEntropySoftmaxBackward(s, t, g, rows, cols);
+}
 }

@@ -106,6 +106,27 @@ def main() -> None:
     a1, a2 = O.randn((37,), 71), O.randn((37,), 72)
     put("add", a=a1, b=a2, out=O.add(a1, a2, backend="reference"))
 
+    # softmax rows with ties, large magnitudes, -inf and a NaN first element
+    sm = O.randn((6, 13), 73, 4.0)
+    sm[1, :5] = 2.5                                           # tied maxima
+    sm[2] *= 40.0                                             # exp underflows for most of the row
+    sm[3, 4] = -np.inf
+    sm[4, 0] = np.nan
+    sm[5, 7] = np.nan                                         # skipped by the max scan
+    put("softmax_6x13", x=sm, y=O.softmax(sm, backend="reference"))
+    # attention core after the QKV projection, from the reference's transpose / batchedMatmul / softmax
+    B_, S_, H_, D_ = 2, 7, 3, 4
+    qkv = O.randn((B_ * S_, 3 * H_ * D_), 74)
+    put("attention_2x7x3x4", qkv=qkv, out=O.attention(qkv, B_, S_, H_, D_, 0.5, backend="reference"))
+    # cross-entropy (clamped zero probability, a row with two targets) and its joint gradient
+    p = O.softmax(O.randn((5, 10), 75, 3.0), backend="reference")
+    p[1, 3] = 0.0
+    t = np.zeros((5, 10), np.float32)
+    t[np.arange(5), [2, 3, 9, 0, 4]] = 1.0
+    t[4, 7] = 0.75
+    put("cross_entropy_5x10", p=p, t=t, loss=np.float32(O.cross_entropy(p, t, backend="reference")),
+        grad=O.cross_entropy_softmax_backward(p, t, backend="reference"))
+
     path = os.path.join(HERE, "reference_cpubackend.npz")
     np.savez_compressed(path, **out)
     print(f"wrote {path} ({os.path.getsize(path)} bytes, {len(out)} arrays)")

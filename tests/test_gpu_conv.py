@@ -6,7 +6,8 @@ the float64 conv of |x| and |w| (plus |bias|), scaled by |gamma| * invStd after
 BN — the conv analogue of sum_k |a_ik||b_kj|. Every ResNet-18 conv shape (the
 benchmark's 20 layers) runs at batch 2 against the oracle and at batch 32 on
 images {0, 1, 30, 31} (tiles straddle image boundaries differently there);
-ResNet-50 shapes, odd geometries and the explicit im2col path follow.
+every distinct ResNet-50 geometry runs at batch 2, the benchmark's batch-64
+plans on sampled images; odd geometries and the explicit im2col path follow.
 """
 import zlib
 
@@ -135,7 +136,17 @@ def test_split_k_finish(hip, geom, variant):
     _check(out, x, wt, bias, bn, 1 if bn is not None else 0, s, p)
 
 
-R50 = [c for c in resnet50_convs() if c[0].endswith((".0.conv1", ".0.conv2", ".0.conv3", ".0.ds", "stem"))]
+def _distinct(convs):
+    """First layer of each distinct geometry (Cin, H, W, Cout, K, stride, pad)."""
+    seen, out = set(), []
+    for c in convs:
+        if c[1:] not in seen:
+            seen.add(c[1:])
+            out.append(c)
+    return out
+
+
+R50 = _distinct(resnet50_convs())     # 23 geometries cover all 53 ResNet-50 convs
 
 
 @pytest.mark.parametrize("shape", R50, ids=[s[0] for s in R50])
@@ -145,8 +156,28 @@ def test_resnet50_layer_fused_b2(hip, shape):
     x = O.randn((2, cin, h, w), seed)
     wt = _kaiming_uniform((cout, cin, k, k), seed + 10)
     bn = _params(cout, seed + 20)
+    print(f"case r50 {name} b2", flush=True)
     out = _run_conv(hip, x, wt, None, bn, 1, s, p)
     _check(out, x, wt, None, bn, 1, s, p)
+
+
+R50_B64 = [c for c in resnet50_convs() if c[0] in ("stem", "l1.1.conv1", "l2.1.conv2", "l3.1.conv1", "l4.1.conv1",
+                                                     "l4.0.ds", "l3.0.conv2", "l4.1.conv3")]
+
+
+@pytest.mark.parametrize("shape", R50_B64, ids=[s[0] for s in R50_B64])
+def test_resnet50_layer_fused_b64_sampled(hip, shape):
+    """The benchmark's batch-64 launch plan (tile counts, split-K factors, remainder pieces and
+    batch chunks) on images {0, 1, 33, 62, 63}."""
+    name, cin, h, w, cout, k, s, p = shape
+    seed = zlib.crc32(("r50b64" + name).encode()) % 10000
+    x = O.randn((64, cin, h, w), seed)
+    wt = _kaiming_uniform((cout, cin, k, k), seed + 10)
+    bn = _params(cout, seed + 20)
+    print(f"case r50 {name} b64", flush=True)
+    out = _run_conv(hip, x, wt, None, bn, 1, s, p)
+    idx = [0, 1, 33, 62, 63]
+    _check(out[idx], np.ascontiguousarray(x[idx]), wt, None, bn, 1, s, p)
 
 
 ODD = [

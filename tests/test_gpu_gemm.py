@@ -6,8 +6,8 @@ where C_ref is the oracle (bit-identical to the reference CPUBackend); the
 same bound is checked against float64 brute force. Shapes cover the fp32
 GEMM sweep (512^3 ... 8192^3, 128x4096x4096, 8192x256x2048; NN and NT), the
 MLP layers, the ViT Q.K^T / P.V shapes and ragged edges; the 4096^3 and
-8192-row cases are checked on sampled rows against float64 so the oracle
-stays within seconds.
+8192^3 cubes are checked on sampled rows against float64 plus a checksum of
+all of C, so the checks stay within seconds.
 """
 import numpy as np
 import pytest
@@ -117,15 +117,17 @@ def test_batched_ones_known_answer(hip):
     assert np.all(dC.numpy() == 4.0)
 
 
+@pytest.mark.parametrize("n", [4096, 8192])
 @pytest.mark.parametrize("trans", [False, True])
-def test_4096_cube_sampled(hip, trans):
-    """4096^3 (the headline shape): rows sampled against float64."""
-    M = K = N = 4096
-    A = O.randn((M, K), 11)
-    B = O.randn((N, K) if trans else (K, N), 12)
-    print(f"case 4096^3 trans={trans}", flush=True)
+def test_cube_sampled(hip, n, trans):
+    """4096^3 (the headline shape) and 8192^3: rows sampled against float64 (first, middle,
+    tile-edge and last rows), and a checksum of every element."""
+    M = K = N = n
+    A = O.randn((M, K), 11 + n)
+    B = O.randn((N, K) if trans else (K, N), 12 + n)
+    print(f"case {n}^3 trans={trans}", flush=True)
     C = _run(hip, "omHipMatmulTransB" if trans else "omHipMatmul", A, B, M, K, N)
-    rows = np.r_[0:8, 1000:1008, 2040:2056, 4088:4096]
+    rows = np.r_[0:8, n // 4 - 8:n // 4 + 8, n // 2 - 8:n // 2 + 8, n - 8:n]
     C64, bound = O.gemm_f64(A[rows], B, transB=trans)
     assert O.normalized_error(C[rows], C64, bound) <= TOL
     # checksum of checksums over all of C: 1^T C 1 = (1^T A)(B 1)

@@ -1,11 +1,17 @@
 """MLP 784->256->128->10 forward + backward through the HAL (batch 128, fp32).
 
 The reference step (train_main.cpp / Linear, linear.ixx:50-58; MatMulBackward,
-autograd.ixx:226-290) is: y = x @ W + b, ReLU, ...; backward dA = G x B^T,
-dW = A^T x G, ReLU mask. On the GPU the transposes are folded into the
-MatmulTransB / MatmulTransA entries. Each GPU op is checked in situ against
-the oracle applied to the same (GPU-produced) inputs with the K-scaled bound,
-and the whole step against the oracle-only chain.
+autograd.ixx:226-290; tensorSoftmaxCrossEntropy tensor_ops.ixx:583-633 with
+SoftmaxCrossEntropyBackward autograd.ixx:440-488; AddBiasBackward
+autograd.ixx:399-433) is: y = x @ W + b, ReLU, ...; softmax, cross-entropy
+against one-hot labels, joint gradient (p - t) / batch; backward dA = G x B^T,
+dW = A^T x G, db = column sums of G, ReLU mask. On the GPU the transposes are
+folded into the MatmulTransB / MatmulTransA entries. Each GPU op is checked in
+situ against the oracle applied to the same (GPU-produced) inputs: GEMMs with
+the K-scaled bound, softmax per element within 2^-24 * (8 + 2(n - 1))
+relative plus 2^-126 absolute (one exp of identical arguments on both sides, two
+fixed-order sums of n positive terms), the loss within 1e-6 relative, the joint gradient, ReLU
+and the bias gradients (rows added in order) bit for bit.
 """
 import numpy as np
 import pytest
@@ -24,13 +30,9 @@ def _kaiming_uniform(fan_in, fan_out, seed):
     return O.uniform((fan_in, fan_out), seed, -b, b)
 
 
-def _ce_grad(logits, labels):
-    z = logits.astype(np.float64)
-    z = z - z.max(axis=1, keepdims=True)
-    p = np.exp(z)
-    p /= p.sum(axis=1, keepdims=True)
-    p[np.arange(len(labels)), labels] -= 1.0
-    return (p / len(labels)).astype(np.float32)
+def softmax_budget(x):
+    """Per-element relative bar of the device softmax against the oracle's on the same rows."""
+    return 2.0 ** -24 * (8.0 + 2.0 * (x.shape[-1] - 1))
 
 
 def test_mlp_step(hip):
@@ -65,9 +67,21 @@ def test_mlp_step(hip):
         else:
             logits = dz.numpy()
 
+    # ---------------- loss ----------------
+    T = np.eye(10, dtype=np.float32)[labels]
+    d_logits, d_T = dz, to_dev(hip, T)
+    d_p, d_loss, dG = empty_dev(hip, (BATCH, 10)), empty_dev(hip, (1,)), empty_dev(hip, (BATCH, 10))
+    H.softmax(d_logits, d_p, BATCH, 10)
+    H.crossEntropyForward(d_p, d_T, d_loss, BATCH, 10)
+    H.crossEntropySoftmaxBackward(d_p, d_T, dG, BATCH, 10)
+    p_gpu, p_ref = d_p.numpy(), O.softmax(logits)
+    assert np.all(np.abs(p_gpu - p_ref) <= softmax_budget(logits) * p_ref + 2.0 ** -126)
+    loss = float(d_loss.numpy()[0])
+    assert abs(loss - O.cross_entropy(p_gpu, T)) <= 1e-6 * abs(loss)
+    G = dG.numpy()
+    assert np.array_equal(G.view(np.uint32), O.cross_entropy_softmax_backward(p_gpu, T).view(np.uint32))
+
     # ---------------- backward ----------------
-    G = _ce_grad(logits, labels)
-    dG = to_dev(hip, G)
     for k in reversed(range(len(LAYERS))):
         i, o = LAYERS[k]
         A = acts[k]
@@ -76,6 +90,9 @@ def test_mlp_step(hip):
         dA_ref, dW_ref = O.matmul_backward(G, A, Ws[k])
         _, bW = O.gemm_f64(A, G, transA=True)
         assert O.normalized_error(dWg.numpy(), dW_ref, bW) <= TOL
+        dbg = empty_dev(hip, (o,))
+        H.addBiasBackward(dG, dbg, BATCH, o, 1)                  # db = column sums of G
+        assert np.array_equal(dbg.numpy().view(np.uint32), O.add_bias_backward(G, BATCH, o).view(np.uint32))
         if k == 0:
             break
         dAg = empty_dev(hip, (BATCH, i))

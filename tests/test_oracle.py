@@ -380,3 +380,109 @@ def test_tolerance_catches_planted_mistakes():
     y64, cb = O.conv_f64(x, w, None, 1, 1)
     wrong = np.roll(O.conv2d(x, w, None, 1, 1), 1, axis=3)
     assert O.normalized_error(wrong, y64, cb) > O.TOL_FP32
+
+
+# ------------------------------------- softmax, attention, loss, bias gradient
+def test_golden_softmax_attention_loss(gold):
+    """Bit-exact against vectors the compiled reference wrote: softmax rows with ties, large
+    magnitudes, -inf and NaN; the attention core composed from the reference's transpose2d,
+    batchedMatmul and softmax; crossEntropy (a clamped zero probability, a row with two
+    targets) and crossEntropySoftmaxBackward."""
+    k = "softmax_6x13"
+    assert np.array_equal(bits(O.softmax(gold[f"{k}.x"])), bits(gold[f"{k}.y"]))
+    k = "attention_2x7x3x4"
+    assert np.array_equal(bits(O.attention(gold[f"{k}.qkv"], 2, 7, 3, 4, 0.5)), bits(gold[f"{k}.out"]))
+    k = "cross_entropy_5x10"
+    loss = np.float32(O.cross_entropy(gold[f"{k}.p"], gold[f"{k}.t"]))
+    assert loss.view(np.uint32) == np.float32(gold[f"{k}.loss"]).view(np.uint32)
+    assert np.array_equal(bits(O.cross_entropy_softmax_backward(gold[f"{k}.p"], gold[f"{k}.t"])), bits(gold[f"{k}.grad"]))
+
+
+@ref_built
+def test_vs_reference_softmax_attention_loss():
+    """Fresh seeded inputs: softmax (ties, magnitudes up to 1e4), the ViT attention core at
+    197 tokens, crossEntropy and its gradient, all bit-exact against the compiled reference."""
+    x = O.randn((64, 197), 81, 30.0)
+    x[::3, 10:20] = 17.0
+    x[5] *= 300.0
+    assert np.array_equal(bits(O.softmax(x)), bits(O.softmax(x, backend="reference")))
+    qkv = O.randn((197, 3 * 2 * 64), 82)
+    assert np.array_equal(bits(O.attention(qkv, 1, 197, 2, 64, 0.125)),
+                          bits(O.attention(qkv, 1, 197, 2, 64, 0.125, backend="reference")))
+    p = O.softmax(O.randn((128, 10), 83, 2.0))
+    t = np.eye(10, dtype=np.float32)[O.rng(84).integers(0, 10, 128)]
+    assert np.float32(O.cross_entropy(p, t)) == np.float32(O.cross_entropy(p, t, backend="reference"))
+    assert np.array_equal(bits(O.cross_entropy_softmax_backward(p, t)),
+                          bits(O.cross_entropy_softmax_backward(p, t, backend="reference")))
+
+
+def _softmax64(x):
+    x = np.asarray(x, np.float64)
+    e = np.exp(x - x.max(axis=-1, keepdims=True))
+    return e / e.sum(axis=-1, keepdims=True)
+
+
+def test_softmax_attention_vs_float64():
+    """Softmax per element within 2^-24 * (2|x - max| + 4 + (n - 1)) relative of float64: the
+    rounding of x - max (amplified by |x - max| through exp), one exp, one division, and the
+    worst case of a sequential sum of n positive terms. The attention core within 1e-6 of the float64 result per context
+    element, relative to sum_j P_ij |V_jd|. A softmax over the wrong axis and attention with
+    unscaled Q must fail these bars."""
+    x = O.randn((32, 197), 91, 5.0)
+    p = O.softmax(x)
+    p64 = _softmax64(x)
+    budget = 2.0 ** -24 * (2.0 * np.abs(x - x.max(axis=1, keepdims=True)) + 4.0 + (x.shape[1] - 1))
+    assert np.all(np.abs(p - p64) / p64 <= budget)
+    assert np.allclose(p.astype(np.float64).sum(axis=1), 1.0, atol=1e-6)
+    wrong = O.softmax(np.ascontiguousarray(x.T)).T
+    assert not np.all(np.abs(wrong[:, :32] - p64[:, :32]) / p64[:, :32] <= budget[:, :32])
+    B_, S_, H_, D_ = 2, 50, 3, 64
+    qkv = O.randn((B_ * S_, 3 * H_ * D_), 92)
+    a = O.attention(qkv, B_, S_, H_, D_, 0.125)
+    a64, bound = O.attention_f64(qkv, B_, S_, H_, D_, 0.125)
+    assert O.normalized_error(a, a64, bound) <= 1e-6
+    unscaled = O.attention(qkv, B_, S_, H_, D_, 1.0)
+    assert O.normalized_error(unscaled, a64, bound) > 1e-2
+
+
+def test_cross_entropy_and_bias_gradient_closed_forms():
+    """crossEntropy equals -mean log(max(p, 1e-7)) over the one-hot entries (float64, 1e-6
+    relative); dropping the clamp turns a zero probability into inf. The joint gradient is
+    (p - t) / batch exactly as float32 arithmetic. The bias gradient equals numpy's sequential
+    float32 cumulative sum over the rows (bit for bit), and an all-ones gradient gives N*HW."""
+    p = O.softmax(O.randn((128, 10), 93, 2.0))
+    lab = O.rng(94).integers(0, 10, 128)
+    t = np.eye(10, dtype=np.float32)[lab]
+    ref = -np.mean(np.log(np.maximum(p[np.arange(128), lab].astype(np.float64), 1e-7)))
+    assert abs(O.cross_entropy(p, t) - ref) <= 1e-6 * abs(ref)
+    p0 = p.copy()
+    p0[0, lab[0]] = 0.0
+    assert np.isfinite(O.cross_entropy(p0, t))
+    with np.errstate(divide="ignore"):
+        assert not np.isfinite(-np.mean(np.log(p0[np.arange(128), lab])))
+    g = O.cross_entropy_softmax_backward(p, t)
+    assert np.array_equal(bits(g), bits((p - t) * np.float32(1.0 / 128)))
+    go = O.randn((300, 37), 95)
+    seq = np.cumsum(go, axis=0, dtype=np.float32)[-1]
+    assert np.array_equal(bits(O.add_bias_backward(go, 300, 37)), bits(seq))
+    go3 = O.randn((4, 6, 25), 96)
+    seq3 = np.cumsum(go3.transpose(1, 0, 2).reshape(6, -1), axis=1, dtype=np.float32)[:, -1]
+    assert np.array_equal(bits(O.add_bias_backward(go3, 4, 6, 25)), bits(seq3))
+    assert np.all(O.add_bias_backward(np.ones((4, 6, 25), np.float32), 4, 6, 25) == 100.0)
+    assert not np.array_equal(bits(O.add_bias_backward(go[:-1], 299, 37)), bits(seq))   # a dropped row shows
+
+
+@ref_built
+def test_resnet18_train_step_oracle_equals_reference():
+    """One image through the whole ResNet-18 training step (forward with batch statistics,
+    backward to every weight) composed from oracle functions equals the same composition of
+    the compiled reference's functions bit for bit."""
+    from resnet_net import cpu_train_step, make_params
+    P = make_params(seed=5, num_classes=10)
+    img = O.randn((1, 3, 224, 224), 97)
+    g = O.randn((1, 10), 98, 0.1)
+    a = cpu_train_step(P, img, g)
+    b = cpu_train_step(P, img, g, backend="reference")
+    assert a.keys() == b.keys()
+    for k in a:
+        assert np.array_equal(bits(a[k]), bits(b[k])), k
