@@ -192,6 +192,18 @@ int omHipGemmStridedBatched(int bTransA, int bTransB, int nBatch, int nM, int nN
                             const float* pA, long long nLda, long long nStrideA,
                             const float* pB, long long nLdb, long long nStrideB,
                             float* pC, long long nLdc, long long nStrideC);
+/* NEW, no counterpart in the reference: omHipGemmStridedBatched for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc). Same arguments and the same results, bit for bit; it calls no hipMalloc,
+ * hipFree or allocating library routine: its split-K partial sums go to a fixed 32 MiB device
+ * array that each GPU the library runs on holds until the process ends (every split plan of a
+ * 256-CU device fits; a plan that would need more fails with -1 and a message). All calls on
+ * one GPU share that array, so calls that overlap on one GPU (on different streams, or from
+ * several threads) race: order them. */
+int omHipGemmStridedBatchedNoAlloc(int bTransA, int bTransB, int nBatch, int nM, int nN, int nK,
+                                   const float* pA, long long nLda, long long nStrideA,
+                                   const float* pB, long long nLdb, long long nStrideB,
+                                   float* pC, long long nLdc, long long nStrideC);
 /* replaces omCudaTranspose (cuh:117): out[c,r] = in[r,c]; CPUBackend::transpose2d cpu_backend.ixx:1535-1539 */
 int omHipTranspose(const float* pIn, float* pOut, int nRows, int nCols);
 

@@ -96,6 +96,7 @@ _SIGS = {
     "omHipBatchedMatmul": [_vp, _vp, _vp, _i, _i, _i, _i],
     "omHipBatchedMatmulTransB": [_vp, _vp, _vp, _i, _i, _i, _i],
     "omHipGemmStridedBatched": [_i, _i, _i, _i, _i, _i, _vp, _ll, _ll, _vp, _ll, _ll, _vp, _ll, _ll],
+    "omHipGemmStridedBatchedNoAlloc": [_i, _i, _i, _i, _i, _i, _vp, _ll, _ll, _vp, _ll, _ll, _vp, _ll, _ll],
     "omHipTranspose": [_vp, _vp, _i, _i],
     "omHipConv2d": [_vp, _vp, _vp, _vp] + [_i] * 9,
     "omHipConv2dIm2col": [_vp, _vp, _vp, _vp] + [_i] * 9,

@@ -14,6 +14,7 @@
 #include "../../include/omhip.h"
 
 #include <algorithm>
+#include <mutex>
 #include <type_traits>
 
 namespace omhip {
@@ -356,7 +357,7 @@ static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 
 // finishing sum.
 static int gemmF32Run(bool ta, bool tb, int batch, int M, int N, int K, const float* A, long long lda, long long sA,
                       const float* B, long long ldb, long long sB, float* C, long long ldc, long long sC,
-                      GemmPlan plan, const float* bias, int act) {
+                      GemmPlan plan, const float* bias, int act, float* fixedWs = nullptr, size_t fixedBytes = 0) {
     GemmF32Params prm{};
     prm.A = A; prm.B = B; prm.C = C;
     prm.bias = bias; prm.act = act;
@@ -369,8 +370,16 @@ static int gemmF32Run(bool ta, bool tb, int batch, int M, int N, int K, const fl
     splits = (K + prm.kChunk - 1) / prm.kChunk;
     const bool partial = splits > 1;
     if (partial) {
-        prm.ws = static_cast<float*>(workspace((size_t)splits * batch * M * N * sizeof(float)));
-        if (!prm.ws) return -1;   // workspace() recorded the cause
+        const size_t need = (size_t)splits * batch * M * N * sizeof(float);
+        if (fixedWs) {
+            if (need > fixedBytes)
+                return fail("gemm: %d split-K partial products need %zu bytes of scratch; the fixed scratch holds %zu",
+                            splits, need, fixedBytes);
+            prm.ws = fixedWs;
+        } else {
+            prm.ws = static_cast<float*>(workspace(need));
+            if (!prm.ws) return -1;   // workspace() recorded the cause
+        }
     }
     // A is K-contiguous unless transposed; the vector axis is K (A) or M (A^T).
     const bool va = aligned16(A) && lda % 4 == 0 && sA % 4 == 0 && (ta ? M % 4 == 0 : K % 4 == 0);
@@ -437,6 +446,45 @@ int gemmF32Checked(const char* name, bool ta, bool tb, int batch, int M, int N, 
     return gemmF32(ta, tb, batch, M, N, K, A, lda, sA, B, ldb, sB, C, ldc, sC);
 }
 
+// ---- fixed scratch of the no-allocation entry ---------------------------------
+// Split-K partial sums of omHipGemmStridedBatchedNoAlloc live in this array,
+// so that entry never allocates. A plan splits K only while the grid holds
+// fewer workgroups than CUs, and stops doubling the split count once it has
+// reached them, so its partials cover fewer than 2 x CUs tiles of at most
+// 128 x 128 floats: 32 MiB on a 256-CU device. Each device the library runs
+// on holds its own copy until the process ends.
+constexpr size_t kNoAllocScratchBytes = (size_t)32 << 20;
+constexpr int kMaxDevices = 64;
+static __device__ __align__(256) float scratch[kNoAllocScratchBytes / sizeof(float)];
+
+static std::once_flag g_scratchOnce[kMaxDevices];
+static float* g_scratchPtr[kMaxDevices];
+static hipError_t g_scratchErr[kMaxDevices];
+
+// Device address of this device's `scratch` (the array's name is a host-side
+// stand-in), looked up once per device with that device current.
+static float* noAllocScratch() {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) {
+        (void)fail("no-allocation GEMM: hipGetDevice: %s", hipGetErrorString(hipGetLastError()));
+        return nullptr;
+    }
+    if (dev < 0 || dev >= kMaxDevices) {
+        (void)fail("no-allocation GEMM: device %d beyond the %d supported", dev, kMaxDevices);
+        return nullptr;
+    }
+    std::call_once(g_scratchOnce[dev], [dev] {
+        void* ptr = nullptr;
+        g_scratchErr[dev] = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        g_scratchPtr[dev] = g_scratchErr[dev] == hipSuccess ? static_cast<float*>(ptr) : nullptr;
+    });
+    if (!g_scratchPtr[dev]) {
+        (void)fail("no-allocation GEMM: hipGetSymbolAddress(scratch): %s", hipGetErrorString(g_scratchErr[dev]));
+        return nullptr;
+    }
+    return g_scratchPtr[dev];
+}
+
 }  // namespace omhip
 
 using namespace omhip;
@@ -499,6 +547,30 @@ int omHipGemmStridedBatched(int bTransA, int bTransB, int nBatch, int nM, int nN
     }
     return gemmF32Checked("omHipGemmStridedBatched", bTransA != 0, bTransB != 0, nBatch, nM, nN, nK,
                           pA, nLda, nStrideA, pB, nLdb, nStrideB, pC, nLdc, nStrideC);
+}
+
+int omHipGemmStridedBatchedNoAlloc(int bTransA, int bTransB, int nBatch, int nM, int nN, int nK,
+                                   const float* pA, long long nLda, long long nStrideA,
+                                   const float* pB, long long nLdb, long long nStrideB,
+                                   float* pC, long long nLdc, long long nStrideC) {
+    clearError();
+    const char* name = "omHipGemmStridedBatchedNoAlloc";
+    if (nBatch <= 0 || nM <= 0 || nN <= 0) return 0;
+    if (!pC) return fail("%s: null output", name);
+    if (nK > 0 && pA && pB) {
+        if (nLda < (bTransA ? nM : nK) || nLdb < (bTransB ? nK : nN) || nLdc < nN)
+            return fail("%s: leading dimension smaller than the row length", name);
+        if (nStrideA < 0 || nStrideB < 0 || nStrideC < 0) return fail("%s: negative batch stride", name);
+    }
+    if (!pA || !pB || nK <= 0) return zeroOutput(pC, nBatch, nM, nN, nLdc, nStrideC);
+    if (nBatch > 65535) return fail("%s: batch %d exceeds 65535", name, nBatch);
+    float* ws = noAllocScratch();
+    if (!ws) return -1;
+    // the same plan as omHipGemmStridedBatched, so the results are the same bits
+    const bool wsOk = (size_t)64 * nBatch * nM * nN * sizeof(float) <= kMaxSplitWorkspace;
+    const GemmPlan plan = planGemm(nM, nN, nK, nBatch, wsOk);
+    return gemmF32Run(bTransA != 0, bTransB != 0, nBatch, nM, nN, nK, pA, nLda, nStrideA, pB, nLdb, nStrideB, pC,
+                      nLdc, nStrideC, plan, nullptr, 0, ws, kNoAllocScratchBytes);
 }
 
 }  // extern "C"
