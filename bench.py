@@ -402,12 +402,17 @@ def bench_vit_half(om, steps: int, warmup: int, bf16: bool):
 
 
 def bench_mlp(om, steps: int, warmup: int, batch: int = 128):
-    """MLP 784-256-128-10 (ReLU) forward + backward, fp32, batch 128: each Linear (+ ReLU) is one
-    fused launch, the backward the reference's NT / TN products and ReLU gates."""
+    """MLP 784-256-128-10 (ReLU) training step, fp32, batch 128, labels uniform in 0..9:
+    each Linear (+ ReLU) is one fused launch; softmax, cross-entropy and its gradient one
+    launch (tensorSoftmaxCrossEntropy + SoftmaxCrossEntropyBackward); the backward the
+    reference's TN / NT products for dW and dA on every layer, the bias gradients
+    (AddBiasBackward) and the ReLU gates. No optimizer update."""
     from omnimatchdeeplearningtool_amd.hiptime import StreamTimer
     H = om.HIPBackend
     dims = [784, 256, 128, 10]
     x = om.DeviceBuffer.from_numpy(syn.uniform((batch, 784), 1))
+    labels = syn.rng(2).integers(0, 10, batch)
+    T = om.DeviceBuffer.from_numpy(np.eye(10, dtype=np.float32)[labels])
     Ws = [om.DeviceBuffer.from_numpy(syn.uniform((i, o), 10 + j, -np.sqrt(6 / i), np.sqrt(6 / i)))
           for j, (i, o) in enumerate(zip(dims[:-1], dims[1:]))]
     bs = [om.DeviceBuffer.from_numpy(np.zeros(o, np.float32)) for o in dims[1:]]
@@ -416,7 +421,8 @@ def bench_mlp(om, steps: int, warmup: int, batch: int = 128):
     g = [om.DeviceBuffer.empty((batch, o)) for o in dims[1:]]
     gA = [om.DeviceBuffer.empty((batch, i)) for i in dims[:-1]]
     gW = [om.DeviceBuffer.empty((i, o)) for i, o in zip(dims[:-1], dims[1:])]
-    H.fillValue(g[-1], batch * 10, 0.01)
+    gb = [om.DeviceBuffer.empty((o,)) for o in dims[1:]]
+    loss = om.DeviceBuffer.empty((1,))
 
     def step():
         # forward: one fused launch per layer, act(x W + b); the hidden layers
@@ -424,9 +430,12 @@ def bench_mlp(om, steps: int, warmup: int, batch: int = 128):
         for j in range(3):
             i, o = dims[j], dims[j + 1]
             H.linearBiasAct(a[j], Ws[j], bs[j], a[j + 1] if j < 2 else z[j], batch, i, o, 1 if j < 2 else 0)
+        # loss and its gradient (p - t) / batch, one launch
+        H.softmaxCrossEntropy(z[2], T, None, loss, g[2], batch, 10)
         for j in reversed(range(3)):
             i, o = dims[j], dims[j + 1]
             H.matmulTransA(a[j], g[j], gW[j], i, batch, o)        # dW = A^T G
+            H.addBiasBackward(g[j], gb[j], batch, o, 1)            # db = column sums of G
             H.matmulTransB(g[j], Ws[j], gA[j], batch, o, i)        # dA = G W^T (as the reference, every layer)
             if j > 0:
                 H.reluBackward(a[j], gA[j], g[j - 1], batch * i)   # a > 0 exactly where x W + b > 0
@@ -443,18 +452,19 @@ def bench_mlp(om, steps: int, warmup: int, batch: int = 128):
     # The same step replayed from a captured graph (its kernels unchanged; the
     # per-launch host cost is gone). Every output is overwritten per step, so
     # the replay's results must equal the eager step's bit for bit.
-    eager_out = [d.numpy().copy() for d in gW + gA]
+    outs = gW + gA + gb + [loss]
+    eager_out = [d.numpy().copy() for d in outs]
     graph = om.Graph(step)
     graph.launch()
     om.synchronize()
-    same = all(np.array_equal(d.numpy(), e) for d, e in zip(gW + gA, eager_out))
+    same = all(np.array_equal(d.numpy(), e) for d, e in zip(outs, eager_out))
     t.start()
     for _ in range(steps):
         graph.launch()
     t.stop()
     graph_ms = t.ms() / steps
     flops = sum(3 * 2.0 * batch * i * o for i, o in zip(dims[:-1], dims[1:]))
-    return ms, flops, graph_ms, same
+    return ms, flops, graph_ms, same, float(eager_out[-1][0])
 
 
 # ---- CPU checks of the GPU legs' results (run with the CPU baseline leg) ----
@@ -587,7 +597,7 @@ def cpu_baseline_mlp(reps: int = 20):
     dims = [784, 256, 128, 10]
     x = O.uniform((128, 784), 1)
     Ws = [O.uniform((i, o), 10 + j, -0.1, 0.1) for j, (i, o) in enumerate(zip(dims[:-1], dims[1:]))]
-    G = O.randn((128, 10), 3, 0.01)
+    T = np.eye(10, dtype=np.float32)[O.rng(2).integers(0, 10, 128)]
 
     def step():
         acts, pre = [x], []
@@ -596,9 +606,12 @@ def cpu_baseline_mlp(reps: int = 20):
             pre.append(z)
             if j < 2:
                 acts.append(O.relu(z, backend=backend))
-        g = G
+        p = O.softmax(pre[-1], backend=backend)
+        O.cross_entropy(p, T, backend=backend)
+        g = O.cross_entropy_softmax_backward(p, T, backend=backend)
         for j in reversed(range(3)):
             O.matmul(O.transpose2d(acts[j], backend=backend), g, backend=backend)
+            O.add_bias_backward(g, g.shape[0], g.shape[1])
             gA = O.matmul(g, O.transpose2d(Ws[j], backend=backend), backend=backend)
             if j > 0:
                 g = O.relu_backward(pre[j - 1], gA, backend=backend)
@@ -749,8 +762,9 @@ def main():
         log(f"vit {'bf16' if bf else 'fp16'} {v_ms:.3f} ms  {v_flops / v_ms / 1e9:.1f} TFLOP/s; fused attention "
             f"{v_fused['ms'] * 1e3:.1f} us ({v_fused['hbm_gb_s']:.0f} GB/s) replaces {v_fused['replaces_ms'] * 1e3:.1f} us "
             f"of Q.K^T + P.V")
-    mlp_ms, mlp_flops, mlp_graph_ms, mlp_graph_same = bench_mlp(om, max(20, args.steps), 5)
-    log(f"mlp step {mlp_ms * 1e3:.1f} us (graph replay {mlp_graph_ms * 1e3:.1f} us, bit-identical {mlp_graph_same})")
+    mlp_ms, mlp_flops, mlp_graph_ms, mlp_graph_same, mlp_loss = bench_mlp(om, max(20, args.steps), 5)
+    log(f"mlp step {mlp_ms * 1e3:.1f} us (graph replay {mlp_graph_ms * 1e3:.1f} us, bit-identical {mlp_graph_same}),"
+        f" loss {mlp_loss:.4f}")
 
     cpu = None
     cpu_r18 = None
@@ -843,6 +857,9 @@ def main():
                                "gflops": round(mlp_flops / mlp_ms / 1e6, 1),
                                "graph_replay": {"us_per_step": round(mlp_graph_ms * 1e3, 2),
                                                 "bit_identical_to_eager": bool(mlp_graph_same)},
+                               "loss": round(mlp_loss, 5),
+                               "scope": "forward, softmax + cross-entropy on labels uniform in 0..9, backward "
+                                        "(dW, db, dA every layer, ReLU gates); no optimizer update",
                                "cpu_baseline": cpu_extra.get("mlp")},
     }
     print(json.dumps(line), flush=True)

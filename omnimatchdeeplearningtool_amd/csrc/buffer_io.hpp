@@ -35,4 +35,16 @@ __device__ __forceinline__ void bufStore1(__amdgpu_buffer_rsrc_t r, uint32_t vof
     __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), r, voff, soff, 0);
 }
 
+// Cache policy sc1: an access coherent at agent scope (the monotonic
+// agent-scope atomic load / store of the gfx94x / gfx950 memory model), so
+// data exchanged between workgroups on different XCDs (each with its own L2)
+// needs no whole-cache writeback or invalidation.
+constexpr int kCpolAgent = 16;
+__device__ __forceinline__ void bufStore1Agent(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff, float v) {
+    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), r, voff, soff, kCpolAgent);
+}
+__device__ __forceinline__ float bufLoad1Agent(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, kCpolAgent));
+}
+
 }  // namespace omhip

@@ -23,8 +23,10 @@
 // with scalar loads.
 //
 // Split-K (for late layers whose Cout x pixels tile count cannot fill 256 CUs)
-// writes fp32 partial tiles to a workspace and a second kernel sums the splits
-// in a fixed order (deterministic) and applies the same epilogue.
+// and the K pieces of remainder tiles write fp32 partial tiles to a
+// workspace; the last block of a tile to finish (counted per tile) sums the
+// parts in a fixed order (deterministic) and applies the same epilogue, so no
+// second launch is needed.
 #include "omhip_internal.hpp"
 #include "mfma_f32_tile.hpp"
 #include "buffer_io.hpp"
@@ -70,6 +72,7 @@ struct ConvParams {
     // run as remPieces K pieces of remChunk, partials in rws [piece][tile - fullTiles][BM][BN].
     int fullTiles, remPieces, remChunk;
     float* rws;
+    unsigned* ctr;       // split-K / remainder tiles: per-tile arrival counters (zero at rest)
     int padOff;          // max(padH,0)*W + max(padW,0): the x buffer view starts this many floats before x
     uint32_t xBytes;     // range of the x buffer view
     FastDiv dHoWo, dWo;  // division by Ho*Wo and by Wo (grid pixel indices are below 2^30)
@@ -315,6 +318,142 @@ __device__ __forceinline__ void storeTile(const ConvParams& p, const f32x16 (&ac
     }
 }
 
+// Output epilogue by variant (BN, residual, ReLU chosen per launch).
+template <class Cfg>
+__device__ __forceinline__ void storeEpilogue(const ConvParams& p, const f32x16 (&acc)[Cfg::FM][Cfg::FN],
+                                              const float* sEpi, int m0, int n0, int wm, int wn, int lane) {
+    switch ((p.gamma ? 1 : 0) | (p.res ? 2 : 0) | (p.act == 1 ? 4 : 0)) {
+        case 0: storeTile<Cfg, false, false, false>(p, acc, sEpi, m0, n0, wm, wn, lane); break;
+        case 1: storeTile<Cfg, true, false, false>(p, acc, sEpi, m0, n0, wm, wn, lane); break;
+        case 2: storeTile<Cfg, false, true, false>(p, acc, sEpi, m0, n0, wm, wn, lane); break;
+        case 3: storeTile<Cfg, true, true, false>(p, acc, sEpi, m0, n0, wm, wn, lane); break;
+        case 4: storeTile<Cfg, false, false, true>(p, acc, sEpi, m0, n0, wm, wn, lane); break;
+        case 5: storeTile<Cfg, true, false, true>(p, acc, sEpi, m0, n0, wm, wn, lane); break;
+        case 6: storeTile<Cfg, false, true, true>(p, acc, sEpi, m0, n0, wm, wn, lane); break;
+        default: storeTile<Cfg, true, true, true>(p, acc, sEpi, m0, n0, wm, wn, lane); break;
+    }
+}
+
+// Writes one block's finished accumulators. A direct block applies the
+// epilogue and writes the output. A K piece (remainder tiles) writes a compact
+// partial tile, a split (split-K) its [Cout][Nq] partials (same row / column
+// ownership and out-of-range handling as storeTile); then the block counts
+// itself in at the tile's counter, and the block that arrives last adds every
+// part's partials in part order (0 + part 0 + part 1 + ...), applies the
+// epilogue, writes the output and returns the counter to zero. The order of
+// the sum does not depend on which block arrives last, so the result is
+// deterministic and equal to a separate finishing pass's. Partials are
+// written and read with agent-coherent accesses (they cross XCDs); a block's
+// stores have completed (s_waitcnt) before its thread 0 increments the
+// counter, and the last block reads the partials only after seeing the
+// final count.
+template <class Cfg>
+__device__ __forceinline__ void finishBlock(const ConvParams& p, f32x16 (&acc)[Cfg::FM][Cfg::FN], const float* sEpi,
+                                            int* sFlag, int m0, int n0, int wm, int wn, int lane, int piece,
+                                            int rtile, int split, bool direct, int ctrIdx) {
+    const int li = lane & 31, h = lane >> 5;
+    if (!direct) {
+        const int tiles = p.tilesM * p.tilesN;
+        const uint32_t nq = (uint32_t)p.Nq;
+        const int nParts = piece >= 0 ? p.remPieces : p.splits;
+        const long long pieceElems = (long long)(tiles - p.fullTiles) * (Cfg::BM * Cfg::BN);
+        float* const rbase = p.rws + (long long)rtile * (Cfg::BM * Cfg::BN);
+        // element (fm, fn, r) of part `part`: compact tile row / column, or [Cout][Nq] position
+        auto rowOf = [&](int fm, int r) { return wm * Cfg::WM + fm * 32 + 8 * (r >> 2) + 4 * h + (r & 3); };
+        if (piece >= 0) {
+            const auto rp = bufferRsrc(rbase + piece * pieceElems, Cfg::BM * Cfg::BN * 4u);
+#pragma unroll
+            for (int fn = 0; fn < Cfg::FN; ++fn)
+#pragma unroll
+                for (int fm = 0; fm < Cfg::FM; ++fm)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r)
+                        bufStore1Agent(rp, (uint32_t)(rowOf(fm, r) * Cfg::BN + wn * Cfg::WN + fn * 32 + li) * 4u, 0u,
+                                       acc[fm][fn][r]);
+        } else {
+            const auto rw = bufferRsrc(p.ws + (long long)split * p.Cout * p.Nq, (uint32_t)p.Cout * nq * 4u);
+#pragma unroll
+            for (int fn = 0; fn < Cfg::FN; ++fn) {
+                const int q = n0 + wn * Cfg::WN + fn * 32 + li;
+#pragma unroll
+                for (int fm = 0; fm < Cfg::FM; ++fm) {
+                    const int rl0 = wm * Cfg::WM + fm * 32 + 4 * h;
+                    const uint32_t vbase = q < p.Nq ? ((uint32_t)(m0 + rl0) * nq + (uint32_t)q) * 4u : kOOB;
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) {
+                        const int rowOff = 8 * (r >> 2) + (r & 3);
+                        const uint32_t vo = m0 + rl0 + rowOff < p.Cout ? vbase : kOOB;
+                        bufStore1Agent(rw, vo, (uint32_t)rowOff * nq * 4u, acc[fm][fn][r]);
+                    }
+                }
+            }
+        }
+        __builtin_amdgcn_s_waitcnt(0);   // this thread's partial stores have completed
+        __syncthreads();
+        if (threadIdx.x == 0)
+            *sFlag = __hip_atomic_fetch_add(p.ctr + ctrIdx, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                     (unsigned)(nParts - 1);
+        __syncthreads();
+        if (!*sFlag) return;
+        // last arrival: acc = 0 + part 0 + part 1 + ...
+#pragma unroll
+        for (int fm = 0; fm < Cfg::FM; ++fm)
+#pragma unroll
+            for (int fn = 0; fn < Cfg::FN; ++fn)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) acc[fm][fn][r] = 0.f;
+        for (int part = 0; part < nParts; ++part) {
+            if (piece >= 0) {
+                const auto rp = bufferRsrc(rbase + part * pieceElems, Cfg::BM * Cfg::BN * 4u);
+#pragma unroll
+                for (int fn = 0; fn < Cfg::FN; ++fn)
+#pragma unroll
+                    for (int fm = 0; fm < Cfg::FM; ++fm)
+#pragma unroll
+                        for (int r = 0; r < 16; ++r)
+                            acc[fm][fn][r] += bufLoad1Agent(
+                                rp, (uint32_t)(rowOf(fm, r) * Cfg::BN + wn * Cfg::WN + fn * 32 + li) * 4u, 0u);
+            } else {
+                const auto rw = bufferRsrc(p.ws + (long long)part * p.Cout * p.Nq, (uint32_t)p.Cout * nq * 4u);
+#pragma unroll
+                for (int fn = 0; fn < Cfg::FN; ++fn) {
+                    const int q = n0 + wn * Cfg::WN + fn * 32 + li;
+#pragma unroll
+                    for (int fm = 0; fm < Cfg::FM; ++fm) {
+                        const int rl0 = wm * Cfg::WM + fm * 32 + 4 * h;
+                        const uint32_t vbase = q < p.Nq ? ((uint32_t)(m0 + rl0) * nq + (uint32_t)q) * 4u : kOOB;
+#pragma unroll
+                        for (int r = 0; r < 16; ++r) {
+                            const int rowOff = 8 * (r >> 2) + (r & 3);
+                            const uint32_t vo = m0 + rl0 + rowOff < p.Cout ? vbase : kOOB;
+                            acc[fm][fn][r] += bufLoad1Agent(rw, vo, (uint32_t)rowOff * nq * 4u);
+                        }
+                    }
+                }
+            }
+        }
+        if (threadIdx.x == 0)   // ready for the next launch
+            __hip_atomic_store(p.ctr + ctrIdx, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    storeEpilogue<Cfg>(p, acc, sEpi, m0, n0, wm, wn, lane);
+}
+
+// Stages the epilogue vectors of output channels m0 .. m0+BM-1 in LDS (bias,
+// mean, invStd, gamma, beta); threads tid < BM each take one channel.
+template <int BM>
+__device__ __forceinline__ void stageEpilogue(const ConvParams& p, float* sEpi, int m0, int tid) {
+    if (tid < BM) {
+        const int co = min(m0 + tid, p.Cout - 1);
+        sEpi[tid] = p.bias ? p.bias[co] : 0.f;
+        if (p.gamma) {
+            sEpi[BM + tid] = p.mean[co];
+            sEpi[2 * BM + tid] = 1.0f / sqrtf(p.var[co] + p.eps);
+            sEpi[3 * BM + tid] = p.gamma[co];
+            sEpi[4 * BM + tid] = p.beta[co];
+        }
+    }
+}
+
 template <class Cfg, bool VA, int MODE>
 __global__ __launch_bounds__(Cfg::NT) void conv_igemm_kernel(ConvParams p) {
     extern __shared__ float smem[];
@@ -322,6 +461,7 @@ __global__ __launch_bounds__(Cfg::NT) void conv_igemm_kernel(ConvParams p) {
     using SB = LdsShape<true, Cfg::BN, Cfg::BK>;
     constexpr int STAGE = SA::SIZE + SB::SIZE;
     float* sEpi = smem + 2 * STAGE;   // [5][BM]: bias, mean, invStd, gamma, beta
+    int* sFlag = reinterpret_cast<int*>(sEpi + 5 * Cfg::BM);   // last-arrival flag of a split tile
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -362,16 +502,7 @@ __global__ __launch_bounds__(Cfg::NT) void conv_igemm_kernel(ConvParams p) {
     lb.init(p, n0 + tid % Cfg::BN, tid);
 
     const bool direct = p.splits == 1 && piece < 0;
-    if (direct && tid < Cfg::BM) {
-        const int co = min(m0 + tid, p.Cout - 1);
-        sEpi[tid] = p.bias ? p.bias[co] : 0.f;
-        if (p.gamma) {
-            sEpi[Cfg::BM + tid] = p.mean[co];
-            sEpi[2 * Cfg::BM + tid] = 1.0f / sqrtf(p.var[co] + p.eps);
-            sEpi[3 * Cfg::BM + tid] = p.gamma[co];
-            sEpi[4 * Cfg::BM + tid] = p.beta[co];
-        }
-    }
+    stageEpilogue<Cfg::BM>(p, sEpi, m0, tid);   // the last part of a split tile applies the epilogue too
 
     f32x16 acc[Cfg::FM][Cfg::FN];
 #pragma unroll
@@ -443,141 +574,8 @@ __global__ __launch_bounds__(Cfg::NT) void conv_igemm_kernel(ConvParams p) {
         }
     }
 
-    const int li = lane & 31, h = lane >> 5;
-    if (piece >= 0) {
-        // compact partial tile; the finishing kernel checks the tile edges
-        float* rp = p.rws + ((long long)piece * (tiles - p.fullTiles) + rtile) * (Cfg::BM * Cfg::BN);
-#pragma unroll
-        for (int fn = 0; fn < Cfg::FN; ++fn)
-#pragma unroll
-            for (int fm = 0; fm < Cfg::FM; ++fm)
-#pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    const int row = wm * Cfg::WM + fm * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
-                    rp[row * Cfg::BN + wn * Cfg::WN + fn * 32 + li] = acc[fm][fn][r];
-                }
-        return;
-    }
-    if (!direct) {
-        // this split's [Cout][Nq] partials (at most 64 MiB); same row / column
-        // ownership and out-of-range handling as storeTile
-        const uint32_t nq = (uint32_t)p.Nq;
-        const auto rw = bufferRsrc(p.ws + (long long)split * p.Cout * p.Nq, (uint32_t)p.Cout * nq * 4u);
-#pragma unroll
-        for (int fn = 0; fn < Cfg::FN; ++fn) {
-            const int q = n0 + wn * Cfg::WN + fn * 32 + li;
-#pragma unroll
-            for (int fm = 0; fm < Cfg::FM; ++fm) {
-                const int rl0 = wm * Cfg::WM + fm * 32 + 4 * h;
-                const uint32_t vbase = q < p.Nq ? ((uint32_t)(m0 + rl0) * nq + (uint32_t)q) * 4u : kOOB;
-#pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    const int rowOff = 8 * (r >> 2) + (r & 3);
-                    const uint32_t vo = m0 + rl0 + rowOff < p.Cout ? vbase : kOOB;
-                    bufStore1(rw, vo, (uint32_t)rowOff * nq * 4u, acc[fm][fn][r]);
-                }
-            }
-        }
-        return;
-    }
-    switch ((p.gamma ? 1 : 0) | (p.res ? 2 : 0) | (p.act == 1 ? 4 : 0)) {
-        case 0: storeTile<Cfg, false, false, false>(p, acc, sEpi, m0, n0, wm, wn, lane); break;
-        case 1: storeTile<Cfg, true, false, false>(p, acc, sEpi, m0, n0, wm, wn, lane); break;
-        case 2: storeTile<Cfg, false, true, false>(p, acc, sEpi, m0, n0, wm, wn, lane); break;
-        case 3: storeTile<Cfg, true, true, false>(p, acc, sEpi, m0, n0, wm, wn, lane); break;
-        case 4: storeTile<Cfg, false, false, true>(p, acc, sEpi, m0, n0, wm, wn, lane); break;
-        case 5: storeTile<Cfg, true, false, true>(p, acc, sEpi, m0, n0, wm, wn, lane); break;
-        case 6: storeTile<Cfg, false, true, true>(p, acc, sEpi, m0, n0, wm, wn, lane); break;
-        default: storeTile<Cfg, true, true, true>(p, acc, sEpi, m0, n0, wm, wn, lane); break;
-    }
-}
-
-// Epilogue constants of output channel co (the BN scale is computed as in the
-// conv kernel's staging, so both paths round identically).
-struct ChanEpi {
-    float bias, mean, inv, gamma, beta;
-};
-
-__device__ __forceinline__ ChanEpi chanEpi(const ConvParams& p, int co) {
-    ChanEpi c{0.f, 0.f, 0.f, 0.f, 0.f};
-    if (p.bias) c.bias = p.bias[co];
-    if (p.gamma) {
-        c.inv = 1.0f / sqrtf(p.var[co] + p.eps);
-        c.mean = p.mean[co];
-        c.gamma = p.gamma[co];
-        c.beta = p.beta[co];
-    }
-    return c;
-}
-
-// Epilogue of one output element (co, grid pixel q) from its finished sum.
-__device__ __forceinline__ void finishOne(const ConvParams& p, const ChanEpi& c, int co, int q, float v) {
-    const int HoWo = p.Ho * p.Wo;
-    if (p.bias) v += c.bias;
-    if (p.gamma) v = __builtin_fmaf(c.gamma, (v - c.mean) * c.inv, c.beta);
-    const int n = (int)p.dHoWo.div((uint32_t)q);
-    const int pix = q - n * HoWo;
-    const long long o = ((long long)n * p.Cout + co) * (p.oH * p.oW) + outPixel(p, pix);
-    if (p.res) v += p.res[o];
-    if (p.act == 1) v = v > 0.f ? v : 0.f;
-    p.out[o] = v;
-}
-
-// Sums split-K partials in split order and applies the epilogue. Block
-// (x, y): channels y, y + gridDim.y, ...; four consecutive grid pixels per
-// thread. VEC (Nq % 4 == 0): the four partials of each split are one aligned
-// 16-byte load. The partial buffer holds splits x Cout x Nq < 2^31 floats.
-template <bool VEC>
-__global__ __launch_bounds__(256) void conv_splitk_finish(ConvParams p) {
-    const int q0 = (blockIdx.x * 256 + threadIdx.x) * 4;
-    if (q0 >= p.Nq) return;
-    const int total = p.Cout * p.Nq;
-    for (int co = blockIdx.y; co < p.Cout; co += gridDim.y) {
-        const float* src = p.ws + co * p.Nq + q0;
-        float v[4] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll 4
-        for (int s = 0; s < p.splits; ++s) {
-            if constexpr (VEC) {
-                const f32x4 t = *reinterpret_cast<const f32x4*>(src + s * total);
-#pragma unroll
-                for (int i = 0; i < 4; ++i) v[i] += t[i];
-            } else {
-#pragma unroll
-                for (int i = 0; i < 4; ++i)
-                    if (q0 + i < p.Nq) v[i] += src[s * total + i];
-            }
-        }
-        const ChanEpi c = chanEpi(p, co);
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-            if (q0 + i < p.Nq) finishOne(p, c, co, q0 + i, v[i]);
-    }
-}
-
-// Sums the K pieces of the remainder tiles in piece order and applies the
-// epilogue. Block (x, y) of one wave: remainder tile x, column quads
-// [64y, 64y + 64) of it; a thread takes four consecutive columns of one tile
-// row (one aligned 16-byte load per piece).
-template <int BM, int BN>
-__global__ __launch_bounds__(64) void conv_rem_finish(ConvParams p) {
-    static_assert(BN % 4 == 0 && (BM * BN / 4) % 64 == 0, "column quads");
-    const int remTiles = p.tilesM * p.tilesN - p.fullTiles;
-    const int rt = blockIdx.x;
-    int tm, tn;
-    grouped_tile(p.fullTiles + rt, p.tilesM, p.tilesN, 4, tm, tn);
-    const int e4 = blockIdx.y * 64 + threadIdx.x;
-    const int row = e4 / (BN / 4), q0 = tn * BN + (e4 % (BN / 4)) * 4;
-    const int co = tm * BM + row;
-    if (co >= p.Cout || q0 >= p.Nq) return;
-    const float* src = p.rws + (size_t)rt * (BM * BN) + e4 * 4;
-    const size_t pieceStride = (size_t)remTiles * (BM * BN);
-    f32x4 v = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll 4
-    for (int k = 0; k < p.remPieces; ++k) v += *reinterpret_cast<const f32x4*>(src + k * pieceStride);
-    const ChanEpi c = chanEpi(p, co);
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-        if (q0 + i < p.Nq) finishOne(p, c, co, q0 + i, v[i]);
+    finishBlock<Cfg>(p, acc, sEpi, sFlag, m0, n0, wm, wn, lane, piece, rtile, split, direct,
+                     piece >= 0 ? rtile : tm * p.tilesN + tn);
 }
 
 // ---- tile configuration -------------------------------------------------------
@@ -599,7 +597,7 @@ using ConvCfg = ConvCfgT<OMHIP_CONV_TILE>;
 template <class Cfg>
 static size_t convLds() {
     // two A+B stages and the epilogue vectors
-    return (2 * (LdsShape<true, Cfg::BM, Cfg::BK>::SIZE + LdsShape<true, Cfg::BN, Cfg::BK>::SIZE) + 5 * Cfg::BM) *
+    return (2 * (LdsShape<true, Cfg::BM, Cfg::BK>::SIZE + LdsShape<true, Cfg::BN, Cfg::BK>::SIZE) + 5 * Cfg::BM + 4) *
            sizeof(float);
 }
 
@@ -627,10 +625,10 @@ struct ConvPlan {
 //    writes and reads of the output (e.g. 512x1568x4608: 5 splits).
 //  * Otherwise, when the tile count is not a multiple of the CU count and the
 //    CUs hold few tiles each: the tiles beyond the last whole round run as K
-//    pieces (one per idle CU, at most 16 per tile) summed by a small second
-//    kernel, e.g. 1568 tiles on 256 CUs: 1536 whole + 32 x 8 pieces, 6.125
-//    tile-times per CU instead of 7 (K >= 256 only: shorter tiles do not pay
-//    for the second launch).
+//    pieces (one per idle CU, at most 16 per tile), summed by each tile's last
+//    piece to finish, e.g. 1568 tiles on 256 CUs: 1536 whole + 32 x 8 pieces,
+//    6.125 tile-times per CU instead of 7 (K >= 256 only: shorter tiles do not
+//    pay for the partial traffic).
 static ConvPlan planConv(const ConvParams& p, bool haveSplitWs) {
     using Cfg = ConvCfg;
     ConvPlan pl{1, p.tilesM * p.tilesN, 1};
@@ -693,19 +691,32 @@ static int launchConv(ConvParams& p, const ConvPlan& pl, float* wsBuf) {
     else
         rc = mode == 0 ? launchConvT<Cfg, false, 0>(p, gridX)
                        : (mode == 1 ? launchConvT<Cfg, false, 1>(p, gridX) : launchConvT<Cfg, false, 2>(p, gridX));
-    if (rc) return rc;
-    if (p.splits > 1) {
-        const dim3 grid((p.Nq + 1023) / 1024, std::min(p.Cout, 65535));
-        if (p.Nq % 4 == 0)
-            hipLaunchKernelGGL(conv_splitk_finish<true>, grid, dim3(256), 0, stream(), p);
-        else
-            hipLaunchKernelGGL(conv_splitk_finish<false>, grid, dim3(256), 0, stream(), p);
-        OMHIP_CHECK_LAUNCH();
-    } else if (p.fullTiles < tiles) {
-        hipLaunchKernelGGL((conv_rem_finish<Cfg::BM, Cfg::BN>), dim3(tiles - p.fullTiles, Cfg::BM * Cfg::BN / 256),
-                           dim3(64), 0, stream(), p);
-        OMHIP_CHECK_LAUNCH();
+    return rc;
+}
+
+// Workspace of a plan's partial sums and the tiles' arrival counters. A plan
+// whose buffers cannot be had runs whole tiles (out of memory), or fails while
+// the stream records a graph (workspace() recorded why).
+static int planBuffers(ConvParams& p, ConvPlan& pl, int tiles, int bm, int bn, float*& ws) {
+    ws = nullptr;
+    p.ctr = nullptr;
+    size_t bytes = 0;
+    if (pl.splits > 1)
+        bytes = (size_t)pl.splits * p.Cout * p.Nq * sizeof(float);
+    else if (pl.fullTiles < tiles)
+        bytes = (size_t)(tiles - pl.fullTiles) * pl.remPieces * bm * bn * sizeof(float);
+    else
+        return 0;
+    ws = static_cast<float*>(workspace(bytes));
+    unsigned* ctr = ws ? static_cast<unsigned*>(workspace((size_t)tiles * sizeof(unsigned), kWsCounters)) : nullptr;
+    if (!ws || !ctr) {
+        if (capturing(stream())) return -1;
+        pl.splits = 1;
+        pl.fullTiles = tiles;
+        ws = nullptr;
+        return 0;
     }
+    p.ctr = ctr;
     return 0;
 }
 
@@ -791,16 +802,7 @@ static int convChunk(ConvParams p, int n0, int nb) {
     const bool wsOk = (size_t)p.Cout * p.Nq * sizeof(float) <= ((size_t)64 << 20);
     ConvPlan pl = planConv(p, wsOk);
     float* ws = nullptr;
-    if (pl.splits > 1) {
-        ws = static_cast<float*>(workspace((size_t)pl.splits * p.Cout * p.Nq * sizeof(float)));
-        if (!ws && capturing(stream())) return -1;
-        if (!ws) pl.splits = 1;   // out of memory: one pass without partials
-    } else if (pl.fullTiles < p.tilesM * p.tilesN) {
-        const size_t remTiles = (size_t)(p.tilesM * p.tilesN - pl.fullTiles);
-        ws = static_cast<float*>(workspace(remTiles * pl.remPieces * ConvCfg::BM * ConvCfg::BN * sizeof(float)));
-        if (!ws && capturing(stream())) return -1;
-        if (!ws) pl.fullTiles = p.tilesM * p.tilesN;
-    }
+    if (planBuffers(p, pl, p.tilesM * p.tilesN, ConvCfg::BM, ConvCfg::BN, ws)) return -1;
     return launchConv(p, pl, ws);
 }
 

@@ -151,13 +151,12 @@ __global__ void bias_grad_cols_kernel(const float* g, float* gb, int rows, int c
     const float* p = g + c;
     float acc = 0.f;
     int r = 0;
-    for (; r + 4 <= rows; r += 4) {   // four loads in flight, adds in row order
-        const float a0 = p[(long long)r * cols], a1 = p[(long long)(r + 1) * cols];
-        const float a2 = p[(long long)(r + 2) * cols], a3 = p[(long long)(r + 3) * cols];
-        acc += a0;
-        acc += a1;
-        acc += a2;
-        acc += a3;
+    for (; r + 32 <= rows; r += 32) {   // 32 loads in flight, then the adds in row order
+        float a[32];
+#pragma unroll
+        for (int i = 0; i < 32; ++i) a[i] = p[(long long)(r + i) * cols];
+#pragma unroll
+        for (int i = 0; i < 32; ++i) acc += a[i];
     }
     for (; r < rows; ++r) acc += p[(long long)r * cols];
     gb[c] = acc;

@@ -35,10 +35,11 @@ void clearError();
 // stream and slot, grown on demand; an outgrown block stays allocated until its
 // last use has finished and no executable graph exists). Reuse is ordered by
 // the stream. Slot 0 holds split-K partial sums, slot 1 a call's temporary
-// operand (flipped weights, an im2col buffer) that slot-0 users read. nullptr
-// with the error recorded on OOM, or when the block must grow while the stream
-// records a graph.
-enum WsSlot { kWsPartials = 0, kWsOperand = 1 };
+// operand (flipped weights, an im2col buffer) that slot-0 users read, slot 2
+// per-tile arrival counters: zero-filled when (re)allocated, and every kernel
+// that counts on them returns them to zero. nullptr with the error recorded on
+// OOM, or when the block must grow while the stream records a graph.
+enum WsSlot { kWsPartials = 0, kWsOperand = 1, kWsCounters = 2 };
 void* workspace(size_t bytes, int slot = kWsPartials);
 
 // Whether stream s is recording a graph.

@@ -208,6 +208,10 @@ void* workspace(size_t bytes, int slot) {
         (void)fail("workspace: out of device memory (%zu bytes)", want);
         return nullptr;
     }
+    if (slot == kWsCounters && byteFill(p, 0, want)) {   // counters start at zero, kernels leave them so
+        g_pool->release(p);
+        return nullptr;
+    }
     w.p = p;
     w.bytes = want;
     return p;
