@@ -8,7 +8,8 @@ Headline (the `value`): fp32 GEMM 4096x4096x4096, row-major A[M,K] x B[K,N]
 value = TFLOP/s over the timed steps (HIP events on the library stream).
 Second metric in the same line (`resnet18_conv`): the ResNet-18 conv stack
 forward at batch 32, 224x224 (20 convs, each conv + BN-inference + ReLU fused),
-as images/s.
+as images/s over eager launches (the same 20 launches replayed from a
+captured HIP graph are timed beside it).
 
 Also reported:
   roofline      — fp32 MFMA roof for the GEMM kernel (achieved = 2MNK / average
@@ -165,6 +166,25 @@ def bench_resnet18(om, steps: int, warmup: int, batch: int = 32):
         forward()
     timer.stop()
     ms = timer.ms() / steps
+    # The same 20 launches replayed from a captured HIP graph (the kernels and
+    # their work are unchanged; the host launch cost and the gaps between
+    # launches go). Every output is overwritten per pass, so a replay must
+    # reproduce the eager outputs bit for bit.
+    eager_out = [d["y"].numpy() for _, d, _ in layers]
+    graph = om.Graph(forward)
+    graph.launch()
+    om.synchronize()
+    same = all(np.array_equal(d["y"].numpy().view(np.uint32), e.view(np.uint32))
+               for (_, d, _), e in zip(layers, eager_out))
+    for _ in range(warmup):
+        graph.launch()
+    om.synchronize()
+    timer.start()
+    for _ in range(steps):
+        graph.launch()
+    timer.stop()
+    graph_ms = timer.ms() / steps
+    graph.destroy()
     # per-layer times (for the roofline table)
     per = []
     for (shape, d, _) in layers:
@@ -185,7 +205,7 @@ def bench_resnet18(om, steps: int, warmup: int, batch: int = 32):
     roof_ms = sum(max(conv_flops(sh, batch) / PEAK_FP32, conv_bytes(sh, batch) / PEAK_HBM) for sh, _, _ in layers) * 1e3
     # outputs of two images of three layers, checked on the CPU
     samples = [(idx, layers[idx][1]["y"].numpy()[[0, batch - 1]]) for idx in RESNET18_CHECKED]
-    return ms, flops, roof_ms, per, samples
+    return ms, flops, roof_ms, per, samples, graph_ms, same
 
 
 def bench_resnet18_net(om, steps: int, warmup: int, batch: int = 32):
@@ -734,9 +754,11 @@ def main():
 
     log("resnet18 conv stack b32")
     r_steps = max(5, args.steps // 2)
-    r_ms, r_flops, r_roof_ms, per, conv_samples = bench_resnet18(om, r_steps, max(2, args.warmup))
+    r_ms, r_flops, r_roof_ms, per, conv_samples, r_graph_ms, r_graph_same = bench_resnet18(
+        om, r_steps, max(2, args.warmup))
     img_s = 32.0 / (r_ms / 1e3)
-    log(f"resnet18 {r_ms:.3f} ms/batch  {img_s:.0f} img/s  roof frac {r_roof_ms / r_ms:.3f}")
+    log(f"resnet18 {r_ms:.3f} ms/batch  {img_s:.0f} img/s  roof frac {r_roof_ms / r_ms:.3f}; graph replay "
+        f"{r_graph_ms:.3f} ms, roof frac {r_roof_ms / r_graph_ms:.3f} (bit-identical {r_graph_same})")
 
     log("resnet18 network b32 (inference forward, training step)")
     n_fwd_ms, n_fl, n_logits2, n_train_ms, n_train_fl = bench_resnet18_net(om, max(5, args.steps // 5), 2)
@@ -831,9 +853,14 @@ def main():
         "gemm_sweep": sweep,
         "parity": {"gemm_sampled_rows_max_err": gemm_err, "conv_sampled_max_err": conv_err, "tol": 1e-4},
         "resnet18_conv": {"value": round(img_s, 1), "unit": "img/s", "batch": 32, "ms_per_batch": round(r_ms, 4),
+                          "launch": "eager: 20 conv launches on the library stream",
                           "tflops": round(r_flops / r_ms / 1e9, 2),
                           "roofline": {"bound": "mfma (per-layer max(flops/157.3T, bytes/8TB/s))",
                                        "roof_ms": round(r_roof_ms, 4), "frac": round(r_roof_ms / r_ms, 4)},
+                          "graph_replay": {"ms_per_batch": round(r_graph_ms, 4),
+                                           "img_s": round(32.0 / r_graph_ms * 1e3, 1),
+                                           "roof_frac": round(r_roof_ms / r_graph_ms, 4),
+                                           "bit_identical_to_eager": bool(r_graph_same)},
                           "layers": per, "cpu_baseline": cpu_r18},
         "resnet18_network": {"batch": 32, "data": "synthetic images N(0,1), Kaiming-uniform weights, seeded BN",
                              "forward": {"ms": round(n_fwd_ms, 4), "img_s": round(32 / n_fwd_ms * 1e3, 1),
