@@ -346,24 +346,28 @@ def bench_resnet50(om, steps: int, warmup: int, batch: int = 64):
     return ms, flops, roof_ms
 
 
-def vit_gemm_shapes(batch: int = 64, tokens: int = 197, d: int = 768, heads: int = 12):
-    """(name, batch, M, N, K, transB) of the ViT-B/16 GEMMs: projections in the
-    Linear-weight layout (x[T,in] x W[out,in]^T), attention Q.K^T (transB) and P.V."""
+def vit_gemm_shapes(batch: int = 64, tokens: int = 197, d: int = 768, heads: int = 12, proj_nt: bool = False):
+    """(name, batch, M, N, K, transB) of the ViT-B/16 GEMMs: the projections x[T,in] x W
+    with W stored [in, out] as the reference's Linear keeps it (linear.ixx:31, :52; NN), or
+    with proj_nt W stored [out, in] (NT); attention Q.K^T (transB) and P.V."""
     T = batch * tokens
     dh = d // heads
-    return [("qkv", 1, T, 3 * d, d, True), ("out_proj", 1, T, d, d, True), ("fc1", 1, T, 4 * d, d, True),
-            ("fc2", 1, T, d, 4 * d, True), ("qk_t", batch * heads, tokens, tokens, dh, True),
+    return [("qkv", 1, T, 3 * d, d, proj_nt), ("out_proj", 1, T, d, d, proj_nt), ("fc1", 1, T, 4 * d, d, proj_nt),
+            ("fc2", 1, T, d, 4 * d, proj_nt), ("qk_t", batch * heads, tokens, tokens, dh, True),
             ("pv", batch * heads, tokens, dh, tokens, False)]
 
 
-def bench_vit_half(om, steps: int, warmup: int, bf16: bool):
-    """The ViT-B/16 GEMM set (batch 64, 197 tokens) with fp16 / bf16 inputs, fp32 accumulate."""
+def bench_vit_half(om, steps: int, warmup: int, bf16: bool, proj_nt: bool = False):
+    """The ViT-B/16 GEMM set (batch 64, 197 tokens) with fp16 / bf16 inputs, fp32 accumulate,
+    projections in the NN (reference) or NT weight layout. With NN, also the fused attention
+    and the whole attention layer (MultiHeadAttention::forward: QKV Linear with bias, fused
+    attention, output Linear with bias)."""
     from omnimatchdeeplearningtool_amd.hiptime import StreamTimer
     H = om.HIPBackend
     dt = 1 if bf16 else 0
     bufs = []
     rng = np.random.default_rng(5)
-    for name, b, m, n, k, tb in vit_gemm_shapes():
+    for name, b, m, n, k, tb in vit_gemm_shapes(proj_nt=proj_nt):
         a = rng.standard_normal(b * m * k, dtype=np.float32)
         w = (rng.standard_normal(b * n * k, dtype=np.float32) * (0.02 if b == 1 else 1.0)).astype(np.float32)
         da, dw = om.DeviceBuffer.from_numpy(a), om.DeviceBuffer.from_numpy(w)
@@ -395,6 +399,8 @@ def bench_vit_half(om, steps: int, warmup: int, bf16: bool):
         flops_total += f
         total_ms += ms
         per.append({"gemm": name, "shape": [b, m, n, k], "ms": round(ms, 4), "tflops": round(f / ms / 1e9, 1)})
+    if proj_nt:
+        return total_ms, flops_total, per, None, None
     # Fused attention on the QKV projection's output layout [T, 3*768] (split + softmax(QK^T/8) V + merge),
     # replacing the two batched products above plus the softmax between them.
     batch, tokens, heads, dh = 64, 197, 12, 64
@@ -418,7 +424,37 @@ def bench_vit_half(om, steps: int, warmup: int, bf16: bool):
              "hbm_gb_s": round(attn_bytes / attn_ms / 1e6, 1), "frac_of_8000_gb_s": round(attn_bytes / attn_ms / 8e9, 4),
              "tflops": round(attn_flops / attn_ms / 1e9, 1),
              "replaces_ms": round(sum(x["ms"] for x in per if x["gemm"] in ("qk_t", "pv")), 4)}
-    return total_ms, flops_total, per, fused
+    # The whole attention layer: x [T, 768] half -> out [T, 768] fp32 (three launches).
+    d = heads * dh
+    x = om.DeviceBuffer.empty((T * d,), np.uint16)
+    H.convertToHalf(om.DeviceBuffer.from_numpy(rng.standard_normal(T * d, dtype=np.float32)), x, T * d, bf16=bf16)
+    wq = om.DeviceBuffer.empty((d * 3 * d,), np.uint16)
+    H.convertToHalf(om.DeviceBuffer.from_numpy(rng.standard_normal(d * 3 * d, dtype=np.float32) * 0.036), wq,
+                    d * 3 * d, bf16=bf16)
+    wo = om.DeviceBuffer.empty((d * d,), np.uint16)
+    H.convertToHalf(om.DeviceBuffer.from_numpy(rng.standard_normal(d * d, dtype=np.float32) * 0.036), wo, d * d,
+                    bf16=bf16)
+    bq = om.DeviceBuffer.from_numpy(rng.standard_normal(3 * d, dtype=np.float32) * 0.1)
+    bo = om.DeviceBuffer.from_numpy(rng.standard_normal(d, dtype=np.float32) * 0.1)
+    y = om.DeviceBuffer.empty((T * d,))
+
+    def layer():
+        H.multiHeadAttentionHalf(x, wq, bq, wo, bo, y, batch, tokens, heads, dh, bf16=bf16)
+
+    for _ in range(warmup):
+        layer()
+    om.synchronize()
+    t = StreamTimer(om.stream_handle())
+    t.start()
+    for _ in range(steps):
+        layer()
+    t.stop()
+    mha_ms = t.ms() / steps
+    mha_flops = 2.0 * T * d * 3 * d + attn_flops + 2.0 * T * d * d
+    mha = {"op": "multi_head_attention_forward", "shape": [batch, tokens, heads, dh], "ms": round(mha_ms, 4),
+           "tflops": round(mha_flops / mha_ms / 1e9, 1),
+           "launches": "QKV Linear (+bias, half out) -> fused attention (half out) -> output Linear (+bias, fp32 out)"}
+    return total_ms, flops_total, per, fused, mha
 
 
 def bench_mlp(om, steps: int, warmup: int, batch: int = 128):
@@ -775,15 +811,24 @@ def main():
     log(f"resnet50 {r50_ms:.3f} ms/batch  {64 / r50_ms * 1e3:.0f} img/s  roof frac {r50_roof / r50_ms:.3f}")
     vit = {}
     for bf in (False, True):
-        v_ms, v_flops, v_per, v_fused = bench_vit_half(om, max(5, args.steps // 5), 2, bf)
+        v_ms, v_flops, v_per, v_fused, v_mha = bench_vit_half(om, max(5, args.steps // 5), 2, bf)
+        t_ms, t_flops, t_per, _, _ = bench_vit_half(om, max(5, args.steps // 5), 2, bf, proj_nt=True)
         lin_ms = sum(x["ms"] for x in v_per if x["gemm"] not in ("qk_t", "pv"))
-        vit["bf16" if bf else "fp16"] = {"ms_per_set": round(v_ms, 4), "tflops": round(v_flops / v_ms / 1e9, 1),
+        vit["bf16" if bf else "fp16"] = {"layout": "projections NN: W stored [in, out] as Linear keeps it",
+                                         "ms_per_set": round(v_ms, 4), "tflops": round(v_flops / v_ms / 1e9, 1),
                                          "frac_of_2516_tflops": round(v_flops / v_ms / 1e9 / 2516.6, 4), "gemms": v_per,
+                                         "nt": {"ms_per_set": round(t_ms, 4), "tflops": round(t_flops / t_ms / 1e9, 1),
+                                                "frac_of_2516_tflops": round(t_flops / t_ms / 1e9 / 2516.6, 4),
+                                                "gemms": t_per},
                                          "attention_fused": v_fused,
-                                         "ms_per_layer_fused": round(lin_ms + v_fused["ms"], 4)}
-        log(f"vit {'bf16' if bf else 'fp16'} {v_ms:.3f} ms  {v_flops / v_ms / 1e9:.1f} TFLOP/s; fused attention "
-            f"{v_fused['ms'] * 1e3:.1f} us ({v_fused['hbm_gb_s']:.0f} GB/s) replaces {v_fused['replaces_ms'] * 1e3:.1f} us "
-            f"of Q.K^T + P.V")
+                                         "ms_per_layer_fused": round(lin_ms + v_fused["ms"], 4),
+                                         "attention_layer": v_mha}
+        log(f"vit {'bf16' if bf else 'fp16'} NN {v_ms:.3f} ms  {v_flops / v_ms / 1e9:.1f} TFLOP/s (NT {t_ms:.3f} ms "
+            f"{t_flops / t_ms / 1e9:.1f}); fused attention {v_fused['ms'] * 1e3:.1f} us ({v_fused['hbm_gb_s']:.0f} GB/s) "
+            f"replaces {v_fused['replaces_ms'] * 1e3:.1f} us of Q.K^T + P.V; attention layer {v_mha['ms'] * 1e3:.1f} us "
+            f"{v_mha['tflops']:.1f} TFLOP/s")
+        for x in v_per:
+            log(f"  {x['gemm']:8s} NN {x['ms'] * 1e3:8.1f} us {x['tflops']:7.1f} TF")
     mlp_ms, mlp_flops, mlp_graph_ms, mlp_graph_same, mlp_loss = bench_mlp(om, max(20, args.steps), 5)
     log(f"mlp step {mlp_ms * 1e3:.1f} us (graph replay {mlp_graph_ms * 1e3:.1f} us, bit-identical {mlp_graph_same}),"
         f" loss {mlp_loss:.4f}")

@@ -364,6 +364,15 @@ int omHipGemmStridedBatchedHalf(int nDtype, int bTransA, int bTransB, int nBatch
                                 const uint16_t* pB, long long nLdb, long long nStrideB,
                                 float* pC, long long nLdc, long long nStrideC);
 
+/* NEW: half-precision Linear, out = act(x W + b) with fp32 accumulate (Linear::forward
+ * linear.ixx:50-58: tensorMatmul then tensorAddBias, on halfToFloat inputs; ReLU after the
+ * bias as omHipLinearBiasAct). pInput [nM, nK] and pWeight in nDtype (0 binary16, 1
+ * bfloat16): [nK, nN] as Linear stores it (bTransW 0), or [nN, nK] (bTransW 1); pBias [nN]
+ * fp32 or NULL; nAct 0 none, 1 ReLU; pOutput [nM, nN] fp32 (nOutHalf 0) or nDtype rounded to
+ * nearest even (nOutHalf 1) — bit-identical to the fp32 output followed by
+ * omHipConvertF32ToF16 / omHipConvertF32ToBF16 for finite values. */
+int omHipLinearHalf(int nDtype, const uint16_t* pInput, const uint16_t* pWeight, int bTransW, const float* pBias,
+                    int nAct, void* pOutput, int nOutHalf, int nM, int nK, int nN);
 /* NEW: fused multi-head attention on half-precision inputs (QKV split with Q scaled,
  * Q x K^T, softmax over the keys, P x V, head merge). Reference composition:
  * MultiHeadAttention::forward vit.ixx:150-239 after the QKV projection —
@@ -375,6 +384,20 @@ int omHipGemmStridedBatchedHalf(int nDtype, int bTransA, int bTransB, int nBatch
  * nSeq <= 384. P is rounded to nDtype before P x V (fp32 accumulate). */
 int omHipAttentionHalf(int nDtype, const uint16_t* pQKV, void* pOut, int nOutHalf,
                        int nBatch, int nSeq, int nHeads, int nHeadDim, float fScale);
+/* NEW: MultiHeadAttention::forward (vit.ixx:150-239) on half-precision activations and
+ * weights, fp32 accumulate: qkv = x Wqkv + bqkv; heads split with Q scaled by
+ * 1/sqrt(nHeadDim); softmax(Q K^T) V; heads merged; out = ctx Wout + bout.
+ * pX [nBatch*nSeq, nDim] in nDtype, nDim = nHeads*nHeadDim; pWqkv [nDim, 3*nDim] and pWout
+ * [nDim, nDim] in nDtype, stored [in, out] as Linear (linear.ixx:31); pBqkv [3*nDim] and
+ * pBout [nDim] fp32 or NULL; pOut [nBatch*nSeq, nDim] fp32 (nOutHalf 0) or nDtype (1).
+ * nHeadDim 64 with nSeq <= 384 runs fused: the projection is rounded to nDtype, then
+ * omHipAttentionHalf (P rounded to nDtype), its context rounded to nDtype. Other shapes
+ * run the reference's unfused chain in fp32 (projection, Q scaled, Q K^T, softmax, P V,
+ * merged heads) with the context rounded to nDtype for the output projection.
+ * Intermediates use the library's per-stream workspace. */
+int omHipMultiHeadAttentionHalf(int nDtype, const uint16_t* pX, const uint16_t* pWqkv, const float* pBqkv,
+                                const uint16_t* pWout, const float* pBout, void* pOut, int nOutHalf,
+                                int nBatch, int nSeq, int nHeads, int nHeadDim);
 
 /* ===== device-resident inference (EngineBridge::inferBatch, EngineBridge.cpp:3525-3772) ===== */
 

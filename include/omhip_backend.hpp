@@ -217,6 +217,21 @@ public:
         check(omHipAttentionHalf(nDtype, pQKV, pOut, bOutHalf ? 1 : 0, nBatch, nSeq, nHeads, nHeadDim, fScale),
               "attentionHalf");
     }
+    // Linear::forward (linear.ixx:50-58) on half inputs: act(x W + b), W [K,N] ([N,K] when bTransW)
+    static void linearHalf(int nDtype, const uint16_t* pInput, const uint16_t* pWeight, bool bTransW,
+                           const float* pBias, int nAct, void* pOutput, bool bOutHalf, int nM, int nK, int nN) {
+        check(omHipLinearHalf(nDtype, pInput, pWeight, bTransW ? 1 : 0, pBias, nAct, pOutput, bOutHalf ? 1 : 0, nM,
+                              nK, nN),
+              "linearHalf");
+    }
+    // MultiHeadAttention::forward (vit.ixx:150-239): QKV Linear -> attention -> output Linear
+    static void multiHeadAttentionHalf(int nDtype, const uint16_t* pX, const uint16_t* pWqkv, const float* pBqkv,
+                                       const uint16_t* pWout, const float* pBout, void* pOut, bool bOutHalf,
+                                       int nBatch, int nSeq, int nHeads, int nHeadDim) {
+        check(omHipMultiHeadAttentionHalf(nDtype, pX, pWqkv, pBqkv, pWout, pBout, pOut, bOutHalf ? 1 : 0, nBatch,
+                                          nSeq, nHeads, nHeadDim),
+              "multiHeadAttentionHalf");
+    }
 
     // ---- entries the reference builds by composition ----
     // transpose2d(B) + matmul (autograd.ixx:261-273)

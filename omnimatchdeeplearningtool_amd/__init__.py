@@ -119,6 +119,8 @@ _SIGS = {
     "omHipBatchNorm2dBackwardRelu": [_vp] * 9 + [_i] * 4 + [_fl],
     "omHipConv2dBiasBnAddAct": [_vp] * 7 + [_fl, _vp, _i, _vp] + [_i] * 9,
     "omHipAttentionHalf": [_i, _vp, _vp, _i, _i, _i, _i, _i, _fl],
+    "omHipLinearHalf": [_i, _vp, _vp, _i, _vp, _i, _vp, _i, _i, _i, _i],
+    "omHipMultiHeadAttentionHalf": [_i, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i],
     "omHipConvertF32ToF16": [_vp, _vp, _i],
     "omHipConvertF32ToBF16": [_vp, _vp, _i],
     "omHipConvertF16ToF32": [_vp, _vp, _i],
@@ -518,6 +520,20 @@ class HIPBackend:
         """Fused QKV split + softmax(scale Q K^T) V + head merge (vit.ixx:150-239)."""
         call("omHipAttentionHalf", 1 if bf16 else 0, _ptr(pQKV), _ptr(pOut), 1 if outHalf else 0, nBatch, nSeq, nHeads,
              nHeadDim, fScale)
+
+    @staticmethod
+    def linearHalf(pInput, pWeight, pBias, pOutput, nM, nK, nN, bf16: bool = False, transW: bool = False,
+                   act: int = 0, outHalf: bool = False) -> None:
+        """Linear::forward (linear.ixx:50-58) on half inputs: act(x W + b), W [K,N] (or [N,K])."""
+        call("omHipLinearHalf", 1 if bf16 else 0, _ptr(pInput), _ptr(pWeight), 1 if transW else 0, _ptr(pBias), act,
+             _ptr(pOutput), 1 if outHalf else 0, nM, nK, nN)
+
+    @staticmethod
+    def multiHeadAttentionHalf(pX, pWqkv, pBqkv, pWout, pBout, pOut, nBatch, nSeq, nHeads, nHeadDim,
+                               bf16: bool = False, outHalf: bool = False) -> None:
+        """MultiHeadAttention::forward (vit.ixx:150-239): QKV Linear, attention, output Linear."""
+        call("omHipMultiHeadAttentionHalf", 1 if bf16 else 0, _ptr(pX), _ptr(pWqkv), _ptr(pBqkv), _ptr(pWout),
+             _ptr(pBout), _ptr(pOut), 1 if outHalf else 0, nBatch, nSeq, nHeads, nHeadDim)
 
     # ---- entries the reference builds by composition ----
     @staticmethod

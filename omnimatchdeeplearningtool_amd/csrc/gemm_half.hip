@@ -1,5 +1,7 @@
 // gemm_half.hip — fp16 / bf16 GEMM with fp32 accumulate on gfx950
-// (v_mfma_f32_32x32x16_f16 / _bf16), fp32 output.
+// (v_mfma_f32_32x32x16_f16 / _bf16); output fp32, or rounded to nearest even
+// into the input type, optionally after a per-column fp32 bias and ReLU (a
+// Linear layer's x W + b in one pass).
 //
 // The reference has no half-precision GEMM: its FP16Converter is a software
 // converter (src/engine/om.engine.fp16.ixx:36-164) and every matmul runs in
@@ -44,14 +46,60 @@ typedef uint16_t u16x8 __attribute__((ext_vector_type(8)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4h __attribute__((ext_vector_type(4)));
 
+// Output: C (element offsets; fp32, or halves of the input type when outHalf)
+// = act(A * B + bias) with bias [N] fp32 or null, act 0 identity, 1 ReLU.
 struct GemmHalfParams {
     const uint16_t* A;
     const uint16_t* B;
-    float* C;
+    void* C;
     int M, N, K;
     long long lda, ldb, ldc, sA, sB, sC;
     int tilesM, tilesN;
+    const float* bias;
+    int act, outHalf;
 };
+
+template <bool BF16>
+__device__ __forceinline__ uint16_t halfBits(float v) {   // round to nearest even
+    if constexpr (BF16)
+        return __builtin_bit_cast(uint16_t, (__bf16)v);
+    else
+        return __builtin_bit_cast(uint16_t, (_Float16)v);
+}
+
+// Epilogue of one output element: the bias add and ReLU in fp32 (in the
+// order of tensorAddBias then relu), then the store in the output type.
+template <bool BF16, class P>
+__device__ __forceinline__ void storeOne(const P& p, long long off, int n, float v) {
+    if (p.bias) v += p.bias[n];
+    if (p.act == 1) v = v > 0.f ? v : 0.f;
+    if (p.outHalf)
+        static_cast<uint16_t*>(p.C)[off] = halfBits<BF16>(v);
+    else
+        static_cast<float*>(p.C)[off] = v;
+}
+
+// Four consecutive columns n .. n+3 of one row (n % 4 == 0, the element
+// offset a multiple of 4 and the base 16-byte (fp32) / 8-byte (half) aligned).
+template <bool BF16, class P>
+__device__ __forceinline__ void storeFour(const P& p, long long off, int n, float v0, float v1, float v2, float v3) {
+    if (p.bias) {
+        v0 += p.bias[n]; v1 += p.bias[n + 1]; v2 += p.bias[n + 2]; v3 += p.bias[n + 3];
+    }
+    if (p.act == 1) {
+        v0 = v0 > 0.f ? v0 : 0.f; v1 = v1 > 0.f ? v1 : 0.f; v2 = v2 > 0.f ? v2 : 0.f; v3 = v3 > 0.f ? v3 : 0.f;
+    }
+    if (p.outHalf) {
+        typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+        const u32x2 w = {(uint32_t)halfBits<BF16>(v0) | ((uint32_t)halfBits<BF16>(v1) << 16),
+                         (uint32_t)halfBits<BF16>(v2) | ((uint32_t)halfBits<BF16>(v3) << 16)};
+        *reinterpret_cast<u32x2*>(static_cast<uint16_t*>(p.C) + off) = w;
+    } else {
+        typedef float f32x4e __attribute__((ext_vector_type(4)));
+        const f32x4e w = {v0, v1, v2, v3};
+        *reinterpret_cast<f32x4e*>(static_cast<float*>(p.C) + off) = w;
+    }
+}
 
 template <int BM_, int BN_, int BK_, int WM_, int WN_>
 struct HCfg {
@@ -214,7 +262,6 @@ __global__ __launch_bounds__(Cfg::NT) void gemm_half_generic(GemmHalfParams p) {
         __syncthreads();
     }
 
-    float* C = p.C + batch * p.sC;
 #pragma unroll
     for (int fm = 0; fm < Cfg::FM; ++fm)
 #pragma unroll
@@ -224,7 +271,7 @@ __global__ __launch_bounds__(Cfg::NT) void gemm_half_generic(GemmHalfParams p) {
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const int row = m0 + wm * Cfg::WM + fm * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
-                if (row < p.M) C[(long long)row * p.ldc + col] = acc[fm][fn][r];
+                if (row < p.M) storeOne<BF16>(p, batch * p.sC + (long long)row * p.ldc + col, col, acc[fm][fn][r]);
             }
         }
 }
@@ -277,11 +324,13 @@ __device__ __forceinline__ u32x4 ld128(__amdgpu_buffer_rsrc_t r, uint32_t voff, 
 struct HalfFastParams {
     const uint16_t* A;
     const uint16_t* B;
-    float* C;
+    void* C;
     int M, N, K;
     int lda, ldb;        // < 2^21
     long long ldc, sA, sB, sC;
     int tilesM, tilesN;
+    const float* bias;   // output as GemmHalfParams
+    int act, outHalf;
 };
 
 // K-major operand whose rows start at any half (an odd leading dimension,
@@ -566,9 +615,10 @@ __device__ __forceinline__ void interleave() {
     }
 }
 
-// SWAP (C rows allow 128-bit stores: N, ldc, batch stride multiples of 4 and a
-// 16-byte aligned base) puts the B fragment first so each lane holds 4
-// consecutive columns; otherwise lanes run along n for coalesced 32-bit stores.
+// SWAP (C rows allow 4-column stores: N, ldc, batch stride multiples of 4 and
+// the base 16-byte aligned for fp32, 8-byte for half output) puts the B
+// fragment first so each lane holds 4 consecutive columns; otherwise lanes run
+// along n for coalesced element stores.
 // RAG: the K-major operands' rows may start at any half (KMajorRaggedSlice).
 template <class Cfg, bool BF16, bool TA, bool TB, bool SWAP, bool RAG>
 __global__ __launch_bounds__(Cfg::NT) void gemm_half_fast(HalfFastParams p) {
@@ -665,7 +715,7 @@ __global__ __launch_bounds__(Cfg::NT) void gemm_half_fast(HalfFastParams p) {
     if (t + 1 < nk) step(t++, std::false_type{});   // the one partial slice at the end of K
     runSlice(t, false);
 
-    float* Cb = p.C + batch * p.sC;
+    const long long cb = batch * p.sC;
     if constexpr (SWAP) {
         // Lane (li, h) holds, for block (fm, fn), C[m][n .. n+3] at
         // m = mBase + li, n = nBase + 8*g + 4*h (registers 4g .. 4g+3).
@@ -673,15 +723,15 @@ __global__ __launch_bounds__(Cfg::NT) void gemm_half_fast(HalfFastParams p) {
         for (int fm = 0; fm < Cfg::FM; ++fm) {
             const int m = m0 + wm * Cfg::WM + fm * 32 + li;
             if (m >= p.M) continue;
-            float* crow = Cb + (long long)m * p.ldc;
+            const long long crow = cb + (long long)m * p.ldc;
 #pragma unroll
             for (int fn = 0; fn < Cfg::FN; ++fn)
 #pragma unroll
                 for (int g = 0; g < 4; ++g) {
                     const int n = n0 + wn * Cfg::WN + fn * 32 + 8 * g + 4 * h;
-                    const f32x4h v = {acc[fm][fn][4 * g], acc[fm][fn][4 * g + 1], acc[fm][fn][4 * g + 2],
-                                      acc[fm][fn][4 * g + 3]};
-                    if (n < p.N) *reinterpret_cast<f32x4h*>(crow + n) = v;   // N % 4 == 0
+                    if (n < p.N)   // N % 4 == 0
+                        storeFour<BF16>(p, crow + n, n, acc[fm][fn][4 * g], acc[fm][fn][4 * g + 1],
+                                        acc[fm][fn][4 * g + 2], acc[fm][fn][4 * g + 3]);
                 }
         }
     } else {
@@ -696,7 +746,7 @@ __global__ __launch_bounds__(Cfg::NT) void gemm_half_fast(HalfFastParams p) {
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
                     const int m = m0 + wm * Cfg::WM + fm * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
-                    if (m < p.M) Cb[(long long)m * p.ldc + n] = acc[fm][fn][r];
+                    if (m < p.M) storeOne<BF16>(p, cb + (long long)m * p.ldc + n, n, acc[fm][fn][r]);
                 }
         }
     }
@@ -795,8 +845,10 @@ static int dispatchH(bool ta, bool tb, const GemmHalfParams& prm, int batch, boo
         HalfFastParams f{};
         f.A = prm.A; f.B = prm.B; f.C = prm.C; f.M = prm.M; f.N = prm.N; f.K = prm.K;
         f.lda = (int)prm.lda; f.ldb = (int)prm.ldb; f.ldc = prm.ldc; f.sA = prm.sA; f.sB = prm.sB; f.sC = prm.sC;
+        f.bias = prm.bias; f.act = prm.act; f.outHalf = prm.outHalf;
+        const uintptr_t cAlign = prm.outHalf ? 7u : 15u;
         const bool vecC = (prm.N % 4 == 0) && (prm.ldc % 4 == 0) && (prm.sC % 4 == 0) &&
-                          ((reinterpret_cast<uintptr_t>(prm.C) & 15u) == 0);
+                          ((reinterpret_cast<uintptr_t>(prm.C) & cAlign) == 0);
         if (!ta && !tb) return launchFastR<BF16, false, false>(f, batch, vecC, rag);
         if (!ta && tb) return launchFastR<BF16, false, true>(f, batch, vecC, rag);
         if (ta && !tb) return launchFastR<BF16, true, false>(f, batch, vecC, rag);
@@ -810,18 +862,28 @@ static int dispatchH(bool ta, bool tb, const GemmHalfParams& prm, int batch, boo
 
 int zeroOutput(float* C, int batch, int M, int N, long long ldc, long long sC);
 
+// C = act(op(A) op(B) + bias), fp32 or (outHalf) the input half type.
 static int gemmHalf(const char* name, int dtype, bool ta, bool tb, int batch, int M, int N, int K,
                     const uint16_t* A, long long lda, long long sA, const uint16_t* B, long long ldb, long long sB,
-                    float* C, long long ldc, long long sC) {
+                    void* C, long long ldc, long long sC, const float* bias = nullptr, int act = 0,
+                    bool outHalf = false) {
     clearError();
     if (batch <= 0 || M <= 0 || N <= 0) return 0;
     if (!C) return fail("%s: null output", name);
-    if (!A || !B || K <= 0) return zeroOutput(C, batch, M, N, ldc, sC);
     if (batch > 65535) return fail("%s: batch %d exceeds 65535", name, batch);
     if (dtype != 0 && dtype != 1) return fail("%s: dtype must be 0 (fp16) or 1 (bf16)", name);
+    if (act != 0 && act != 1) return fail("%s: activation must be 0 (none) or 1 (ReLU)", name);
+    const bool empty = !A || !B || K <= 0;   // a product with no terms: act(0 + bias)
+    if (empty && !bias && !outHalf) return zeroOutput(static_cast<float*>(C), batch, M, N, ldc, sC);
     GemmHalfParams prm{};
-    prm.A = A; prm.B = B; prm.C = C; prm.M = M; prm.N = N; prm.K = K;
+    prm.A = empty ? nullptr : A; prm.B = empty ? nullptr : B; prm.C = C; prm.M = M; prm.N = N;
+    prm.K = empty ? 0 : K;
     prm.lda = lda; prm.ldb = ldb; prm.ldc = ldc; prm.sA = sA; prm.sB = sB; prm.sC = sC;
+    prm.bias = bias; prm.act = act; prm.outHalf = outHalf ? 1 : 0;
+    if (empty) {   // the generic kernel's loads are all masked off when K is 0
+        return dtype == 1 ? launchGenericC<true, false, false>(prm, batch, false, false)
+                          : launchGenericC<false, false, false>(prm, batch, false, false);
+    }
     auto al = [](const void* q) { return (reinterpret_cast<uintptr_t>(q) & 15u) == 0; };
     const bool va = al(A) && lda % 8 == 0 && sA % 8 == 0 && (ta ? M % 8 == 0 : K % 8 == 0);
     const bool vb = al(B) && ldb % 8 == 0 && sB % 8 == 0 && (tb ? K % 8 == 0 : N % 8 == 0);
@@ -845,6 +907,11 @@ int omHipMatmulTransBF16(const uint16_t* pA, const uint16_t* pB, float* pC, int 
 }
 int omHipMatmulTransBBF16(const uint16_t* pA, const uint16_t* pB, float* pC, int nM, int nK, int nN) {
     return gemmHalf("omHipMatmulTransBBF16", 1, false, true, 1, nM, nN, nK, pA, nK, 0, pB, nK, 0, pC, nN, 0);
+}
+int omHipLinearHalf(int nDtype, const uint16_t* pInput, const uint16_t* pWeight, int bTransW, const float* pBias,
+                    int nAct, void* pOutput, int nOutHalf, int nM, int nK, int nN) {
+    return gemmHalf("omHipLinearHalf", nDtype, false, bTransW != 0, 1, nM, nN, nK, pInput, nK, 0, pWeight,
+                    bTransW ? nK : nN, 0, pOutput, nN, 0, pBias, nAct, nOutHalf != 0);
 }
 int omHipGemmStridedBatchedHalf(int nDtype, int bTransA, int bTransB, int nBatch, int nM, int nN, int nK,
                                 const uint16_t* pA, long long nLda, long long nStrideA, const uint16_t* pB,

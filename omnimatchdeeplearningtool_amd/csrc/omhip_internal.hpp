@@ -37,9 +37,11 @@ void clearError();
 // the stream. Slot 0 holds split-K partial sums, slot 1 a call's temporary
 // operand (flipped weights, an im2col buffer) that slot-0 users read, slot 2
 // per-tile arrival counters: zero-filled when (re)allocated, and every kernel
-// that counts on them returns them to zero. nullptr with the error recorded on
-// OOM, or when the block must grow while the stream records a graph.
-enum WsSlot { kWsPartials = 0, kWsOperand = 1, kWsCounters = 2 };
+// that counts on them returns them to zero; slot 3 the intermediates of a
+// composed layer (the attention block's projections), which the ops it calls
+// do not touch. nullptr with the error recorded on OOM, or when the block must
+// grow while the stream records a graph.
+enum WsSlot { kWsPartials = 0, kWsOperand = 1, kWsCounters = 2, kWsStaging = 3 };
 void* workspace(size_t bytes, int slot = kWsPartials);
 
 // Whether stream s is recording a graph.
