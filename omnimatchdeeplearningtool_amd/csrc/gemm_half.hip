@@ -15,16 +15,17 @@
 //    loads whose per-lane offset is fixed for the whole K walk (the slice
 //    start rides in the scalar offset; rows past the matrix fall outside the
 //    buffer range and read 0), so the mainloop spends almost no VALU on
-//    addressing. Both operands sit K-contiguous in LDS, so an MFMA fragment (8
-//    consecutive k of one row) is one ds_read_b128. A 16-byte-aligned K-major
-//    operand goes straight from the buffer into LDS (buffer_load ... lds, a
-//    swizzled unpadded layout); one that is only 2-byte aligned (odd K or
-//    leading dimension) is fetched 16 bytes at a time from the dword boundary
-//    below and funnel-shifted into place in registers. An operand that is
-//    R-contiguous in HBM (B of A*B, A of A^T*B) is loaded as 8x8 blocks and
-//    transposed in registers with v_perm before the LDS store. The MFMA takes
-//    the B fragment as its first operand, so each lane ends up holding 4
-//    consecutive output columns and the fp32 tile leaves in 128-bit stores.
+//    addressing. A 16-byte-aligned K-major operand goes straight from the
+//    buffer into LDS (buffer_load ... lds) in a swizzled unpadded [R][BK]
+//    layout, and an MFMA fragment (8 consecutive k of one row) is one
+//    ds_read_b128; one that is only 2-byte aligned (odd K or leading
+//    dimension) is fetched 16 bytes at a time from the dword boundary below,
+//    funnel-shifted into place in registers and stored to padded rows. An
+//    operand that is R-contiguous in HBM (B of A*B, A of A^T*B) also goes
+//    straight into LDS, in its own [BK][R] layout, and is transposed by the
+//    fragment read (two ds_read_b64_tr_b16 per fragment). The MFMA takes the
+//    B fragment as its first operand, so each lane ends up holding 4
+//    consecutive output columns and the tile leaves in 128-bit stores.
 //  * gemm_half_generic: any other layout (element loads with bounds checks).
 //
 // Within a 16-deep MFMA step the two 32-lane halves supply k = 0..7 and
@@ -347,7 +348,7 @@ struct HalfFastParams {
 // last slice: there the next row's data lies, not the end of the view.
 template <int R, int BK, int NT>
 struct KMajorRaggedSlice {
-    static constexpr bool DMA = false, SWZ = false;
+    static constexpr bool DMA = false, SWZ = false, TR = false;
     static constexpr int CH = BK / 8;
     static constexpr int PER_T = R * CH / NT;
     static_assert(R * CH % NT == 0, "slice must split evenly");
@@ -418,7 +419,7 @@ typedef __attribute__((address_space(3))) void* LdsPtr;
 template <int R, int BK, int NT>
 struct KMajorDmaSlice {
     static_assert(BK == 64, "8 chunks of 8 halves per row");
-    static constexpr bool DMA = true, SWZ = true;
+    static constexpr bool DMA = true, SWZ = true, TR = false;
     static constexpr int NW = NT / 64;
     static constexpr int INSTR = R / 8 / NW;   // instructions per wave and slice
     static_assert(R % (8 * NW) == 0, "rows must split evenly over the waves");
@@ -471,68 +472,113 @@ __device__ __forceinline__ int ldsChunk(int r, int c) {
         return r * LDP + (c << 3);
 }
 
-// R-major operand: element (r,k) at P[k*ld + r]. A slice is (R/8) x (BK/8)
-// blocks of 8 k x 8 r; block e is (rb = e / (BK/8), kb = e % (BK/8)). A thread
-// loads its block's 8 rows (one 16-byte load each; the row step rides in the
-// scalar offset) and transposes it in registers into 8 K-contiguous 16-byte
-// LDS rows. The view starts at the tile's first column and ends after row
-// K-1's last valid column, so rows past K read 0; blocks past the matrix's
-// columns are pointed outside the view.
+// 16 bytes per lane from the buffer straight into LDS at dst + 16 * lane.
+__device__ __forceinline__ void dmaLoad16(__amdgpu_buffer_rsrc_t r, uint16_t* dst, uint32_t voff, uint32_t soff) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (LdsPtr)dst, 16, voff, soff, 0, 0);
+}
+
 template <int R, int BK, int NT>
-struct RMajorSlice {
-    static constexpr bool DMA = false, SWZ = false;
-    static constexpr int KB = BK / 8;
-    static constexpr int BLKS = (R / 8) * KB;
-    static constexpr bool PARTIAL = BLKS < NT;   // only threads < BLKS carry a block
-    static constexpr int PER_T = PARTIAL ? 1 : BLKS / NT;
-    static_assert(PARTIAL ? (BLKS % 64 == 0) : (BLKS % NT == 0), "blocks must split evenly over waves");
-    static constexpr int NLOADS = 8 * PER_T, NSTORES = 8 * PER_T;   // per loading thread and slice
-    struct Regs {
-        u32x4 v[PER_T][8];
-    };
+struct RMajorDmaSlice {
+    static constexpr bool DMA = true, SWZ = false, TR = true;
+    static constexpr int NW = NT / 64;
+    static constexpr int CH = R / 8;              // chunks per k row
+    static constexpr int ROWS_PER_I = 64 / CH;    // k rows per DMA instruction
+    static constexpr int INSTR = BK / ROWS_PER_I / NW;
+    static_assert(CH >= 8 && CH <= 64 && BK % (ROWS_PER_I * NW) == 0, "k rows must split evenly over the waves");
+    static constexpr int NLOADS = INSTR, NSTORES = 0;
+    struct Regs {};
     __amdgpu_buffer_rsrc_t r;
-    uint32_t voff[PER_T];
+    uint32_t voff[INSTR];
     uint32_t ld2;
+    int wave;
+
+    static __device__ __forceinline__ int swz(int k) { return ((k & 1) * 10 + ((k >> 1) & 1) * 4) & (CH - 1); }
 
     __device__ void init(const uint16_t* base, int ld, int colsValid, int K, int tid) {
         ld2 = (uint32_t)ld * 2u;
         const int cv = colsValid < R ? colsValid : R;
         r = halfRsrc(base, (uint32_t)(K - 1) * ld2 + (uint32_t)cv * 2u);
+        wave = tid >> 6;
+        const int lane = tid & 63;
 #pragma unroll
-        for (int i = 0; i < PER_T; ++i) {
-            const int e = tid + i * NT;
-            const int rb = e / KB, kb = e % KB;
-            voff[i] = (rb * 8 < cv) ? (uint32_t)(kb * 8) * ld2 + (uint32_t)(rb * 16) : kOOBH;   // cols % 8 == 0
+        for (int i = 0; i < INSTR; ++i) {
+            const int k = (wave + i * NW) * ROWS_PER_I + lane / CH;
+            const int c = (lane % CH) ^ swz(k);
+            voff[i] = (c * 8 < cv) ? (uint32_t)k * ld2 + (uint32_t)c * 16u : kOOBH;   // cols % 8 == 0
         }
     }
     template <bool FULL>   // rows past K read 0 either way
-    __device__ void load(int k0, int /*K*/, int tid, Regs& g) const {
-        if (PARTIAL && tid >= BLKS) return;
+    __device__ void dma(int k0, int /*K*/, uint16_t* dst) const {
+        const uint32_t soff = (uint32_t)k0 * ld2;
 #pragma unroll
-        for (int i = 0; i < PER_T; ++i)
-#pragma unroll
-            for (int j = 0; j < 8; ++j) g.v[i][j] = ld128(r, voff[i], (uint32_t)(k0 + j) * ld2);
+        for (int i = 0; i < INSTR; ++i)
+            dmaLoad16(r, dst + (wave + i * NW) * 512, voff[i], soff);
     }
-    static __device__ __forceinline__ uint32_t pair(uint32_t lo, uint32_t hi, bool upper) {
-        // (lo.half[upper], hi.half[upper]) packed low-to-high
-        return __builtin_amdgcn_perm(hi, lo, upper ? 0x07060302u : 0x05040100u);
-    }
+    template <bool FULL>
+    __device__ void load(int, int, int, Regs&) const {}
     template <int LD>
-    __device__ void store(uint16_t* s, int tid, const Regs& g) const {
-        if (PARTIAL && tid >= BLKS) return;
+    __device__ void store(uint16_t*, int, const Regs&) const {}
+};
+
+// Per-lane LDS offsets of an R-major operand's F fragments (rows base + 32j
+// .. +31, k = 16s + 8h .. +7 of step s). ds_read_b64_tr_b16 returns to lane i
+// of each 16-lane group the 4 halves E[4j + i/4][i%4], j = 0..3, where E[q] is
+// what lane q of the group addressed; so lane q addresses k row 8h + q/4 (+4
+// for the second read) at column 16g + 4(q%4) (g = lane bit 4), and lane l
+// then holds rows base + 32j + l%32, k = 8h + 0..7: the MFMA operand layout.
+//
+// The reads are issued as inline assembly: the compiler treats the
+// ds_read_tr builtin as possibly aliasing the in-flight LDS DMA of the next
+// slice (which writes the other stage) and waits for every global load before
+// the first one, which serialises the load latency with the slice's MFMAs.
+// The compiler does not count these reads, so wait() (lgkmcnt 0, with the
+// fragments passed through so their MFMAs stay behind it) must precede any
+// use; the compiler's own LDS waits stay correct because LDS reads complete
+// in issue order and extra reads in between only make its counts stricter.
+typedef uint32_t u32x2t __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ uint32_t ldsAddr(const uint16_t* p) { return (uint32_t)(uintptr_t)(LdsPtr)(p); }
+
+template <int I, int N, class F>
+__device__ __forceinline__ void staticFor(F&& f) {
+    if constexpr (I < N) {
+        f(std::integral_constant<int, I>{});
+        staticFor<I + 1, N>(f);
+    }
+}
+
+template <int R, int F>
+struct TrFrags {
+    uint32_t off[F];   // bytes from the operand's stage base, step 0, first read
+    __device__ void init(int base, int lane) {
+        const int q = lane & 15, g = (lane >> 4) & 1, h = lane >> 5;
+        const int k = 8 * h + (q >> 2);
+        const int sw = RMajorDmaSlice<R, 64, 64>::swz(k);
 #pragma unroll
-        for (int i = 0; i < PER_T; ++i) {
-            const int e = tid + i * NT;
-            const int rb = e / KB, kb = e % KB;
-#pragma unroll
-            for (int n = 0; n < 8; ++n) {
-                const int d = n >> 1;
-                const bool up = (n & 1) != 0;
-                const u32x4 col = {pair(g.v[i][0][d], g.v[i][1][d], up), pair(g.v[i][2][d], g.v[i][3][d], up),
-                                   pair(g.v[i][4][d], g.v[i][5][d], up), pair(g.v[i][6][d], g.v[i][7][d], up)};
-                *reinterpret_cast<u32x4*>(s + (rb * 8 + n) * LD + kb * 8) = col;
-            }
+        for (int j = 0; j < F; ++j) {
+            const int c = (base + 32 * j) / 8 + 2 * g + ((q & 3) >> 1);
+            off[j] = 2u * (uint32_t)(k * R + ((c ^ sw) << 3) + 4 * (q & 1));
         }
+    }
+    // One read (half HH of fragment J at step STEP) from the stage base b (LDS bytes).
+    template <int STEP, int J, int HH>
+    __device__ __forceinline__ u32x2t half(uint32_t b) const {
+        u32x2t r;
+        asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(r) : "v"(b + off[J]), "i"(STEP * 32 * R + HH * 8 * R));
+        return r;
+    }
+    template <int STEP>
+    __device__ __forceinline__ void issue(const uint16_t* s, u32x4 (&dst)[F]) const {
+        const uint32_t b = ldsAddr(s);
+        staticFor<0, F>([&](auto J) {
+            const u32x2t lo = half<STEP, decltype(J)::value, 0>(b), hi = half<STEP, decltype(J)::value, 1>(b);
+            dst[J] = u32x4{lo[0], lo[1], hi[0], hi[1]};
+        });
+    }
+    static __device__ __forceinline__ void wait(u32x4 (&f)[F]) {
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+        for (int j = 0; j < F; ++j) asm volatile("" : "+v"(f[j]));
     }
 };
 
@@ -556,35 +602,38 @@ __device__ __forceinline__ f32x16h mfma16u(const u32x4& a, const u32x4& b, const
 // Scheduling-group masks of __builtin_amdgcn_sched_group_barrier.
 constexpr int kSgMfma = 0x008, kSgVmemRead = 0x020, kSgDsRead = 0x100, kSgDsWrite = 0x200;
 
-template <int I, int N, class F>
-__device__ __forceinline__ void staticFor(F&& f) {
-    if constexpr (I < N) {
-        f(std::integral_constant<int, I>{});
-        staticFor<I + 1, N>(f);
-    }
-}
-
 // Fragments of 16-deep MFMA step s: 8 consecutive k (lane half h: k = 16s+8h ..)
 // of rows li of each 32-row block of the wave's sub-tile.
-template <class Cfg, bool SWZA, bool SWZB>
-__device__ __forceinline__ void readFrags(const uint16_t* sA, const uint16_t* sB, int s, u32x4 (&a)[Cfg::FM],
-                                          u32x4 (&b)[Cfg::FN], int wm, int wn, int li, int h) {
-    const int c = s * 2 + h;   // chunk of 8 k
+// K-major operands' fragments of step s; an R-major operand (TR) is issued
+// through its TrFrags instead.
+template <class Cfg, class LA, class LB, int S, bool KONLY = false>
+__device__ __forceinline__ void readFrags(const uint16_t* sA, const uint16_t* sB, u32x4 (&a)[Cfg::FM],
+                                          u32x4 (&b)[Cfg::FN], int wm, int wn, int li, int h,
+                                          const TrFrags<Cfg::BM, Cfg::FM>& tra, const TrFrags<Cfg::BN, Cfg::FN>& trb) {
+    const int c = S * 2 + h;   // chunk of 8 k
+    if constexpr (LA::TR) {
+        if constexpr (!KONLY) tra.template issue<S>(sA, a);
+    } else {
 #pragma unroll
-    for (int fm = 0; fm < Cfg::FM; ++fm)
-        a[fm] = *reinterpret_cast<const u32x4*>(sA + ldsChunk<SWZA, Cfg::LD, Cfg::BK>(wm * Cfg::WM + fm * 32 + li, c));
+        for (int fm = 0; fm < Cfg::FM; ++fm)
+            a[fm] = *reinterpret_cast<const u32x4*>(sA + ldsChunk<LA::SWZ, Cfg::LD, Cfg::BK>(wm * Cfg::WM + fm * 32 + li, c));
+    }
+    if constexpr (LB::TR) {
+        if constexpr (!KONLY) trb.template issue<S>(sB, b);
+    } else {
 #pragma unroll
-    for (int fn = 0; fn < Cfg::FN; ++fn)
-        b[fn] = *reinterpret_cast<const u32x4*>(sB + ldsChunk<SWZB, Cfg::LD, Cfg::BK>(wn * Cfg::WN + fn * 32 + li, c));
+        for (int fn = 0; fn < Cfg::FN; ++fn)
+            b[fn] = *reinterpret_cast<const u32x4*>(sB + ldsChunk<LB::SWZ, Cfg::LD, Cfg::BK>(wn * Cfg::WN + fn * 32 + li, c));
+    }
 }
 
 // Loader types and LDS footprint of the fast kernel for a layout.
 template <class Cfg, bool TA, bool TB, bool RAG>
 struct HalfOps {
-    using LA = std::conditional_t<TA, RMajorSlice<Cfg::BM, Cfg::BK, Cfg::NT>, KMajorFor<RAG, Cfg::BM, Cfg::BK, Cfg::NT>>;
-    using LB = std::conditional_t<TB, KMajorFor<RAG, Cfg::BN, Cfg::BK, Cfg::NT>, RMajorSlice<Cfg::BN, Cfg::BK, Cfg::NT>>;
-    static constexpr int SA = Cfg::BM * (LA::SWZ ? Cfg::BK : Cfg::LD);
-    static constexpr int SB = Cfg::BN * (LB::SWZ ? Cfg::BK : Cfg::LD);
+    using LA = std::conditional_t<TA, RMajorDmaSlice<Cfg::BM, Cfg::BK, Cfg::NT>, KMajorFor<RAG, Cfg::BM, Cfg::BK, Cfg::NT>>;
+    using LB = std::conditional_t<TB, KMajorFor<RAG, Cfg::BN, Cfg::BK, Cfg::NT>, RMajorDmaSlice<Cfg::BN, Cfg::BK, Cfg::NT>>;
+    static constexpr int SA = Cfg::BM * (LA::SWZ || LA::TR ? Cfg::BK : Cfg::LD);
+    static constexpr int SB = Cfg::BN * (LB::SWZ || LB::TR ? Cfg::BK : Cfg::LD);
     static constexpr int STAGE = SA + SB;
     static constexpr size_t LDS_BYTES = 2 * (size_t)STAGE * sizeof(uint16_t);
     static constexpr bool ANY_DMA = LA::DMA || LB::DMA;
@@ -599,6 +648,38 @@ __device__ __forceinline__ void mfmaStep(const u32x4 (&a)[Cfg::FM], const u32x4 
 #pragma unroll
         for (int fn = 0; fn < Cfg::FN; ++fn)
             acc[fm][fn] = SWAP ? mfma16u<BF16>(b[fn], a[fm], acc[fm][fn]) : mfma16u<BF16>(a[fm], b[fn], acc[fm][fn]);
+}
+
+// The MFMAs of one step with the next step's R-major (TR) fragment reads
+// issued one before each MFMA (the rest after the last), each pair closed by
+// a scheduling barrier: left alone, the scheduler moves the MFMAs around the
+// read asm freely (it does not see LDS reads in it) and bunches the reads.
+template <class Cfg, bool BF16, bool SWAP, class LA, class LB, int SN>
+__device__ __forceinline__ void mfmaStepTr(const u32x4 (&a)[Cfg::FM], const u32x4 (&b)[Cfg::FN], u32x4 (&an)[Cfg::FM],
+                                           u32x4 (&bn)[Cfg::FN], f32x16h (&acc)[Cfg::FM][Cfg::FN], const uint16_t* sA,
+                                           const uint16_t* sB, const TrFrags<Cfg::BM, Cfg::FM>& tra,
+                                           const TrFrags<Cfg::BN, Cfg::FN>& trb) {
+    constexpr int RA = LA::TR ? 2 * Cfg::FM : 0, RB = LB::TR ? 2 * Cfg::FN : 0, NM = Cfg::FM * Cfg::FN;
+    u32x2t pa[2 * Cfg::FM], pb[2 * Cfg::FN];
+    const uint32_t baseA = ldsAddr(sA), baseB = ldsAddr(sB);
+    auto rd = [&](auto R) {
+        constexpr int r = decltype(R)::value;
+        if constexpr (r < RA) pa[r] = tra.template half<SN, r / 2, r % 2>(baseA);
+        else pb[r - RA] = trb.template half<SN, (r - RA) / 2, (r - RA) % 2>(baseB);
+    };
+    staticFor<0, NM>([&](auto I) {
+        constexpr int m = decltype(I)::value, fm = m / Cfg::FN, fn = m % Cfg::FN;
+        if constexpr (m < RA + RB) rd(I);
+        acc[fm][fn] = SWAP ? mfma16u<BF16>(b[fn], a[fm], acc[fm][fn]) : mfma16u<BF16>(a[fm], b[fn], acc[fm][fn]);
+        __builtin_amdgcn_sched_barrier(0);
+    });
+    staticFor<NM, RA + RB>(rd);
+    if constexpr (LA::TR)
+#pragma unroll
+        for (int j = 0; j < Cfg::FM; ++j) an[j] = u32x4{pa[2 * j][0], pa[2 * j][1], pa[2 * j + 1][0], pa[2 * j + 1][1]};
+    if constexpr (LB::TR)
+#pragma unroll
+        for (int j = 0; j < Cfg::FN; ++j) bn[j] = u32x4{pb[2 * j][0], pb[2 * j][1], pb[2 * j + 1][0], pb[2 * j + 1][1]};
 }
 
 // Interleaves NMEM memory instructions of kind MASK with NMFMA MFMAs (spread
@@ -669,7 +750,11 @@ __global__ __launch_bounds__(Cfg::NT) void gemm_half_fast(HalfFastParams p) {
     // make the stage offset a constant lets the scheduler interleave both
     // bodies and run out of VGPRs.)
     constexpr int STEPS = Cfg::BK / 16;
-    constexpr int NFRAG = Cfg::FM + Cfg::FN;
+    constexpr int NFRAG = (LA::TR ? 0 : Cfg::FM) + (LB::TR ? 0 : Cfg::FN);   // compiler-issued LDS reads per step
+    TrFrags<Cfg::BM, Cfg::FM> tra;
+    TrFrags<Cfg::BN, Cfg::FN> trb;
+    if constexpr (LA::TR) tra.init(wm * Cfg::WM, lane);
+    if constexpr (LB::TR) trb.init(wn * Cfg::WN, lane);
     // Runs slice t from LDS stage t&1 as a software pipeline: the fragments of
     // step s+1 are read while the MFMAs of step s run, and the next slice's
     // registers (fetched at the top) are written to the other stage during the
@@ -679,14 +764,22 @@ __global__ __launch_bounds__(Cfg::NT) void gemm_half_fast(HalfFastParams p) {
         const uint16_t* sB = sA + SA;
         uint16_t* nxt = hsm + ((t & 1) ^ 1) * STAGE;
         u32x4 fa[2][Cfg::FM], fb[2][Cfg::FN];
-        readFrags<Cfg, LA::SWZ, LB::SWZ>(sA, sB, 0, fa[0], fb[0], wm, wn, li, h);
+        readFrags<Cfg, LA, LB, 0>(sA, sB, fa[0], fb[0], wm, wn, li, h, tra, trb);
         __builtin_amdgcn_sched_group_barrier(kSgDsRead, NFRAG, 0);
         staticFor<0, STEPS>([&](auto I) {
             constexpr int st = decltype(I)::value;
+            if constexpr (LA::TR || LB::TR) {   // this step's fragments landed (and nothing else is read yet)
+                if constexpr (LA::TR) TrFrags<Cfg::BM, Cfg::FM>::wait(fa[st & 1]);
+                if constexpr (LB::TR) TrFrags<Cfg::BN, Cfg::FN>::wait(fb[st & 1]);
+            }
             if constexpr (st + 1 < STEPS) {
-                readFrags<Cfg, LA::SWZ, LB::SWZ>(sA, sB, st + 1, fa[(st + 1) & 1], fb[(st + 1) & 1], wm, wn, li, h);
-                mfmaStep<Cfg, BF16, SWAP>(fa[st & 1], fb[st & 1], acc);
-                interleave<kSgDsRead, NFRAG, Cfg::FM * Cfg::FN>();
+                readFrags<Cfg, LA, LB, st + 1, true>(sA, sB, fa[(st + 1) & 1], fb[(st + 1) & 1], wm, wn, li, h, tra, trb);
+                if constexpr (LA::TR || LB::TR)
+                    mfmaStepTr<Cfg, BF16, SWAP, LA, LB, st + 1>(fa[st & 1], fb[st & 1], fa[(st + 1) & 1], fb[(st + 1) & 1],
+                                                             acc, sA, sB, tra, trb);
+                else
+                    mfmaStep<Cfg, BF16, SWAP>(fa[st & 1], fb[st & 1], acc);
+                if constexpr (!(LA::TR || LB::TR)) interleave<kSgDsRead, NFRAG, Cfg::FM * Cfg::FN>();
             } else {
                 if (more) {
                     if constexpr (!LA::DMA) la.template store<Cfg::LD>(nxt, tid, ra);
