@@ -13,8 +13,10 @@ captured HIP graph are timed beside it).
 
 Also reported:
   roofline      — fp32 MFMA roof for the GEMM kernel (achieved = 2MNK / average
-                  launch time, peak 157.3 TFLOP/s), traffic from the committed
-                  rocprofv3 FETCH_SIZE / WRITE_SIZE counters when present;
+                  launch time, peak 157.3 TFLOP/s); traffic is read from the
+                  committed rocprofv3 FETCH_SIZE / WRITE_SIZE summary
+                  (profiles/traffic.json), not measured in this run, and
+                  roofline.traffic_source says so;
   cpu_baseline  — the reference CPUBackend itself (oracle/_ref, built from the
                   reference sources) timed on this host's cores on a bounded
                   sample of the same workloads;
@@ -893,7 +895,9 @@ def main():
         "pct_mfma_peak": round(100.0 * tflops * 1e12 / PEAK_FP32, 1),
         "roofline": {"bound": "mfma", "achieved": round(flops / gemm_kernel_ms / 1e9, 2), "peak": 157.3,
                      "unit": "TFLOP/s", "frac": round(flops / gemm_kernel_ms / 1e9 / 157.3, 4),
-                     "traffic": traffic},
+                     "traffic": traffic,
+                     "traffic_source": "profiles/traffic.json: rocprofv3 FETCH_SIZE and WRITE_SIZE passes over "
+                                       "`bench.py --traffic-probe`, copy-calibrated (recorded, not measured in this run)"},
         "cpu_baseline": cpu,
         "gemm_sweep": sweep,
         "parity": {"gemm_sampled_rows_max_err": gemm_err, "conv_sampled_max_err": conv_err, "tol": 1e-4},
