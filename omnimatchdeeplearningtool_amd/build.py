@@ -31,8 +31,10 @@ SOURCES = ["runtime.cpp", "eltwise.hip", "gemm_f32.hip", "conv.hip", "conv_wgrad
            "pool.hip", "attention.hip", "infer.hip", "loss.hip", "mha.hip"]
 # conv tiles keep at most 128 accumulators per lane: forcing the VGPR form of
 # the MFMA operands stops the register allocator from copying every
-# accumulator between AGPRs and VGPRs on each trip of the mainloop.
-EXTRA_FLAGS = {"conv.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"], "conv_wgrad.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
+# accumulator between AGPRs and VGPRs on each trip of the mainloop (and, in
+# the fused attention, every score back to VGPRs for the softmax).
+EXTRA_FLAGS = {"conv.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"], "conv_wgrad.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+               "attention.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
 
 
 def _run(cmd):
