@@ -24,6 +24,7 @@
 #include "omhip_internal.hpp"
 #include "buffer_io.hpp"
 #include "conv.hpp"
+#include "fastdiv.hpp"
 #include "../../include/omhip.h"
 
 #include <algorithm>
@@ -57,10 +58,19 @@ __host__ __device__ inline long long phaseOffset(int Cout, int Cin, int KH, int 
 
 // Phase (a, b) sub-kernel: wf[ci][co][jf][lf] = W[co][ci][ra + s*(KHa-1-jf)][rb + s*(KWb-1-lf)].
 // Every tap belongs to exactly one phase, so the sub-kernels tile a buffer of W's size.
-// One thread per weight (reads coalesced); all index arithmetic is 32-bit
+// Per tap (kh, kw) of W the host precomputes where it lands: wf index =
+// base + (ci*Cout + co) * span + inner. One thread per weight (reads
+// coalesced); the divisions by taps and Cin use launch-time magic numbers
 // (Cout*Cin*KH*KW < 2^28 by the conv limits).
-__global__ void phase_flip_kernel(const float* __restrict__ w, float* __restrict__ wf, int Cout, int Cin, int KH,
-                                  int KW, int s, int p) {
+constexpr int kMaxFlipTaps = 256;   // the table travels in the kernel arguments (3 KB)
+struct FlipTaps {
+    int base[kMaxFlipTaps];    // offset of the tap's phase sub-kernel
+    int span[kMaxFlipTaps];    // KHa * KWb of that phase
+    int inner[kMaxFlipTaps];   // jf * KWb + lf
+};
+// Kernels with more taps than the table holds: the same map computed per weight.
+__global__ void phase_flip_generic_kernel(const float* __restrict__ w, float* __restrict__ wf, int Cout, int Cin,
+                                          int KH, int KW, int s, int p) {
     const int taps = KH * KW;
     const int total = Cout * Cin * taps;
     for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < total; i += gridDim.x * blockDim.x) {
@@ -73,6 +83,17 @@ __global__ void phase_flip_kernel(const float* __restrict__ w, float* __restrict
         const int KHa = phaseTaps(KH, s, p, a), KWb = phaseTaps(KW, s, p, b);
         const int jf = KHa - 1 - kh / s, lf = KWb - 1 - kw / s;
         wf[phaseOffset(Cout, Cin, KH, KW, s, p, a, b) + ((ci * Cout + co) * KHa + jf) * KWb + lf] = w[i];
+    }
+}
+
+__global__ void phase_flip_kernel(const float* __restrict__ w, float* __restrict__ wf, int Cout, int Cin, int taps,
+                                  FastDiv dTaps, FastDiv dCin, FlipTaps ft) {
+    const int total = Cout * Cin * taps;
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < total; i += gridDim.x * blockDim.x) {
+        const int t = (int)dTaps.div((uint32_t)i);
+        const int tap = i - t * taps;
+        const int co = (int)dCin.div((uint32_t)t), ci = t - co * Cin;
+        wf[ft.base[tap] + (ci * Cout + co) * ft.span[tap] + ft.inner[tap]] = w[i];
     }
 }
 
@@ -136,41 +157,79 @@ __device__ __forceinline__ float partSum(const float* __restrict__ part, int c, 
 // (bit-identical to the reference's sum / count).  MODE 2: sum dy*xhat and
 // sum dy, xhat = (x - mean) * invStd, dy gated by mask > 0 when mask is given
 // (the reference's reluBackward folded in). part[(c*P + p)*2 + k].
-template <int MODE>
+//
+// The part's images n0..n1-1 are one sequence of (image, element) pairs —
+// elements in groups of V (V = 4: 16-byte loads, when HW % 4 == 0 and the
+// buffers are 16-byte aligned) — walked 256 groups per trip, so small planes
+// keep every lane busy. U trips are loaded before any is added, so U loads of
+// each lane are in flight at once; a lane adds its elements in sequence order
+// (a fixed order: the result does not depend on timing).
+template <int MODE, int V>
 __global__ __launch_bounds__(256) void chan_partial_kernel(const float* __restrict__ x, const float* __restrict__ dy,
                                                            const float* __restrict__ mask,
                                                            const float* __restrict__ mean,
                                                            const float* __restrict__ invStd,
                                                            const float* __restrict__ prev, float* __restrict__ part,
                                                            int N, int C, int HW, int P, float cnt) {
+    typedef float fv __attribute__((ext_vector_type(V)));
+    constexpr int U = 4;
     __shared__ float red[2 * 256];
     const int c = blockIdx.x, p = blockIdx.y;
     const int n0 = (int)((long long)p * N / P), n1 = (int)((long long)(p + 1) * N / P);
     const float m = MODE == 1 ? partSum(prev, c, P, 0) / cnt : (MODE == 2 ? mean[c] : 0.f);
     const float is = MODE == 2 ? invStd[c] : 0.f;
+    const int HWV = HW / V;   // groups per plane
     float v[2] = {0.f, 0.f};
-    // The part's images n0..n1-1 as one sequence of (image, pixel) pairs, 256
-    // consecutive pairs per trip, so small planes keep every lane busy.
-    const int dn = 256 / HW, ds = 256 % HW;
-    int n = n0 + (int)threadIdx.x / HW, s = (int)threadIdx.x % HW;
-    while (n < n1) {
-        const long long e = ((long long)n * C + c) * HW + s;
-        if constexpr (MODE == 0) {
-            v[0] += x[e];
-        } else if constexpr (MODE == 1) {
-            const float d = x[e] - m;
-            v[0] = __builtin_fmaf(d, d, v[0]);
-        } else {
-            const float g = (mask && !(mask[e] > 0.f)) ? 0.f : dy[e];
-            const float xh = (x[e] - m) * is;
-            v[0] = __builtin_fmaf(g, xh, v[0]);
-            v[1] += g;
+    const int dn = 256 / HWV, ds = 256 % HWV;
+    int n = n0 + (int)threadIdx.x / HWV, sg = (int)threadIdx.x % HWV;
+    auto advance = [&](int& nn, int& ss) {
+        nn += dn;
+        ss += ds;
+        if (ss >= HWV) {
+            ss -= HWV;
+            ++nn;
         }
-        n += dn;
-        s += ds;
-        if (s >= HW) {
-            s -= HW;
-            ++n;
+    };
+    while (n < n1) {
+        fv xv[U], gv[U], mv[U];
+        bool ok[U];
+        {
+            int nn = n, ss = sg;
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                ok[u] = nn < n1;
+                const long long e = ((long long)nn * C + c) * HW + (long long)ss * V;
+                if (ok[u]) {
+                    xv[u] = *reinterpret_cast<const fv*>(x + e);
+                    if constexpr (MODE == 2) {
+                        gv[u] = *reinterpret_cast<const fv*>(dy + e);
+                        if (mask) mv[u] = *reinterpret_cast<const fv*>(mask + e);
+                    }
+                }
+                advance(nn, ss);
+            }
+            n = nn;
+            sg = ss;
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            if (!ok[u]) continue;
+#pragma unroll
+            for (int k = 0; k < V; ++k) {
+                const float xe = V == 1 ? xv[u][0] : xv[u][k];
+                if constexpr (MODE == 0) {
+                    v[0] += xe;
+                } else if constexpr (MODE == 1) {
+                    const float d = xe - m;
+                    v[0] = __builtin_fmaf(d, d, v[0]);
+                } else {
+                    const float ge = V == 1 ? gv[u][0] : gv[u][k];
+                    const float g = (mask && !((V == 1 ? mv[u][0] : mv[u][k]) > 0.f)) ? 0.f : ge;
+                    const float xh = (xe - m) * is;
+                    v[0] = __builtin_fmaf(g, xh, v[0]);
+                    v[1] += g;
+                }
+            }
         }
     }
     blockSum<2>(v, red);
@@ -192,153 +251,161 @@ __global__ void chan_finish_kernel(const float* __restrict__ part, float* out0, 
     if (out1) out1[c] = accumulate ? out1[c] + b / divisor : b / divisor;
 }
 
-// BatchNorm training forward, second half (cpu_backend.ixx:796-840): batch
+// BatchNorm training forward, statistics (cpu_backend.ixx:796-822): batch
 // mean = sum(x)/cnt and biased variance = sum((x-mean)^2)/cnt from the two
-// passes' parts, invStd = 1/sqrt(var+eps), then
-//   y = act(gamma*((x-mean)*invStd) + beta [+ res])
-// (the reference's batchNorm2d, add and relu, each rounded as there). The
-// n = 0 plane of each channel also writes the saved statistics and the
-// running averages fma(1-m, run, m*batch).
-__global__ void bn_train_apply_kernel(const float* __restrict__ x, float* __restrict__ y,
-                                      const float* __restrict__ gamma, const float* __restrict__ beta,
-                                      const float* __restrict__ part0, const float* __restrict__ part1, int P,
-                                      float cnt, float eps, float momentum, const float* __restrict__ res, int act,
-                                      float* savedMean, float* savedInvStd, float* runMean, float* runVar, int C,
-                                      int HW, int plane0, int G, int planes) {
+// passes' parts (summed in part order), invStd = 1/sqrt(var+eps); stat[c] =
+// (mean, invStd); also the saved statistics and the running averages
+// fma(1-m, run, m*batch). One wave per channel: its lanes load the parts
+// together (partSum), lane 0 writes.
+__global__ __launch_bounds__(256) void bn_stats_kernel(const float* __restrict__ part0, const float* __restrict__ part1,
+                                                       int P, float cnt, float eps, float momentum, float* savedMean,
+                                                       float* savedInvStd, float* runMean, float* runVar,
+                                                       float* __restrict__ stat, int C) {
 #pragma clang fp contract(off)
-    // G == 1: workgroup (bx, y) covers plane plane0 + y (channel uniform across
-    // the workgroup). G > 1: planes of HW <= 128 pixels, G of them per workgroup,
-    // thread t on pixel t % HW of plane t / HW.
-    int plane, i0, di;
-    if (G == 1) {
-        plane = plane0 + blockIdx.y;
-        i0 = blockIdx.x * blockDim.x + threadIdx.x;
-        di = gridDim.x * blockDim.x;
-    } else {
-        plane = plane0 + blockIdx.y * G + (int)threadIdx.x / HW;
-        i0 = (int)threadIdx.x % HW;
-        di = HW;
-        if ((int)threadIdx.x >= G * HW || plane >= planes) return;
-    }
-    const int c = plane % C;
-    const long long base = (long long)plane * HW;
-    // the first (up to) four elements are loaded before the statistics so the
-    // two memory latencies overlap (planes of up to 1024 pixels need no more)
-    constexpr int PRE = 4;
-    float xv[PRE], rv[PRE];
-#pragma unroll
-    for (int k = 0; k < PRE; ++k) {
-        const int i = i0 + k * di;
-        xv[k] = i < HW ? x[base + i] : 0.f;
-        rv[k] = (res && i < HW) ? res[base + i] : 0.f;
-    }
-    const float sum0 = G == 1 ? partSum(part0, c, P, 0) : partSumSerial(part0, c, P, 0);
-    const float sum1 = G == 1 ? partSum(part1, c, P, 0) : partSumSerial(part1, c, P, 0);
-    const float mu = sum0 / cnt;
-    const float var = sum1 / cnt;
+    const int c = blockIdx.x * 4 + (threadIdx.x >> 6);   // wave-uniform
+    if (c >= C) return;
+    const float mu = partSum(part0, c, P, 0) / cnt;
+    const float var = partSum(part1, c, P, 0) / cnt;
+    if ((threadIdx.x & 63) != 0) return;
     const float inv = 1.0f / sqrtf(var + eps);
-    if (plane < C && (G == 1 ? blockIdx.x == 0 && threadIdx.x == 0 : i0 == 0)) {
-        if (savedMean) savedMean[c] = mu;
-        if (savedInvStd) savedInvStd[c] = inv;
-        runMean[c] = __builtin_fmaf(1.0f - momentum, runMean[c], momentum * mu);
-        runVar[c] = __builtin_fmaf(1.0f - momentum, runVar[c], momentum * var);
+    stat[2 * c] = mu;
+    stat[2 * c + 1] = inv;
+    if (savedMean) savedMean[c] = mu;
+    if (savedInvStd) savedInvStd[c] = inv;
+    runMean[c] = __builtin_fmaf(1.0f - momentum, runMean[c], momentum * mu);
+    runVar[c] = __builtin_fmaf(1.0f - momentum, runVar[c], momentum * var);
+}
+
+// BatchNorm backward, statistics: stat[c] = (sum(dy*xhat), sum(dy)) from the
+// parts in part order; also gradGamma and gradBeta. One wave per channel.
+__global__ __launch_bounds__(256) void bn_bwd_stats_kernel(const float* __restrict__ part, int P, float* gradGamma,
+                                                           float* gradBeta, float* __restrict__ stat, int C) {
+    const int c = blockIdx.x * 4 + (threadIdx.x >> 6);   // wave-uniform
+    if (c >= C) return;
+    const float sg = partSum(part, c, P, 0), sb = partSum(part, c, P, 1);
+    if ((threadIdx.x & 63) != 0) return;
+    stat[2 * c] = sg;
+    stat[2 * c + 1] = sb;
+    if (gradGamma) gradGamma[c] = sg;
+    if (gradBeta) gradBeta[c] = sb;
+}
+
+// Element-wise BatchNorm passes over planes plane0 .. of an [N*C][HW] tensor
+// (x etc. point at plane plane0; fewer than 2^30 elements per launch), V
+// elements per thread and trip (V = 4: 16-byte accesses when HW % 4 == 0 and
+// every buffer is 16-byte aligned). Element e's channel is
+// (c0 + e / HW) mod C, both divisions by launch-time magic numbers.
+struct BnFlat {
+    long long total;   // elements in this launch
+    FastDiv dHW, dC;
+    int C, c0;         // channel of the launch's first plane
+    __device__ __forceinline__ int channel(uint32_t e) const {
+        const uint32_t pl = dHW.div(e) + (uint32_t)c0;
+        return (int)(pl - dC.div(pl) * (uint32_t)C);
     }
-    const float g = gamma[c], b = beta[c];
+};
+
+// y = act(gamma*((x-mean)*invStd) + beta [+ res]) (the reference's
+// batchNorm2d, add and relu, each rounded as there).
+template <int V>
+__global__ __launch_bounds__(256) void bn_train_apply_kernel(const float* __restrict__ x, float* __restrict__ y,
+                                                             const float* __restrict__ gamma,
+                                                             const float* __restrict__ beta,
+                                                             const float* __restrict__ stat,
+                                                             const float* __restrict__ res, int act, BnFlat f) {
+#pragma clang fp contract(off)
+    typedef float fv __attribute__((ext_vector_type(V)));
+    const long long groups = f.total / V;
+    for (long long i = blockIdx.x * 256LL + threadIdx.x; i < groups; i += (long long)gridDim.x * 256) {
+        const uint32_t e = (uint32_t)(i * V);
+        const int c = f.channel(e);
+        const fv xv = *reinterpret_cast<const fv*>(x + e);
+        fv rv{};
+        if (res) rv = *reinterpret_cast<const fv*>(res + e);
+        const float mu = stat[2 * c], inv = stat[2 * c + 1], g = gamma[c], b = beta[c];
+        fv out;
 #pragma unroll
-    for (int k = 0; k < PRE; ++k) {
-        const int i = i0 + k * di;
-        if (i < HW) {
+        for (int k = 0; k < V; ++k) {
             float v = __builtin_fmaf(g, (xv[k] - mu) * inv, b);
             if (res) v = v + rv[k];
             if (act == 1) v = v > 0.f ? v : 0.f;
-            y[base + i] = v;
+            out[k] = v;
         }
-    }
-    for (int i = i0 + PRE * di; i < HW; i += di) {
-        float v = __builtin_fmaf(g, (x[base + i] - mu) * inv, b);
-        if (res) v = v + res[base + i];
-        if (act == 1) v = v > 0.f ? v : 0.f;
-        y[base + i] = v;
+        *reinterpret_cast<fv*>(y + e) = out;
     }
 }
 
 // dx = gamma*invStd*(1/cnt) * (cnt*dy - sum(dy) - xhat*sum(dy*xhat)) (cpu_backend.ixx:883-886),
 // with the multiply-adds fused as the reference compiled by clang fuses them;
-// dy gated by mask > 0 when mask is given. The sums come from the parts; the
-// n = 0 plane of each channel writes gradGamma = sum(dy*xhat), gradBeta = sum(dy).
-__global__ void bn_backward_apply_kernel(const float* __restrict__ dy, const float* __restrict__ mask,
-                                         const float* __restrict__ x, const float* __restrict__ mean,
-                                         const float* __restrict__ invStd, const float* __restrict__ gamma,
-                                         const float* __restrict__ part, int P, float* gradGamma, float* gradBeta,
-                                         float* __restrict__ dx, int C, int HW, float cnt, float invCnt, int plane0,
-                                         int G, int planes) {
-    // plane / pixel assignment as bn_train_apply_kernel
-    int plane, i0, di;
-    if (G == 1) {
-        plane = plane0 + blockIdx.y;
-        i0 = blockIdx.x * blockDim.x + threadIdx.x;
-        di = gridDim.x * blockDim.x;
-    } else {
-        plane = plane0 + blockIdx.y * G + (int)threadIdx.x / HW;
-        i0 = (int)threadIdx.x % HW;
-        di = HW;
-        if ((int)threadIdx.x >= G * HW || plane >= planes) return;
-    }
-    const int c = plane % C;
-    const long long base = (long long)plane * HW;
-    // first elements loaded before the statistics, as in bn_train_apply_kernel
-    constexpr int PRE = 4;
-    float dv[PRE], xv[PRE];
+// dy gated by mask > 0 when mask is given.
+template <int V>
+__global__ __launch_bounds__(256) void bn_backward_apply_kernel(const float* __restrict__ dy,
+                                                                const float* __restrict__ mask,
+                                                                const float* __restrict__ x,
+                                                                const float* __restrict__ mean,
+                                                                const float* __restrict__ invStd,
+                                                                const float* __restrict__ gamma,
+                                                                const float* __restrict__ stat, float* __restrict__ dx,
+                                                                float cnt, float invCnt, BnFlat f) {
+    typedef float fv __attribute__((ext_vector_type(V)));
+    const long long groups = f.total / V;
+    for (long long i = blockIdx.x * 256LL + threadIdx.x; i < groups; i += (long long)gridDim.x * 256) {
+        const uint32_t e = (uint32_t)(i * V);
+        const int c = f.channel(e);
+        const fv dv = *reinterpret_cast<const fv*>(dy + e);
+        const fv xv = *reinterpret_cast<const fv*>(x + e);
+        fv mv{};
+        if (mask) mv = *reinterpret_cast<const fv*>(mask + e);
+        const float m = mean[c], is = invStd[c], sg = stat[2 * c], sb = stat[2 * c + 1];
+        const float k = gamma[c] * is * invCnt;
+        fv out;
 #pragma unroll
-    for (int k = 0; k < PRE; ++k) {
-        const int i = i0 + k * di;
-        dv[k] = (i < HW && !(mask && !(mask[base + i] > 0.f))) ? dy[base + i] : 0.f;
-        xv[k] = i < HW ? x[base + i] : 0.f;
-    }
-    const float m = mean[c], is = invStd[c], g = gamma[c];
-    const float sg = G == 1 ? partSum(part, c, P, 0) : partSumSerial(part, c, P, 0);
-    const float sb = G == 1 ? partSum(part, c, P, 1) : partSumSerial(part, c, P, 1);
-    if (plane < C && (G == 1 ? blockIdx.x == 0 && threadIdx.x == 0 : i0 == 0)) {
-        if (gradGamma) gradGamma[c] = sg;
-        if (gradBeta) gradBeta[c] = sb;
-    }
-    const float k = g * is * invCnt;
-#pragma unroll
-    for (int j = 0; j < PRE; ++j) {
-        const int i = i0 + j * di;
-        if (i < HW) {
+        for (int j = 0; j < V; ++j) {
+            const float d = (mask && !(mv[j] > 0.f)) ? 0.f : dv[j];
             const float xh = (xv[j] - m) * is;
-            dx[base + i] = k * __builtin_fmaf(-xh, sg, __builtin_fmaf(cnt, dv[j], -sb));
+            out[j] = k * __builtin_fmaf(-xh, sg, __builtin_fmaf(cnt, d, -sb));
         }
-    }
-    for (int i = i0 + PRE * di; i < HW; i += di) {
-        const float d = (mask && !(mask[base + i] > 0.f)) ? 0.f : dy[base + i];
-        const float xh = (x[base + i] - m) * is;
-        dx[base + i] = k * __builtin_fmaf(-xh, sg, __builtin_fmaf(cnt, d, -sb));
+        *reinterpret_cast<fv*>(dx + e) = out;
     }
 }
 
-// Launches a per-plane kernel over N*C planes: one workgroup row per plane
-// (grid.y <= 65535 per launch), or, for planes of at most 128 pixels, G =
-// 256 / HW planes per workgroup. launch(grid, firstPlane, G).
+// Runs an element-wise BatchNorm pass over the N*C planes of HW elements in
+// launches of whole planes with fewer than 2^30 elements each. launch(grid,
+// vec4, elementOffset, BnFlat).
 template <class F>
-static int forPlanes(int planes, int HW, F launch) {
-    const int G = HW <= 128 ? 256 / HW : 1;
-    if (G > 1) {
-        const long long groups = ((long long)planes + G - 1) / G;
-        for (long long g0 = 0; g0 < groups; g0 += 65535) {
-            const int cnt = (int)std::min<long long>(65535, groups - g0);
-            launch(dim3(1, cnt), (int)(g0 * G), G);
-            OMHIP_CHECK_LAUNCH();
-        }
-        return 0;
-    }
-    const int bx = std::max(1, std::min((HW + 255) / 256, std::max(1, 4096 / std::max(1, planes))));
-    for (int p0 = 0; p0 < planes; p0 += 65535) {
-        const int cnt = std::min(65535, planes - p0);
-        launch(dim3(bx, cnt), p0, 1);
+static int forElements(int planes, int HW, int C, bool vec4, F launch) {
+    const long long perLaunch = std::max<long long>(1, ((1LL << 30) - 1) / HW);
+    for (long long p0 = 0; p0 < planes; p0 += perLaunch) {
+        const long long np = std::min<long long>(perLaunch, planes - p0);
+        BnFlat f{};
+        f.total = np * HW;
+        f.dHW = FastDiv::make((uint32_t)HW);
+        f.dC = FastDiv::make((uint32_t)C);
+        f.C = C;
+        f.c0 = (int)(p0 % C);
+        const long long groups = f.total / (vec4 ? 4 : 1);
+        const int grid = (int)std::max<long long>(1, std::min<long long>((groups + 255) / 256, (long long)cuCount() * 32));
+        launch(dim3(grid), vec4, p0 * HW, f);
         OMHIP_CHECK_LAUNCH();
     }
+    return 0;
+}
+
+static bool aligned16(const void* q) { return (reinterpret_cast<uintptr_t>(q) & 15u) == 0; }
+
+// Per-channel sums into out0/out1 (divided by divisor): MODE as chan_partial_kernel.
+// Partial sums of every channel over P parts (MODE as chan_partial_kernel).
+template <int MODE>
+static int launchPartial(const float* x, const float* dy, const float* mask, const float* mean, const float* invStd,
+                         const float* prev, float* part, int N, int C, int HW, int P, float cnt) {
+    const bool vec = HW % 4 == 0 && aligned16(x) && (MODE != 2 || (aligned16(dy) && (!mask || aligned16(mask))));
+    if (vec)
+        hipLaunchKernelGGL((chan_partial_kernel<MODE, 4>), dim3(C, P), dim3(256), 0, stream(), x, dy, mask, mean, invStd,
+                           prev, part, N, C, HW, P, cnt);
+    else
+        hipLaunchKernelGGL((chan_partial_kernel<MODE, 1>), dim3(C, P), dim3(256), 0, stream(), x, dy, mask, mean, invStd,
+                           prev, part, N, C, HW, P, cnt);
+    OMHIP_CHECK_LAUNCH();
     return 0;
 }
 
@@ -349,9 +416,7 @@ static int channelSums(const float* x, const float* dy, const float* mean, const
     const int P = channelParts(N, C);
     float* part = static_cast<float*>(workspace((size_t)C * P * 2 * sizeof(float)));
     if (!part) return -1;   // workspace() recorded the cause
-    hipLaunchKernelGGL(chan_partial_kernel<MODE>, dim3(C, P), dim3(256), 0, stream(), x, dy, nullptr, mean, invStd,
-                       nullptr, part, N, C, HW, P, 1.0f);
-    OMHIP_CHECK_LAUNCH();
+    if (launchPartial<MODE>(x, dy, nullptr, mean, invStd, nullptr, part, N, C, HW, P, 1.0f)) return -1;
     hipLaunchKernelGGL(chan_finish_kernel, dim3((C + 255) / 256), dim3(256), 0, stream(), part, out0, out1, C, P,
                        divisor, accumulate ? 1 : 0);
     OMHIP_CHECK_LAUNCH();
@@ -364,20 +429,25 @@ int batchNorm2dTrainAct(const float* x, float* y, const float* gamma, const floa
     const int HW = H * W;
     const float cnt = (float)((long long)N * HW);
     const int P = channelParts(N, C);
-    float* part = static_cast<float*>(workspace((size_t)C * P * 4 * sizeof(float)));
+    float* part = static_cast<float*>(workspace((size_t)C * P * 4 * sizeof(float) + (size_t)C * 2 * sizeof(float)));
     if (!part) return -1;
     float* part0 = part;
     float* part1 = part + (size_t)C * P * 2;
+    float* stat = part + (size_t)C * P * 4;
     // two passes, as the reference: sum(x), then sum((x-mean)^2) with the first pass's mean
-    hipLaunchKernelGGL(chan_partial_kernel<0>, dim3(C, P), dim3(256), 0, stream(), x, nullptr, nullptr, nullptr,
-                       nullptr, nullptr, part0, N, C, HW, P, cnt);
+    if (launchPartial<0>(x, nullptr, nullptr, nullptr, nullptr, nullptr, part0, N, C, HW, P, cnt)) return -1;
+    if (launchPartial<1>(x, nullptr, nullptr, nullptr, nullptr, part0, part1, N, C, HW, P, cnt)) return -1;
+    hipLaunchKernelGGL(bn_stats_kernel, dim3((C + 3) / 4), dim3(256), 0, stream(), part0, part1, P, cnt, eps,
+                       momentum, savedMean, savedInvStd, runMean, runVar, stat, C);
     OMHIP_CHECK_LAUNCH();
-    hipLaunchKernelGGL(chan_partial_kernel<1>, dim3(C, P), dim3(256), 0, stream(), x, nullptr, nullptr, nullptr,
-                       nullptr, part0, part1, N, C, HW, P, cnt);
-    OMHIP_CHECK_LAUNCH();
-    return forPlanes(N * C, HW, [&](dim3 g, int p0, int G) {
-        hipLaunchKernelGGL(bn_train_apply_kernel, g, dim3(256), 0, stream(), x, y, gamma, beta, part0, part1, P, cnt,
-                           eps, momentum, res, act, savedMean, savedInvStd, runMean, runVar, C, HW, p0, G, N * C);
+    const bool vec = HW % 4 == 0 && aligned16(x) && aligned16(y) && (!res || aligned16(res));
+    return forElements(N * C, HW, C, vec, [&](dim3 g, bool v4, long long off, const BnFlat& f) {
+        if (v4)
+            hipLaunchKernelGGL(bn_train_apply_kernel<4>, g, dim3(256), 0, stream(), x + off, y + off, gamma, beta, stat,
+                               res ? res + off : nullptr, act, f);
+        else
+            hipLaunchKernelGGL(bn_train_apply_kernel<1>, g, dim3(256), 0, stream(), x + off, y + off, gamma, beta, stat,
+                               res ? res + off : nullptr, act, f);
     });
 }
 
@@ -395,17 +465,24 @@ static int batchNorm2dBackwardMasked(const char* name, const float* gO, const fl
     if (!gO || !x || !mean || !invStd || !gamma || !gI) return fail("%s: null pointer", name);
     const int HW = H * W;
     const int P = channelParts(N, C);
-    float* part = static_cast<float*>(workspace((size_t)C * P * 2 * sizeof(float)));
+    float* part = static_cast<float*>(workspace((size_t)C * P * 2 * sizeof(float) + (size_t)C * 2 * sizeof(float)));
     if (!part) return -1;
-    hipLaunchKernelGGL(chan_partial_kernel<2>, dim3(C, P), dim3(256), 0, stream(), x, gO, mask, mean, invStd, nullptr,
-                       part, N, C, HW, P, 1.0f);
+    float* stat = part + (size_t)C * P * 2;
+    if (launchPartial<2>(x, gO, mask, mean, invStd, nullptr, part, N, C, HW, P, 1.0f)) return -1;
+    hipLaunchKernelGGL(bn_bwd_stats_kernel, dim3((C + 3) / 4), dim3(256), 0, stream(), part, P, gGamma, gBeta, stat,
+                       C);
     OMHIP_CHECK_LAUNCH();
     const long long cntL = (long long)N * HW;
     const float fcnt = (float)cntL;
     const float invCnt = 1.0f / fcnt;
-    return forPlanes(N * C, HW, [&](dim3 g, int p0, int G) {
-        hipLaunchKernelGGL(bn_backward_apply_kernel, g, dim3(256), 0, stream(), gO, mask, x, mean, invStd, gamma, part,
-                           P, gGamma, gBeta, gI, C, HW, fcnt, invCnt, p0, G, N * C);
+    const bool vec = HW % 4 == 0 && aligned16(gO) && aligned16(x) && aligned16(gI) && (!mask || aligned16(mask));
+    return forElements(N * C, HW, C, vec, [&](dim3 g, bool v4, long long off, const BnFlat& f) {
+        if (v4)
+            hipLaunchKernelGGL(bn_backward_apply_kernel<4>, g, dim3(256), 0, stream(), gO + off,
+                               mask ? mask + off : nullptr, x + off, mean, invStd, gamma, stat, gI + off, fcnt, invCnt, f);
+        else
+            hipLaunchKernelGGL(bn_backward_apply_kernel<1>, g, dim3(256), 0, stream(), gO + off,
+                               mask ? mask + off : nullptr, x + off, mean, invStd, gamma, stat, gI + off, fcnt, invCnt, f);
     });
 }
 
@@ -448,8 +525,25 @@ int omHipConv2dBackwardInput(const float* pGradOutput, const float* pWeight, flo
     }
     float* wf = static_cast<float*>(workspace((size_t)wsz * sizeof(float), kWsOperand));
     if (!wf) return -1;   // workspace() recorded the cause
-    hipLaunchKernelGGL(phase_flip_kernel, dim3(gridFor(wsz)), dim3(256), 0, stream(), pWeight, wf, nCout, nCin, nKH,
-                       nKW, s, p);
+    if (nKH * nKW > kMaxFlipTaps) {
+        hipLaunchKernelGGL(phase_flip_generic_kernel, dim3(gridFor(wsz)), dim3(256), 0, stream(), pWeight, wf, nCout,
+                           nCin, nKH, nKW, s, p);
+    } else {
+        FlipTaps ft{};
+        for (int kh = 0; kh < nKH; ++kh)
+            for (int kw = 0; kw < nKW; ++kw) {
+                const int a = ((kh % s) - (p % s) + s) % s;
+                const int b = ((kw % s) - (p % s) + s) % s;
+                const int KHa = phaseTaps(nKH, s, p, a), KWb = phaseTaps(nKW, s, p, b);
+                const int jf = KHa - 1 - kh / s, lf = KWb - 1 - kw / s;
+                const int tap = kh * nKW + kw;
+                ft.base[tap] = (int)phaseOffset(nCout, nCin, nKH, nKW, s, p, a, b);
+                ft.span[tap] = KHa * KWb;
+                ft.inner[tap] = jf * KWb + lf;
+            }
+        hipLaunchKernelGGL(phase_flip_kernel, dim3(gridFor(wsz)), dim3(256), 0, stream(), pWeight, wf, nCout, nCin,
+                           nKH * nKW, FastDiv::make((uint32_t)(nKH * nKW)), FastDiv::make((uint32_t)nCin), ft);
+    }
     int rc = hipGetLastError() == hipSuccess ? 0 : fail("%s: flip launch failed", name);
     for (int a = 0; a < std::min(s, nH) && !rc; ++a) {
         const int KHa = phaseTaps(nKH, s, p, a);
