@@ -329,24 +329,29 @@ struct GemmPlan {
 };
 
 // Tile and split-K choice: the largest tile that gives every CU a workgroup.
-// When even 64x64 tiles leave CUs idle and K is long (few rows or columns:
-// 128 x 4096 x 4096, weight gradients), K is split: the smallest power of two
-// (at most 64) that gives every CU a workgroup while each split keeps >= 256
-// of K, over the 128x128 tile (64x64 when M or N is below 128). The partials
-// cost one fp32 write and read of C per split. Measured on MI355X:
-// 128 x 4096 x 4096 runs at 72 TFLOP/s split 8 ways against 34 unsplit;
-// K = 512 problems run faster unsplit.
+// When even 64x64 tiles give fewer than two workgroups per CU and K is long
+// (few rows or columns: 128 x 4096 x 4096, weight gradients), K is split over
+// the 64x64 tile: the smallest power of two (at most 64) that gives every CU
+// two workgroups while each split keeps >= 256 of K. The partials cost one
+// fp32 write and read of C per split. Measured on MI355X (TFLOP/s, against
+// splitting the 128x128 tile until every CU had one workgroup): 128 x 4096 x
+// 4096 86 (76), 64 x 4096 x 4096 69 (56), 128 x 1024 x 4096 47 (29),
+// 512 x 1024 x 2048 72 (56), 256 x 4096 x 4096 96 (75); K < 1024 runs
+// faster unsplit. The partials of a plan stay below 4 x CUs tiles of 64 x 64
+// floats (16 MiB on 256 CUs).
 static GemmPlan planGemm(int M, int N, int K, int batch, bool wsOk) {
     const long long cus = cuCount();
     auto tiles = [&](int bm, int bn) { return (long long)((M + bm - 1) / bm) * ((N + bn - 1) / bn) * batch; };
     if (tiles(256, 256) >= cus) return {0, 1};
     if (tiles(128, 128) >= cus) return {1, 1};
-    if (tiles(64, 64) >= cus || !wsOk || K < 1024) return {2, 1};
-    const int cfg = (M >= 128 && N >= 128) ? 1 : 2;
-    const long long t = cfg == 1 ? tiles(128, 128) : tiles(64, 64);
+    const long long t = tiles(64, 64);
+    if (t >= 2 * cus || !wsOk || K < 1024) return {2, 1};
+    // with one tile per CU already, a split must keep >= 1024 of K (1024^3
+    // ran 79 TFLOP/s unsplit, 70 split in two)
+    const int minK = t >= cus ? 1024 : 256;
     int s = 1;
-    while (s < 64 && t * s < cus && K / (2 * s) >= 256) s *= 2;
-    return {cfg, s};
+    while (s < 64 && t * s < 2 * cus && K / (2 * s) >= minK) s *= 2;
+    return {2, s};
 }
 
 template <bool TA, bool TB>
@@ -453,11 +458,12 @@ int gemmF32Checked(const char* name, bool ta, bool tb, int batch, int M, int N, 
 
 // ---- fixed scratch of the no-allocation entry ---------------------------------
 // Split-K partial sums of omHipGemmStridedBatchedNoAlloc live in this array,
-// so that entry never allocates. A plan splits K only while the grid holds
-// fewer workgroups than CUs, and stops doubling the split count once it has
-// reached them, so its partials cover fewer than 2 x CUs tiles of at most
-// 128 x 128 floats: 32 MiB on a 256-CU device. Each device the library runs
-// on holds its own copy until the process ends.
+// so that entry never allocates. A plan splits K only over 64 x 64 tiles and
+// only while the grid holds fewer than 2 x CUs workgroups, and stops doubling
+// the split count once it has reached them, so its partials cover fewer than
+// 4 x CUs tiles of 64 x 64 floats: 16 MiB on a 256-CU device (the array holds
+// twice that). Each device the library runs on holds its own copy until the
+// process ends.
 constexpr size_t kNoAllocScratchBytes = (size_t)32 << 20;
 constexpr int kMaxDevices = 64;
 static __device__ __align__(256) float scratch[kNoAllocScratchBytes / sizeof(float)];
