@@ -142,6 +142,74 @@ __global__ void __launch_bounds__(1024) softmax_ce_fused_kernel(const float* log
     if (loss) finishLoss(acc, loss, rows, lds);
 }
 
+// The same fused pass for rows of at most 64 * CPL classes with the row in
+// registers: a wave loads RB rows at once (logits and targets, lane l holding
+// classes l, l+64, ...), then each row runs the same operations in the same
+// order as softmaxRow / rowLoss / the gradient above — only the values stay in
+// registers instead of being written and read back — so every output is
+// bit-identical to the three kernels'.
+template <int CPL>
+__global__ void __launch_bounds__(1024) softmax_ce_fused_reg_kernel(const float* logits, const float* tgt, float* prob,
+                                                                    float* loss, float* grad, int rows, int cols,
+                                                                    float scale) {
+    __shared__ float lds[kLossWaves];
+    constexpr int RB = 8;   // rows of a wave whose loads are in flight together
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    float acc = 0.f;
+    for (long long r0 = wave; r0 < rows; r0 += (long long)kLossWaves * RB) {
+        float x[RB][CPL], t[RB][CPL];
+#pragma unroll
+        for (int i = 0; i < RB; ++i) {
+            const long long r = r0 + (long long)i * kLossWaves;
+#pragma unroll
+            for (int c = 0; c < CPL; ++c) {
+                const int j = lane + 64 * c;
+                const bool ok = r < rows && j < cols;
+                x[i][c] = ok ? logits[r * cols + j] : 0.f;
+                t[i][c] = ok ? tgt[r * cols + j] : 0.f;
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < RB; ++i) {
+            const long long r = r0 + (long long)i * kLossWaves;
+            if (r >= rows) break;   // wave-uniform
+            // rowMax: the first element when it is NaN, else the largest non-NaN element
+            float m = -INFINITY;
+#pragma unroll
+            for (int c = 0; c < CPL; ++c)
+                if (lane + 64 * c < cols) m = gtMax(m, x[i][c]);
+            m = waveMax(m);
+            const float e0 = __shfl(x[i][0], 0, 64);
+            m = e0 != e0 ? e0 : gtMax(e0, m);
+            float sum = 0.f;
+#pragma unroll
+            for (int c = 0; c < CPL; ++c)
+                if (lane + 64 * c < cols) {
+                    const float e = expf(x[i][c] - m);
+                    x[i][c] = e;
+                    sum += e;
+                }
+            sum = waveSum(sum);
+            float la = 0.f;
+#pragma unroll
+            for (int c = 0; c < CPL; ++c) {
+                const int j = lane + 64 * c;
+                if (j >= cols) continue;
+                const float pv = x[i][c] / sum;
+                if (prob) prob[r * cols + j] = pv;
+                if (loss && t[i][c] > 0.5f) {
+                    float q = pv;
+                    if (q < 1e-7f) q = 1e-7f;
+                    la -= logf(q);
+                }
+                if (grad) grad[r * cols + j] = (pv - t[i][c]) * scale;
+            }
+            if (loss) acc += waveSum(la);
+        }
+    }
+    if (loss) finishLoss(acc, loss, rows, lds);
+}
+
 // Bias gradient, nHW == 1 (a Linear layer's [rows, cols] gradient): a thread per
 // column adds the rows in order, starting from 0 — the reference's loop order
 // (autograd.ixx:428-433), so the result is bit-identical to it.
@@ -151,12 +219,12 @@ __global__ void bias_grad_cols_kernel(const float* g, float* gb, int rows, int c
     const float* p = g + c;
     float acc = 0.f;
     int r = 0;
-    for (; r + 32 <= rows; r += 32) {   // 32 loads in flight, then the adds in row order
-        float a[32];
+    for (; r + 64 <= rows; r += 64) {   // 64 loads in flight, then the adds in row order
+        float a[64];
 #pragma unroll
-        for (int i = 0; i < 32; ++i) a[i] = p[(long long)(r + i) * cols];
+        for (int i = 0; i < 64; ++i) a[i] = p[(long long)(r + i) * cols];
 #pragma unroll
-        for (int i = 0; i < 32; ++i) acc += a[i];
+        for (int i = 0; i < 64; ++i) acc += a[i];
     }
     for (; r < rows; ++r) acc += p[(long long)r * cols];
     gb[c] = acc;
@@ -254,13 +322,20 @@ int omHipSoftmaxCrossEntropy(const float* pLogits, const float* pTarget, float* 
     if (!pSoftmax && !pGradLogits && (long long)kLossWaves * nClasses > (1LL << 20))
         return fail("omHipSoftmaxCrossEntropy: %d classes need the softmax or gradient output", nClasses);
     float* rowBuf = nullptr;
-    if (!pSoftmax && !pGradLogits) {
+    if (!pSoftmax && !pGradLogits && nClasses > 256) {
         rowBuf = static_cast<float*>(workspace((size_t)kLossWaves * nClasses * sizeof(float)));
         if (!rowBuf) return -1;
     }
     const float scale = 1.0f / static_cast<float>(nBatch);
-    hipLaunchKernelGGL(softmax_ce_fused_kernel, dim3(1), dim3(64 * kLossWaves), 0, stream(), pLogits, pTarget,
-                       pSoftmax, pLoss, pGradLogits, rowBuf, nBatch, nClasses, scale);
+    if (nClasses <= 64)
+        hipLaunchKernelGGL(softmax_ce_fused_reg_kernel<1>, dim3(1), dim3(64 * kLossWaves), 0, stream(), pLogits,
+                           pTarget, pSoftmax, pLoss, pGradLogits, nBatch, nClasses, scale);
+    else if (nClasses <= 256)
+        hipLaunchKernelGGL(softmax_ce_fused_reg_kernel<4>, dim3(1), dim3(64 * kLossWaves), 0, stream(), pLogits,
+                           pTarget, pSoftmax, pLoss, pGradLogits, nBatch, nClasses, scale);
+    else
+        hipLaunchKernelGGL(softmax_ce_fused_kernel, dim3(1), dim3(64 * kLossWaves), 0, stream(), pLogits, pTarget,
+                           pSoftmax, pLoss, pGradLogits, rowBuf, nBatch, nClasses, scale);
     OMHIP_CHECK_LAUNCH();
     return 0;
 }

@@ -85,7 +85,7 @@ def test_cross_entropy_and_gradient(hip, rows, cols):
     assert np.array_equal(_bits(dg.numpy()), _bits(O.cross_entropy_softmax_backward(p, t)))
 
 
-@pytest.mark.parametrize("rows,cols", [(128, 10), (200, 1000), (16, 7)])
+@pytest.mark.parametrize("rows,cols", [(128, 10), (200, 1000), (16, 7), (300, 200), (129, 64), (1, 65)])
 def test_fused_softmax_cross_entropy(hip, rows, cols):
     """omHipSoftmaxCrossEntropy = softmax -> crossEntropy -> crossEntropySoftmaxBackward, bit for
     bit, with every combination of outputs requested."""
