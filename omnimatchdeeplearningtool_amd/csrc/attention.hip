@@ -33,6 +33,10 @@
 // The key order inside a P.V step (keys 32ks + 4g4 + r and 32ks + 16 + 4g4 +
 // r) is the order of the score tiles the lane holds; the sum over keys is
 // order-free, so only rounding order differs from the reference chain.
+// Latency hiding inside a wave: the first block's Q fragments load under the
+// K / V copy and each later block's during the previous block's math; the
+// transposing V^T reads of P.V step ks + 1 are in flight during step ks's
+// MFMAs.
 #include "omhip_internal.hpp"
 #include "../../include/omhip.h"
 
@@ -218,33 +222,48 @@ __device__ __forceinline__ void attnBlock(const uint16_t* sK, uint32_t sVa, cons
     f32x4a rs = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int dt = 0; dt < 4; ++dt) o[dt] = f32x4a{0.f, 0.f, 0.f, 0.f};
+    // V^T fragments of step ks: rows 32ks + 4g4 + j (first read) and + 16
+    // (second read; a missing tile re-reads the first rows, whose weights are
+    // zero), into buffer ks & 1. Step ks + 1's reads are issued before step
+    // ks's MFMAs; LDS reads return in order, so "at most 8 outstanding" means
+    // step ks's 8 have landed. The reads are inline assembly and waited for
+    // here: through the builtin the compiler would also wait for any LDS DMA
+    // in flight, i.e. for every global load still outstanding.
+    u32x2a lo[2][4], up[2][4];
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt) {
+        const uint32_t a = sVa + 2u * L.vOff[dt];
+        asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(lo[0][dt]) : "v"(a), "i"(0));
+        asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(up[0][dt]) : "v"(a), "i"(NT > 1 ? 16 * kD * 2 : 0));
+    }
 #pragma unroll
     for (int ks = 0; ks < NKS; ++ks) {
+        const int cur = ks & 1;
+        if (ks + 1 < NKS) {
+            const bool hin = 2 * (ks + 1) + 1 < NT;
+#pragma unroll
+            for (int dt = 0; dt < 4; ++dt) {
+                const uint32_t a = sVa + 2u * L.vOff[dt];
+                asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2"
+                             : "=v"(lo[cur ^ 1][dt]) : "v"(a), "i"((ks + 1) * 32 * kD * 2));
+                asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2"
+                             : "=v"(up[cur ^ 1][dt]) : "v"(a), "i"((ks + 1) * 32 * kD * 2 + (hin ? 16 * kD * 2 : 0)));
+            }
+            asm volatile("s_waitcnt lgkmcnt(8)" ::: "memory");
+        } else {
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        }
         const f32x4a& a0 = s[2 * ks];
         constexpr int dummy = 0;
         const bool hi = 2 * ks + 1 < NT;   // the second score tile of this step exists
         const f32x4a& a1 = s[hi ? 2 * ks + 1 : dummy];
         const u32x4a pf = {pack2<BF16>(a0[0], a0[1]), pack2<BF16>(a0[2], a0[3]), hi ? pack2<BF16>(a1[0], a1[1]) : 0u,
                            hi ? pack2<BF16>(a1[2], a1[3]) : 0u};
-        // V^T fragments: rows 32ks + 4g4 + j (first read) and + 16 (second
-        // read; a missing tile re-reads the first rows, whose weights are
-        // zero). The reads are inline assembly and waited for here: through the
-        // builtin the compiler would also wait for any LDS DMA in flight, i.e.
-        // for every global load still outstanding.
-        u32x2a lo[4], up[4];
-#pragma unroll
-        for (int dt = 0; dt < 4; ++dt) {
-            const uint32_t a = sVa + 2u * L.vOff[dt];
-            asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(lo[dt]) : "v"(a), "i"(ks * 32 * kD * 2));
-            asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2"
-                         : "=v"(up[dt]) : "v"(a), "i"(ks * 32 * kD * 2 + (hi ? 16 * kD * 2 : 0)));
-        }
-        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
         rs = mfma16<BF16>(ones, pf, rs);
 #pragma unroll
         for (int dt = 0; dt < 4; ++dt) {
-            asm volatile("" : "+v"(lo[dt]), "+v"(up[dt]));
-            const u32x4a vf = {lo[dt][0], lo[dt][1], up[dt][0], up[dt][1]};
+            asm volatile("" : "+v"(lo[cur][dt]), "+v"(up[cur][dt]));
+            const u32x4a vf = {lo[cur][dt][0], lo[cur][dt][1], up[cur][dt][0], up[cur][dt][1]};
             o[dt] = mfma16<BF16>(vf, pf, o[dt]);
         }
     }
@@ -291,6 +310,8 @@ __global__ __launch_bounds__(NW * 64) void attention_kernel(AttnParams p) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int l16 = lane & 15, g4 = lane >> 4;
     const int b = blockIdx.x / p.H, h = blockIdx.x % p.H;
+    u32x4a qf[2];
+    loadQ(p, b, h, wave * 16 + l16, g4, qf);   // the first block's queries load under the K / V copy
     dmaHead<SP>(p, b, h, sK, sV, wave, NW, lane);
     AttnLane L;
     L.init(l16, g4);
@@ -302,17 +323,19 @@ __global__ __launch_bounds__(NW * 64) void attention_kernel(AttnParams p) {
     const int nb = (p.S + 15) >> 4;
     for (int jb = wave; jb < nb; jb += NW) {   // wave-uniform; nothing below synchronises the workgroup
         const int qa = jb * 16 + l16;
-        u32x4a qf[2];
-        loadQ(p, b, h, qa, g4, qf);
+        u32x4a qn[2] = {qf[0], qf[1]};
+        if (jb + NW < nb) loadQ(p, b, h, qa + NW * 16, g4, qn);   // the next block's queries
         f32x4a o[4];
         float inv;
         attnBlock<BF16, NT>(sK, sVa, L, qf, p.S, c, g4, o, inv);
         if (qa < p.S) storeBlock<BF16, OUT_HALF>(p, outOffset(p, b, h, qa, g4), o, inv);
+        qf[0] = qn[0];
+        qf[1] = qn[1];
     }
 }
 
 // Key tiles (16 keys each) are a compile-time count: NT = ceil(S / 16).
-// Eight waves per head: at 197 tokens (96 VGPRs, 52 KB of LDS) two heads share
+// Eight waves per head: at 197 tokens (122 VGPRs, 52 KB of LDS) two heads share
 // a CU, and the 768 heads of ViT-B/16 at batch 64 run in 1.5 rounds, whose
 // second half loads while the first computes; measured against 4 waves
 // (three heads per CU, one round), two or three workgroups per head and a
