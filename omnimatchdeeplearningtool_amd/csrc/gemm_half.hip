@@ -183,14 +183,20 @@ __device__ __forceinline__ f32x16h mfma16(const u16x8& a, const u16x8& b, const 
                                                       0, 0, 0);
 }
 
-__device__ __forceinline__ void tileCoordsH(int bid, int total, int tilesM, int tilesN, int& tm, int& tn) {
-    constexpr int XCDS = 8, GROUP_M = 8;
-    int t = bid;
-    if (total >= XCDS) {
-        const int q = total / XCDS, rem = total % XCDS;
-        const int xcd = bid % XCDS, idx = bid / XCDS;
-        t = (xcd < rem) ? xcd * (q + 1) + idx : rem * (q + 1) + (xcd - rem) * q + idx;
-    }
+// Workgroup id -> logical index such that each XCD (ids bid % 8) runs one
+// contiguous range of the logical order: neighbouring tiles, which share
+// operand rows or columns, then share one L2.
+__device__ __forceinline__ int xcdRemap(int bid, int total) {
+    constexpr int XCDS = 8;
+    if (total < XCDS) return bid;
+    const int q = total / XCDS, rem = total % XCDS;
+    const int xcd = bid % XCDS, idx = bid / XCDS;
+    return (xcd < rem) ? xcd * (q + 1) + idx : rem * (q + 1) + (xcd - rem) * q + idx;
+}
+
+// Logical tile index t -> (tm, tn): groups of 8 tile rows walked column by column.
+__device__ __forceinline__ void groupCoords(int t, int tilesM, int tilesN, int& tm, int& tn) {
+    constexpr int GROUP_M = 8;
     const int perGroup = GROUP_M * tilesN;
     const int g = t / perGroup;
     const int firstM = g * GROUP_M;
@@ -198,6 +204,10 @@ __device__ __forceinline__ void tileCoordsH(int bid, int total, int tilesM, int 
     const int inG = t - g * perGroup;
     tm = firstM + inG % gsz;
     tn = inG / gsz;
+}
+
+__device__ __forceinline__ void tileCoordsH(int bid, int total, int tilesM, int tilesN, int& tm, int& tn) {
+    groupCoords(xcdRemap(bid, total), tilesM, tilesN, tm, tn);
 }
 
 template <class Cfg, bool BF16, bool TA, bool TB, bool VA, bool VB>
@@ -332,6 +342,9 @@ struct HalfFastParams {
     int tilesM, tilesN;
     const float* bias;   // output as GemmHalfParams
     int act, outHalf;
+    int batch;
+    int flat;      // grid x runs over (batch, tile) pairs (else x = tile, z = batch)
+    int compact;   // one tile holds a batch's whole C, stored through LDS (gemm_half_fast)
 };
 
 // K-major operand whose rows start at any half (an odd leading dimension,
@@ -696,6 +709,58 @@ __device__ __forceinline__ void interleave() {
     }
 }
 
+// Compact store (fp32 C, no bias or activation, one tile covering all M x N,
+// ldc == N, 16-byte aligned base): the batch's C is one contiguous run of
+// M*N floats whose rows need not start on a 16-byte boundary (e.g. 197 x 197
+// attention scores). Element stores of such rows leave partly written cache
+// lines behind each store instruction; here the finished tile goes to LDS in
+// C's own layout, a group of wave rows at a time, and the workgroup writes
+// the run with aligned 16-byte stores (a scalar head and tail). LDS element
+// pre + j holds C element cb + r0*N + j, where pre = cb mod 4 and r0*N is a
+// multiple of 4, so the 16-byte LDS reads are aligned exactly when the
+// global stores are.
+template <class Cfg, size_t LDS_BYTES>
+__device__ __forceinline__ void storeCompact(const HalfFastParams& p, const f32x16h (&acc)[Cfg::FM][Cfg::FN],
+                                             uint16_t* hsm, long long cb, int wm, int wn, int li, int h, int tid) {
+    constexpr int WR = Cfg::BM / Cfg::WM;                   // wave rows of the tile
+    constexpr int LDSF = (int)(LDS_BYTES / sizeof(float));
+    static_assert(Cfg::WM * Cfg::BN + 4 <= LDSF, "one wave row of the tile fits in LDS");
+    float* cs = reinterpret_cast<float*>(hsm);
+    float* C = static_cast<float*>(p.C);
+    const int pre = (int)(cb & 3);
+    const int g = min(WR, (LDSF - 4) / (Cfg::WM * p.N));   // wave rows per pass (>= 1: N <= BN)
+    for (int w0 = 0; w0 < WR; w0 += g) {
+        const int r0 = w0 * Cfg::WM;
+        if (r0 >= p.M) break;
+        const int r1 = min(p.M, (w0 + g) * Cfg::WM);
+        __syncthreads();   // LDS free: the mainloop's or the previous pass's reads are done
+        if (wm >= w0 && wm < w0 + g) {
+#pragma unroll
+            for (int fn = 0; fn < Cfg::FN; ++fn) {
+                const int n = wn * Cfg::WN + fn * 32 + li;
+#pragma unroll
+                for (int fm = 0; fm < Cfg::FM; ++fm)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) {
+                        const int m = wm * Cfg::WM + fm * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
+                        if (m < p.M && n < p.N) cs[pre + (m - r0) * p.N + n] = acc[fm][fn][r];
+                    }
+            }
+        }
+        __syncthreads();
+        const long long gb = cb + (long long)r0 * p.N;   // C element of LDS element pre
+        const int cnt = (r1 - r0) * p.N;
+        const int head = min(cnt, (int)((4 - (gb & 3)) & 3));   // elements before the first aligned one
+        const int nvec = (cnt - head) >> 2;
+        for (int j = tid; j < head; j += Cfg::NT) C[gb + j] = cs[pre + j];
+        for (int v = tid; v < nvec; v += Cfg::NT) {
+            const int j = head + 4 * v;
+            *reinterpret_cast<f32x4h*>(C + gb + j) = *reinterpret_cast<const f32x4h*>(cs + pre + j);
+        }
+        for (int j = head + 4 * nvec + tid; j < cnt; j += Cfg::NT) C[gb + j] = cs[pre + j];
+    }
+}
+
 // SWAP (C rows allow 4-column stores: N, ldc, batch stride multiples of 4 and
 // the base 16-byte aligned for fp32, 8-byte for half output) puts the B
 // fragment first so each lane holds 4 consecutive columns; otherwise lanes run
@@ -708,8 +773,16 @@ __global__ __launch_bounds__(Cfg::NT) void gemm_half_fast(HalfFastParams p) {
     const int wm = wave / Cfg::WAVES_N, wn = wave % Cfg::WAVES_N;
     const int li = lane & 31, h = lane >> 5;
     int tm, tn;
-    tileCoordsH(blockIdx.x, p.tilesM * p.tilesN, p.tilesM, p.tilesN, tm, tn);
-    const long long batch = blockIdx.z;
+    long long batch;
+    if (p.flat) {   // the tiles of one batch run on one XCD and share its L2
+        const int tiles = p.tilesM * p.tilesN;
+        const int t = xcdRemap(blockIdx.x, tiles * p.batch);
+        batch = t / tiles;
+        groupCoords(t - (int)batch * tiles, p.tilesM, p.tilesN, tm, tn);
+    } else {
+        tileCoordsH(blockIdx.x, p.tilesM * p.tilesN, p.tilesM, p.tilesN, tm, tn);
+        batch = blockIdx.z;
+    }
     const int m0 = tm * Cfg::BM, n0 = tn * Cfg::BN;
     const uint16_t* Ab = p.A + batch * p.sA;
     const uint16_t* Bb = p.B + batch * p.sB;
@@ -830,6 +903,10 @@ __global__ __launch_bounds__(Cfg::NT) void gemm_half_fast(HalfFastParams p) {
     } else {
         // Lane (li, h) holds C[m][n] at n = nBase + li,
         // m = mBase + 8*(r/4) + 4*h + (r%4): 32 lanes store one row's 128 bytes.
+        if (p.compact) {
+            storeCompact<Cfg, Ops::LDS_BYTES>(p, acc, hsm, cb, wm, wn, li, h, tid);
+            return;
+        }
 #pragma unroll
         for (int fn = 0; fn < Cfg::FN; ++fn) {
             const int n = n0 + wn * Cfg::WN + fn * 32 + li;
@@ -865,7 +942,12 @@ static int launchFast(HalfFastParams prm, int batch) {
     OMHIP_CHECK(OMHIP_SET_MAX_DYNAMIC_LDS_ONCE(kern, lds));
     prm.tilesM = (prm.M + Cfg::BM - 1) / Cfg::BM;
     prm.tilesN = (prm.N + Cfg::BN - 1) / Cfg::BN;
-    hipLaunchKernelGGL(kern, dim3(prm.tilesM * prm.tilesN, 1, batch), dim3(Cfg::NT), lds, stream(), prm);
+    const long long tiles = (long long)prm.tilesM * prm.tilesN;
+    prm.batch = batch;
+    prm.flat = batch > 1 && tiles * batch * Cfg::NT < (1LL << 31);
+    prm.compact = !SWAP && prm.compact && tiles == 1;
+    const dim3 grid = prm.flat ? dim3((unsigned)(tiles * batch)) : dim3((unsigned)tiles, 1, batch);
+    hipLaunchKernelGGL(kern, grid, dim3(Cfg::NT), lds, stream(), prm);
     OMHIP_CHECK_LAUNCH();
     return 0;
 }
@@ -940,8 +1022,9 @@ static int dispatchH(bool ta, bool tb, const GemmHalfParams& prm, int batch, boo
         f.lda = (int)prm.lda; f.ldb = (int)prm.ldb; f.ldc = prm.ldc; f.sA = prm.sA; f.sB = prm.sB; f.sC = prm.sC;
         f.bias = prm.bias; f.act = prm.act; f.outHalf = prm.outHalf;
         const uintptr_t cAlign = prm.outHalf ? 7u : 15u;
-        const bool vecC = (prm.N % 4 == 0) && (prm.ldc % 4 == 0) && (prm.sC % 4 == 0) &&
-                          ((reinterpret_cast<uintptr_t>(prm.C) & cAlign) == 0);
+        const bool cAligned = (reinterpret_cast<uintptr_t>(prm.C) & cAlign) == 0;
+        const bool vecC = (prm.N % 4 == 0) && (prm.ldc % 4 == 0) && (prm.sC % 4 == 0) && cAligned;
+        f.compact = !prm.outHalf && !prm.bias && prm.act == 0 && prm.ldc == prm.N && cAligned;   // + one tile
         if (!ta && !tb) return launchFastR<BF16, false, false>(f, batch, vecC, rag);
         if (!ta && tb) return launchFastR<BF16, false, true>(f, batch, vecC, rag);
         if (ta && !tb) return launchFastR<BF16, true, false>(f, batch, vecC, rag);

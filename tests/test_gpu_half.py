@@ -94,6 +94,44 @@ def test_half_layouts_tiles(hip, bf16, transA, transB, batch, M, N, K):
     assert O.normalized_error(dC.numpy(), C64, bound) <= 1e-4
 
 
+# (batch, M, N, K, transB, gap): one tile holds a batch's whole C, whose rows
+# (N % 4 != 0, or a batch stride M*N + gap with gap % 4 != 0) cannot leave
+# through 16-byte row stores: C is written through LDS as one contiguous run
+# per batch. On a 256-CU MI355X the tile model picks 256x256 (rows 0-127 and
+# 128-196 in two LDS passes: the ViT-B/16 b64 Q.K^T; 200 rows in passes of
+# 192 and 8), 128x128 (one pass; two passes of 64 rows) and 64x64 tiles.
+COMPACT_SHAPES = [(768, 197, 197, 64, 1, 0), (400, 200, 130, 48, 0, 0), (512, 100, 102, 72, 0, 0),
+                  (512, 120, 128, 32, 1, 3), (512, 50, 61, 40, 1, 0), (2048, 33, 47, 24, 0, 0)]
+
+
+@pytest.mark.parametrize("bf16", [False, True], ids=["f16", "bf16"])
+@pytest.mark.parametrize("batch,M,N,K,transB,gap", COMPACT_SHAPES)
+def test_half_compact_store(hip, bf16, batch, M, N, K, transB, gap):
+    """Whole-C-in-one-tile batches: values against float64 on sampled batches, every gap and the
+    bytes past the last batch untouched."""
+    seed = batch + M + N + K + transB + gap
+    A = O.randn((batch, M, K), seed)
+    B = O.randn((batch, N, K) if transB else (batch, K, N), seed + 1)
+    dA, dB = to_dev(hip, _bits(A, bf16)), to_dev(hip, _bits(B, bf16))
+    sC = M * N + gap
+    tail = 67
+    C0 = np.full(batch * sC + tail, np.nan, np.float32)   # no product of finite inputs is NaN
+    dC = to_dev(hip, C0)
+    hip.HIPBackend.gemmStridedBatchedHalf(1 if bf16 else 0, 0, transB, batch, M, N, K, dA, K, M * K, dB,
+                                          K if transB else N, N * K, dC, N, sC)
+    C = dC.numpy()
+    Ar, Br = _round(A, bf16), _round(B, bf16)
+    picks = sorted({0, 1, 2, batch // 2 - 1, batch // 2, batch - 2, batch - 1})
+    for b in picks:
+        C64, bound = O.gemm_f64(Ar[b], Br[b], transB=bool(transB))
+        got = C[b * sC:b * sC + M * N].reshape(M, N)
+        assert O.normalized_error(got, C64, bound) <= 1e-4, f"batch {b}"
+    runs = C[:batch * sC].reshape(batch, sC)
+    assert np.all(np.isnan(runs[:, M * N:])), "batch gaps must stay untouched"
+    assert np.all(np.isnan(C[batch * sC:])), "nothing past the last batch is written"
+    assert not np.any(np.isnan(runs[:, :M * N])), "every element of every batch is written"
+
+
 def test_half_strided_views(hip):
     """Leading dimensions wider than the rows and batch strides with gaps (sub-matrix views)."""
     batch, M, N, K = 3, 72, 80, 96
