@@ -287,7 +287,9 @@ __device__ __forceinline__ void storeBlock(const AttnParams& p, long long ob, co
         } else {
             float* op = static_cast<float*>(p.out) + ob + 16 * dt;
             if (p.outVec) {
-                *reinterpret_cast<f32x4a*>(op) = f32x4a{v0, v1, v2, v3};
+                // streaming store: 23.2 -> 22.0 us at ViT-B/16 b64 (for the
+                // 8-byte half stores it was slower)
+                __builtin_nontemporal_store(f32x4a{v0, v1, v2, v3}, reinterpret_cast<f32x4a*>(op));
             } else {
                 op[0] = v0; op[1] = v1; op[2] = v2; op[3] = v3;
             }

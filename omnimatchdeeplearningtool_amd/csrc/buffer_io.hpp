@@ -35,6 +35,14 @@ __device__ __forceinline__ void bufStore1(__amdgpu_buffer_rsrc_t r, uint32_t vof
     __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), r, voff, soff, 0);
 }
 
+// Cache policy nt: a streaming store (the line is not kept in L2 for reuse),
+// for outputs written once that the next kernel reads: they drain to memory
+// while the kernel still runs instead of in the L2 write-back at its end.
+constexpr int kCpolStream = 2;
+__device__ __forceinline__ void bufStore1Stream(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff, float v) {
+    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), r, voff, soff, kCpolStream);
+}
+
 // Cache policy sc1: an access coherent at agent scope (the monotonic
 // agent-scope atomic load / store of the gfx94x / gfx950 memory model), so
 // data exchanged between workgroups on different XCDs (each with its own L2)

@@ -261,7 +261,10 @@ __device__ __forceinline__ int outPixel(const ConvParams& p, int pix) {
 // byte offset past the lane's first row is the wave-uniform (8j + r%4) * row
 // stride, carried in soffset. Columns past Nq and rows past Cout get an
 // out-of-range voffset and store nothing. The output view (chunk images x
-// Cout x oH x oW floats) is at most 2^30 bytes.
+// Cout x oH x oW floats) is at most 2^30 bytes. The stores are streaming (nt):
+// every block of a launch finishes at about the same time, and the output
+// then drains to memory as it is written rather than in the L2 write-back at
+// the end of the launch (ResNet-18 b32 stack -1 %).
 template <class Cfg, bool BN, bool RES, bool RELU>
 __device__ __forceinline__ void storeTile(const ConvParams& p, const f32x16 (&acc)[Cfg::FM][Cfg::FN],
                                           const float* sEpi, int m0, int n0, int wm, int wn, int lane) {
@@ -310,7 +313,7 @@ __device__ __forceinline__ void storeTile(const ConvParams& p, const f32x16 (&ac
                     if constexpr (BN) v = __builtin_fmaf(g[i], (v - mu[i]) * is[i], be[i]);
                     if constexpr (RES) v += rv[i];
                     if constexpr (RELU) v = v > 0.f ? v : 0.f;
-                    bufStore1(ro, vo[i], (8 * j + i) * oHW * 4u, v);
+                    bufStore1Stream(ro, vo[i], (8 * j + i) * oHW * 4u, v);
                 }
                 __builtin_amdgcn_sched_barrier(0);   // keeps one group's registers live at a time
             }

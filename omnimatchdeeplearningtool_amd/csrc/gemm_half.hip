@@ -715,7 +715,7 @@ __device__ __forceinline__ void interleave() {
 // attention scores). Element stores of such rows leave partly written cache
 // lines behind each store instruction; here the finished tile goes to LDS in
 // C's own layout, a group of wave rows at a time, and the workgroup writes
-// the run with aligned 16-byte stores (a scalar head and tail). LDS element
+// the run with aligned 16-byte streaming (nt) stores (a scalar head and tail). LDS element
 // pre + j holds C element cb + r0*N + j, where pre = cb mod 4 and r0*N is a
 // multiple of 4, so the 16-byte LDS reads are aligned exactly when the
 // global stores are.
@@ -755,7 +755,7 @@ __device__ __forceinline__ void storeCompact(const HalfFastParams& p, const f32x
         for (int j = tid; j < head; j += Cfg::NT) C[gb + j] = cs[pre + j];
         for (int v = tid; v < nvec; v += Cfg::NT) {
             const int j = head + 4 * v;
-            *reinterpret_cast<f32x4h*>(C + gb + j) = *reinterpret_cast<const f32x4h*>(cs + pre + j);
+            __builtin_nontemporal_store(*reinterpret_cast<const f32x4h*>(cs + pre + j), reinterpret_cast<f32x4h*>(C + gb + j));
         }
         for (int j = head + 4 * nvec + tid; j < cnt; j += Cfg::NT) C[gb + j] = cs[pre + j];
     }
