@@ -712,7 +712,8 @@ __device__ __forceinline__ void interleave() {
 // Compact store (fp32 C, no bias or activation, one tile covering all M x N,
 // ldc == N, 16-byte aligned base): the batch's C is one contiguous run of
 // M*N floats whose rows need not start on a 16-byte boundary (e.g. 197 x 197
-// attention scores). Element stores of such rows leave partly written cache
+// blocks of a batched product with K > 64; one-slice products such as the
+// attention scores take 64x64 tiles instead). Element stores of such rows leave partly written cache
 // lines behind each store instruction; here the finished tile goes to LDS in
 // C's own layout, a group of wave rows at a time, and the workgroup writes
 // the run with aligned 16-byte streaming (nt) stores (a scalar head and tail). LDS element
@@ -962,11 +963,15 @@ static int launchFast(HalfFastParams prm, int batch) {
 // where the model picks the fastest tile or one within 4 % of it: e.g.
 // 12608 x 2304 x 768 and 4096^3 take 256x256, 2048 x 4096 x 4096 128x128,
 // 768 x (197 x 64 x 197), 2048^3 and 1024^3 64x64.
-static int pickFastTile(int M, int N, int batch) {
+static int pickFastTile(int M, int N, int K, int batch) {
     const long long cus = cuCount();
     struct T { int bm, bn, slots; double rate; };
     const T cand[3] = {{256, 256, 1, 1.0}, {128, 128, 2, 0.75}, {64, 64, 4, 0.5}};
-    // TILE-HOOK
+    // A product of one K slice is bound by its C stores, not its MFMAs: many
+    // small workgroups overlap one another's stores (batched Q.K^T 768 x 197
+    // x 197 x 64: 64x64 42.3 us, 256x256 with the compact store 46.0 us,
+    // 128x128 55.4 us).
+    if (K <= 64) return 2;
     int best = 0;
     double bestCost = 0;
     for (int c = 0; c < 3; ++c) {
@@ -981,7 +986,7 @@ static int pickFastTile(int M, int N, int batch) {
 
 template <bool BF16, bool TA, bool TB, bool SWAP, bool RAG>
 static int launchFastT(const HalfFastParams& prm, int batch) {
-    switch (pickFastTile(prm.M, prm.N, batch)) {
+    switch (pickFastTile(prm.M, prm.N, prm.K, batch)) {
         case 0: return launchFast<FCfgL, BF16, TA, TB, SWAP, RAG>(prm, batch);
         case 1: return launchFast<FCfgM, BF16, TA, TB, SWAP, RAG>(prm, batch);
         default: return launchFast<FCfgS, BF16, TA, TB, SWAP, RAG>(prm, batch);

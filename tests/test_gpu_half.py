@@ -97,11 +97,13 @@ def test_half_layouts_tiles(hip, bf16, transA, transB, batch, M, N, K):
 # (batch, M, N, K, transB, gap): one tile holds a batch's whole C, whose rows
 # (N % 4 != 0, or a batch stride M*N + gap with gap % 4 != 0) cannot leave
 # through 16-byte row stores: C is written through LDS as one contiguous run
-# per batch. On a 256-CU MI355X the tile model picks 256x256 (rows 0-127 and
-# 128-196 in two LDS passes: the ViT-B/16 b64 Q.K^T; 200 rows in passes of
-# 192 and 8), 128x128 (one pass; two passes of 64 rows) and 64x64 tiles.
-COMPACT_SHAPES = [(768, 197, 197, 64, 1, 0), (400, 200, 130, 48, 0, 0), (512, 100, 102, 72, 0, 0),
-                  (512, 120, 128, 32, 1, 3), (512, 50, 61, 40, 1, 0), (2048, 33, 47, 24, 0, 0)]
+# per batch. On a 256-CU MI355X the tile model picks 256x256 (197 rows in LDS
+# passes of 128 and 69; 200 rows in passes of 192 and 8), 128x128 (one pass;
+# two passes of 64 rows) and 64x64 tiles. The first shape is the ViT-B/16 b64
+# Q.K^T itself (K = 64: one slice, so 64x64 tiles and element stores).
+COMPACT_SHAPES = [(768, 197, 197, 64, 1, 0), (768, 197, 197, 72, 1, 0), (400, 200, 130, 80, 0, 0),
+                  (512, 100, 102, 72, 0, 0), (512, 120, 128, 96, 1, 3), (512, 50, 61, 72, 1, 0),
+                  (2048, 33, 47, 88, 0, 0)]
 
 
 @pytest.mark.parametrize("bf16", [False, True], ids=["f16", "bf16"])
