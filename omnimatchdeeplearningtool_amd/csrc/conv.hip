@@ -174,7 +174,10 @@ struct WeightLoader {
 // contiguous in its pixel's LDS row (128-bit stores). Per pixel: one byte offset
 // (into a buffer view that starts pad*W+pad floats before x, so it is never
 // negative) and the mask of taps that fall outside the image.
-//   MODE: gatherMode(KH*KW).
+//   MODE: gatherMode(KH*KW), or 3 for an unpadded 1x1 kernel whose taps all
+//   lie inside the image: no mask, and in slices wholly inside K (FULL) no
+//   per-element arithmetic at all (rows past K still read 0: their table
+//   code is nonzero).
 template <int BN, int BK, int NT, int MODE>
 struct GatherLoader {
     static constexpr int TPC = NT / BN;
@@ -203,6 +206,10 @@ struct GatherLoader {
         ih0 = colValid ? oh * p.stride - p.padH : -(1 << 29);   // a padding column matches no tap
         iw0 = ow * p.stride - p.padW;
         voffPix = (uint32_t)(n * p.Cin * p.H * p.W + (colValid ? ih0 : 0) * W + iw0 + p.padOff) * 4u;
+        if constexpr (MODE == 3) {
+            if (!colValid) voffPix = kOOB;   // a padding column reads zeros
+            return;
+        }
         uint64_t inside = 0;
         if constexpr (MODE != 2) {
             // Taps (kh, kw) inside the image: kw in [cl, ch), kh in [rl, rh).
@@ -217,14 +224,22 @@ struct GatherLoader {
         invHi = ~(uint32_t)(inside >> 32);
     }
 
-    // Issues this thread's RPT loads of the slice starting at row kk0.
+    // Issues this thread's RPT loads of the slice starting at row kk0 (FULL:
+    // the slice lies wholly inside K).
+    template <bool FULL = false>
     __device__ void load(int kk0, int /*tid*/) {
         const int base = kk0 + rowOff;
 #pragma unroll
         for (int j = 0; j < RPT; ++j) {
             const uint2 e = tab[base + j];
             uint32_t inv;
-            if constexpr (MODE == 0) {
+            if constexpr (MODE == 3) {
+                if constexpr (FULL) {
+                    v[j] = bufLoad1(r, voffPix, e.x);
+                    continue;
+                }
+                inv = e.y != 0u;   // 0 for the single tap, 31 for rows past K
+            } else if constexpr (MODE == 0) {
                 inv = __builtin_amdgcn_ubfe(invLo, e.y, 1);
             } else if constexpr (MODE == 1) {
                 inv = (uint32_t)((((uint64_t)invHi << 32) | invLo) >> e.y) & 1u;
@@ -531,7 +546,7 @@ __global__ __launch_bounds__(Cfg::NT) void conv_igemm_kernel(ConvParams p) {
     const int nFull = (kEnd - kBeg) / Cfg::BK;
     int t = 0;
     for (; t + 2 < nFull; t += 2) {
-        lb.load(kBeg + (t + 1) * Cfg::BK, tid);
+        lb.template load<true>(kBeg + (t + 1) * Cfg::BK, tid);
         la.template load<true>(kBeg + (t + 1) * Cfg::BK, kEnd, tid);
         __builtin_amdgcn_sched_barrier(0);
         mma_slice<Cfg, true, true>(smem, smem + SA::SIZE, acc, wm, wn, lane);
@@ -539,7 +554,7 @@ __global__ __launch_bounds__(Cfg::NT) void conv_igemm_kernel(ConvParams p) {
         la.store(smem + STAGE, tid);
         lb.store(smem + STAGE + SA::SIZE, tid);
         __syncthreads();
-        lb.load(kBeg + (t + 2) * Cfg::BK, tid);
+        lb.template load<true>(kBeg + (t + 2) * Cfg::BK, tid);
         la.template load<true>(kBeg + (t + 2) * Cfg::BK, kEnd, tid);
         __builtin_amdgcn_sched_barrier(0);
         mma_slice<Cfg, true, true>(smem + STAGE, smem + STAGE + SA::SIZE, acc, wm, wn, lane);
@@ -686,13 +701,18 @@ static int launchConv(ConvParams& p, const ConvPlan& pl, float* wsBuf) {
     }
     const bool va = (p.K % 4 == 0) && ((reinterpret_cast<uintptr_t>(p.w) & 15u) == 0);
     const int khw = p.KH * p.KW;
-    const int mode = gatherMode(khw);
+    // an unpadded 1x1 kernel whose grid stays inside the image never gathers a padding tap
+    const bool inside = p.KH == 1 && p.KW == 1 && p.padH == 0 && p.padW == 0 &&
+                        (long long)(p.Ho - 1) * p.stride < p.H && (long long)(p.Wo - 1) * p.stride < p.W;
+    const int mode = inside ? 3 : gatherMode(khw);
     int rc;
     if (va)
-        rc = mode == 0 ? launchConvT<Cfg, true, 0>(p, gridX)
+        rc = mode == 3 ? launchConvT<Cfg, true, 3>(p, gridX)
+           : mode == 0 ? launchConvT<Cfg, true, 0>(p, gridX)
                        : (mode == 1 ? launchConvT<Cfg, true, 1>(p, gridX) : launchConvT<Cfg, true, 2>(p, gridX));
     else
-        rc = mode == 0 ? launchConvT<Cfg, false, 0>(p, gridX)
+        rc = mode == 3 ? launchConvT<Cfg, false, 3>(p, gridX)
+           : mode == 0 ? launchConvT<Cfg, false, 0>(p, gridX)
                        : (mode == 1 ? launchConvT<Cfg, false, 1>(p, gridX) : launchConvT<Cfg, false, 2>(p, gridX));
     return rc;
 }
