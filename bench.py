@@ -5,7 +5,9 @@
 
 Headline (the `value`): fp32 GEMM 4096x4096x4096, row-major A[M,K] x B[K,N]
 (CPUBackend::matmul's layout), inputs resident in HBM; one step = one GEMM;
-value = TFLOP/s over the timed steps (HIP events on the library stream).
+value = TFLOP/s over the timed steps (HIP events on the library stream). It is
+timed right after the fp32 GEMM sweep, whose last shapes are 8192^3: an idle
+MI355X runs its first ~20 ms of load at lower clocks.
 Second metric in the same line (`resnet18_conv`): the ResNet-18 conv stack
 forward at batch 32, 224x224 (20 convs, each conv + BN-inference + ReLU fused),
 as images/s over eager launches (the same 20 launches replayed from a
@@ -63,12 +65,24 @@ def _traffic(name: str):
 GEMM_ROWS = np.r_[0:4, 2046:2050, 4092:4096]   # rows of the 4096^3 product checked on the CPU
 
 
-def bench_gemm(om, steps: int, warmup: int):
-    from omnimatchdeeplearningtool_amd.hiptime import StreamTimer
+def read_rows(om, buf, rows, ncols: int) -> np.ndarray:
+    """Rows `rows` of a row-major fp32 device matrix with ncols columns (only those bytes cross PCIe)."""
+    out = np.empty((len(rows), ncols), np.float32)
+    for i, r in enumerate(rows):
+        om.call("omHipCopyD2H", out[i].ctypes.data, buf.ptr + int(r) * ncols * 4, ncols * 4)
+    return out
+
+
+def gemm_inputs(om):
+    """The headline GEMM's seeded inputs, uploaded to HBM."""
     A = syn.randn((M, K), 11)
     B = syn.randn((K, N), 12)
-    dA, dB = om.DeviceBuffer.from_numpy(A), om.DeviceBuffer.from_numpy(B)
-    dC = om.DeviceBuffer.empty((M, N))
+    return om.DeviceBuffer.from_numpy(A), om.DeviceBuffer.from_numpy(B), om.DeviceBuffer.empty((M, N))
+
+
+def bench_gemm(om, bufs, steps: int, warmup: int):
+    from omnimatchdeeplearningtool_amd.hiptime import StreamTimer
+    dA, dB, dC = bufs
     H = om.HIPBackend
     for _ in range(warmup):
         H.matmul(dA, dB, dC, M, K, N)
@@ -84,11 +98,13 @@ def bench_gemm(om, steps: int, warmup: int):
     wall = time.perf_counter() - t0
     ms = ms_total / steps
     flops = 2.0 * M * N * K
-    return ms, flops, wall, dC.numpy()[GEMM_ROWS]
+    return ms, flops, wall, read_rows(om, dC, GEMM_ROWS, N)
 
 
-GEMM_SWEEP = [(512, 512, 512), (1024, 1024, 1024), (2048, 2048, 2048), (4096, 4096, 4096), (8192, 8192, 8192),
-              (128, 4096, 4096), (8192, 256, 2048)]   # (M, N, K)
+# (M, N, K); the cubes last, so the sweep ends with 8192^3 launches (the
+# headline GEMM is timed right after it, on clocks that are already up)
+GEMM_SWEEP = [(128, 4096, 4096), (8192, 256, 2048), (512, 512, 512), (1024, 1024, 1024), (2048, 2048, 2048),
+              (4096, 4096, 4096), (8192, 8192, 8192)]
 
 
 def bench_gemm_sweep(om, steps: int, warmup: int):
@@ -115,7 +131,7 @@ def bench_gemm_sweep(om, steps: int, warmup: int):
             timer.stop()
             ms = timer.ms() / reps
             rows = np.unique(np.r_[0, m // 2, m - 1])
-            samples.append(((m, n, k, layout), rows, dC.numpy()[rows]))
+            samples.append(((m, n, k, layout), rows, read_rows(om, dC, rows, n)))
             tf = 2.0 * m * n * k / ms / 1e9
             out.append({"M": m, "N": n, "K": k, "layout": layout, "ms": round(ms, 4), "tflops": round(tf, 1),
                         "frac_of_157_3": round(tf / 157.3, 3), "parity": None})
@@ -140,10 +156,9 @@ def resnet18_layer_inputs(li: int, batch: int):
     return x, wt, g, b, m, v
 
 
-def bench_resnet18(om, steps: int, warmup: int, batch: int = 32):
-    from omnimatchdeeplearningtool_amd.hiptime import StreamTimer
-    from resnet_shapes import conv_bytes, conv_flops, out_hw, resnet18_convs
-    H = om.HIPBackend
+def resnet18_setup(om, batch: int = 32):
+    """The 20 ResNet-18 conv layers' seeded inputs, uploaded to HBM."""
+    from resnet_shapes import out_hw, resnet18_convs
     layers = []
     for li, (name, cin, h, w, cout, k, s, p) in enumerate(resnet18_convs()):
         x, wt, g, b, m, v = resnet18_layer_inputs(li, batch)
@@ -153,6 +168,13 @@ def bench_resnet18(om, steps: int, warmup: int, batch: int = 32):
                    m=om.DeviceBuffer.from_numpy(m), v=om.DeviceBuffer.from_numpy(v),
                    y=om.DeviceBuffer.empty((batch, cout, ho, wo)))
         layers.append(((name, cin, h, w, cout, k, s, p), dev, (x, wt, g, b, m, v)))
+    return layers
+
+
+def bench_resnet18(om, layers, steps: int, warmup: int, batch: int = 32):
+    from omnimatchdeeplearningtool_amd.hiptime import StreamTimer
+    from resnet_shapes import conv_bytes, conv_flops
+    H = om.HIPBackend
 
     def forward():
         for (name, cin, h, w, cout, k, s, p), d, _ in layers:
@@ -170,14 +192,10 @@ def bench_resnet18(om, steps: int, warmup: int, batch: int = 32):
     ms = timer.ms() / steps
     # The same 20 launches replayed from a captured HIP graph (the kernels and
     # their work are unchanged; the host launch cost and the gaps between
-    # launches go). Every output is overwritten per pass, so a replay must
-    # reproduce the eager outputs bit for bit.
-    eager_out = [d["y"].numpy() for _, d, _ in layers]
+    # launches go), timed straight after the eager passes; the replays'
+    # outputs are compared with an eager pass's bit for bit at the end, once
+    # every timing is done (the read-backs would leave the GPU idle).
     graph = om.Graph(forward)
-    graph.launch()
-    om.synchronize()
-    same = all(np.array_equal(d["y"].numpy().view(np.uint32), e.view(np.uint32))
-               for (_, d, _), e in zip(layers, eager_out))
     for _ in range(warmup):
         graph.launch()
     om.synchronize()
@@ -186,7 +204,6 @@ def bench_resnet18(om, steps: int, warmup: int, batch: int = 32):
         graph.launch()
     timer.stop()
     graph_ms = timer.ms() / steps
-    graph.destroy()
     # per-layer times (for the roofline table)
     per = []
     for (shape, d, _) in layers:
@@ -205,9 +222,28 @@ def bench_resnet18(om, steps: int, warmup: int, batch: int = 32):
                     "roof_frac": round(roof / lms, 3)})
     flops = sum(conv_flops(sh, batch) for sh, _, _ in layers)
     roof_ms = sum(max(conv_flops(sh, batch) / PEAK_FP32, conv_bytes(sh, batch) / PEAK_HBM) for sh, _, _ in layers) * 1e3
+    return ms, flops, roof_ms, per, graph_ms, (forward, graph)
+
+
+def resnet18_checks(om, layers, run, batch: int = 32):
+    """After the timed GPU legs: the graph replay's outputs against an eager
+    pass's, bit for bit (every output is overwritten per pass), and two images
+    of three layers kept for the CPU check."""
+    forward, graph = run
+    forward()
+    eager_out = [d["y"].numpy() for _, d, _ in layers]
+    graph.launch()
+    om.synchronize()
+    same = all(np.array_equal(d["y"].numpy().view(np.uint32), e.view(np.uint32))
+               for (_, d, _), e in zip(layers, eager_out))
+    graph.destroy()
     # outputs of two images of three layers, checked on the CPU
-    samples = [(idx, layers[idx][1]["y"].numpy()[[0, batch - 1]]) for idx in RESNET18_CHECKED]
-    return ms, flops, roof_ms, per, samples, graph_ms, same
+    samples = []
+    for idx in RESNET18_CHECKED:   # images 0 and batch-1 only (the next leg starts with no long host gap)
+        y = layers[idx][1]["y"]
+        per_img = int(np.prod(y.shape[1:]))
+        samples.append((idx, read_rows(om, y, [0, batch - 1], per_img).reshape((2,) + tuple(y.shape[1:]))))
+    return samples, same
 
 
 def bench_resnet18_net(om, steps: int, warmup: int, batch: int = 32):
@@ -314,11 +350,9 @@ def cpu_baseline_resnet18_net(n_img: int = 2, reps: int = 3):
     return kind, n_img / float(np.median(f)), n_img / float(np.median(t)), float(np.median(f)), float(np.median(t))
 
 
-def bench_resnet50(om, steps: int, warmup: int, batch: int = 64):
-    """ResNet-50 conv stack forward (53 convs, fused conv+BN+ReLU) at batch 64."""
-    from omnimatchdeeplearningtool_amd.hiptime import StreamTimer
-    from resnet_shapes import conv_bytes, conv_flops, out_hw, resnet50_convs
-    H = om.HIPBackend
+def resnet50_setup(om, batch: int = 64):
+    """The 53 ResNet-50 conv layers' seeded inputs, uploaded to HBM."""
+    from resnet_shapes import out_hw, resnet50_convs
     layers = []
     for li, (name, cin, h, w, cout, k, s, p) in enumerate(resnet50_convs()):
         bnd = np.sqrt(6.0 / (cin * k * k))
@@ -329,6 +363,14 @@ def bench_resnet50(om, steps: int, warmup: int, batch: int = 64):
                                                        syn.randn((cout,), 1100 + li, 0.1), syn.uniform((cout,), 1200 + li, 0.5, 1.5))]
         y = om.DeviceBuffer.empty((batch, cout, ho, wo))
         layers.append(((name, cin, h, w, cout, k, s, p), x, wt, bn, y))
+    return layers
+
+
+def bench_resnet50(om, layers, steps: int, warmup: int, batch: int = 64):
+    """ResNet-50 conv stack forward (53 convs, fused conv+BN+ReLU) at batch 64."""
+    from omnimatchdeeplearningtool_amd.hiptime import StreamTimer
+    from resnet_shapes import conv_bytes, conv_flops
+    H = om.HIPBackend
 
     def forward():
         for (name, cin, h, w, cout, k, s, p), x, wt, bn, y in layers:
@@ -783,20 +825,36 @@ def main():
     dev = om.device_name(0)
     log(f"device {dev}")
 
-    log(f"gemm 4096^3 NN: warmup {args.warmup}, steps {args.steps}")
-    ms, flops, wall, gemm_rows = bench_gemm(om, args.steps, args.warmup)
+    # The headline GEMM is timed right after the sweep (whose last shapes are
+    # the 8192^3 products), and the two conv stacks right after it, all inputs
+    # uploaded before the sweep: an MI355X that has been idle needs about 20
+    # ms of load before its clocks settle (4096^3 with 5 warm-up launches after
+    # 0.5 s idle: 129-132 TFLOP/s; after 30 ms of other GEMMs, or with 25
+    # warm-up launches: 140), and host work between the legs (generating the
+    # next leg's inputs) would leave it idle again.
+    gemm_bufs = gemm_inputs(om)
+    r18_layers = resnet18_setup(om, 32)
+    r50_layers = resnet50_setup(om, 64)
+    sweep, sweep_samples = bench_gemm_sweep(om, args.steps, 2)
+
+    log(f"gemm 4096^3 NN: warmup {args.warmup}, steps {args.steps} (timed right after the sweep)")
+    ms, flops, wall, gemm_rows = bench_gemm(om, gemm_bufs, args.steps, args.warmup)
     tflops = flops / ms / 1e9
     log(f"gemm {ms:.4f} ms/step  {tflops:.1f} TFLOP/s")
 
-    sweep, sweep_samples = bench_gemm_sweep(om, args.steps, 2)
-
     log("resnet18 conv stack b32")
     r_steps = max(5, args.steps // 2)
-    r_ms, r_flops, r_roof_ms, per, conv_samples, r_graph_ms, r_graph_same = bench_resnet18(
-        om, r_steps, max(2, args.warmup))
+    r_ms, r_flops, r_roof_ms, per, r_graph_ms, r18_run = bench_resnet18(om, r18_layers, r_steps, max(2, args.warmup))
     img_s = 32.0 / (r_ms / 1e3)
     log(f"resnet18 {r_ms:.3f} ms/batch  {img_s:.0f} img/s  roof frac {r_roof_ms / r_ms:.3f}; graph replay "
-        f"{r_graph_ms:.3f} ms, roof frac {r_roof_ms / r_graph_ms:.3f} (bit-identical {r_graph_same})")
+        f"{r_graph_ms:.3f} ms, roof frac {r_roof_ms / r_graph_ms:.3f}")
+
+    log("resnet50 conv stack b64")
+    r50_ms, r50_flops, r50_roof = bench_resnet50(om, r50_layers, max(3, args.steps // 10), 1)
+    log(f"resnet50 {r50_ms:.3f} ms/batch  {64 / r50_ms * 1e3:.0f} img/s  roof frac {r50_roof / r50_ms:.3f}")
+    del r50_layers
+    conv_samples, r_graph_same = resnet18_checks(om, r18_layers, r18_run)
+    log(f"resnet18 graph replay bit-identical to eager: {r_graph_same}")
 
     log("resnet18 network b32 (inference forward, training step)")
     n_fwd_ms, n_fl, n_logits2, n_train_ms, n_train_fl = bench_resnet18_net(om, max(5, args.steps // 5), 2)
@@ -808,9 +866,6 @@ def main():
     log(f"inferBatch {infer['img_s']:.0f} img/s end to end; resident forward {infer['resident_forward']['ms']:.3f} ms, "
         f"graph replay {infer['resident_forward_graph']['ms']:.3f} ms")
 
-    log("resnet50 conv stack b64")
-    r50_ms, r50_flops, r50_roof = bench_resnet50(om, max(3, args.steps // 10), 1)
-    log(f"resnet50 {r50_ms:.3f} ms/batch  {64 / r50_ms * 1e3:.0f} img/s  roof frac {r50_roof / r50_ms:.3f}")
     vit = {}
     for bf in (False, True):
         v_ms, v_flops, v_per, v_fused, v_mha = bench_vit_half(om, max(5, args.steps // 5), 2, bf)
@@ -891,7 +946,9 @@ def main():
         "dtype": "fp32",
         "data": "synthetic (seeded N(0,1) matrices; seeded N(0,1) images, Kaiming-uniform weights, seeded BN stats)",
         "config": {"workload": "fp32 GEMM 4096x4096x4096, row-major A[M,K] x B[K,N] (CPUBackend::matmul layout)",
-                   "M": M, "N": N, "K": K, "layout": "NN", "device": dev},
+                   "M": M, "N": N, "K": K, "layout": "NN", "device": dev,
+                   "timed": "right after the fp32 GEMM sweep (last shape 8192^3), inputs uploaded before it: "
+                            "an idle MI355X needs ~20 ms of load before its clocks settle"},
         "pct_mfma_peak": round(100.0 * tflops * 1e12 / PEAK_FP32, 1),
         "roofline": {"bound": "mfma", "achieved": round(flops / gemm_kernel_ms / 1e9, 2), "peak": 157.3,
                      "unit": "TFLOP/s", "frac": round(flops / gemm_kernel_ms / 1e9 / 157.3, 4),
