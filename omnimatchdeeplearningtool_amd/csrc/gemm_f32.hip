@@ -337,9 +337,9 @@ struct GemmPlan {
 // splitting the 128x128 tile until every CU had one workgroup): 128 x 4096 x
 // 4096 86 (76), 64 x 4096 x 4096 69 (56), 128 x 1024 x 4096 47 (29),
 // 512 x 1024 x 2048 72 (56), 256 x 4096 x 4096 96 (75). With 512 <= K <
-// 1024 only grids of at most CUs / 8 tiles split (pieces of >= 128 of K:
+// 1024 only grids of at most CUs / 4 tiles split (pieces of >= 128 of K:
 // 128 x 256 x 784, the MLP's first layer, 18.9 -> 11.5 us; 256 x 512 x 768
-// 18.9 -> 12.8); shorter K runs faster unsplit. The partials of a plan stay
+// 18.9 -> 12.8; 512^3 14.2 -> 11.7); shorter K runs faster unsplit. The partials of a plan stay
 // below 4 x CUs tiles of 64 x 64 floats (16 MiB on 256 CUs).
 static GemmPlan planGemm(int M, int N, int K, int batch, bool wsOk) {
     const long long cus = cuCount();
@@ -347,8 +347,8 @@ static GemmPlan planGemm(int M, int N, int K, int batch, bool wsOk) {
     if (tiles(256, 256) >= cus) return {0, 1};
     if (tiles(128, 128) >= cus) return {1, 1};
     const long long t = tiles(64, 64);
-    if (t >= 2 * cus || !wsOk || K < 512 || (K < 1024 && t * 8 > cus)) return {2, 1};
-    if (K < 1024) {   // very few tiles (at most CUs / 8): splits of >= 128 of K
+    if (t >= 2 * cus || !wsOk || K < 512 || (K < 1024 && t * 4 > cus)) return {2, 1};
+    if (K < 1024) {   // very few tiles (at most CUs / 4): splits of >= 128 of K
         int s = 1;
         while (s < 64 && t * s < 2 * cus && K / (2 * s) >= 128) s *= 2;
         return {2, s};
