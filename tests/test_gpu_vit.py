@@ -45,7 +45,10 @@ def _from_bits(u, bf16):
     return (u.astype(np.uint32) << 16).view(np.float32) if bf16 else u.view(np.float16).astype(np.float32)
 
 
-LINEAR_SHAPES = [(394, 768, 2304), (394, 768, 768), (197, 3072, 768), (33, 40, 17), (128, 256, 260), (2, 3, 4)]
+# (4500, 96, 4100): 306 tiles of 256 x 256, more than one round on 256 CUs (the
+# register store path for fp32, the staged one for half output).
+LINEAR_SHAPES = [(394, 768, 2304), (394, 768, 768), (197, 3072, 768), (33, 40, 17), (128, 256, 260), (2, 3, 4),
+                 (4500, 96, 4100)]
 
 
 @pytest.mark.parametrize("bf16", [False, True], ids=["f16", "bf16"])
