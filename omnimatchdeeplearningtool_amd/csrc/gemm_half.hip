@@ -778,8 +778,12 @@ __device__ __forceinline__ void storeCompact(const HalfFastParams& p, const f32x
 // (fc2 76.7 -> 71.9 us); fp32 grids of several rounds were 2-4 % slower with
 // it and keep the register stores. LDS is wave-private after the block
 // barrier that ends the mainloop, and a wave's LDS accesses complete in order.
+// Compiled into the 256 x 256 tile (8 waves) only, where it was measured: in
+// the small tiles the extra path cost the register path its allocation
+// (batched P.V, 64 x 64 tiles: 28.8 -> 31.8 us).
 template <class Cfg>
 struct StagedStore {
+    static constexpr bool USED = Cfg::NT == 512;
     static constexpr int PF = Cfg::WN + 4;   // floats per staged row (bank offset 4 from row to row)
     static constexpr size_t LDS_BYTES = (size_t)(Cfg::NT / 64) * 32 * PF * sizeof(float);
 };
@@ -956,10 +960,12 @@ __global__ __launch_bounds__(Cfg::NT) void gemm_half_fast(HalfFastParams p) {
 
     const long long cb = batch * p.sC;
     if constexpr (SWAP) {
-        if (p.staged) {
-            __syncthreads();   // every wave is done reading the stages
-            storeStaged<Cfg, BF16>(p, acc, hsm, cb, m0, n0, wm, wn, li, h, lane, wave);
-            return;
+        if constexpr (StagedStore<Cfg>::USED) {
+            if (p.staged) {
+                __syncthreads();   // every wave is done reading the stages
+                storeStaged<Cfg, BF16>(p, acc, hsm, cb, m0, n0, wm, wn, li, h, lane, wave);
+                return;
+            }
         }
         // Lane (li, h) holds, for block (fm, fn), C[m][n .. n+3] at
         // m = mBase + li, n = nBase + 8*g + 4*h (registers 4g .. 4g+3).
@@ -1016,8 +1022,9 @@ using FCfgS = FCfg<64, 64, 64, 32, 32>;
 template <class Cfg, bool BF16, bool TA, bool TB, bool SWAP, bool RAG>
 static int launchFast(HalfFastParams prm, int batch) {
     auto kern = gemm_half_fast<Cfg, BF16, TA, TB, SWAP, RAG>;
-    constexpr size_t lds = SWAP ? std::max(HalfOps<Cfg, TA, TB, RAG>::LDS_BYTES, StagedStore<Cfg>::LDS_BYTES)
-                                : HalfOps<Cfg, TA, TB, RAG>::LDS_BYTES;
+    constexpr bool stageable = SWAP && StagedStore<Cfg>::USED;
+    constexpr size_t lds = stageable ? std::max(HalfOps<Cfg, TA, TB, RAG>::LDS_BYTES, StagedStore<Cfg>::LDS_BYTES)
+                                     : HalfOps<Cfg, TA, TB, RAG>::LDS_BYTES;
     OMHIP_CHECK(OMHIP_SET_MAX_DYNAMIC_LDS_ONCE(kern, lds));
     prm.tilesM = (prm.M + Cfg::BM - 1) / Cfg::BM;
     prm.tilesN = (prm.N + Cfg::BN - 1) / Cfg::BN;
@@ -1025,7 +1032,7 @@ static int launchFast(HalfFastParams prm, int batch) {
     prm.batch = batch;
     prm.flat = batch > 1 && tiles * batch * Cfg::NT < (1LL << 31);
     prm.compact = !SWAP && prm.compact && tiles == 1;
-    prm.staged = SWAP && (prm.outHalf || tiles * batch <= cuCount());
+    prm.staged = stageable && (prm.outHalf || tiles * batch <= cuCount());
     const dim3 grid = prm.flat ? dim3((unsigned)(tiles * batch)) : dim3((unsigned)tiles, 1, batch);
     hipLaunchKernelGGL(kern, grid, dim3(Cfg::NT), lds, stream(), prm);
     OMHIP_CHECK_LAUNCH();
