@@ -779,9 +779,10 @@ def traffic_probe():
 
 
 def workload_probe(name: str):
-    """A short dispatch sequence for kernel-trace profiling (no timing, no JSON):
+    """A short dispatch sequence for kernel-trace profiling (no JSON):
     resnet18_train — three ResNet-18 b32 training steps; vit_attention — ten fused
-    attentions (ViT-B/16 b64, fp16) after the ten Q.K^T / P.V batched products they replace."""
+    attentions (ViT-B/16 b64, fp16) after the ten Q.K^T / P.V batched products they replace;
+    half_power — the fp16 GEMM on constant and on random operands (same kernel and shape)."""
     import omnimatchdeeplearningtool_amd as om
     om.init(0)
     H = om.HIPBackend
@@ -808,6 +809,32 @@ def workload_probe(name: str):
             H.gemmStridedBatchedHalf(0, 0, 0, b * heads, S, dh, S, p16, S, S * S, q, dh, S * dh, pv, dh, S * dh)
         for _ in range(10):
             H.attentionHalf(qkv, ctx, b, S, heads, dh, 0.125, outHalf=True)
+    elif name == "half_power":
+        # One kernel and one shape (fp16 NT 8192^3, A times its own transpose), two
+        # operand sets: every element 1.0, and N(0,1). The instruction stream is the
+        # same; only the bit activity of the data differs. Blocks of ten launches
+        # alternate after a warm-up so the clock ramp of an idle GPU is not counted.
+        from omnimatchdeeplearningtool_amd.hiptime import StreamTimer
+        n = 8192
+        sets = {}
+        for tag, host in (("ones", np.ones(n * n, np.float32)), ("randn", syn.randn((n * n,), 11))):
+            src = om.DeviceBuffer.from_numpy(host)
+            sets[tag] = om.DeviceBuffer.empty((n * n,), np.uint16)
+            H.convertToHalf(src, sets[tag], n * n)
+            src.free()
+        c = om.DeviceBuffer.empty((n * n,))
+        run = lambda a: H.gemmStridedBatchedHalf(0, 0, 1, 1, n, n, n, a, n, 0, a, n, 0, c, n, 0)
+        for _ in range(20):
+            run(sets["randn"])
+        om.synchronize()
+        for tag in ("ones", "randn", "ones", "randn"):
+            t = StreamTimer(om.stream_handle())
+            t.start()
+            for _ in range(10):
+                run(sets[tag])
+            t.stop()
+            ms = t.ms() / 10
+            log(f"half_power {tag}: {ms * 1e3:.1f} us per launch, {2.0 * n ** 3 / ms / 1e9:.0f} TFLOP/s")
     else:
         raise SystemExit(f"unknown probe {name}")
     om.synchronize()
@@ -820,7 +847,7 @@ def main():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--probe", choices=["resnet18_train", "vit_attention"],
+    ap.add_argument("--probe", choices=["resnet18_train", "vit_attention", "half_power"],
                     help="run only a short dispatch sequence for kernel-trace profiling (no JSON line)")
     ap.add_argument("--traffic-probe", action="store_true",
                     help="run only the dispatch sequence profiled for HBM traffic (no JSON line)")
