@@ -66,14 +66,18 @@ GEMM_ROWS = np.r_[0:4, 2046:2050, 4092:4096]   # rows of the 4096^3 product chec
 
 
 def settle(om, fn, seconds: float = 0.03) -> None:
-    """Runs fn (and waits for it) back to back for at least `seconds`, untimed: an
-    MI355X that has been idle needs about 20 ms of load before its clocks settle,
-    and the secondary legs start after host set-up. (The headline leg keeps
-    exactly its W warm-up steps: it follows the sweep with no idle gap.)"""
+    """Runs fn back to back for at least `seconds`, untimed: an MI355X that has been
+    idle needs about 20 ms of load before its clocks settle, and every leg but the
+    headline starts after host set-up (the headline keeps exactly its W warm-up steps:
+    it follows the sweep with no idle gap). Calls go out in doubling batches between
+    waits, so launches of a few microseconds also keep the GPU busy."""
     t0 = time.perf_counter()
+    batch = 1
     while time.perf_counter() - t0 < seconds:
-        fn()
+        for _ in range(batch):
+            fn()
         om.synchronize()
+        batch = min(2 * batch, 1024)
 
 
 def read_rows(om, buf, rows, ncols: int) -> np.ndarray:
@@ -133,6 +137,7 @@ def bench_gemm_sweep(om, steps: int, warmup: int):
             B = syn.randn((k, n) if layout == "NN" else (n, k), 22 + n)
             dB = om.DeviceBuffer.from_numpy(B)
             f = (lambda: H.matmul(dA, dB, dC, m, k, n)) if layout == "NN" else (lambda: H.matmulTransB(dA, dB, dC, m, k, n))
+            settle(om, f)   # the inputs were made on the host meanwhile: the GPU sat idle
             for _ in range(warmup):
                 f()
             om.synchronize()
