@@ -525,9 +525,10 @@ def bench_vit_half(om, steps: int, warmup: int, bf16: bool, proj_nt: bool = Fals
 def bench_mlp(om, steps: int, warmup: int, batch: int = 128):
     """MLP 784-256-128-10 (ReLU) training step, fp32, batch 128, labels uniform in 0..9:
     each Linear (+ ReLU) is one fused launch; softmax, cross-entropy and its gradient one
-    launch (tensorSoftmaxCrossEntropy + SoftmaxCrossEntropyBackward); the backward the
-    reference's TN / NT products for dW and dA on every layer, the bias gradients
-    (AddBiasBackward) and the ReLU gates. No optimizer update."""
+    launch (tensorSoftmaxCrossEntropy + SoftmaxCrossEntropyBackward); each layer's backward
+    one launch (omHipLinearBackward: the reference's TN / NT products for dW and dA, the bias
+    gradient of AddBiasBackward and the ReLU gate of the layer below, each element equal to
+    the separate entries'). No optimizer update."""
     from omnimatchdeeplearningtool_amd.hiptime import StreamTimer
     H = om.HIPBackend
     dims = [784, 256, 128, 10]
@@ -555,11 +556,11 @@ def bench_mlp(om, steps: int, warmup: int, batch: int = 128):
         H.softmaxCrossEntropy(z[2], T, None, loss, g[2], batch, 10)
         for j in reversed(range(3)):
             i, o = dims[j], dims[j + 1]
-            H.matmulTransA(a[j], g[j], gW[j], i, batch, o)        # dW = A^T G
-            H.addBiasBackward(g[j], gb[j], batch, o, 1)            # db = column sums of G
-            H.matmulTransB(g[j], Ws[j], gA[j], batch, o, i)        # dA = G W^T (as the reference, every layer)
-            if j > 0:
-                H.reluBackward(a[j], gA[j], g[j - 1], batch * i)   # a > 0 exactly where x W + b > 0
+            # dW = A^T G, db = column sums of G, dA = G W^T (as the reference, every layer);
+            # above the first layer dA goes through the ReLU gate below it (a > 0 exactly
+            # where x W + b > 0) straight into that layer's output gradient
+            H.linearBackward(a[j], g[j], Ws[j], a[j] if j > 0 else None, gW[j], gb[j],
+                             g[j - 1] if j > 0 else gA[0], batch, i, o)
 
     settle(om, step)
     for _ in range(warmup):
@@ -574,7 +575,7 @@ def bench_mlp(om, steps: int, warmup: int, batch: int = 128):
     # The same step replayed from a captured graph (its kernels unchanged; the
     # per-launch host cost is gone). Every output is overwritten per step, so
     # the replay's results must equal the eager step's bit for bit.
-    outs = gW + gA + gb + [loss]
+    outs = gW + [gA[0]] + g + gb + [loss]
     eager_out = [d.numpy().copy() for d in outs]
     graph = om.Graph(step)
     graph.launch()

@@ -179,6 +179,18 @@ int omHipMatmulTransA(const float* pA, const float* pB, float* pC, int nM, int n
  * the same sum, then + bias, then x > 0 ? x : 0. */
 int omHipLinearBiasAct(const float* pA, const float* pW, const float* pBias, float* pOut, int nM, int nK, int nN,
                        int nAct);
+/* NEW: a Linear layer's backward in one launch. From X [nBatch, nIn] (the layer's input),
+ * G [nBatch, nOut] (the gradient of its output) and W [nIn, nOut]:
+ *   pGradWeight [nIn, nOut] = X^T G            (MatMulBackward's dB half, autograd.ixx:276-286)
+ *   pGradBias   [nOut]      = column sums of G (AddBiasBackward, autograd.ixx:399-433; nullable)
+ *   pGradInput  [nBatch, nIn] = G W^T          (MatMulBackward's dA half, autograd.ixx:261-273; nullable)
+ * and, when pGate (the previous layer's ReLU output [nBatch, nIn]) is given, pGradInput is
+ * gated as omHipReLUBackward(pGate, G W^T) would gate it (cpu_backend.ixx:337-346): the
+ * ReLU backward of the layer below fused into the product. Every element equals the separate
+ * entries' value whenever their products do not split K (each output tile here sums K in
+ * one pass, in the same order). */
+int omHipLinearBackward(const float* pInput, const float* pGradOut, const float* pWeight, const float* pGate,
+                        float* pGradWeight, float* pGradBias, float* pGradInput, int nBatch, int nIn, int nOut);
 /* replaces omCudaBatchedMatmul (cuh:112): C[b] = A[b] * B[b], strides M*K, K*N, M*N
  * (CPUBackend::batchedMatmul cpu_backend.ixx:1520-1532) */
 int omHipBatchedMatmul(const float* pA, const float* pB, float* pC, int nBatch, int nM, int nK, int nN);

@@ -247,6 +247,15 @@ public:
                               int nN, int nAct) {
         check(omHipLinearBiasAct(pA, pW, pBias, pOut, nM, nK, nN, nAct), "linearBiasAct");
     }
+    // A Linear layer's backward in one launch: dW = X^T G, db = column sums of G, dX = G W^T
+    // gated by the previous layer's ReLU output when pGate is given (pGradBias, pGradInput and
+    // pGate nullable).
+    static void linearBackward(const float* pInput, const float* pGradOut, const float* pWeight, const float* pGate,
+                               float* pGradWeight, float* pGradBias, float* pGradInput, int nBatch, int nIn, int nOut) {
+        check(omHipLinearBackward(pInput, pGradOut, pWeight, pGate, pGradWeight, pGradBias, pGradInput, nBatch, nIn,
+                                  nOut),
+              "linearBackward");
+    }
     static void batchedMatmulTransB(const float* pA, const float* pB, float* pC, int nBatch, int nM, int nK, int nN) {
         check(omHipBatchedMatmulTransB(pA, pB, pC, nBatch, nM, nK, nN), "batchedMatmulTransB");
     }

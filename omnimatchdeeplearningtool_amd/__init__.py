@@ -93,6 +93,7 @@ _SIGS = {
     "omHipMatmulTransB": [_vp, _vp, _vp, _i, _i, _i],
     "omHipMatmulTransA": [_vp, _vp, _vp, _i, _i, _i],
     "omHipLinearBiasAct": [_vp, _vp, _vp, _vp, _i, _i, _i, _i],
+    "omHipLinearBackward": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i],
     "omHipBatchedMatmul": [_vp, _vp, _vp, _i, _i, _i, _i],
     "omHipBatchedMatmulTransB": [_vp, _vp, _vp, _i, _i, _i, _i],
     "omHipGemmStridedBatched": [_i, _i, _i, _i, _i, _i, _vp, _ll, _ll, _vp, _ll, _ll, _vp, _ll, _ll],
@@ -550,6 +551,15 @@ class HIPBackend:
     def linearBiasAct(pA, pW, pBias, pOut, nM: int, nK: int, nN: int, nAct: int) -> None:
         """act(A[M,K] * W[K,N] + bias[N]) in one pass (bias may be None; nAct 0 / 1 = ReLU)."""
         call("omHipLinearBiasAct", _ptr(pA), _ptr(pW), _ptr(pBias), _ptr(pOut), nM, nK, nN, nAct)
+
+    @staticmethod
+    def linearBackward(pInput, pGradOut, pWeight, pGate, pGradWeight, pGradBias, pGradInput, nBatch: int, nIn: int,
+                       nOut: int) -> None:
+        """A Linear layer's backward in one launch (MatMulBackward autograd.ixx:261-286, AddBiasBackward
+        :399-433, and the ReLU backward below it when pGate is given): dW = X^T G, db = column sums of
+        G, dX = G W^T (kept where pGate > 0)."""
+        call("omHipLinearBackward", _ptr(pInput), _ptr(pGradOut), _ptr(pWeight), _ptr(pGate), _ptr(pGradWeight),
+             _ptr(pGradBias), _ptr(pGradInput), nBatch, nIn, nOut)
 
     @staticmethod
     def batchedMatmulTransB(pA, pB, pC, nBatch: int, nM: int, nK: int, nN: int) -> None:

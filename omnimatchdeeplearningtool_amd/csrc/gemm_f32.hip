@@ -104,9 +104,15 @@ template <bool KMAJOR, int LK, int R, int BK, int NT>
 using GemmLoader = std::conditional_t<LK == 2, BufVecLoader<KMAJOR, R, BK, NT>,
                                       DenseLoaderAdapter<KMAJOR, LK == 1, R, BK, NT>>;
 
-template <class Cfg, bool TA, bool TB, int LA, int LB>
-__global__ __launch_bounds__(Cfg::NT) void gemm_f32_kernel(GemmF32Params p) {
-    extern __shared__ float smem[];
+// One output tile (bid: the tile's linear index, batch, split) of C =
+// op(A) * op(B). BSUM (B stored [K, N]): the workgroups of the first row of
+// tiles also add B's columns over K, row after row from 0, into p.colSum (the
+// bias gradient of a Linear layer whose output gradient is B). GATE: each
+// element of C is kept where p.gate (same shape, row stride p.ldg) is > 0 and
+// set to 0 elsewhere (a ReLU's backward applied to the product).
+template <class Cfg, bool TA, bool TB, int LA, int LB, bool BSUM = false, bool GATE = false>
+__device__ __forceinline__ void gemmF32Tile(const GemmF32Params& p, float* smem, int bid, long long batch, int split) {
+    static_assert(!BSUM || !TB, "column sums of a B stored [K, N]");
     constexpr bool A_KMAJOR = !TA;
     constexpr bool B_KMAJOR = TB;
     using SA = LdsShape<A_KMAJOR, Cfg::BM, Cfg::BK>;
@@ -120,14 +126,25 @@ __global__ __launch_bounds__(Cfg::NT) void gemm_f32_kernel(GemmF32Params p) {
     const int wn = wave % Cfg::WAVES_N;
 
     int tm, tn;
-    tile_coords(blockIdx.x, p.tilesM * p.tilesN, p.tilesM, p.tilesN, 8, tm, tn);
-    const long long batch = blockIdx.z;
-    const int split = blockIdx.y;
+    tile_coords(bid, p.tilesM * p.tilesN, p.tilesM, p.tilesN, 8, tm, tn);
     const int m0 = tm * Cfg::BM;
     const int n0 = tn * Cfg::BN;
     // This split's K range; the loaders treat kEnd as the end of K.
     const int kBeg = split * p.kChunk;
     const int kEnd = min(p.K, kBeg + p.kChunk);
+    // BSUM: thread tid < BN owns column n0 + tid; the slice at k0 is in the B
+    // region of an LDS stage as [BK][BN + 4].
+    const bool doSum = BSUM && p.colSum && tm == 0 && tid < Cfg::BN && n0 + tid < p.N;
+    float colAcc = 0.f;
+    auto colSum = [&](const float* sB, int k0) {
+        if constexpr (BSUM) {
+            if (doSum) {
+#pragma unroll
+                for (int k = 0; k < Cfg::BK; ++k)
+                    if (k0 + k < kEnd) colAcc += sB[k * SB::LD + tid];
+            }
+        }
+    };
 
     GemmLoader<A_KMAJOR, LA, Cfg::BM, Cfg::BK, Cfg::NT> la;
     la.init(p.A + batch * p.sA, p.lda, p.M, m0, tid);
@@ -160,6 +177,7 @@ __global__ __launch_bounds__(Cfg::NT) void gemm_f32_kernel(GemmF32Params p) {
         la.template load<true>(kBeg + (t + 1) * Cfg::BK, kEnd, tid);
         lb.template load<true>(kBeg + (t + 1) * Cfg::BK, kEnd, tid);
         __builtin_amdgcn_sched_barrier(0);
+        colSum(smem + SA::SIZE, kBeg + t * Cfg::BK);
         mma_slice_split<Cfg, A_KMAJOR, B_KMAJOR>(smem, smem + SA::SIZE, acc, wm, wn, lane, [&] {
             la.store(smem + STAGE, tid);
             lb.store(smem + STAGE + SA::SIZE, tid);
@@ -168,6 +186,7 @@ __global__ __launch_bounds__(Cfg::NT) void gemm_f32_kernel(GemmF32Params p) {
         la.template load<true>(kBeg + (t + 2) * Cfg::BK, kEnd, tid);
         lb.template load<true>(kBeg + (t + 2) * Cfg::BK, kEnd, tid);
         __builtin_amdgcn_sched_barrier(0);
+        colSum(smem + STAGE + SA::SIZE, kBeg + (t + 1) * Cfg::BK);
         mma_slice_split<Cfg, A_KMAJOR, B_KMAJOR>(smem + STAGE, smem + STAGE + SA::SIZE, acc, wm, wn, lane, [&] {
             la.store(smem, tid);
             lb.store(smem + SA::SIZE, tid);
@@ -181,6 +200,7 @@ __global__ __launch_bounds__(Cfg::NT) void gemm_f32_kernel(GemmF32Params p) {
                 la.template load<false>(kBeg + (t + 1) * Cfg::BK, kEnd, tid);
                 lb.template load<false>(kBeg + (t + 1) * Cfg::BK, kEnd, tid);
             }
+            colSum(smem + SA::SIZE, kBeg + t * Cfg::BK);
             mma_slice<Cfg, A_KMAJOR, B_KMAJOR>(smem, smem + SA::SIZE, acc, wm, wn, lane);
             if (more) {
                 la.store(smem + STAGE, tid);
@@ -194,6 +214,7 @@ __global__ __launch_bounds__(Cfg::NT) void gemm_f32_kernel(GemmF32Params p) {
                 la.template load<false>(kBeg + (t + 2) * Cfg::BK, kEnd, tid);
                 lb.template load<false>(kBeg + (t + 2) * Cfg::BK, kEnd, tid);
             }
+            colSum(smem + STAGE + SA::SIZE, kBeg + (t + 1) * Cfg::BK);
             mma_slice<Cfg, A_KMAJOR, B_KMAJOR>(smem + STAGE, smem + STAGE + SA::SIZE, acc, wm, wn, lane);
             if (more) {
                 la.store(smem, tid);
@@ -212,6 +233,9 @@ __global__ __launch_bounds__(Cfg::NT) void gemm_f32_kernel(GemmF32Params p) {
     // finish applies them to partial products' sum).
     const bool bias = !partial && p.bias != nullptr;
     const bool relu = !partial && p.act == 1;
+    if constexpr (BSUM) {
+        if (doSum) p.colSum[n0 + tid] = colAcc;
+    }
 #pragma unroll
     for (int fm = 0; fm < Cfg::FM; ++fm) {
 #pragma unroll
@@ -225,10 +249,19 @@ __global__ __launch_bounds__(Cfg::NT) void gemm_f32_kernel(GemmF32Params p) {
                 float v = acc[fm][fn][r];
                 if (bias) v += b;
                 if (relu) v = v > 0.f ? v : 0.f;
-                if (row < p.M) C[(long long)row * ldc + col] = v;
+                if (row < p.M) {
+                    if constexpr (GATE) v = p.gate[(long long)row * p.ldg + col] > 0.f ? v : 0.f;
+                    C[(long long)row * ldc + col] = v;
+                }
             }
         }
     }
+}
+
+template <class Cfg, bool TA, bool TB, int LA, int LB>
+__global__ __launch_bounds__(Cfg::NT) void gemm_f32_kernel(GemmF32Params p) {
+    extern __shared__ float smem[];
+    gemmF32Tile<Cfg, TA, TB, LA, LB>(p, smem, blockIdx.x, blockIdx.z, blockIdx.y);
 }
 
 // Sums the partials of every split in split order and writes C (+ bias, act).
@@ -463,6 +496,56 @@ int gemmF32Checked(const char* name, bool ta, bool tb, int batch, int M, int N, 
     return gemmF32(ta, tb, batch, M, N, K, A, lda, sA, B, ldb, sB, C, ldc, sC);
 }
 
+// ---- Linear backward in one launch -------------------------------------------
+// Workgroups [0, tilesW) compute dW = X^T G over 64 x 64 tiles, those of the
+// first tile row also adding G's columns into db (BSUM); the rest compute
+// dX = G W^T, kept where the gate is > 0 when one is given (GATE). K is not
+// split, so every element is the same sum, in the same order, as the separate
+// products compute whenever they do not split K either (e.g. every layer of the
+// 784-256-128-10 MLP at batch 128).
+template <int LK, bool GATE>
+__global__ __launch_bounds__(CfgS::NT) void linear_backward_kernel(GemmF32Params pw, GemmF32Params pa, int tilesW) {
+    extern __shared__ float smem[];
+    if ((int)blockIdx.x < tilesW)
+        gemmF32Tile<CfgS, true, false, LK, LK, true, false>(pw, smem, blockIdx.x, 0, 0);
+    else
+        gemmF32Tile<CfgS, false, true, LK, LK, false, GATE>(pa, smem, blockIdx.x - tilesW, 0, 0);
+}
+
+template <int LK, bool GATE>
+static int launchLinearBackward(const GemmF32Params& pw, const GemmF32Params& pa, int tilesW, int tilesX) {
+    auto kern = linear_backward_kernel<LK, GATE>;
+    const size_t lds = std::max(ldsBytesFor<CfgS, true, false>(), ldsBytesFor<CfgS, false, true>());
+    OMHIP_CHECK(OMHIP_SET_MAX_DYNAMIC_LDS_ONCE(kern, lds));
+    hipLaunchKernelGGL(kern, dim3(tilesW + tilesX), dim3(CfgS::NT), lds, stream(), pw, pa, tilesW);
+    OMHIP_CHECK_LAUNCH();
+    return 0;
+}
+
+static int linearBackward(const float* X, const float* G, const float* W, const float* gate, float* dW, float* db,
+                          float* dX, int B, int I, int O) {
+    GemmF32Params pw{}, pa{};
+    // dW [I, O] = X^T G: A = X stored [K = B, M = I], B = G stored [K = B, N = O]
+    pw.A = X; pw.B = G; pw.C = dW; pw.M = I; pw.N = O; pw.K = B;
+    pw.lda = I; pw.ldb = O; pw.ldc = O; pw.kChunk = B; pw.colSum = db;
+    pw.tilesM = (I + CfgS::BM - 1) / CfgS::BM; pw.tilesN = (O + CfgS::BN - 1) / CfgS::BN;
+    // dX [B, I] = G W^T: A = G stored [M = B, K = O], B = W stored [N = I, K = O]
+    pa.A = G; pa.B = W; pa.C = dX; pa.M = B; pa.N = I; pa.K = O;
+    pa.lda = O; pa.ldb = O; pa.ldc = I; pa.kChunk = O; pa.gate = gate; pa.ldg = I;
+    pa.tilesM = (B + CfgS::BM - 1) / CfgS::BM; pa.tilesN = (I + CfgS::BN - 1) / CfgS::BN;
+    const long long tilesW = (long long)pw.tilesM * pw.tilesN, tilesX = dX ? (long long)pa.tilesM * pa.tilesN : 0;
+    if (tilesW + tilesX > 0x7fffffffLL) return fail("omHipLinearBackward: %lld tiles exceed the grid", tilesW + tilesX);
+    // 16-byte operand loads: every operand's contiguous axis (I or O) and base in whole vectors
+    bool vec = I % 4 == 0 && O % 4 == 0 && aligned16(X) && aligned16(G) && (!dX || aligned16(W));
+    vec = vec && bufVecOk<false, CfgS::BM, CfgS::BK>(true, I) && bufVecOk<false, CfgS::BN, CfgS::BK>(true, O) &&
+          bufVecOk<true, CfgS::BM, CfgS::BK>(true, O) && bufVecOk<true, CfgS::BN, CfgS::BK>(true, O);
+    if (vec)
+        return gate ? launchLinearBackward<2, true>(pw, pa, (int)tilesW, (int)tilesX)
+                    : launchLinearBackward<2, false>(pw, pa, (int)tilesW, (int)tilesX);
+    return gate ? launchLinearBackward<0, true>(pw, pa, (int)tilesW, (int)tilesX)
+                : launchLinearBackward<0, false>(pw, pa, (int)tilesW, (int)tilesX);
+}
+
 // ---- fixed scratch of the no-allocation entry ---------------------------------
 // Split-K partial sums of omHipGemmStridedBatchedNoAlloc live in this array,
 // so that entry never allocates. A plan splits K only over 64 x 64 tiles and
@@ -540,6 +623,31 @@ int omHipLinearBiasAct(const float* pA, const float* pW, const float* pBias, flo
         return 0;
     }
     return gemmF32(false, false, 1, nM, nN, nK, pA, nK, 0, pW, nN, 0, pOut, nN, 0, pBias, nAct);
+}
+
+int omHipLinearBackward(const float* pInput, const float* pGradOut, const float* pWeight, const float* pGate,
+                        float* pGradWeight, float* pGradBias, float* pGradInput, int nBatch, int nIn, int nOut) {
+    clearError();
+    if (nBatch < 0 || nIn < 0 || nOut < 0) return fail("omHipLinearBackward: negative size");
+    if (!pGradWeight && nIn > 0 && nOut > 0) return fail("omHipLinearBackward: null weight gradient");
+    if (pGradInput && nBatch > 0 && nIn > 0 && nOut > 0 && !pWeight) return fail("omHipLinearBackward: null weight");
+    if (nBatch == 0 || nIn == 0 || nOut == 0 || !pInput || !pGradOut) {
+        // some product has no terms or no elements: the separate entries, whose degenerate cases match the chain's
+        if (omHipMatmulTransA(pInput, pGradOut, pGradWeight, nIn, nBatch, nOut)) return -1;
+        if (pGradBias && omHipAddBiasBackward(pGradOut, pGradBias, nBatch, nOut, 1)) return -1;
+        if (pGradInput) {
+            if (omHipMatmulTransB(pGradOut, pWeight, pGradInput, nBatch, nOut, nIn)) return -1;
+            if (pGate) {
+                const long long total = (long long)nBatch * nIn;
+                for (long long off = 0; off < total; off += 1LL << 30)
+                    if (omHipReLUBackward(pGate + off, pGradInput + off, pGradInput + off,
+                                          (int)std::min(total - off, 1LL << 30)))
+                        return -1;
+            }
+        }
+        return 0;
+    }
+    return linearBackward(pInput, pGradOut, pWeight, pGate, pGradWeight, pGradBias, pGradInput, nBatch, nIn, nOut);
 }
 
 int omHipBatchedMatmul(const float* pA, const float* pB, float* pC, int nBatch, int nM, int nK, int nN) {

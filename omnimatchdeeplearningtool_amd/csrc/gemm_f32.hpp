@@ -16,6 +16,9 @@ struct GemmF32Params {
     float* ws;              // split-K partials [split][batch][M][N] (null: write C directly)
     const float* bias;      // [N] added to every row of C, or null
     int act;                // 0 identity, 1 ReLU (after the bias)
+    const float* gate;      // Linear backward: C kept where gate > 0 (row stride ldg)
+    long long ldg;
+    float* colSum;          // Linear backward: B's column sums (the bias gradient)
 };
 
 // C[b] = op(A[b]) * op(B[b]); ta: A stored [K,M]; tb: B stored [N,K].

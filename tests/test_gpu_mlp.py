@@ -136,3 +136,68 @@ def test_linear_bias_act(hip, M, K, N, act, with_bias):
         y = O.relu(y)
     C64, bound = O.gemm_f64(A, W)
     assert O.normalized_error(got, y, bound + (np.abs(b)[None, :] if with_bias else 0)) <= TOL
+
+
+# (batch, in, out): the three MLP layers at batch 128, ragged sizes, sizes that are not
+# whole 16-byte vectors (scalar loaders) and a batch above one K slice of 16 rows.
+LINEAR_BACKWARD_SHAPES = [(128, 784, 256), (128, 256, 128), (128, 128, 10), (37, 50, 3), (64, 64, 64), (5, 130, 66),
+                          (300, 96, 40)]
+
+
+@pytest.mark.parametrize("nb,ni,no", LINEAR_BACKWARD_SHAPES, ids=lambda v: str(v))
+@pytest.mark.parametrize("gated", [False, True], ids=["plain", "relu_gate"])
+def test_linear_backward(hip, nb, ni, no, gated):
+    """omHipLinearBackward (dW = X^T G, db = column sums of G, dX = G W^T, gated by the layer
+    below's ReLU output) against the separate entries it fuses, bit for bit (none of these
+    products splits K), and against the oracle within the K-scaled bound."""
+    H = hip.HIPBackend
+    x = O.randn((nb, ni), nb + ni)
+    x[x < 0] *= 0.0   # a ReLU output: the gate of the layer below (zeros where it was inactive)
+    g = O.randn((nb, no), nb + no + 1)
+    w = _kaiming_uniform(ni, no, ni + no)
+    dx_, dg, dw = to_dev(hip, x), to_dev(hip, g), to_dev(hip, w)
+    gW, gb, gX = empty_dev(hip, (ni, no)), empty_dev(hip, (no,)), empty_dev(hip, (nb, ni))
+    H.linearBackward(dx_, dg, dw, dx_ if gated else None, gW, gb, gX, nb, ni, no)
+    # the separate entries
+    cW, cb, cX = empty_dev(hip, (ni, no)), empty_dev(hip, (no,)), empty_dev(hip, (nb, ni))
+    H.matmulTransA(dx_, dg, cW, ni, nb, no)
+    H.addBiasBackward(dg, cb, nb, no, 1)
+    H.matmulTransB(dg, dw, cX, nb, no, ni)
+    if gated:
+        H.reluBackward(dx_, cX, cX, nb * ni)
+    for got, want in ((gW, cW), (gb, cb), (gX, cX)):
+        assert np.array_equal(got.numpy().view(np.uint32), want.numpy().view(np.uint32))
+    # the oracle
+    refW, bW = O.gemm_f64(x, g, transA=True)
+    assert O.normalized_error(gW.numpy(), refW, bW) <= TOL
+    assert np.array_equal(gb.numpy(), O.add_bias_backward(g, nb, no))   # rows added in order from 0
+    refX, bX = O.gemm_f64(g, w, transB=True)
+    if gated:
+        refX = np.where(x > 0, refX, 0.0)
+    assert O.normalized_error(gX.numpy(), refX, bX) <= TOL
+
+
+def test_linear_backward_optional_outputs(hip):
+    """Null db / dX are skipped; the outputs that are asked for match the full call's."""
+    H = hip.HIPBackend
+    nb, ni, no = 96, 72, 40
+    x, g, w = O.randn((nb, ni), 5), O.randn((nb, no), 6), O.randn((ni, no), 7)
+    dx_, dg, dw = to_dev(hip, x), to_dev(hip, g), to_dev(hip, w)
+    full = [empty_dev(hip, s) for s in ((ni, no), (no,), (nb, ni))]
+    H.linearBackward(dx_, dg, dw, None, *full, nb, ni, no)
+    only_w = empty_dev(hip, (ni, no))
+    H.linearBackward(dx_, dg, None, None, only_w, None, None, nb, ni, no)
+    assert np.array_equal(only_w.numpy(), full[0].numpy())
+
+
+def test_linear_backward_degenerate(hip):
+    """No rows: dW and db are zero. No output features: dX is zero (gated or not)."""
+    H = hip.HIPBackend
+    gW, gb = to_dev(hip, np.full((8, 4), 7.0, np.float32)), to_dev(hip, np.full((4,), 7.0, np.float32))
+    x, g, w = to_dev(hip, O.randn((1, 8), 1)), to_dev(hip, O.randn((1, 4), 2)), to_dev(hip, O.randn((8, 4), 3))
+    H.linearBackward(x, g, w, None, gW, gb, None, 0, 8, 4)
+    assert not gW.numpy().any() and not gb.numpy().any()
+    gX = to_dev(hip, np.full((3, 8), 7.0, np.float32))
+    xs = to_dev(hip, np.abs(O.randn((3, 8), 4)))
+    H.linearBackward(xs, g, w, xs, None, None, gX, 3, 8, 0)
+    assert not gX.numpy().any()
