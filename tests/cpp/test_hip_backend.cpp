@@ -165,6 +165,23 @@ static void testLinearBiasAct() {
     std::printf("LinearBiasAct done\n");
 }
 
+static void testLinearBackward() {
+    // x = [[1 2 0], [3 0 4]] (a ReLU output: batch 2, in 3), gY = [[1 -1], [2 0.5]] (out 2),
+    // W = [[1 0], [0 1], [1 1]] (in 3 x out 2): dW = x^T gY, db = column sums of gY,
+    // gX = (x > 0 ? gY W^T : 0)
+    Dev x(std::vector<float>{1, 2, 0, 3, 0, 4}), g(std::vector<float>{1, -1, 2, 0.5f});
+    Dev w(std::vector<float>{1, 0, 0, 1, 1, 1}), gw(6), gb(2), gx(6);
+    HIPBackend::linearBackward(x.p, g.p, w.p, x.p, gw.p, gb.p, gx.p, 2, 3, 2);
+    const float wantW[6] = {7, 0.5f, 2, -2, 8, 2}, wantX[6] = {1, -1, 0, 2, 0, 2.5f};
+    auto hw = gw.host(), hb = gb.host(), hx = gx.host();
+    for (int i = 0; i < 6; ++i) {
+        EXPECT_NEAR(hw[i], wantW[i], 0);
+        EXPECT_NEAR(hx[i], wantX[i], 0);
+    }
+    EXPECT_NEAR(hb[0], 3, 0); EXPECT_NEAR(hb[1], -0.5, 0);
+    std::printf("LinearBackward done\n");
+}
+
 int main() {
     try {
         HIPBackend::init(0);
@@ -173,6 +190,7 @@ int main() {
         testBatchedMatmulForward();
         testLinearZeroInput();
         testLinearBiasAct();
+        testLinearBackward();
         testConvAllOnes();
         testReluAndErrors();
         testTrainingPieces();
