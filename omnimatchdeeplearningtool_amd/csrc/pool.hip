@@ -333,6 +333,29 @@ __global__ void adaptive_avgpool_kernel(const float* __restrict__ x, float* __re
     }
 }
 
+// The global case (OH = OW = 1, a plane of at most kGlobalPoolMaxHW pixels: the
+// network's final pooling): a workgroup copies 64 consecutive planes into LDS
+// with coalesced loads, then each of 64 threads adds its plane in the order
+// above (rows, then columns, from 0) and divides by the count: the same
+// result, without a thread per plane striding over 64 planes per load.
+constexpr int kGlobalPoolPlanes = 64, kGlobalPoolMaxHW = 256;
+__global__ __launch_bounds__(256) void global_avgpool_kernel(const float* __restrict__ x, float* __restrict__ y,
+                                                             int NC, int HW) {
+    __shared__ float tile[kGlobalPoolPlanes * kGlobalPoolMaxHW];
+    const long long nc0 = (long long)blockIdx.x * kGlobalPoolPlanes;
+    const int planes = (int)min<long long>(kGlobalPoolPlanes, NC - nc0);
+    const int n = planes * HW;
+    const float* src = x + nc0 * HW;
+    for (int i = threadIdx.x; i < n; i += blockDim.x) tile[i] = src[i];
+    __syncthreads();
+    if ((int)threadIdx.x < planes) {
+        const float* t = tile + threadIdx.x * HW;
+        float sum = 0.f;
+        for (int i = 0; i < HW; ++i) sum += t[i];
+        y[nc0 + threadIdx.x] = sum / (float)HW;
+    }
+}
+
 // cpu_backend.ixx:1491-1510: the regions partition the input (each region's end
 // is the next one's start), so every input element takes gO / count of its one region.
 __global__ void adaptive_avgpool_backward_kernel(const float* __restrict__ gO, float* __restrict__ gI, int NC, int H,
@@ -487,6 +510,14 @@ int omHipAdaptiveAvgPool2d(const float* pIn, float* pOut, int nN, int nC, int nH
     if (nN <= 0 || nC <= 0 || nH <= 0 || nW <= 0 || nOutH <= 0 || nOutW <= 0)
         return fail("omHipAdaptiveAvgPool2d: invalid geometry");
     if (!pIn || !pOut) return fail("omHipAdaptiveAvgPool2d: null pointer");
+    const long long nc = (long long)nN * nC, hw = (long long)nH * nW;
+    if (nOutH == 1 && nOutW == 1 && hw <= kGlobalPoolMaxHW &&
+        (nc + kGlobalPoolPlanes - 1) / kGlobalPoolPlanes <= 0x7fffffffLL) {
+        hipLaunchKernelGGL(global_avgpool_kernel, dim3((unsigned)((nc + kGlobalPoolPlanes - 1) / kGlobalPoolPlanes)),
+                           dim3(256), 0, stream(), pIn, pOut, (int)nc, (int)hw);
+        OMHIP_CHECK_LAUNCH();
+        return 0;
+    }
     hipLaunchKernelGGL(adaptive_avgpool_kernel, dim3(gridFor((long long)nN * nC * nOutH * nOutW)), dim3(256), 0,
                        stream(), pIn, pOut, nN * nC, nH, nW, nOutH, nOutW);
     OMHIP_CHECK_LAUNCH();

@@ -98,7 +98,11 @@ def test_avgpool(hip, g):
     assert np.array_equal(bits(dgi.numpy()), bits(O.avgpool2d_backward(gO, H, W, K, s, p)))
 
 
-@pytest.mark.parametrize("g", [(2, 512, 7, 7, 1, 1), (2, 3, 11, 11, 3, 4), (1, 2, 2, 3, 3, 5), (2, 4, 9, 9, 9, 9)],
+# global pooling (1 x 1 output) through the LDS-staged path: the network's 7 x 7 planes, a
+# plane count that is not a multiple of 64 at the largest staged plane (16 x 16), and a
+# plane one row past it (the general kernel)
+@pytest.mark.parametrize("g", [(2, 512, 7, 7, 1, 1), (3, 37, 16, 16, 1, 1), (1, 5, 17, 16, 1, 1), (2, 3, 11, 11, 3, 4),
+                               (1, 2, 2, 3, 3, 5), (2, 4, 9, 9, 9, 9)],
                          ids=lambda g: "N{}C{}H{}W{}o{}x{}".format(*g))
 def test_adaptive_avgpool(hip, g):
     N, C, H, W, OH, OW = g
