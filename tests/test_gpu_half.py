@@ -216,3 +216,41 @@ def test_half_ragged_views(hip, transB, offA, offB):
             bm = Br[offB + b * sB:offB + b * sB + K * ldb].reshape(K, ldb)
         C64, bound = O.gemm_f64(a, bm, transB=bool(transB))
         assert O.normalized_error(C[b], C64, bound) <= 1e-4
+
+
+# 256 x 256 tiles in a single round (150 tiles on 256 CUs: the ViT-B/16 output projection over
+# 12608 tokens, and ragged M / N with a partial last K slice in the NT layout): fp32 output
+# leaves through the staged streaming store, as does the half output of the fused Linear.
+ONE_ROUND_SHAPES = [(12608, 768, 768, 0), (12603, 760, 1000, 1)]
+
+
+def _sample_rows(M):
+    return np.unique(np.concatenate([np.arange(0, M, 97), np.arange(M - 5, M)]))
+
+
+@pytest.mark.parametrize("bf16", [False, True], ids=["f16", "bf16"])
+@pytest.mark.parametrize("M,N,K,transB", ONE_ROUND_SHAPES, ids=lambda v: str(v))
+def test_half_one_round_staged(hip, bf16, M, N, K, transB):
+    """Against float64 on sampled rows of the rounded inputs (all columns), and the fused
+    Linear epilogue (bias, ReLU, half output) equal to gemm -> addBias -> relu -> convert."""
+    H = hip.HIPBackend
+    A = O.randn((M, K), M + K + 3)
+    B = O.randn((N, K) if transB else (K, N), N + 5, 0.02)
+    dA, dB = to_dev(hip, _bits(A, bf16)), to_dev(hip, _bits(B, bf16))
+    dt = 1 if bf16 else 0
+    C = empty_dev(hip, (M, N))
+    H.gemmStridedBatchedHalf(dt, 0, transB, 1, M, N, K, dA, K, 0, dB, K if transB else N, 0, C, N, 0)
+    c = C.numpy()
+    rows = _sample_rows(M)
+    Ar, Br = _round(A, bf16)[rows].astype(np.float64), _round(B, bf16).astype(np.float64)
+    Bm = Br.T if transB else Br
+    assert O.normalized_error(c[rows], Ar @ Bm, np.abs(Ar) @ np.abs(Bm)) <= 1e-4
+    bias = O.randn((N,), N + 11, 0.5)
+    db = to_dev(hip, bias)
+    out16 = empty_dev(hip, (M, N), np.uint16)
+    H.linearHalf(dA, dB, db, out16, M, K, N, bf16=bf16, transW=bool(transB), act=1, outHalf=True)
+    H.addBias(C, db, C, M, N)
+    H.relu(C, C, M * N)
+    chain16 = empty_dev(hip, (M, N), np.uint16)
+    H.convertToHalf(C, chain16, M * N, bf16=bf16)
+    assert np.array_equal(out16.numpy(), chain16.numpy())
