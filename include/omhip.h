@@ -45,15 +45,27 @@ int omHipSynchronize(void);
 int omHipSyncComputeStream(void);
 /* replaces omCudaCleanup (cuda_kernels.cuh:69): frees the pool, destroys the stream */
 int omHipCleanup(void);
+/* replaces omCudaForceReset (cuda_kernels.cu:429-438; EngineBridge's recovery call,
+ * src/engine/bridge/EngineBridge.cpp:143, :4047): waits for the whole device, clears the
+ * sticky HIP error, then releases what omHipCleanup releases (pool, workspaces, tables,
+ * streams) without resetting the device. Device pointers from omHipMalloc are invalid
+ * afterwards; the next call initialises the library again. */
+int omHipForceReset(void);
 /* NEW: the library stream as a hipStream_t (for event timing / interop) */
 int omHipGetStream(void** ppStream);
 /* NEW: route subsequent work to a caller-owned hipStream_t (NULL restores the
  * library stream). The caller keeps ownership of the stream. Each stream gets its own
- * split-K workspace (kept until omHipCleanup), so work on different streams may overlap. */
+ * split-K workspace (kept until omHipCleanup), so work on different streams may overlap.
+ * Memory and streams: omHipFree is ordered on the stream current at the free. Work later
+ * enqueued on that stream may receive the block at once; work on another stream receives it
+ * only after everything enqueued on the freeing stream before the free has finished (an
+ * event, no host wait). Work on a third stream that still reads the block at the free must be
+ * ordered before the free by the caller. */
 int omHipSetStream(void* pStream);
 /* NEW: the caller is done with a stream it passed to omHipSetStream (call before destroying
  * it): waits for the stream, returns its workspace to the pool (held back while any executable
- * graph exists) and, if it is the current stream, restores the library stream. */
+ * graph exists) and, if it is the current stream, restores the library stream. Fails (-1)
+ * while a graph captured on that stream exists: destroy such graphs first. */
 int omHipReleaseStream(void* pStream);
 /* NEW: message of the last failing call on this thread ("" if none) */
 const char* omHipGetLastError(void);
@@ -110,10 +122,12 @@ int omHipGraphBeginCapture(void);
 /* replaces omCudaGraphEndCapture (cuh:519): ends the recording, returns an executable graph */
 int omHipGraphEndCapture(void** ppGraphExec);
 /* replaces omCudaGraphLaunch (cuh:524): replays the graph on the stream it was captured on
- * (its nodes use that stream's workspace). While any executable graph exists, workspaces
+ * (its nodes use that stream's workspace), so that stream must still exist (omHipReleaseStream
+ * refuses to release it while the graph lives). While any executable graph exists, workspaces
  * the library outgrows are kept allocated, so a replay never touches reused memory. */
 int omHipGraphLaunch(void* pGraphExec);
-/* replaces omCudaGraphDestroy (cuh:528): waits for the graph's stream, then frees the graph */
+/* replaces omCudaGraphDestroy (cuh:528): waits for the device (not for the capture stream, which
+ * may be gone by then), then frees the graph */
 int omHipGraphDestroy(void* pGraphExec);
 
 /* ===== fills / copy (src/cuda/cuda_kernels.cuh:257-266; CPUBackend cpu_backend.ixx:65-77, :444-446) ===== */
@@ -160,6 +174,39 @@ int omHipSoftmaxCrossEntropy(const float* pLogits, const float* pTarget, float* 
  * rows are added in order from 0, bit-identical to the reference loop, up to 4096 rows (more
  * rows: 16 ordered parts). nHW > 1: a fixed-order reduction per channel. */
 int omHipAddBiasBackward(const float* pGradOut, float* pGradBias, int nN, int nC, int nHW);
+
+/* ===== global reductions (cuda_kernels.cuh:127-130) ===== */
+
+/* replaces omCudaSum (cuh:127; CUDABackend::sum om.hal.cuda_backend.ixx:732, called by
+ * tensorSum tensor_ops.ixx:409-440): pResult[0] (device) = sum of pData[0..nCount). The
+ * order is fixed (contiguous chunks, then the chunk sums), so repeated calls agree bit for
+ * bit; against CPUBackend::sum's sequential loop (cpu_backend.ixx:290-294) the difference is
+ * rounding only. nCount <= 0 writes 0. */
+int omHipSum(const float* pData, float* pResult, int nCount);
+/* replaces omCudaMean (cuh:130): the sum of omHipSum multiplied by 1.0f / nCount
+ * (cuda_kernels.cu:1506-1513); nCount <= 0 writes 0. */
+int omHipMean(const float* pData, float* pResult, int nCount);
+
+/* ===== ViT attention, fp32 (cuda_kernels.cuh:488-495) ===== */
+
+/* replaces omCudaQkvSplitHeads (cuh:488; CUDABackend::qkvSplitHeads om.hal.cuda_backend.ixx:967):
+ * pQkv [nBatch*nSeqLen, 3*D] (D = nHeads*nHeadDim, each token's row Q | K | V) ->
+ * pQ, pK, pV [nBatch*nHeads, nSeqLen, nHeadDim] with Q multiplied by fScale — the index maps
+ * of MultiHeadAttention::forward's CPU branch (vit.ixx:196-212), bit-identical. */
+int omHipQkvSplitHeads(const float* pQkv, float* pQ, float* pK, float* pV, int nBatch, int nSeqLen, int nHeads,
+                       int nHeadDim, float fScale);
+/* replaces omCudaMergeHeads (cuh:493; CUDABackend::mergeHeads om.hal.cuda_backend.ixx:977):
+ * pIn [nBatch*nHeads, nSeqLen, nHeadDim] -> pOut [nBatch*nSeqLen, nHeads*nHeadDim]
+ * (vit.ixx:220-232), bit-identical. */
+int omHipMergeHeads(const float* pIn, float* pOut, int nBatch, int nSeqLen, int nHeads, int nHeadDim);
+/* NEW: the attention core of MultiHeadAttention::forward's GPU branch on fp32 data
+ * (vit.ixx:163-187): qkvSplitHeads (Q times fScale), tensorTranspose2dBatched +
+ * tensorBatchedMatmul (Q K^T), tensorSoftmaxLastDim, tensorBatchedMatmul (P V),
+ * mergeHeads. pQKV [nBatch*nSeq, 3*D] -> pOut [nBatch*nSeq, D], both fp32. Q is scaled as
+ * qkvSplitHeads scales it; the products read the heads where they lie (no transpose or split
+ * copy) and accumulate in fp32; the softmax is omHipSoftmax's. Intermediates use the
+ * stream's staging workspace. */
+int omHipAttention(const float* pQKV, float* pOut, int nBatch, int nSeq, int nHeads, int nHeadDim, float fScale);
 
 /* ===== fp32 GEMM (cuda_kernels.cuh:109-117) ===== */
 

@@ -28,6 +28,8 @@ public:
     // ---- device ----
     static void init(int nDevice = 0) { check(omHipInit(nDevice), "omHipInit"); }
     static void synchronize() { check(omHipSynchronize(), "omHipSynchronize"); }
+    // omCudaForceReset (EngineBridge.cpp:4047): device sync, sticky error cleared, library state released
+    static void forceReset() { check(omHipForceReset(), "forceReset"); }
     // ---- transfer stream and pinned host memory (cuda_kernels.cuh:56-66, :497-505) ----
     static void* mallocHost(size_t nBytes) {
         void* p = nullptr;
@@ -69,6 +71,33 @@ public:
     }
     static void transpose2d(const float* pA, float* pB, int nRows, int nCols) {
         check(omHipTranspose(pA, pB, nRows, nCols), "transpose2d");
+    }
+    // CUDABackend's name for the same op (cuda_backend.ixx:340), called per batch by
+    // tensorTranspose2dBatched's GPU branch (tensor_ops.ixx:1595-1604)
+    static void transpose(const float* pIn, float* pOut, int nRows, int nCols) {
+        check(omHipTranspose(pIn, pOut, nRows, nCols), "transpose");
+    }
+
+    // ---- reductions (cpu_backend.ixx:290-294; CUDABackend::sum cuda_backend.ixx:732) ----
+    // CUDABackend::sum's form, used by tensorSum's GPU branch (tensor_ops.ixx:413-417): the
+    // result stays on the device
+    static void sum(const float* pData, float* pResult, int nCount) {
+        check(omHipSum(pData, pResult, nCount), "sum");
+    }
+    // CPUBackend::sum's form: the sum is copied back to the host (waits for the stream)
+    static float sum(const float* pData, size_t nCount) {
+        float* d = nullptr;
+        check(omHipMalloc(reinterpret_cast<void**>(&d), sizeof(float)), "sum");
+        float v = 0.f;
+        const int rc = omHipSum(pData, d, toInt(nCount));
+        const int rc2 = rc ? rc : omHipCopyD2H(&v, d, sizeof(float));
+        omHipFree(d);
+        check(rc2, "sum");
+        return v;
+    }
+    // omCudaMean (cuda_kernels.cu:1506-1513): the sum times 1 / nCount, on the device
+    static void mean(const float* pData, float* pResult, int nCount) {
+        check(omHipMean(pData, pResult, nCount), "mean");
     }
 
     // ---- activations / bias (cpu_backend.ixx:317-346, :433-440) ----
@@ -209,6 +238,20 @@ public:
     static void addReluBackward(const float* pA, const float* pInput, const float* pGradOutput, float* pOut,
                                 size_t nCount) {
         check(omHipAddReluBackward(pA, pInput, pGradOutput, pOut, toInt(nCount)), "addReluBackward");
+    }
+
+    // ---- ViT attention on fp32 data (CUDABackend cuda_backend.ixx:967-985; vit.ixx:163-187) ----
+    static void qkvSplitHeads(const float* pQkv, float* pQ, float* pK, float* pV, int nBatch, int nSeqLen,
+                              int nHeads, int nHeadDim, float fScale) {
+        check(omHipQkvSplitHeads(pQkv, pQ, pK, pV, nBatch, nSeqLen, nHeads, nHeadDim, fScale), "qkvSplitHeads");
+    }
+    static void mergeHeads(const float* pIn, float* pOut, int nBatch, int nSeqLen, int nHeads, int nHeadDim) {
+        check(omHipMergeHeads(pIn, pOut, nBatch, nSeqLen, nHeads, nHeadDim), "mergeHeads");
+    }
+    // qkvSplitHeads .. mergeHeads of the GPU branch in one call: qkv [B*S, 3*H*D] -> out [B*S, H*D]
+    static void attention(const float* pQKV, float* pOut, int nBatch, int nSeq, int nHeads, int nHeadDim,
+                          float fScale) {
+        check(omHipAttention(pQKV, pOut, nBatch, nSeq, nHeads, nHeadDim, fScale), "attention");
     }
 
     // ---- fused attention (vit.ixx:150-239): qkv [B*S, 3*H*D] half -> out [B*S, H*D] ----

@@ -51,6 +51,12 @@ _SIGS = {
     "omHipSynchronize": [],
     "omHipSyncComputeStream": [],
     "omHipCleanup": [],
+    "omHipForceReset": [],
+    "omHipSum": [_vp, _vp, _i],
+    "omHipMean": [_vp, _vp, _i],
+    "omHipQkvSplitHeads": [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _fl],
+    "omHipMergeHeads": [_vp, _vp, _i, _i, _i, _i],
+    "omHipAttention": [_vp, _vp, _i, _i, _i, _i, _fl],
     "omHipGetStream": [ctypes.POINTER(_vp)],
     "omHipSoftmax": [_vp, _vp, _i, _i],
     "omHipCrossEntropy": [_vp, _vp, _vp, _i, _i],
@@ -360,6 +366,31 @@ class HIPBackend:
     @staticmethod
     def transpose2d(pA, pB, nRows: int, nCols: int) -> None:
         call("omHipTranspose", _ptr(pA), _ptr(pB), nRows, nCols)
+
+    # ---- reductions (CUDABackend::sum cuda_backend.ixx:732; omCudaMean cuda_kernels.cu:1506) ----
+    @staticmethod
+    def sum(pData, pResult, nCount: int) -> None:
+        """pResult[0] (device) = sum of pData[0..nCount) (tensorSum's GPU branch, tensor_ops.ixx:413-417)."""
+        call("omHipSum", _ptr(pData), _ptr(pResult), nCount)
+
+    @staticmethod
+    def mean(pData, pResult, nCount: int) -> None:
+        call("omHipMean", _ptr(pData), _ptr(pResult), nCount)
+
+    # ---- ViT attention on fp32 data (cuda_backend.ixx:967-985; vit.ixx:163-187) ----
+    @staticmethod
+    def qkvSplitHeads(pQkv, pQ, pK, pV, nBatch, nSeqLen, nHeads, nHeadDim, fScale) -> None:
+        call("omHipQkvSplitHeads", _ptr(pQkv), _ptr(pQ), _ptr(pK), _ptr(pV), nBatch, nSeqLen, nHeads, nHeadDim,
+             fScale)
+
+    @staticmethod
+    def mergeHeads(pIn, pOut, nBatch, nSeqLen, nHeads, nHeadDim) -> None:
+        call("omHipMergeHeads", _ptr(pIn), _ptr(pOut), nBatch, nSeqLen, nHeads, nHeadDim)
+
+    @staticmethod
+    def attention(pQKV, pOut, nBatch, nSeq, nHeads, nHeadDim, fScale) -> None:
+        """qkvSplitHeads .. mergeHeads of MultiHeadAttention::forward's GPU branch on fp32 data."""
+        call("omHipAttention", _ptr(pQKV), _ptr(pOut), nBatch, nSeq, nHeads, nHeadDim, fScale)
 
     # ---- activations / bias (cpu_backend.ixx:317-346, :433-440) ----
     @staticmethod

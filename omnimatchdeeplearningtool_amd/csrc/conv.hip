@@ -734,6 +734,7 @@ static int planBuffers(ConvParams& p, ConvPlan& pl, int tiles, int bm, int bn, f
     unsigned* ctr = ws ? static_cast<unsigned*>(workspace((size_t)tiles * sizeof(unsigned), kWsCounters)) : nullptr;
     if (!ws || !ctr) {
         if (capturing(stream())) return -1;
+        clearError();   // the whole-tile plan below succeeds: drop workspace()'s out-of-memory note
         pl.splits = 1;
         pl.fullTiles = tiles;
         ws = nullptr;

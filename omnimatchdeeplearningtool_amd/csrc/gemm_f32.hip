@@ -356,42 +356,9 @@ using CfgL = TileCfg<256, 256, OMHIP_GEMM_BK, 64, 128>;
 using CfgM = TileCfg<128, 128, 16, 64, 64>;
 using CfgS = TileCfg<64, 64, 16, 32, 32>;
 
-struct GemmPlan {
-    int cfg;      // 0: 256x256, 1: 128x128, 2: 64x64
-    int splits;   // K splits (1: none)
-};
-
-// Tile and split-K choice: the largest tile that gives every CU a workgroup.
-// When even 64x64 tiles give fewer than two workgroups per CU and K is long
-// (few rows or columns: 128 x 4096 x 4096, weight gradients), K is split over
-// the 64x64 tile: the smallest power of two (at most 64) that gives every CU
-// two workgroups while each split keeps >= 256 of K. The partials cost one
-// fp32 write and read of C per split. Measured on MI355X (TFLOP/s, against
-// splitting the 128x128 tile until every CU had one workgroup): 128 x 4096 x
-// 4096 86 (76), 64 x 4096 x 4096 69 (56), 128 x 1024 x 4096 47 (29),
-// 512 x 1024 x 2048 72 (56), 256 x 4096 x 4096 96 (75). With 512 <= K <
-// 1024 only grids of at most CUs / 4 tiles split (pieces of >= 128 of K:
-// 128 x 256 x 784, the MLP's first layer, 18.9 -> 11.5 us; 256 x 512 x 768
-// 18.9 -> 12.8; 512^3 14.2 -> 11.7); shorter K runs faster unsplit. The partials of a plan stay
-// below 4 x CUs tiles of 64 x 64 floats (16 MiB on 256 CUs).
+// Tile and split-K choice (planGemmFor in gemm_f32.hpp) for this device.
 static GemmPlan planGemm(int M, int N, int K, int batch, bool wsOk) {
-    const long long cus = cuCount();
-    auto tiles = [&](int bm, int bn) { return (long long)((M + bm - 1) / bm) * ((N + bn - 1) / bn) * batch; };
-    if (tiles(256, 256) >= cus) return {0, 1};
-    if (tiles(128, 128) >= cus) return {1, 1};
-    const long long t = tiles(64, 64);
-    if (t >= 2 * cus || !wsOk || K < 512 || (K < 1024 && t * 4 > cus)) return {2, 1};
-    if (K < 1024) {   // very few tiles (at most CUs / 4): splits of >= 128 of K
-        int s = 1;
-        while (s < 64 && t * s < 2 * cus && K / (2 * s) >= 128) s *= 2;
-        return {2, s};
-    }
-    // with one tile per CU already, a split must keep >= 1024 of K (1024^3
-    // ran 79 TFLOP/s unsplit, 70 split in two)
-    const int minK = t >= cus ? 1024 : 256;
-    int s = 1;
-    while (s < 64 && t * s < 2 * cus && K / (2 * s) >= minK) s *= 2;
-    return {2, s};
+    return planGemmFor(M, N, K, batch, wsOk, cuCount());
 }
 
 template <bool TA, bool TB>
@@ -414,10 +381,7 @@ static int gemmF32Run(bool ta, bool tb, int batch, int M, int N, int K, const fl
     prm.M = M; prm.N = N; prm.K = K;
     prm.lda = lda; prm.ldb = ldb; prm.ldc = ldc;
     prm.sA = sA; prm.sB = sB; prm.sC = sC;
-    const int bk = 16;
-    int splits = plan.splits;
-    prm.kChunk = ((K + splits - 1) / splits + bk - 1) / bk * bk;
-    splits = (K + prm.kChunk - 1) / prm.kChunk;
+    const int splits = splitPieces(K, plan.splits, &prm.kChunk);
     const bool partial = splits > 1;
     if (partial) {
         const size_t need = (size_t)splits * batch * M * N * sizeof(float);
@@ -554,13 +518,19 @@ static int linearBackward(const float* X, const float* G, const float* W, const 
 // 4 x CUs tiles of 64 x 64 floats: 16 MiB on a 256-CU device (the array holds
 // twice that). Each device the library runs on holds its own copy until the
 // process ends.
-constexpr size_t kNoAllocScratchBytes = (size_t)32 << 20;
 constexpr int kMaxDevices = 64;
 static __device__ __align__(256) float scratch[kNoAllocScratchBytes / sizeof(float)];
 
 static std::once_flag g_scratchOnce[kMaxDevices];
 static float* g_scratchPtr[kMaxDevices];
 static hipError_t g_scratchErr[kMaxDevices];
+// Ordering of the calls that use a device's array: the stream of the last such
+// call and an event recorded after its kernels. A call on another stream first
+// makes its stream wait for that event (no host wait, no device memory).
+static std::mutex g_scratchMutex[kMaxDevices];
+static hipEvent_t g_scratchEvent[kMaxDevices];
+static hipStream_t g_scratchLast[kMaxDevices];
+static bool g_scratchRecorded[kMaxDevices];
 
 // Device address of this device's `scratch` (the array's name is a host-side
 // stand-in), looked up once per device with that device current.
@@ -584,6 +554,27 @@ static float* noAllocScratch() {
         return nullptr;
     }
     return g_scratchPtr[dev];
+}
+
+// Runs `launch` (kernels that use the device's array) ordered after the last
+// call that used it, whatever stream that call ran on. A stream that records a
+// graph neither waits nor records: ordering a replay against other streams is
+// the caller's.
+template <class F>
+static int withScratchOrder(F&& launch) {
+    int dev = 0;
+    OMHIP_CHECK(hipGetDevice(&dev));
+    const hipStream_t s = stream();
+    if (capturing(s)) return launch();
+    std::lock_guard<std::mutex> lock(g_scratchMutex[dev]);
+    if (!g_scratchEvent[dev]) OMHIP_CHECK(hipEventCreateWithFlags(&g_scratchEvent[dev], hipEventDisableTiming));
+    if (g_scratchRecorded[dev] && g_scratchLast[dev] != s) OMHIP_CHECK(hipStreamWaitEvent(s, g_scratchEvent[dev], 0));
+    const int rc = launch();
+    if (rc) return rc;
+    OMHIP_CHECK(hipEventRecord(g_scratchEvent[dev], s));
+    g_scratchLast[dev] = s;
+    g_scratchRecorded[dev] = true;
+    return 0;
 }
 
 }  // namespace omhip
@@ -695,8 +686,12 @@ int omHipGemmStridedBatchedNoAlloc(int bTransA, int bTransB, int nBatch, int nM,
     // the same plan as omHipGemmStridedBatched, so the results are the same bits
     const bool wsOk = (size_t)64 * nBatch * nM * nN * sizeof(float) <= kMaxSplitWorkspace;
     const GemmPlan plan = planGemm(nM, nN, nK, nBatch, wsOk);
-    return gemmF32Run(bTransA != 0, bTransB != 0, nBatch, nM, nN, nK, pA, nLda, nStrideA, pB, nLdb, nStrideB, pC,
-                      nLdc, nStrideC, plan, nullptr, 0, ws, kNoAllocScratchBytes);
+    auto run = [&] {
+        return gemmF32Run(bTransA != 0, bTransB != 0, nBatch, nM, nN, nK, pA, nLda, nStrideA, pB, nLdb, nStrideB, pC,
+                          nLdc, nStrideC, plan, nullptr, 0, ws, kNoAllocScratchBytes);
+    };
+    if (plan.splits <= 1) return run();   // the array is not touched
+    return withScratchOrder(run);
 }
 
 }  // extern "C"

@@ -788,6 +788,16 @@ struct StagedStore {
     static constexpr size_t LDS_BYTES = (size_t)(Cfg::NT / 64) * 32 * PF * sizeof(float);
 };
 
+// Orders a wave's own LDS accesses across lanes: the writes before it are
+// complete and visible to every lane of the wave before the reads after it
+// (and the reads before it before the writes after it). No instruction is
+// needed on gfx950 beyond keeping the compiler from moving accesses across it.
+__device__ __forceinline__ void waveLdsOrder() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
 template <class Cfg, bool BF16>
 __device__ __forceinline__ void storeStaged(const HalfFastParams& p, const f32x16h (&acc)[Cfg::FM][Cfg::FN],
                                             uint16_t* hsm, long long cb, int m0, int n0, int wm, int wn, int li,
@@ -813,6 +823,7 @@ __device__ __forceinline__ void storeStaged(const HalfFastParams& p, const f32x1
             for (int g = 0; g < 4; ++g)
                 *reinterpret_cast<f32x4h*>(st + li * PF + fn * 32 + 8 * g + 4 * h) =
                     f32x4h{acc[fm][fn][4 * g], acc[fm][fn][4 * g + 1], acc[fm][fn][4 * g + 2], acc[fm][fn][4 * g + 3]};
+        waveLdsOrder();   // rows written by one lane are read by others
         const int mb = m0 + wm * Cfg::WM + fm * 32;   // first row of the 32-row block
 #pragma unroll
         for (int i = 0; i < 32 / RPI; ++i) {
@@ -835,6 +846,7 @@ __device__ __forceinline__ void storeStaged(const HalfFastParams& p, const f32x1
                     __builtin_nontemporal_store(v, reinterpret_cast<f32x4h*>(static_cast<float*>(p.C) + off));
             }
         }
+        waveLdsOrder();   // every lane has read this block before the next block's writes
     }
 }
 

@@ -53,6 +53,11 @@ struct RetiredWs {
 std::map<std::pair<hipStream_t, int>, WsBlock> g_ws;   // (stream, slot)
 std::vector<RetiredWs> g_wsRetired;
 int g_liveGraphs = 0;   // executable graphs not yet destroyed (guarded by g_wsMutex)
+std::map<hipStream_t, int> g_graphsOn;   // live graphs per capture stream (guarded by g_wsMutex)
+// Set once a second stream has been current: from then on every omHipFree
+// records a fence on the freeing stream, so another stream reuses the block only
+// after that stream's earlier work has finished.
+std::atomic<bool> g_multiStream{false};
 
 // Graph handle: the executable graph and the stream it was captured on (its
 // nodes use that stream's workspace, so replays are ordered on that stream).
@@ -81,8 +86,33 @@ int initLocked(int nDev) {
             void* p = nullptr;
             return hipMalloc(&p, n) == hipSuccess ? p : ((void)hipGetLastError(), nullptr);
         },
-        [](void* p) { (void)hipFree(p); });
+        [](void* p) { (void)hipFree(p); },
+        [](void* ev) {
+            const hipError_t e = hipEventQuery(static_cast<hipEvent_t>(ev));
+            if (e != hipSuccess) (void)hipGetLastError();   // hipErrorNotReady
+            return e == hipSuccess;
+        },
+        [] { (void)hipDeviceSynchronize(); });
     return 0;
+}
+
+uintptr_t tagOf(hipStream_t s) { return reinterpret_cast<uintptr_t>(s); }
+
+// A fence on stream s: an event recorded now (nullptr while s records a graph,
+// or when the event cannot be made; the block then keeps its stream tag only).
+CachingPool::Fence fenceOn(hipStream_t s) {
+    if (capturing(s)) return nullptr;
+    hipEvent_t ev = nullptr;
+    if (hipEventCreateWithFlags(&ev, hipEventDisableTiming) != hipSuccess) {
+        (void)hipGetLastError();
+        return nullptr;
+    }
+    if (hipEventRecord(ev, s) != hipSuccess) {
+        (void)hipGetLastError();
+        (void)hipEventDestroy(ev);
+        return nullptr;
+    }
+    return CachingPool::Fence(static_cast<void*>(ev), [](void* e) { (void)hipEventDestroy(static_cast<hipEvent_t>(e)); });
 }
 
 int ensureInit(int nDev, bool bExplicit) {
@@ -203,13 +233,13 @@ void* workspace(size_t bytes, int slot) {
         w = WsBlock{};
     }
     const size_t want = (bytes + (1u << 20) - 1) / (1u << 20) * (1u << 20);   // 1 MiB steps
-    void* p = g_pool->allocate(want);
+    void* p = g_pool->allocate(want, tagOf(s));
     if (!p) {
         (void)fail("workspace: out of device memory (%zu bytes)", want);
         return nullptr;
     }
     if (slot == kWsCounters && byteFill(p, 0, want)) {   // counters start at zero, kernels leave them so
-        g_pool->release(p);
+        g_pool->release(p, tagOf(s));
         return nullptr;
     }
     w.p = p;
@@ -307,12 +337,33 @@ int omHipCleanup(void) {
     return 0;
 }
 
+int omHipForceReset(void) {
+    clearError();
+    if (!g_inited.load(std::memory_order_acquire)) {
+        (void)hipGetLastError();
+        return 0;
+    }
+    (void)hipDeviceSynchronize();   // every kernel has finished (its status is not ours to report)
+    (void)hipGetLastError();        // clear the sticky error left by a failed call
+    const int rc = omHipCleanup();  // pool, workspaces, tables and streams; the next call re-initialises
+    (void)hipGetLastError();
+    return rc;
+}
+
 int omHipReleaseStream(void* pStream) {
     clearError();
     if (!pStream || !g_inited.load(std::memory_order_acquire)) return 0;
     const hipStream_t s = static_cast<hipStream_t>(pStream);
     if (capturing(s)) return fail("omHipReleaseStream: the stream records a graph");
+    {
+        std::lock_guard<std::mutex> lock(g_wsMutex);
+        auto g = g_graphsOn.find(s);
+        if (g != g_graphsOn.end() && g->second > 0)
+            return fail("omHipReleaseStream: %d graph(s) captured on this stream still exist; destroy them first",
+                        g->second);
+    }
     OMHIP_CHECK(hipStreamSynchronize(s));
+    g_pool->retire(tagOf(s));   // every block freed on the stream is idle now
     std::lock_guard<std::mutex> lock(g_wsMutex);
     for (auto it = g_ws.begin(); it != g_ws.end();) {
         if (it->first.first != s) {
@@ -346,6 +397,15 @@ int omHipGetStream(void** ppStream) {
 int omHipSetStream(void* pStream) {
     clearError();
     if (ensureInit(0, false)) return -1;
+    const hipStream_t prev = stream();
+    const hipStream_t next = pStream ? static_cast<hipStream_t>(pStream) : g_ownStream;
+    if (next != prev) {
+        // blocks freed on the previous stream become reusable elsewhere once its
+        // work so far has finished; later frees carry a fence of their own
+        g_multiStream.store(true, std::memory_order_release);
+        CachingPool::Fence f = fenceOn(prev);
+        if (f) g_pool->fenceTag(tagOf(prev), f);
+    }
     g_userStream.store(static_cast<hipStream_t>(pStream), std::memory_order_release);
     return 0;
 }
@@ -357,7 +417,7 @@ int omHipMalloc(void** ppDevPtr, size_t nBytes) {
     if (!ppDevPtr) return fail("omHipMalloc: null output");
     *ppDevPtr = nullptr;
     if (ensureInit(0, false)) return -1;
-    void* p = g_pool->allocate(nBytes);
+    void* p = g_pool->allocate(nBytes, tagOf(stream()));
     if (!p) return fail("omHipMalloc(%zu): out of device memory after flushing the pool", nBytes);
     *ppDevPtr = p;
     return 0;
@@ -370,9 +430,11 @@ int omHipFree(void* pDevPtr) {
         OMHIP_CHECK(hipFree(pDevPtr));
         return 0;
     }
-    // Blocks are recycled by later allocations whose kernels are enqueued on the
-    // same stream, so stream order already protects a block still being read.
-    g_pool->release(pDevPtr);
+    // The free is ordered on the current stream: later work on that stream may
+    // reuse the block at once (stream order protects it); work on another stream
+    // only once the fence recorded here has completed.
+    const hipStream_t s = stream();
+    g_pool->release(pDevPtr, tagOf(s), g_multiStream.load(std::memory_order_acquire) ? fenceOn(s) : nullptr);
     return 0;
 }
 
@@ -386,8 +448,7 @@ int omHipPoolStats(size_t* pHeldBytes, size_t* pUsedBytes) {
 int omHipPoolTrim(void) {
     clearError();
     if (!g_pool) return 0;
-    OMHIP_CHECK(hipStreamSynchronize(stream()));
-    g_pool->trim();
+    g_pool->trim();   // drains the device first
     return 0;
 }
 
@@ -518,6 +579,7 @@ int omHipGraphEndCapture(void** ppGraphExec) {
     {
         std::lock_guard<std::mutex> lock(g_wsMutex);
         ++g_liveGraphs;
+        ++g_graphsOn[s];
     }
     *ppGraphExec = static_cast<void*>(new GraphHandle{exec, s});
     return 0;
@@ -535,14 +597,18 @@ int omHipGraphDestroy(void* pGraphExec) {
     clearError();
     if (!pGraphExec) return 0;
     GraphHandle* h = static_cast<GraphHandle*>(pGraphExec);
-    // replays still running may use retired workspaces: let them finish first
-    const hipError_t es = hipStreamSynchronize(h->stream);
+    // replays still running may use retired workspaces: let them finish first.
+    // The whole device is waited for, so a handle that outlives its capture
+    // stream never touches that stream.
+    const hipError_t es = hipDeviceSynchronize();
     const hipError_t ed = hipGraphExecDestroy(h->exec);
-    delete h;
     {
         std::lock_guard<std::mutex> lock(g_wsMutex);
         --g_liveGraphs;
+        auto g = g_graphsOn.find(h->stream);
+        if (g != g_graphsOn.end() && --g->second <= 0) g_graphsOn.erase(g);
     }
+    delete h;
     OMHIP_CHECK(es);
     OMHIP_CHECK(ed);
     return 0;

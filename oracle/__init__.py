@@ -97,6 +97,8 @@ def lib() -> ctypes.CDLL:
             "omrefAdd": [_f, _f, _f, _sz],
             "omrefSoftmax": [_f, _f, _i, _i],
             "omrefAttention": [_f, _f, _i, _i, _i, _i, ctypes.c_float],
+            "omrefQkvSplitHeads": [_f, _f, _f, _f, _i, _i, _i, _i, ctypes.c_float],
+            "omrefMergeHeads": [_f, _f, _i, _i, _i, _i],
             "omrefCrossEntropySoftmaxBackward": [_f, _f, _f, _i, _i],
             "omrefAddBiasBackward": [_f, _f, _i, _i, _i],
         }
@@ -106,6 +108,8 @@ def lib() -> ctypes.CDLL:
             fn.restype = None
         L.omrefCrossEntropy.argtypes = [_f, _f, _i, _i]
         L.omrefCrossEntropy.restype = ctypes.c_float
+        L.omrefSum.argtypes = [_f, _sz]
+        L.omrefSum.restype = ctypes.c_float
         L.omrefHasAvx2.restype = ctypes.c_int
         L.omrefMaxThreads.restype = ctypes.c_int
         _LIB = L
@@ -150,6 +154,9 @@ def ref_lib() -> Optional[ctypes.CDLL]:
                 fn.restype = None
             R.refCrossEntropy.argtypes = [_f, _f, _i, _i]
             R.refCrossEntropy.restype = ctypes.c_float
+            if hasattr(R, "refSum"):
+                R.refSum.argtypes = [_f, _sz]
+                R.refSum.restype = ctypes.c_float
             _REF = R
     return _REF
 
@@ -509,6 +516,33 @@ def attention(qkv, B, S, H, D, scale, backend: str = "oracle") -> np.ndarray:
     P = softmax(sc, backend="reference")
     ctx = batched_matmul(P, V, backend="reference")
     return np.ascontiguousarray(ctx.reshape(B, H, S, D).transpose(0, 2, 1, 3)).reshape(B * S, H * D)
+
+
+def sum_(x, backend: str = "oracle") -> np.float32:
+    """CPUBackend::sum (cpu_backend.ixx:290-294): a float accumulator over the elements in order."""
+    x = _f32(x).reshape(-1)
+    if backend == "reference":
+        R = ref_lib()
+        if R is None or not hasattr(R, "refSum"):
+            raise RuntimeError("the compiled reference (oracle/_ref) is not built")
+        return np.float32(R.refSum(_p(x), x.size))
+    return np.float32(lib().omrefSum(_p(x), x.size))
+
+
+def qkv_split_heads(qkv, B, S, H, D, scale):
+    """MultiHeadAttention::forward's split (vit.ixx:196-212): Q*scale, K, V as [B*H, S, D]."""
+    qkv = _f32(qkv)
+    q, k, v = (np.empty((B * H, S, D), np.float32) for _ in range(3))
+    lib().omrefQkvSplitHeads(_p(qkv), _p(q), _p(k), _p(v), B, S, H, D, ctypes.c_float(scale))
+    return q, k, v
+
+
+def merge_heads(x, B, S, H, D):
+    """MultiHeadAttention::forward's merge (vit.ixx:220-232): [B*H, S, D] -> [B*S, H*D]."""
+    x = _f32(x)
+    out = np.empty((B * S, H * D), np.float32)
+    lib().omrefMergeHeads(_p(x), _p(out), B, S, H, D)
+    return out
 
 
 def attention_f64(qkv, B, S, H, D, scale):

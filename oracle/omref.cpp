@@ -522,6 +522,40 @@ void omrefAttention(const float* qkv, float* out, int B, int S, int H, int D, fl
     }
 }
 
+// cpu_backend.ixx:290-294 — CPUBackend::sum: one float accumulator, elements in order.
+float omrefSum(const float* x, size_t n) {
+    float s = 0.0f;
+    for (size_t i = 0; i < n; ++i) s += x[i];
+    return s;
+}
+
+// vit.ixx:196-212 (MultiHeadAttention::forward, CPU branch) — qkv [B*S, 3*H*D] split into
+// Q, K, V [B*H, S, D], Q multiplied by scale (the map omCudaQkvSplitHeads also uses).
+void omrefQkvSplitHeads(const float* qkv, float* q, float* k, float* v, int B, int S, int H, int D, float scale) {
+    const int Dm = H * D;
+    for (int n = 0; n < B; ++n)
+        for (int s = 0; s < S; ++s) {
+            const float* row = qkv + ((size_t)n * S + s) * 3 * Dm;
+            for (int h = 0; h < H; ++h)
+                for (int d = 0; d < D; ++d) {
+                    const size_t o = (((size_t)n * H + h) * S + s) * D + d;
+                    q[o] = row[h * D + d] * scale;
+                    k[o] = row[Dm + h * D + d];
+                    v[o] = row[2 * Dm + h * D + d];
+                }
+        }
+}
+
+// vit.ixx:220-232 — [B*H, S, D] merged back into [B*S, H*D].
+void omrefMergeHeads(const float* in, float* out, int B, int S, int H, int D) {
+    const int Dm = H * D;
+    for (int n = 0; n < B; ++n)
+        for (int s = 0; s < S; ++s)
+            for (int h = 0; h < H; ++h)
+                for (int d = 0; d < D; ++d)
+                    out[((size_t)n * S + s) * Dm + h * D + d] = in[(((size_t)n * H + h) * S + s) * D + d];
+}
+
 // cpu_backend.ixx:147-160, simd.ixx:180-200 — elementwise a + b.
 void omrefAdd(const float* a, const float* b, float* out, size_t n) {
     for (size_t i = 0; i < n; ++i) out[i] = a[i] + b[i];

@@ -61,6 +61,7 @@ void refAdaptiveAvgPool2dBackward(const float* gO, float* gI, int n, int c, int 
     om::CPUBackend::adaptiveAvgPool2dBackward(gO, gI, n, c, h, w, oh, ow);
 }
 void refAdd(const float* a, const float* b, float* out, size_t n) { om::CPUBackend::add(a, b, out, n); }
+float refSum(const float* x, size_t n) { return om::CPUBackend::sum(x, n); }
 void refSoftmax(const float* in, float* out, int rows, int cols) { om::CPUBackend::softmax(in, out, rows, cols); }
 float refCrossEntropy(const float* p, const float* t, int rows, int cols) {
     return om::CPUBackend::crossEntropy(p, t, rows, cols);

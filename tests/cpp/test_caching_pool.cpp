@@ -1,7 +1,8 @@
 // CPU test of omhip::CachingPool with a fake device allocator: reuse,
 // rounding, flush-and-retry on allocation failure (the reference pool's OOM
 // path, src/cuda/cuda_kernels.cu:220-245), unknown-pointer free, trim/clear
-// accounting and concurrent use. Exit status 0 = all checks passed.
+// accounting, concurrent use and cross-stream reuse (stream tags and fences).
+// Exit status 0 = all checks passed.
 #include <atomic>
 #include <cstdio>
 #include <cstdlib>
@@ -120,6 +121,52 @@ int main() {
         for (auto& x : th) x.join();
         CHECK(nullCount == 0);
         CHECK(pool.usedBytes() == 0);
+        pool.clear();
+        CHECK(dev.used == 0);
+    }
+    // --- streams: a block freed on stream 1 goes back to stream 1 at once, to stream 2 only
+    // once its fence has completed (or the stream was retired); flushes drain first ---
+    {
+        FakeDevice dev{1 << 20};
+        std::vector<std::pair<void*, size_t>> sizes;
+        int drains = 0;
+        omhip::CachingPool pool([&](size_t n) { void* p = dev.alloc(n); if (p) sizes.push_back({p, n}); return p; },
+                                [&](void* p) { for (auto& s : sizes) if (s.first == p) dev.release(p, s.second); },
+                                [](void* f) { return *static_cast<bool*>(f); }, [&] { ++drains; });
+        auto makeFence = [] { return omhip::CachingPool::Fence(new bool(false), [](void* p) { delete static_cast<bool*>(p); }); };
+        auto done = [](const omhip::CachingPool::Fence& f) { *static_cast<bool*>(f.get()) = true; };
+        void* a = pool.allocate(1000, 1);
+        auto f1 = makeFence();
+        pool.release(a, 1, f1);
+        void* b = pool.allocate(1000, 2);         // the fence is pending: stream 2 gets a fresh block
+        CHECK(b != a && dev.allocs == 2);
+        void* c = pool.allocate(1000, 1);         // stream 1 itself: stream order protects the block
+        CHECK(c == a);
+        pool.release(c, 1, f1);
+        done(f1);
+        void* d = pool.allocate(1000, 2);         // fence completed: free for every stream
+        CHECK(d == a);
+        pool.release(d, 1, nullptr);              // no fence: only stream 1 (or a retire) may take it
+        void* e = pool.allocate(1000, 2);
+        CHECK(e != a && e != b);
+        pool.retire(1);                           // stream 1 synchronised: its blocks are idle
+        void* g = pool.allocate(1000, 2);
+        CHECK(g == a);
+        pool.release(g, 1, nullptr);
+        auto f2 = makeFence();
+        pool.fenceTag(1, f2);                     // stream 1 stops being current
+        void* h = pool.allocate(1000, 3);
+        CHECK(h != a);
+        done(f2);
+        void* i = pool.allocate(1000, 3);
+        CHECK(i == a);
+        pool.release(b, 2, makeFence());          // pending fence on a cached block ...
+        CHECK(drains == 0);
+        pool.trim();                              // ... so the flush drains the device first
+        CHECK(drains == 1 && pool.cachedBlocks() == 0);
+        pool.release(e, 2);
+        pool.release(h, 3);
+        pool.release(i, 3);
         pool.clear();
         CHECK(dev.used == 0);
     }

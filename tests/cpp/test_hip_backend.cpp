@@ -182,6 +182,65 @@ static void testLinearBackward() {
     std::printf("LinearBackward done\n");
 }
 
+// MultiHeadAttention::forward's GPU branch (vit.ixx:163-187) written as the engine writes it,
+// with HIPBackend in CUDABackend's place: qkvSplitHeads, tensorTranspose2dBatched (transpose
+// per head), tensorBatchedMatmul, tensorSoftmaxLastDim (softmax), tensorBatchedMatmul,
+// mergeHeads. Known answers for the split and merge; the chain equals HIPBackend::attention.
+static void testVitBranchAndSum() {
+    const int B = 2, S = 3, H = 2, D = 4, Dm = H * D, BH = B * H;
+    std::vector<float> qkvH(B * S * 3 * Dm);
+    for (size_t i = 0; i < qkvH.size(); ++i) qkvH[i] = 0.01f * (float)((i * 37) % 101) - 0.5f;
+    Dev qkv(qkvH), q(BH * S * D), k(BH * S * D), v(BH * S * D);
+    const float scale = 0.5f;   // 1 / sqrt(D)
+    HIPBackend::qkvSplitHeads(qkv.p, q.p, k.p, v.p, B, S, H, D, scale);
+    auto hq = q.host(), hk = k.host(), hv = v.host();
+    for (int n = 0; n < B; ++n)
+        for (int s = 0; s < S; ++s)
+            for (int h = 0; h < H; ++h)
+                for (int d = 0; d < D; ++d) {
+                    const size_t o = (((size_t)n * H + h) * S + s) * D + d, r = ((size_t)n * S + s) * 3 * Dm;
+                    EXPECT_NEAR(hq[o], qkvH[r + h * D + d] * scale, 0);
+                    EXPECT_NEAR(hk[o], qkvH[r + Dm + h * D + d], 0);
+                    EXPECT_NEAR(hv[o], qkvH[r + 2 * Dm + h * D + d], 0);
+                }
+    Dev kT(BH * D * S), scores(BH * S * S), attnW(BH * S * S), ctx(BH * S * D), outFlat(B * S * Dm);
+    for (int b = 0; b < BH; ++b) HIPBackend::transpose(k.p + b * S * D, kT.p + b * S * D, S, D);
+    HIPBackend::batchedMatmul(q.p, kT.p, scores.p, BH, S, D, S);
+    HIPBackend::softmax(scores.p, attnW.p, BH * S, S);
+    HIPBackend::batchedMatmul(attnW.p, v.p, ctx.p, BH, S, S, D);
+    HIPBackend::mergeHeads(ctx.p, outFlat.p, B, S, H, D);
+    Dev fused(B * S * Dm);
+    HIPBackend::attention(qkv.p, fused.p, B, S, H, D, scale);
+    auto ho = outFlat.host(), hf = fused.host(), hc = ctx.host();
+    for (size_t i = 0; i < ho.size(); ++i) EXPECT_NEAR(hf[i], ho[i], 1e-6);
+    for (int n = 0; n < B; ++n)   // merge is the inverse map of the split's
+        for (int s = 0; s < S; ++s)
+            for (int h = 0; h < H; ++h)
+                for (int d = 0; d < D; ++d)
+                    EXPECT_NEAR(ho[((size_t)n * S + s) * Dm + h * D + d], hc[(((size_t)n * H + h) * S + s) * D + d], 0);
+    // tensorSum's GPU branch (tensor_ops.ixx:413-417): the sum lands on the device
+    // (integer values whose every partial sum stays below 2^24, so any order is exact)
+    std::vector<float> ramp(10000);
+    for (int i = 0; i < 10000; ++i) ramp[i] = (float)(i % 100 + 1);
+    Dev r(ramp), res(1);
+    HIPBackend::sum(r.p, res.p, 10000);
+    EXPECT_NEAR(res.host()[0], 505000.0, 0);
+    HIPBackend::mean(r.p, res.p, 100);
+    EXPECT_NEAR(res.host()[0], 50.5, 0);
+    EXPECT_NEAR(HIPBackend::sum(r.p, (size_t)100), 5050.0, 0);
+    std::printf("VitBranchAndSum done\n");
+}
+
+// EngineBridge's recovery call (EngineBridge.cpp:4047): the library comes back on the next call.
+static void testForceReset() {
+    HIPBackend::forceReset();
+    Dev a(std::vector<float>{1, 2, 3, 4}), b(std::vector<float>{5, 6, 7, 8}), c(4);
+    HIPBackend::matmul(a.p, b.p, c.p, 2, 2, 2);
+    auto h = c.host();
+    EXPECT_NEAR(h[0], 19, 0); EXPECT_NEAR(h[3], 50, 0);
+    std::printf("ForceReset done\n");
+}
+
 int main() {
     try {
         HIPBackend::init(0);
@@ -194,6 +253,8 @@ int main() {
         testConvAllOnes();
         testReluAndErrors();
         testTrainingPieces();
+        testVitBranchAndSum();
+        testForceReset();
         HIPBackend::synchronize();
     } catch (const std::exception& e) {
         std::printf("FAIL: exception %s\n", e.what());

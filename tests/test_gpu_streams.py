@@ -186,3 +186,61 @@ def test_capture_refuses_new_workspace_and_tables(hip, streams):
     finally:
         g1.destroy()
         g2.destroy()
+
+
+def test_free_on_one_stream_reuse_on_another(hip, streams):
+    """A buffer freed on stream A while A's GEMM still reads it must not be handed to stream B:
+    B's first split-K GEMM (128x4096x4096, 8 MiB of partials: a fresh workspace block of the
+    freed buffer's size) runs right after the free with no host wait. A's product must equal
+    the single-stream result bit for bit, and so must B's."""
+    H = hip.HIPBackend
+    M, K, N = 512, 4096, 4096                        # A operand: 8 MiB, read by a 17 GFLOP product
+    A_np, B_np = O.randn((M, K), 81), O.randn((K, N), 82)
+    m, k, n = 128, 4096, 4096
+    a_np, b_np = O.randn((m, k), 83), O.randn((k, n), 84)
+    dB, db = to_dev(hip, B_np), to_dev(hip, b_np)
+    da = to_dev(hip, a_np)
+    C, C_ref = empty_dev(hip, (M, N)), empty_dev(hip, (M, N))
+    c, c_ref = empty_dev(hip, (m, n)), empty_dev(hip, (m, n))
+    dA_ref = to_dev(hip, A_np)
+    H.matmul(dA_ref, dB, C_ref, M, K, N)             # references on the library stream
+    H.matmul(da, db, c_ref, m, k, n)
+    hip.synchronize()
+    sA, sB = streams.create(), streams.create()
+    print(f"[streams] free on {sA:#x}, reuse on {sB:#x}", flush=True)
+    for r in range(3):
+        dA = to_dev(hip, A_np)                       # uploaded and synchronised on the library stream
+        hip.set_stream(sA)
+        H.matmul(dA, dB, C, M, K, N)
+        dA.free()                                    # ordered on A: A's GEMM may still be reading it
+        hip.set_stream(sB)
+        H.matmul(da, db, c, m, k, n)                 # split-K on B: a workspace of dA's size
+        streams.sync(sA)
+        streams.sync(sB)
+        hip.set_stream(None)
+        assert np.array_equal(_bits(C.numpy()), _bits(C_ref.numpy())), r
+        assert np.array_equal(_bits(c.numpy()), _bits(c_ref.numpy())), r
+        hip.release_stream(sB)                       # B's workspace goes back: the next round grows it again
+
+
+def test_release_stream_refused_while_graph_lives(hip, streams):
+    """omHipReleaseStream fails while a graph captured on that stream exists, and succeeds once
+    the graph is destroyed; the graph replays correctly meanwhile."""
+    H = hip.HIPBackend
+    m, k, n = 64, 2048, 1024
+    a, b = to_dev(hip, O.randn((m, k), 91)), to_dev(hip, O.randn((k, n), 92))
+    c, c_ref = empty_dev(hip, (m, n)), empty_dev(hip, (m, n))
+    s = streams.create()
+    hip.set_stream(s)
+    H.matmul(a, b, c_ref, m, k, n)
+    g = hip.Graph(lambda: H.matmul(a, b, c, m, k, n))
+    try:
+        hip.set_stream(None)
+        with pytest.raises(hip.OmHipError, match="graph"):
+            hip.release_stream(s)
+        g.launch()
+        streams.sync(s)
+        assert np.array_equal(_bits(c.numpy()), _bits(c_ref.numpy()))
+    finally:
+        g.destroy()
+    hip.release_stream(s)

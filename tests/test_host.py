@@ -63,6 +63,16 @@ def test_caching_pool(tmp_path):
     assert r.returncode == 0 and "ALL PASSED" in r.stdout
 
 
+def test_gemm_plan_partials_fit_the_fixed_scratch(tmp_path):
+    """Every split-K plan's partial sums fit omHipGemmStridedBatchedNoAlloc's fixed array."""
+    exe = tmp_path / "plan"
+    subprocess.run(["g++", "-std=c++17", "-O2", "-Wall", "-Werror", os.path.join(ROOT, "tests", "cpp", "test_gemm_plan.cpp"),
+                    "-o", str(exe)], check=True)
+    r = subprocess.run([str(exe)], stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True, timeout=120)
+    print(r.stdout)
+    assert r.returncode == 0 and "ALL PASSED" in r.stdout
+
+
 def test_bench_refuses_multi_gpu():
     r = subprocess.run([sys.executable, os.path.join(ROOT, "bench.py"), "--gpus", "2"], stdout=subprocess.PIPE,
                        stderr=subprocess.PIPE, text=True, timeout=120)

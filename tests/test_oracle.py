@@ -486,3 +486,42 @@ def test_resnet18_train_step_oracle_equals_reference():
     assert a.keys() == b.keys()
     for k in a:
         assert np.array_equal(bits(a[k]), bits(b[k])), k
+
+
+def test_sum_and_head_maps_closed_forms():
+    """CPUBackend::sum: exact on integer-valued data, ones sum to n below 2^24, and the float
+    sequential order (2^24 + 1 + 1 ... stays 2^24, which a pairwise or float64 sum would not).
+    The head split / merge (vit.ixx:196-232): exact permutations against numpy reshapes, Q
+    scaled by one float multiply, merge(split) returning the Q, K and V thirds of the input."""
+    assert O.sum_(np.ones(1000, np.float32)) == np.float32(1000.0)
+    ints = O.rng(95).integers(-1000, 1000, 4099).astype(np.float32)
+    assert O.sum_(ints) == np.float32(ints.astype(np.int64).sum())
+    seq = np.array([2.0 ** 24] + [1.0] * 8, np.float32)
+    assert O.sum_(seq) == np.float32(2.0 ** 24)                # each +1 rounds away in float
+    assert np.float32(seq.astype(np.float64).sum()) == np.float32(2.0 ** 24 + 8)
+    assert O.sum_(np.zeros(0, np.float32)) == np.float32(0.0)
+    B_, S_, H_, D_ = 3, 5, 4, 6
+    qkv = O.randn((B_ * S_, 3 * H_ * D_), 96)
+    q, k, v = O.qkv_split_heads(qkv, B_, S_, H_, D_, 0.37)
+    t = qkv.reshape(B_, S_, 3, H_, D_).transpose(2, 0, 3, 1, 4).reshape(3, B_ * H_, S_, D_)
+    assert np.array_equal(bits(q), bits(t[0] * np.float32(0.37)))
+    assert np.array_equal(bits(k), bits(t[1]))
+    assert np.array_equal(bits(v), bits(t[2]))
+    for i, part in enumerate((k, v)):
+        merged = O.merge_heads(part, B_, S_, H_, D_)
+        assert np.array_equal(bits(merged), bits(qkv[:, (i + 1) * H_ * D_:(i + 2) * H_ * D_]))
+    swapped = O.merge_heads(np.ascontiguousarray(k.reshape(B_, H_, S_, D_).transpose(0, 2, 1, 3)).reshape(
+        B_ * H_, S_, D_), B_, S_, H_, D_)
+    assert not np.array_equal(bits(swapped), bits(qkv[:, H_ * D_:2 * H_ * D_]))
+
+
+@ref_built
+def test_vs_reference_sum():
+    """CPUBackend::sum bit-exact against the compiled reference, on sizes around the AVX2
+    width and a large array whose sequential rounding differs from float64."""
+    R = O.ref_lib()
+    if not hasattr(R, "refSum"):
+        pytest.skip("compiled reference predates refSum: rebuild oracle/_ref")
+    for n, seed in ((1, 1), (7, 2), (8, 3), (31, 4), (1000, 5), (1 << 20, 6)):
+        x = O.randn((n,), 97 + seed, 3.0)
+        assert O.sum_(x).view(np.uint32) == O.sum_(x, backend="reference").view(np.uint32), n

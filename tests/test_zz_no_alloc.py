@@ -8,6 +8,7 @@ within the 1e-4 K-scaled bar of the float64 product. The library's pool must hol
 out the same bytes before and after (the entry allocates nothing).
 """
 import ctypes
+import os
 
 import numpy as np
 import pytest
@@ -17,9 +18,12 @@ from conftest import empty_dev, to_dev
 
 pytestmark = pytest.mark.gpu
 
-# (transA, transB, batch, M, N, K): pairs of calls in a row, the second smaller;
-# 128x4096x4096 splits K 8 ways (16 MiB of partials), 64x1024x2048 8 ways (2 MiB).
+# (transA, transB, batch, M, N, K): pairs of calls in a row, the second smaller. On a
+# 256-CU device 128x4096x4096 splits K 4 ways (8 MiB of partials), 64x1024x2048 8 ways
+# (2 MiB), and 448x4672x2048 (511 tiles of 64x64) 2 ways: 16.5 MB, the largest plan any
+# shape reaches there (the bound a CPU test checks over a grid of shapes).
 PAIRS = [
+    ((0, 0, 1, 448, 4672, 2048), (0, 0, 1, 128, 4096, 4096)),
     ((0, 0, 1, 128, 4096, 4096), (0, 0, 1, 64, 1024, 2048)),
     ((0, 1, 1, 128, 4096, 4096), (0, 1, 2, 64, 256, 2048)),
     ((1, 0, 3, 128, 512, 4096), (1, 1, 1, 96, 200, 1536)),
@@ -82,3 +86,65 @@ def test_no_alloc_degenerate(hip):
     with pytest.raises(hip.OmHipError, match="leading dimension"):
         A, B = to_dev(hip, np.ones((4, 3), np.float32)), to_dev(hip, np.ones((3, 5), np.float32))
         hip.call("omHipGemmStridedBatchedNoAlloc", 0, 0, 1, 4, 5, 3, A.ptr, 2, 12, B.ptr, 5, 15, dC.ptr, 5, 20)
+
+
+class _Streams:
+    """Two caller-owned HIP streams (non-blocking, default priority)."""
+
+    def __init__(self):
+        path = "libamdhip64.so"
+        for d in ("/opt/rocm/lib", "/opt/rocm/lib64"):
+            if os.path.exists(os.path.join(d, path)):
+                path = os.path.join(d, path)
+                break
+        self.rt = ctypes.CDLL(path)
+        self.made = []
+
+    def create(self) -> int:
+        s = ctypes.c_void_p()
+        assert self.rt.hipStreamCreateWithFlags(ctypes.byref(s), ctypes.c_uint(1)) == 0
+        self.made.append(s.value)
+        return s.value
+
+    def destroy_all(self, om) -> None:
+        for s in self.made:
+            om.release_stream(s)
+            self.rt.hipStreamDestroy(ctypes.c_void_p(s))
+        self.made = []
+
+
+def test_no_alloc_two_streams_ordered(hip):
+    """Split-K no-allocation calls alternate between two caller streams with no host wait: the
+    calls share one fixed array, so each must be ordered after the previous one (an event wait
+    on the device). Every output must equal the allocating entry's on the library stream, bit
+    for bit."""
+    cases = [(0, 0, 1, 128, 4096, 4096), (0, 1, 1, 128, 4096, 4096), (0, 0, 1, 64, 1024, 2048),
+             (1, 0, 2, 128, 512, 4096)]
+    data = []
+    for i, case in enumerate(cases):
+        A, B = _operands(case, 300 + 7 * i)
+        ta, tb, b, M, N, K = case
+        data.append((case, to_dev(hip, A), to_dev(hip, B), empty_dev(hip, (b, M, N)), empty_dev(hip, (b, M, N))))
+    for case, dA, dB, _, dRef in data:
+        _call(hip, "omHipGemmStridedBatched", case, dA, dB, dRef)
+    hip.synchronize()
+    st = _Streams()
+    try:
+        s = [st.create(), st.create()]
+        for rep in range(3):
+            for i, (case, dA, dB, dC, _) in enumerate(data):
+                hip.set_stream(s[(i + rep) % 2])
+                print(f"case no-alloc stream {(i + rep) % 2} {case}", flush=True)
+                _call(hip, "omHipGemmStridedBatchedNoAlloc", case, dA, dB, dC)
+            for x in s:
+                assert st.rt.hipStreamSynchronize(ctypes.c_void_p(x)) == 0
+            hip.set_stream(None)
+            for case, _, _, dC, dRef in data:
+                assert np.array_equal(_bits(dC.numpy()), _bits(dRef.numpy())), (rep, case)
+    finally:
+        hip.set_stream(None)
+        st.destroy_all(hip)
+
+
+def _bits(a):
+    return np.ascontiguousarray(a).view(np.uint32)
