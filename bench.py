@@ -22,8 +22,13 @@ Also reported:
   cpu_baseline  — the reference CPUBackend itself (oracle/_ref, built from the
                   reference sources) timed on this host's cores on a bounded
                   sample of the same workloads;
-  parity        — sampled rows of the timed GEMM and two sampled images of the
-                  conv stack against float64 (K-scaled error, bar 1e-4).
+  parity        — every leg's sampled outputs against float64 or the reference
+                  chain on the CPU: rows of the timed GEMM and of each sweep
+                  shape, two images of three layers of each conv stack, the
+                  network logits, each op and weight gradient of the training
+                  step, rows / batches of every ViT GEMM, two images of the
+                  fused attention and of the attention layer, and every layer,
+                  gradient and the loss of the MLP step (bars in parity.bars).
 Only one GPU is used: --gpus above 1 exits with a message.
 """
 from __future__ import annotations
@@ -80,11 +85,12 @@ def settle(om, fn, seconds: float = 0.03) -> None:
         batch = min(2 * batch, 1024)
 
 
-def read_rows(om, buf, rows, ncols: int) -> np.ndarray:
-    """Rows `rows` of a row-major fp32 device matrix with ncols columns (only those bytes cross PCIe)."""
-    out = np.empty((len(rows), ncols), np.float32)
+def read_rows(om, buf, rows, ncols: int, dtype=np.float32) -> np.ndarray:
+    """Rows `rows` of a row-major device matrix with ncols columns (only those bytes cross PCIe)."""
+    out = np.empty((len(rows), ncols), dtype)
+    nb = ncols * out.itemsize
     for i, r in enumerate(rows):
-        om.call("omHipCopyD2H", out[i].ctypes.data, buf.ptr + int(r) * ncols * 4, ncols * 4)
+        om.call("omHipCopyD2H", out[i].ctypes.data, buf.ptr + int(r) * nb, nb)
     return out
 
 
@@ -300,7 +306,9 @@ def bench_resnet18_net(om, steps: int, warmup: int, batch: int = 32):
     fl = forward_flops(batch)
     stem = 2.0 * batch * 64 * 112 * 112 * 3 * 49
     train_fl = 3.0 * fl - stem        # forward + input gradients (none for the image) + weight gradients
-    return fwd_ms, fl, got, train_ms, train_fl
+    # the last timed step's forward state and weight gradients, for the CPU check
+    train_state = (tnet.forward_state(img), tnet.grads())
+    return fwd_ms, fl, got, train_ms, train_fl, train_state
 
 
 def bench_infer_pipeline(om, n_img: int = 512, batch: int = 32, reps: int = 3):
@@ -368,20 +376,43 @@ def cpu_baseline_resnet18_net(n_img: int = 2, reps: int = 3):
     return kind, n_img / float(np.median(f)), n_img / float(np.median(t)), float(np.median(f)), float(np.median(t))
 
 
+RESNET50_CHECKED = (0, 26, 52)   # layers whose outputs (two images) are checked on the CPU
+
+
+def resnet50_layer_inputs(li: int, batch: int):
+    """Seeded input, Kaiming-uniform weight and BN vectors of ResNet-50 conv layer li."""
+    from resnet_shapes import resnet50_convs
+    name, cin, h, w, cout, k, s, p = resnet50_convs()[li]
+    bnd = np.sqrt(6.0 / (cin * k * k))
+    x = syn.randn((batch, cin, h, w), 700 + li)
+    wt = syn.uniform((cout, cin, k, k), 800 + li, -bnd, bnd)
+    bn = (syn.uniform((cout,), 900 + li, 0.5, 1.5), syn.randn((cout,), 1000 + li, 0.1),
+          syn.randn((cout,), 1100 + li, 0.1), syn.uniform((cout,), 1200 + li, 0.5, 1.5))
+    return x, wt, bn
+
+
 def resnet50_setup(om, batch: int = 64):
     """The 53 ResNet-50 conv layers' seeded inputs, uploaded to HBM."""
     from resnet_shapes import out_hw, resnet50_convs
     layers = []
     for li, (name, cin, h, w, cout, k, s, p) in enumerate(resnet50_convs()):
-        bnd = np.sqrt(6.0 / (cin * k * k))
         ho, wo = out_hw(h, k, s, p), out_hw(w, k, s, p)
-        x = om.DeviceBuffer.from_numpy(syn.randn((batch, cin, h, w), 700 + li))
-        wt = om.DeviceBuffer.from_numpy(syn.uniform((cout, cin, k, k), 800 + li, -bnd, bnd))
-        bn = [om.DeviceBuffer.from_numpy(a) for a in (syn.uniform((cout,), 900 + li, 0.5, 1.5), syn.randn((cout,), 1000 + li, 0.1),
-                                                       syn.randn((cout,), 1100 + li, 0.1), syn.uniform((cout,), 1200 + li, 0.5, 1.5))]
+        xh, wh, bnh = resnet50_layer_inputs(li, batch)
+        x, wt = om.DeviceBuffer.from_numpy(xh), om.DeviceBuffer.from_numpy(wh)
+        bn = [om.DeviceBuffer.from_numpy(a) for a in bnh]
         y = om.DeviceBuffer.empty((batch, cout, ho, wo))
         layers.append(((name, cin, h, w, cout, k, s, p), x, wt, bn, y))
     return layers
+
+
+def resnet50_samples(om, layers, batch: int = 64):
+    """Images 0 and batch-1 of the checked layers' outputs (every output is overwritten per pass)."""
+    out = []
+    for li in RESNET50_CHECKED:
+        y = layers[li][4]
+        per_img = int(np.prod(y.shape[1:]))
+        out.append((li, read_rows(om, y, [0, batch - 1], per_img).reshape((2,) + tuple(y.shape[1:]))))
+    return out
 
 
 def bench_resnet50(om, layers, steps: int, warmup: int, batch: int = 64):
@@ -462,8 +493,17 @@ def bench_vit_half(om, steps: int, warmup: int, bf16: bool, proj_nt: bool = Fals
         flops_total += f
         total_ms += ms
         per.append({"gemm": name, "shape": [b, m, n, k], "ms": round(ms, 4), "tflops": round(f / ms / 1e9, 1)})
+    # sampled outputs for the CPU check: rows 0, M/2, M-1 of a projection, the first and last
+    # batch of an attention product (each launch overwrites its whole C)
+    samples = {}
+    for name, b, m, n, k, tb, ha, hw, c in bufs:
+        if b == 1:
+            rows = [0, m // 2, m - 1]
+            samples[name] = (rows, read_rows(om, c, rows, n))
+        else:
+            samples[name] = ([0, b - 1], read_rows(om, c, [0, b - 1], m * n).reshape(2, m, n))
     if proj_nt:
-        return total_ms, flops_total, per, None, None
+        return total_ms, flops_total, per, None, None, samples
     # Fused attention on the QKV projection's output layout [T, 3*768] (split + softmax(QK^T/8) V + merge),
     # replacing the two batched products above plus the softmax between them.
     batch, tokens, heads, dh = 64, 197, 12, 64
@@ -519,7 +559,11 @@ def bench_vit_half(om, steps: int, warmup: int, bf16: bool, proj_nt: bool = Fals
     mha = {"op": "multi_head_attention_forward", "shape": [batch, tokens, heads, dh], "ms": round(mha_ms, 4),
            "tflops": round(mha_flops / mha_ms / 1e9, 1),
            "launches": "QKV Linear (+bias, half out) -> fused attention (half out) -> output Linear (+bias, fp32 out)"}
-    return total_ms, flops_total, per, fused, mha
+    # images 0 and 63 of the fused attention's context (half) and of the layer's output
+    imgs = [0, batch - 1]
+    samples["attention_fused"] = (imgs, read_rows(om, ctx, imgs, tokens * d, np.uint16).reshape(2, tokens, d))
+    samples["attention_layer"] = (imgs, read_rows(om, y, imgs, tokens * d).reshape(2, tokens, d))
+    return total_ms, flops_total, per, fused, mha, samples
 
 
 def bench_mlp(om, steps: int, warmup: int, batch: int = 128):
@@ -587,7 +631,11 @@ def bench_mlp(om, steps: int, warmup: int, batch: int = 128):
     t.stop()
     graph_ms = t.ms() / steps
     flops = sum(3 * 2.0 * batch * i * o for i, o in zip(dims[:-1], dims[1:]))
-    return ms, flops, graph_ms, same, float(eager_out[-1][0])
+    # the step's state for the CPU check (every buffer is rewritten each step)
+    state = {"a": [a[j].numpy() for j in (1, 2)], "z3": z[2].numpy(), "g": [d.numpy() for d in g],
+             "gW": [d.numpy() for d in gW], "gb": [d.numpy() for d in gb], "gA0": gA[0].numpy(),
+             "loss": float(eager_out[-1][0]), "labels": labels}
+    return ms, flops, graph_ms, same, float(eager_out[-1][0]), state
 
 
 # ---- CPU checks of the GPU legs' results (run with the CPU baseline leg) ----
@@ -620,6 +668,140 @@ def cpu_check_resnet18(samples: list, batch: int = 32) -> float:
         o64, bound = O.conv_f64(x[[0, batch - 1]], wt, None, s, p, gamma=g, beta=b, mean=m, var=v, act=1)
         errs.append(O.normalized_error(y, o64, bound))
     return max(errs)
+
+
+def cpu_check_resnet50(samples: list, batch: int = 64) -> float:
+    import oracle as O
+    from resnet_shapes import resnet50_convs
+    errs = []
+    for li, y in samples:
+        name, cin, h, w, cout, k, s, p = resnet50_convs()[li]
+        x, wt, (g, b, m, v) = resnet50_layer_inputs(li, batch)
+        o64, bound = O.conv_f64(x[[0, batch - 1]], wt, None, s, p, gamma=g, beta=b, mean=m, var=v, act=1)
+        errs.append(O.normalized_error(y, o64, bound))
+    return max(errs)
+
+
+def _half_round(x, bf16: bool) -> np.ndarray:
+    import oracle as O
+    return O.bf16_round(x) if bf16 else np.asarray(x, np.float32).astype(np.float16).astype(np.float32)
+
+
+def cpu_check_vit(vit_samples: dict) -> dict:
+    """The ViT legs' sampled outputs against float64 on the same rounded inputs (the seeded
+    draws of bench_vit_half regenerated in the same order): projection rows and attention
+    product batches K-scaled (bar 1e-4: fp32 accumulate of exact half products), the fused
+    attention's half context per element against sum_j P_ij |V_jd| (bar 2e-3 fp16, 1.2e-2
+    bf16) and the attention layer's output against ((B_ctx + |ctx|) |W_out| + |b_out|)
+    (bar 2u + 1e-4, u = 2^-11 fp16, 2^-8 bf16)."""
+    import oracle as O
+    rng = np.random.default_rng(5)
+    draws = []
+    for name, b, m, n, k, tb in vit_gemm_shapes():
+        a = rng.standard_normal(b * m * k, dtype=np.float32)
+        w = (rng.standard_normal(b * n * k, dtype=np.float32) * (0.02 if b == 1 else 1.0)).astype(np.float32)
+        draws.append((name, b, m, n, k, a, w))
+    batch, tokens, heads, dh = 64, 197, 12, 64
+    T, d = batch * tokens, heads * dh
+    qkv = (rng.standard_normal(T * 3 * d, dtype=np.float32) * 0.5)
+    x = rng.standard_normal(T * d, dtype=np.float32)
+    wq = rng.standard_normal(d * 3 * d, dtype=np.float32) * 0.036
+    wo = rng.standard_normal(d * d, dtype=np.float32) * 0.036
+    bq = rng.standard_normal(3 * d, dtype=np.float32) * 0.1
+    bo = rng.standard_normal(d, dtype=np.float32) * 0.1
+    out = {}
+    for bf, (nn_smp, nt_smp) in vit_samples.items():
+        tag = "bf16" if bf else "fp16"
+        worst = 0.0
+        for layout, smp in (("NN", nn_smp), ("NT", nt_smp)):
+            for name, b, m, n, k, a, w in draws:
+                picks, got = smp[name]
+                ar, wr = _half_round(a, bf).reshape(b, m, k), _half_round(w, bf)
+                tb = name == "qk_t" or (layout == "NT" and b == 1)
+                wr = wr.reshape(b, n, k) if tb else wr.reshape(b, k, n)
+                for i, pk in enumerate(picks):
+                    if b == 1:
+                        A, W, g = ar[0][[pk]], wr[0], got[i][None, :]
+                    else:
+                        A, W, g = ar[pk], wr[pk], got[i]
+                    C64, bound = O.gemm_f64(A, W, transB=tb)
+                    worst = max(worst, O.normalized_error(g, C64, bound))
+        out[tag + "_gemms_max_err"] = worst
+        # fused attention (half context) and the attention layer, images 0 and 63
+        imgs, ctx = nn_smp["attention_fused"]
+        ctx = (ctx.astype(np.uint32) << 16).view(np.float32) if bf else ctx.view(np.float16).astype(np.float32)
+        qr = _half_round(qkv, bf).reshape(batch, tokens, 3 * d)
+        e = 0.0
+        for i, img in enumerate(imgs):
+            ref64, bnd = O.attention_f64(qr[img], 1, tokens, heads, dh, 0.125)
+            e = max(e, O.normalized_error(ctx[i], ref64, bnd))
+        out[tag + "_attention_fused_err"] = e
+        _, y = nn_smp["attention_layer"]
+        xr = _half_round(x, bf).reshape(batch, tokens, d)
+        wqr, wor = _half_round(wq, bf).reshape(d, 3 * d).astype(np.float64), _half_round(wo, bf).reshape(d, d).astype(np.float64)
+        scale = float(np.float32(1.0 / np.sqrt(np.float32(dh))))
+        e = 0.0
+        for i, img in enumerate(imgs):
+            q64 = xr[img].astype(np.float64) @ wqr + bq.astype(np.float64)
+            ctx64, bctx = O.attention_f64(_half_round(q64.astype(np.float32), bf), 1, tokens, heads, dh, scale)
+            o64 = ctx64 @ wor + bo.astype(np.float64)
+            bnd = (bctx + np.abs(ctx64)) @ np.abs(wor) + np.abs(bo.astype(np.float64))
+            e = max(e, O.normalized_error(y[i], o64, bnd))
+        out[tag + "_attention_layer_err"] = e
+    return out
+
+
+def cpu_check_mlp(st: dict, batch: int = 128) -> dict:
+    """The MLP step layer by layer in float64 on the GPU's own inputs to each op (so a ReLU
+    input within rounding of 0 takes the GPU's side): each layer's output and each gradient
+    K-scaled (bar 1e-4), the loss against the oracle's softmax + cross-entropy of the GPU
+    logits (relative 1e-5) and the logit gradient (p - t) / batch (relative Frobenius 1e-5)."""
+    import oracle as O
+    dims = [784, 256, 128, 10]
+    x = syn.uniform((batch, 784), 1).astype(np.float64)
+    Ws = [syn.uniform((i, o), 10 + j, -np.sqrt(6 / i), np.sqrt(6 / i)).astype(np.float64)
+          for j, (i, o) in enumerate(zip(dims[:-1], dims[1:]))]
+    T = np.eye(10, dtype=np.float32)[st["labels"]]
+    acts = [x] + [a.astype(np.float64) for a in st["a"]]
+    errs = []
+    for j in range(3):                       # act(a_j W_j + 0), biases are zero
+        ref = acts[j] @ Ws[j]
+        bound = np.abs(acts[j]) @ np.abs(Ws[j])
+        got = st["a"][j] if j < 2 else st["z3"]
+        errs.append(O.normalized_error(got, np.maximum(ref, 0) if j < 2 else ref, bound))
+    p = O.softmax(st["z3"])
+    loss_err = abs(st["loss"] - O.cross_entropy(p, T)) / abs(st["loss"])
+    glogit_err = O.frobenius_rel(st["g"][2], O.cross_entropy_softmax_backward(p, T))
+    for j in range(3):
+        g = st["g"][j].astype(np.float64)
+        errs.append(O.normalized_error(st["gW"][j], acts[j].T @ g, np.abs(acts[j]).T @ np.abs(g)))
+        errs.append(O.normalized_error(st["gb"][j], g.sum(axis=0), np.abs(g).sum(axis=0)))
+        dA = g @ Ws[j].T
+        bound = np.abs(g) @ np.abs(Ws[j]).T
+        if j > 0:
+            gate = st["a"][j - 1] > 0
+            errs.append(O.normalized_error(st["g"][j - 1], np.where(gate, dA, 0.0), bound))
+        else:
+            errs.append(O.normalized_error(st["gA0"], dA, bound))
+    return {"layers_and_gradients_max_err": max(errs), "loss_rel_err": loss_err, "grad_logits_rel_err": glogit_err}
+
+
+def cpu_check_resnet18_train(state) -> dict:
+    """The timed b32 training step: each forward op against the CPU op on the GPU's own input
+    to it (relative Frobenius, bar 1e-4), and every weight gradient against the reference
+    backward replayed on the GPU's forward state (bar 1e-3)."""
+    import oracle as O
+    from resnet_net import conv_list, cpu_backward, cpu_forward_local, make_params
+    f, grads = state
+    P = make_params(seed=1)
+    g_logits = syn.randn((32, 1000), 901, 0.01)
+    local = cpu_forward_local(P, f)
+    op_err = max(O.frobenius_rel(f[k].reshape(v.shape), v) for k, v in local.items())
+    del local
+    ref = cpu_backward(P, f, g_logits)
+    g_err = max(O.frobenius_rel(grads[n].reshape(ref[n].shape), ref[n])
+                for n in [c for c, *_ in conv_list()] + ["fc.w", "fc.b"])
+    return {"forward_ops_max_rel_err": op_err, "weight_grads_max_rel_err": g_err}
 
 
 def cpu_check_resnet18_net(logits2) -> float:
@@ -788,6 +970,7 @@ def workload_probe(name: str):
     """A short dispatch sequence for kernel-trace profiling (no JSON):
     resnet18_train — three ResNet-18 b32 training steps; vit_attention — ten fused
     attentions (ViT-B/16 b64, fp16) after the ten Q.K^T / P.V batched products they replace;
+    vit_gemms — each ViT-B/16 b64 GEMM (fp16, fp32 output) three times;
     half_power — the fp16 GEMM on constant and on random operands (same kernel and shape)."""
     import omnimatchdeeplearningtool_amd as om
     om.init(0)
@@ -815,6 +998,27 @@ def workload_probe(name: str):
             H.gemmStridedBatchedHalf(0, 0, 0, b * heads, S, dh, S, p16, S, S * S, q, dh, S * dh, pv, dh, S * dh)
         for _ in range(10):
             H.attentionHalf(qkv, ctx, b, S, heads, dh, 0.125, outHalf=True)
+    elif name == "vit_gemms":
+        # The ViT-B/16 b64 GEMM set (fp16 inputs, fp32 output, projections NN), each GEMM
+        # three times after a 30 ms warm-up of the whole set, one after another.
+        bufs = []
+        for gname, b, m, n, k, tb in vit_gemm_shapes():
+            a = om.DeviceBuffer.from_numpy(syn.randn((b * m * k,), 31))
+            w = om.DeviceBuffer.from_numpy(syn.randn((b * n * k,), 32, 0.02 if b == 1 else 1.0))
+            ha, hw = om.DeviceBuffer.empty((b * m * k,), np.uint16), om.DeviceBuffer.empty((b * n * k,), np.uint16)
+            H.convertToHalf(a, ha, b * m * k)
+            H.convertToHalf(w, hw, b * n * k)
+            a.free(); w.free()
+            bufs.append((gname, b, m, n, k, tb, ha, hw, om.DeviceBuffer.empty((b * m * n,))))
+        run = lambda it: H.gemmStridedBatchedHalf(0, 0, it[5], it[1], it[2], it[3], it[4], it[6], it[4], it[2] * it[4],
+                                                  it[7], it[4] if it[5] else it[3], it[3] * it[4], it[8], it[3],
+                                                  it[2] * it[3])
+        settle(om, lambda: [run(it) for it in bufs])
+        for it in bufs:
+            for _ in range(3):
+                run(it)
+            om.synchronize()
+            log(f"vit_gemms {it[0]} done")
     elif name == "half_power":
         # One kernel and one shape (fp16 NT 8192^3, A times its own transpose), two
         # operand sets: every element 1.0, and N(0,1). The instruction stream is the
@@ -853,7 +1057,7 @@ def main():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--probe", choices=["resnet18_train", "vit_attention", "half_power"],
+    ap.add_argument("--probe", choices=["resnet18_train", "vit_attention", "half_power", "vit_gemms"],
                     help="run only a short dispatch sequence for kernel-trace profiling (no JSON line)")
     ap.add_argument("--traffic-probe", action="store_true",
                     help="run only the dispatch sequence profiled for HBM traffic (no JSON line)")
@@ -902,12 +1106,13 @@ def main():
     log("resnet50 conv stack b64")
     r50_ms, r50_flops, r50_roof = bench_resnet50(om, r50_layers, max(3, args.steps // 10), 1)
     log(f"resnet50 {r50_ms:.3f} ms/batch  {64 / r50_ms * 1e3:.0f} img/s  roof frac {r50_roof / r50_ms:.3f}")
+    r50_samples = resnet50_samples(om, r50_layers)
     del r50_layers
     conv_samples, r_graph_same = resnet18_checks(om, r18_layers, r18_run)
     log(f"resnet18 graph replay bit-identical to eager: {r_graph_same}")
 
     log("resnet18 network b32 (inference forward, training step)")
-    n_fwd_ms, n_fl, n_logits2, n_train_ms, n_train_fl = bench_resnet18_net(om, max(5, args.steps // 5), 2)
+    n_fwd_ms, n_fl, n_logits2, n_train_ms, n_train_fl, n_train_state = bench_resnet18_net(om, max(5, args.steps // 5), 2)
     log(f"resnet18 net forward {n_fwd_ms:.3f} ms  {32 / n_fwd_ms * 1e3:.0f} img/s; "
         f"train step {n_train_ms:.3f} ms  {32 / n_train_ms * 1e3:.0f} img/s")
 
@@ -917,9 +1122,11 @@ def main():
         f"graph replay {infer['resident_forward_graph']['ms']:.3f} ms")
 
     vit = {}
+    vit_samples = {}
     for bf in (False, True):
-        v_ms, v_flops, v_per, v_fused, v_mha = bench_vit_half(om, max(5, args.steps // 5), 2, bf)
-        t_ms, t_flops, t_per, _, _ = bench_vit_half(om, max(5, args.steps // 5), 2, bf, proj_nt=True)
+        v_ms, v_flops, v_per, v_fused, v_mha, v_smp = bench_vit_half(om, max(5, args.steps // 5), 2, bf)
+        t_ms, t_flops, t_per, _, _, t_smp = bench_vit_half(om, max(5, args.steps // 5), 2, bf, proj_nt=True)
+        vit_samples[bf] = (v_smp, t_smp)
         lin_ms = sum(x["ms"] for x in v_per if x["gemm"] not in ("qk_t", "pv"))
         vit["bf16" if bf else "fp16"] = {"layout": "projections NN: W stored [in, out] as Linear keeps it",
                                          "ms_per_set": round(v_ms, 4), "tflops": round(v_flops / v_ms / 1e9, 1),
@@ -936,22 +1143,27 @@ def main():
             f"{v_mha['tflops']:.1f} TFLOP/s")
         for x in v_per:
             log(f"  {x['gemm']:8s} NN {x['ms'] * 1e3:8.1f} us {x['tflops']:7.1f} TF")
-    mlp_ms, mlp_flops, mlp_graph_ms, mlp_graph_same, mlp_loss = bench_mlp(om, max(20, args.steps), 5)
+    mlp_ms, mlp_flops, mlp_graph_ms, mlp_graph_same, mlp_loss, mlp_state = bench_mlp(om, max(20, args.steps), 5)
     log(f"mlp step {mlp_ms * 1e3:.1f} us (graph replay {mlp_graph_ms * 1e3:.1f} us, bit-identical {mlp_graph_same}),"
         f" loss {mlp_loss:.4f}")
 
     cpu = None
     cpu_r18 = None
     cpu_extra = {}
-    gemm_err = conv_err = n_err = None
+    gemm_err = conv_err = n_err = r50_err = None
+    vit_err, mlp_err, train_err = {}, {}, {}
     if rank == 0 and not args.no_cpu:
         log("cpu checks of the sampled GPU results (oracle, float64)")
         gemm_err = cpu_check_gemm(gemm_rows)
         cpu_check_sweep(sweep, sweep_samples)
         conv_err = cpu_check_resnet18(conv_samples)
+        r50_err = cpu_check_resnet50(r50_samples)
         n_err = cpu_check_resnet18_net(n_logits2)
+        vit_err = cpu_check_vit(vit_samples)
+        mlp_err = cpu_check_mlp(mlp_state)
+        train_err = cpu_check_resnet18_train(n_train_state)
         log(f"parity: gemm {gemm_err:.2e}, sweep max {max(e['parity'] for e in sweep):.2e}, conv {conv_err:.2e}, "
-            f"network logits {n_err:.1e}")
+            f"resnet50 {r50_err:.2e}, network logits {n_err:.1e}, vit {vit_err}, mlp {mlp_err}, train {train_err}")
         threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
         log(f"cpu baseline (reference CPUBackend, {threads} threads)")
         kind, cpu_tf, cpu_dt, n1 = cpu_baseline_gemm()
@@ -980,6 +1192,7 @@ def main():
         cpu_extra["mlp"] = {"value": round(msm, 3), "unit": "ms/step", "cores": threads, "kind": km if km == "reference" else "port",
                             "sample": "mean of 20 MLP fwd+bwd steps after one warm-up"}
 
+    del n_train_state
     gemm_kernel_ms = ms
     traffic = _traffic("gemm_f32_4096_nn")
     line = {
@@ -1007,7 +1220,18 @@ def main():
                                        "`bench.py --traffic-probe`, copy-calibrated (recorded, not measured in this run)"},
         "cpu_baseline": cpu,
         "gemm_sweep": sweep,
-        "parity": {"gemm_sampled_rows_max_err": gemm_err, "conv_sampled_max_err": conv_err, "tol": 1e-4},
+        "parity": {"gemm_sampled_rows_max_err": gemm_err, "conv_sampled_max_err": conv_err, "tol": 1e-4,
+                   "resnet50_conv_sampled_max_err": r50_err,
+                   "resnet18_network_logits_rel_err": n_err,
+                   "resnet18_train_step": train_err,
+                   "vit": vit_err,
+                   "mlp_step": mlp_err,
+                   "bars": {"gemm, conv, resnet50, vit gemms, mlp layers and gradients": "1e-4 K-scaled (float64)",
+                            "resnet18 logits": "1e-4 relative Frobenius",
+                            "train step": "forward ops 1e-4, weight gradients 1e-3 relative Frobenius",
+                            "attention fused (half context)": "2e-3 fp16 / 1.2e-2 bf16 of sum_j P_ij |V_jd|",
+                            "attention layer": "2u + 1e-4 of (B_ctx + |ctx|) |W_out| + |b_out|",
+                            "mlp loss, logit gradient": "1e-5 relative"}},
         "resnet18_conv": {"value": round(img_s, 1), "unit": "img/s", "batch": 32, "ms_per_batch": round(r_ms, 4),
                           "launch": "eager: 20 conv launches on the library stream",
                           "tflops": round(r_flops / r_ms / 1e9, 2),

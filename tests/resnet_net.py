@@ -403,6 +403,39 @@ def cpu_forward_train(P: dict, img: np.ndarray, backend: str = "oracle") -> dict
     return f
 
 
+def cpu_forward_local(P: dict, f: dict, backend: str = "oracle") -> dict:
+    """Each op of the training forward recomputed on the CPU from the GPU's own input to
+    that op (f = GpuResNet18.forward_state of a fused step): conv2d, batchNorm2d (training
+    statistics), relu, add, maxPool2d and adaptiveAvgPool2d, one layer at a time. Checks
+    each kernel without the drift a deep chain accumulates from rounding differences."""
+    import oracle as O
+    out = {}
+
+    def conv_bn(x, name, s, p, key):
+        out[key + ".z"] = O.conv2d(x, P[name + ".w"], None, s, p, backend=backend)
+        y, _, _, sm, si = O.batchnorm2d_train(f[key + ".z"], P[name + ".gamma"], P[name + ".beta"],
+                                              P[name + ".mean"].copy(), P[name + ".var"].copy(), EPS, MOMENTUM,
+                                              backend=backend)
+        out[key + ".sm"], out[key + ".si"] = sm, si
+        return y
+
+    out["stem.a"] = O.relu(conv_bn(f["img"], "stem", 2, 3, "stem"), backend=backend)
+    out["pool"], _ = O.maxpool2d(f["stem.a"], 3, 2, 1, backend=backend)
+    x = f["pool"]
+    for pre, ci, co, s, ds, hw in blocks():
+        out[pre + ".a1"] = O.relu(conv_bn(x, pre + ".conv1", s, 1, pre + ".c1"), backend=backend)
+        y2 = conv_bn(f[pre + ".a1"], pre + ".conv2", 1, 1, pre + ".c2")
+        if ds:
+            out[pre + ".ds.y"] = conv_bn(x, pre + ".ds", s, 0, pre + ".ds")
+            sc = f[pre + ".ds.y"]
+        else:
+            sc = x
+        out[pre + ".out"] = O.relu(O.add(y2, sc, backend=backend), backend=backend)
+        x = f[pre + ".out"]
+    out["pooled"] = O.adaptive_avgpool2d(x, 1, 1, backend=backend).reshape(x.shape[0], -1)
+    return out
+
+
 def _block_inputs(f: dict) -> list:
     ins, x = [], f["pool"]
     for pre, *_ in blocks():
