@@ -999,8 +999,16 @@ def workload_probe(name: str):
         for _ in range(10):
             H.attentionHalf(qkv, ctx, b, S, heads, dh, 0.125, outHalf=True)
     elif name == "vit_gemms":
-        # The ViT-B/16 b64 GEMM set (fp16 inputs, fp32 output, projections NN), each GEMM
-        # three times after a 30 ms warm-up of the whole set, one after another.
+        # A 256 MiB device copy (the calibration of the traffic counters), then the ViT-B/16
+        # b64 GEMM set (fp16 inputs, fp32 output, projections NN), each GEMM three times after
+        # a 30 ms warm-up of the whole set, one after another.
+        n = 64 << 20
+        src, dst = om.DeviceBuffer.empty((n,)), om.DeviceBuffer.empty((n,))
+        H.fillValue(src, n, 1.0)
+        om.synchronize()
+        H.copy(src, dst, n)
+        om.synchronize()
+        src.free(); dst.free()
         bufs = []
         for gname, b, m, n, k, tb in vit_gemm_shapes():
             a = om.DeviceBuffer.from_numpy(syn.randn((b * m * k,), 31))
