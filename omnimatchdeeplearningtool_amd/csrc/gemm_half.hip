@@ -1023,11 +1023,19 @@ __global__ __launch_bounds__(Cfg::NT) void gemm_half_fast(HalfFastParams p) {
 // 128 x 128 (one wave per SIMD cannot hide its own LDS and barrier latency)
 // and BK = 32 (twice the barriers). 128 x 128 x 64 (4 waves of 64 x 64, two
 // workgroups per CU) and 64 x 64 x 64 (4 waves of 32 x 32) serve problems
-// whose large-tile count would leave CUs idle.
+// whose large-tile count would leave CUs idle. 192 x 256 x 64 (8 waves of
+// 96 x 64) fills more CUs than 256 x 256 when a problem is one round of
+// large tiles on part of the chip (12608 x 768: 198 tiles instead of 150);
+// its A rows are K-major (192 rows are not a power-of-two run of 16-byte
+// chunks for the R-major loader).
 #ifndef OMHIP_HALF_L
 #define OMHIP_HALF_L 256, 256, 64, 64, 128
 #endif
+#ifndef OMHIP_HALF_R_RATE
+#define OMHIP_HALF_R_RATE 0.95
+#endif
 using FCfgL = FCfg<OMHIP_HALF_L>;
+using FCfgR = FCfg<192, 256, 64, 96, 64>;
 using FCfgM = FCfg<128, 128, 64, 64, 64>;
 using FCfgS = FCfg<64, 64, 64, 32, 32>;
 
@@ -1061,10 +1069,10 @@ static int launchFast(HalfFastParams prm, int batch) {
 // where the model picks the fastest tile or one within 4 % of it: e.g.
 // 12608 x 2304 x 768 and 4096^3 take 256x256, 2048 x 4096 x 4096 128x128,
 // 768 x (197 x 64 x 197), 2048^3 and 1024^3 64x64.
-static int pickFastTile(int M, int N, int K, int batch) {
+static int pickFastTile(int M, int N, int K, int batch, bool transA) {
     const long long cus = cuCount();
     struct T { int bm, bn, slots; double rate; };
-    const T cand[3] = {{256, 256, 1, 1.0}, {128, 128, 2, 0.75}, {64, 64, 4, 0.5}};
+    const T cand[4] = {{256, 256, 1, 1.0}, {128, 128, 2, 0.75}, {64, 64, 4, 0.5}, {192, 256, 1, OMHIP_HALF_R_RATE}};
     // A product of one K slice is bound by its C stores, not its MFMAs: many
     // small workgroups overlap one another's stores (batched Q.K^T 768 x 197
     // x 197 x 64: 64x64 42.3 us, 256x256 with the compact store 46.0 us,
@@ -1072,7 +1080,7 @@ static int pickFastTile(int M, int N, int K, int batch) {
     if (K <= 64) return 2;
     int best = 0;
     double bestCost = 0;
-    for (int c = 0; c < 3; ++c) {
+    for (int c = 0; c < (transA ? 3 : 4); ++c) {
         const long long tiles = (long long)((M + cand[c].bm - 1) / cand[c].bm) * ((N + cand[c].bn - 1) / cand[c].bn) * batch;
         const long long n = (tiles + cus - 1) / cus;
         const double fill = (double)std::min<long long>(n, cand[c].slots) / cand[c].slots;
@@ -1084,9 +1092,12 @@ static int pickFastTile(int M, int N, int K, int batch) {
 
 template <bool BF16, bool TA, bool TB, bool SWAP, bool RAG>
 static int launchFastT(const HalfFastParams& prm, int batch) {
-    switch (pickFastTile(prm.M, prm.N, prm.K, batch)) {
+    switch (pickFastTile(prm.M, prm.N, prm.K, batch, TA)) {
         case 0: return launchFast<FCfgL, BF16, TA, TB, SWAP, RAG>(prm, batch);
         case 1: return launchFast<FCfgM, BF16, TA, TB, SWAP, RAG>(prm, batch);
+        case 3:
+            if constexpr (!TA) return launchFast<FCfgR, BF16, TA, TB, SWAP, RAG>(prm, batch);
+            [[fallthrough]];
         default: return launchFast<FCfgS, BF16, TA, TB, SWAP, RAG>(prm, batch);
     }
 }

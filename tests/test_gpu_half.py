@@ -69,8 +69,9 @@ def test_attention_batched(hip, bf16):
     assert O.normalized_error(dS.numpy(), O.batched_matmul_transB(Q, Kt), bS32) <= O.TOL_HALF
 
 
-# (batch, M, N, K): on a 256-CU MI355X these select the 256x256 tile (first),
-# the 128x128 tile (second) and the 64x64 tile (third); every one has ragged
+# (batch, M, N, K): on a 256-CU MI355X these select the 192x256 tile (first; the
+# 256x256 tile in the TN / TT layouts, whose A is R-major), the 128x128 tile
+# (second) and the 64x64 tile (third); every one has ragged
 # M, N and a K that ends inside a 64-deep slice. The last shape has N % 4 != 0,
 # so C leaves through 32-bit stores.
 FAST_SHAPES = [(40, 392, 392, 136), (24, 392, 392, 72), (4, 296, 264, 136), (3, 104, 262, 200)]
@@ -254,3 +255,35 @@ def test_half_one_round_staged(hip, bf16, M, N, K, transB):
     chain16 = empty_dev(hip, (M, N), np.uint16)
     H.convertToHalf(C, chain16, M * N, bf16=bf16)
     assert np.array_equal(out16.numpy(), chain16.numpy())
+
+
+# (M, N, K): one round of 192 x 256 tiles on a 256-CU MI355X (the tile model prefers it
+# when 256 x 256 tiles would leave more CUs idle: 8000 x 1500 is 252 tiles against 192);
+# ragged M, N and K, an odd K (the ragged K-major loader) and the ViT-B/16 b64 output
+# projection itself.
+TILE192_SHAPES = [(8000, 1500, 200), (8000, 1500, 201), (12608, 768, 768)]
+
+
+@pytest.mark.parametrize("bf16", [False, True], ids=["f16", "bf16"])
+@pytest.mark.parametrize("transB", [0, 1], ids=["NN", "NT"])
+@pytest.mark.parametrize("M,N,K", TILE192_SHAPES, ids=lambda v: str(v))
+def test_half_tile_192(hip, bf16, transB, M, N, K):
+    """Sampled rows (every 97th and the last five, all columns) against float64, and every
+    row sum and column sum of C against A (B 1) and (1^T A) B, K-scaled (tol 1e-4)."""
+    A = O.randn((M, K), M + N + K)
+    B = O.randn((N, K) if transB else (K, N), M + N + K + 1, 0.05)
+    dA, dB = to_dev(hip, _bits(A, bf16)), to_dev(hip, _bits(B, bf16))
+    dC = empty_dev(hip, (M, N))
+    hip.HIPBackend.gemmStridedBatchedHalf(1 if bf16 else 0, 0, transB, 1, M, N, K, dA, K, 0, dB,
+                                          K if transB else N, 0, dC, N, 0)
+    C = dC.numpy()
+    A64 = _round(A, bf16).astype(np.float64)
+    B64 = _round(B, bf16).astype(np.float64)
+    B64 = B64.T if transB else B64
+    rows = _sample_rows(M)
+    assert O.normalized_error(C[rows], A64[rows] @ B64, np.abs(A64[rows]) @ np.abs(B64)) <= 1e-4
+    C64 = C.astype(np.float64)
+    rs_bound = np.abs(A64) @ np.abs(B64).sum(axis=1)
+    assert np.max(np.abs(C64.sum(axis=1) - A64 @ B64.sum(axis=1)) / rs_bound) <= 1e-4
+    cs_bound = np.abs(A64).sum(axis=0) @ np.abs(B64)
+    assert np.max(np.abs(C64.sum(axis=0) - A64.sum(axis=0) @ B64) / cs_bound) <= 1e-4
