@@ -361,10 +361,15 @@ __device__ __forceinline__ void storeEpilogue(const ConvParams& p, const f32x16 
 // epilogue, writes the output and returns the counter to zero. The order of
 // the sum does not depend on which block arrives last, so the result is
 // deterministic and equal to a separate finishing pass's. Partials are
-// written and read with agent-coherent accesses (they cross XCDs); a block's
-// stores have completed (s_waitcnt) before its thread 0 increments the
-// counter, and the last block reads the partials only after seeing the
-// final count.
+// written and read with agent-coherent (sc1) accesses — the encoding of
+// monotonic agent-scope atomic loads / stores in the gfx942 / gfx950 memory
+// model, performed at the device coherence point past the per-XCD L2s; a
+// block's stores have completed (s_waitcnt) before its thread 0 increments the
+// counter, and the last block reads the partials only after seeing the final
+// count. An acquire-release counter add would add an L2 write-back to every
+// arrival and an L2 invalidate to each, which exist for non-coherent accesses
+// (none cross between the blocks here): measured on MI355X, the ResNet-18 b32
+// stack then ran 1134 -> 1361 us (layer-3 3x3 convs 71 -> 95 us).
 template <class Cfg>
 __device__ __forceinline__ void finishBlock(const ConvParams& p, f32x16 (&acc)[Cfg::FM][Cfg::FN], const float* sEpi,
                                             int* sFlag, int m0, int n0, int wm, int wn, int lane, int piece,

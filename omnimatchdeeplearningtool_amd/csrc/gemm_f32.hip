@@ -104,6 +104,95 @@ template <bool KMAJOR, int LK, int R, int BK, int NT>
 using GemmLoader = std::conditional_t<LK == 2, BufVecLoader<KMAJOR, R, BK, NT>,
                                       DenseLoaderAdapter<KMAJOR, LK == 1, R, BK, NT>>;
 
+// Split-K arrival of one piece of a tile. The piece's accumulators go to its
+// slot of ws in the tile's own register layout ([split][batch][tile] blocks of
+// BM x BN floats, a lane's 16 values of a fragment as four 16-byte words), with
+// device-coherent (sc1) stores; once every wave's stores have completed (each
+// waits on its own, the block barrier orders them before the add), thread 0
+// bumps the tile's counter. The piece that arrives last replaces acc by
+// 0 + part 0 + part 1 + ... in split order (device-coherent loads, four splits
+// in flight), resets the counter for the next launch and returns true; the
+// others return false. The sum order does not depend on which piece arrives
+// last, so the result is deterministic.
+//
+// Ordering. Every access to the exchanged data is an sc1 buffer access, the
+// encoding of a monotonic agent-scope atomic load / store in the gfx942 /
+// gfx950 memory model: it is performed at the device coherence point, past
+// the per-XCD L2s. A piece's stores have completed there (vmcnt 0) before its
+// counter add is issued, and the last piece's loads are issued after its add
+// has returned, so they read every piece's data. An agent-scope release /
+// acquire on the counter would add an L2 write-back (buffer_wbl2 sc1) to every
+// arrival and an L2 invalidate (buffer_inv sc1) to the last one; both exist to
+// make non-coherent (non-sc1) accesses visible, and none cross between the
+// pieces here. Measured on MI355X, they cost 128 x 4096 x 4096 42.5 -> 52.6 us
+// (release on the add and acquire in the last piece: 50.5) and 512^3 11.3 ->
+// 13.6 us.
+typedef uint32_t u32x4s __attribute__((ext_vector_type(4)));
+
+template <class Cfg>
+__device__ __forceinline__ bool splitArrive(const GemmF32Params& p, f32x16 (&acc)[Cfg::FM][Cfg::FN], float* smem,
+                                            int lane, long long batch, int split, int bid) {
+    constexpr int TILE = Cfg::BM * Cfg::BN;   // floats per tile and split
+    constexpr int LANE_FLOATS = Cfg::FM * Cfg::FN * 16;
+    const long long tiles = (long long)p.tilesM * p.tilesN * gridDim.z;
+    const long long slot = batch * p.tilesM * p.tilesN + bid;
+    // byte offset of this lane's first word in split 0's block of the tile
+    const uint32_t laneOff = (uint32_t)((threadIdx.x >> 6) * 64 * LANE_FLOATS + lane * 4) * 4u;
+    const auto rw = bufferRsrc(p.ws, (uint32_t)(tiles * p.splits * TILE * 4));
+    const uint32_t own = (uint32_t)(((long long)split * tiles + slot) * TILE * 4);
+#pragma unroll
+    for (int fm = 0; fm < Cfg::FM; ++fm)
+#pragma unroll
+        for (int fn = 0; fn < Cfg::FN; ++fn)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const f32x4 v = {acc[fm][fn][4 * q], acc[fm][fn][4 * q + 1], acc[fm][fn][4 * q + 2], acc[fm][fn][4 * q + 3]};
+                __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4s, v), rw,
+                                                       laneOff + (uint32_t)((fm * Cfg::FN + fn) * 4 + q) * 1024u, own,
+                                                       kCpolAgent);
+            }
+    __builtin_amdgcn_s_waitcnt(0);   // this wave's partial stores have completed
+    int* flag = reinterpret_cast<int*>(smem);
+    __syncthreads();                 // every wave's have (and the LDS stages are free)
+    unsigned* ctr = p.ctr + slot;
+    if (threadIdx.x == 0)
+        *flag = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (unsigned)(p.splits - 1);
+    __syncthreads();
+    if (!*flag) return false;
+#pragma unroll
+    for (int fm = 0; fm < Cfg::FM; ++fm)
+#pragma unroll
+        for (int fn = 0; fn < Cfg::FN; ++fn)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[fm][fn][r] = 0.f;
+    const uint32_t stride = (uint32_t)(tiles * TILE * 4);   // bytes from one split's block of the tile to the next
+    const uint32_t base = (uint32_t)(slot * TILE * 4);
+    for (int s0 = 0; s0 < p.splits; s0 += 4) {
+        f32x4 w[4][Cfg::FM * Cfg::FN * 4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int i = 0; i < Cfg::FM * Cfg::FN * 4; ++i)   // splits past the last read zero (out of range)
+                w[j][i] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                    rw, s0 + j < p.splits ? laneOff + (uint32_t)i * 1024u : kOOB, base + (uint32_t)(s0 + j) * stride,
+                    kCpolAgent));
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            if (s0 + j >= p.splits) break;
+#pragma unroll
+            for (int fm = 0; fm < Cfg::FM; ++fm)
+#pragma unroll
+                for (int fn = 0; fn < Cfg::FN; ++fn)
+#pragma unroll
+                    for (int q = 0; q < 4; ++q)
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) acc[fm][fn][4 * q + e] += w[j][(fm * Cfg::FN + fn) * 4 + q][e];
+        }
+    }
+    if (threadIdx.x == 0) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return true;
+}
+
 // One output tile (bid: the tile's linear index, batch, split) of C =
 // op(A) * op(B). BSUM (B stored [K, N]): the workgroups of the first row of
 // tiles also add B's columns over K, row after row from 0, into p.colSum (the
@@ -224,18 +313,19 @@ __device__ __forceinline__ void gemmF32Tile(const GemmF32Params& p, float* smem,
         }
     }
 
-    // Split-K / batch-reduce partials go densely to [split][batch][M][N].
-    const bool partial = p.ws != nullptr;
-    float* C = partial ? p.ws + ((long long)split * gridDim.z + batch) * p.M * p.N : p.C + batch * p.sC;
-    const long long ldc = partial ? p.N : p.ldc;
     const int li = lane & 31, h = lane >> 5;
-    // Bias and activation apply to the finished sums only (the split-K
-    // finish applies them to partial products' sum).
-    const bool bias = !partial && p.bias != nullptr;
-    const bool relu = !partial && p.act == 1;
     if constexpr (BSUM) {
         if (doSum) p.colSum[n0 + tid] = colAcc;
     }
+    if (p.ws) {
+        // Split-K: the last piece of the tile to arrive sums every piece's
+        // partial product in split order and writes C.
+        if (!splitArrive<Cfg>(p, acc, smem, lane, batch, split, bid)) return;
+    }
+    float* C = p.C + batch * p.sC;
+    const long long ldc = p.ldc;
+    const bool bias = p.bias != nullptr;
+    const bool relu = p.act == 1;
 #pragma unroll
     for (int fm = 0; fm < Cfg::FM; ++fm) {
 #pragma unroll
@@ -262,47 +352,6 @@ template <class Cfg, bool TA, bool TB, int LA, int LB>
 __global__ __launch_bounds__(Cfg::NT) void gemm_f32_kernel(GemmF32Params p) {
     extern __shared__ float smem[];
     gemmF32Tile<Cfg, TA, TB, LA, LB>(p, smem, blockIdx.x, blockIdx.z, blockIdx.y);
-}
-
-// Sums the partials of every split in split order and writes C (+ bias, act).
-// Block (x, y, z): columns [4 * 256x, ...) of rows y, y + gridDim.y, ... of
-// batch z; a thread takes four consecutive columns. VEC (N % 4 == 0, ldc and
-// the buffers 16-byte aligned): one 16-byte load per split and one store.
-template <bool VEC>
-__global__ __launch_bounds__(256) void gemm_splitk_finish(const float* ws, float* C, int splits, int batch, int M,
-                                                          int N, long long ldc, long long sC, const float* bias,
-                                                          int act) {
-    const int c0 = (blockIdx.x * 256 + threadIdx.x) * 4;
-    if (c0 >= N) return;
-    const long long b = blockIdx.z;
-    const long long plane = (long long)M * N;
-    const long long sStride = plane * batch;
-    for (int r = blockIdx.y; r < M; r += gridDim.y) {
-        const float* src = ws + b * plane + (long long)r * N + c0;
-        f32x4 v = {0.f, 0.f, 0.f, 0.f};
-        for (int s = 0; s < splits; ++s) {
-            if constexpr (VEC) {
-                v += *reinterpret_cast<const f32x4*>(src + s * sStride);
-            } else {
-#pragma unroll
-                for (int w = 0; w < 4; ++w)
-                    if (c0 + w < N) v[w] += src[s * sStride + w];
-            }
-        }
-#pragma unroll
-        for (int w = 0; w < 4; ++w) {
-            if (bias && c0 + w < N) v[w] += bias[c0 + w];
-            if (act == 1) v[w] = v[w] > 0.f ? v[w] : 0.f;
-        }
-        float* dst = C + b * sC + (long long)r * ldc + c0;
-        if constexpr (VEC) {
-            *reinterpret_cast<f32x4*>(dst) = v;
-        } else {
-#pragma unroll
-            for (int w = 0; w < 4; ++w)
-                if (c0 + w < N) dst[w] = v[w];
-        }
-    }
 }
 
 template <class Cfg, bool TA, bool TB>
@@ -370,8 +419,8 @@ static int launchCfg(const GemmF32Params& prm, int batch, int splits, int cfg, b
 
 static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
-// Launches the GEMM (partials to ws when splits > 1) and, if needed, the
-// finishing sum.
+// Launches the GEMM (split-K: partials to ws, summed in the same launch by
+// each tile's last piece).
 static int gemmF32Run(bool ta, bool tb, int batch, int M, int N, int K, const float* A, long long lda, long long sA,
                       const float* B, long long ldb, long long sB, float* C, long long ldc, long long sC,
                       GemmPlan plan, const float* bias, int act, float* fixedWs = nullptr, size_t fixedBytes = 0) {
@@ -382,17 +431,22 @@ static int gemmF32Run(bool ta, bool tb, int batch, int M, int N, int K, const fl
     prm.lda = lda; prm.ldb = ldb; prm.ldc = ldc;
     prm.sA = sA; prm.sB = sB; prm.sC = sC;
     const int splits = splitPieces(K, plan.splits, &prm.kChunk);
-    const bool partial = splits > 1;
-    if (partial) {
-        const size_t need = (size_t)splits * batch * M * N * sizeof(float);
+    prm.splits = splits;
+    if (splits > 1) {
+        const size_t tiles = (size_t)((M + 63) / 64) * ((N + 63) / 64) * batch;   // the split plans' 64 x 64 tiles
+        const size_t need = (size_t)splits * tiles * 64 * 64 * sizeof(float);
+        if (need >= kMaxBufferBytes) return fail("gemm: %zu bytes of split-K partial products exceed 2^30", need);
         if (fixedWs) {
-            if (need > fixedBytes)
+            if (need > fixedBytes - kNoAllocCounterBytes || tiles * sizeof(unsigned) > kNoAllocCounterBytes)
                 return fail("gemm: %d split-K partial products need %zu bytes of scratch; the fixed scratch holds %zu",
-                            splits, need, fixedBytes);
+                            splits, need, fixedBytes - kNoAllocCounterBytes);
             prm.ws = fixedWs;
+            prm.ctr = reinterpret_cast<unsigned*>(reinterpret_cast<char*>(fixedWs) + fixedBytes - kNoAllocCounterBytes);
         } else {
             prm.ws = static_cast<float*>(workspace(need));
             if (!prm.ws) return -1;   // workspace() recorded the cause
+            prm.ctr = static_cast<unsigned*>(workspace(tiles * sizeof(unsigned), kWsCounters));
+            if (!prm.ctr) return -1;
         }
     }
     // A is K-contiguous unless transposed; the vector axis is K (A) or M (A^T).
@@ -403,17 +457,7 @@ static int gemmF32Run(bool ta, bool tb, int batch, int M, int N, int K, const fl
     else if (!ta && tb) rc = launchCfg<false, true>(prm, batch, splits, plan.cfg, va, vb);
     else if (ta && !tb) rc = launchCfg<true, false>(prm, batch, splits, plan.cfg, va, vb);
     else rc = launchCfg<true, true>(prm, batch, splits, plan.cfg, va, vb);
-    if (rc || !partial) return rc;
-    const dim3 grid((N + 1023) / 1024, std::min(M, 65535), batch);
-    const bool vec = N % 4 == 0 && ldc % 4 == 0 && sC % 4 == 0 && aligned16(C) && aligned16(prm.ws);
-    if (vec)
-        hipLaunchKernelGGL(gemm_splitk_finish<true>, grid, dim3(256), 0, stream(), prm.ws, C, splits, batch, M, N,
-                           ldc, sC, prm.bias, prm.act);
-    else
-        hipLaunchKernelGGL(gemm_splitk_finish<false>, grid, dim3(256), 0, stream(), prm.ws, C, splits, batch, M, N,
-                           ldc, sC, prm.bias, prm.act);
-    OMHIP_CHECK_LAUNCH();
-    return 0;
+    return rc;
 }
 
 // Split-K partials are kept to at most this many bytes of workspace.

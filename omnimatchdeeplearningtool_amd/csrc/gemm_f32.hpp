@@ -56,8 +56,11 @@ inline int splitPieces(int K, int splits, int* kChunk = nullptr) {
 }
 
 // Bytes of the fixed device array behind omHipGemmStridedBatchedNoAlloc: twice
-// the bound above for a 256-CU device.
+// the bound above for a 256-CU device. Its last kNoAllocCounterBytes hold the
+// tiles' split-K arrival counters (zero at load, and every launch leaves them
+// zero); the partials use the rest.
 constexpr size_t kNoAllocScratchBytes = (size_t)32 << 20;
+constexpr size_t kNoAllocCounterBytes = (size_t)64 << 10;
 
 struct GemmF32Params {
     const float* A;
@@ -69,6 +72,8 @@ struct GemmF32Params {
     int tilesM, tilesN;
     int kChunk;             // split-K: split s covers k in [s*kChunk, min(K, (s+1)*kChunk))
     float* ws;              // split-K partials [split][batch][M][N] (null: write C directly)
+    unsigned* ctr;          // split-K: per (batch, tile) arrival counters, zero at rest
+    int splits;             // split-K: pieces of K (the last arrival of a tile sums them)
     const float* bias;      // [N] added to every row of C, or null
     int act;                // 0 identity, 1 ReLU (after the bias)
     const float* gate;      // Linear backward: C kept where gate > 0 (row stride ldg)

@@ -1,6 +1,7 @@
 // CPU test of the fp32 GEMM's tile / split-K plan (omhip::planGemmFor): the
 // split-K partial sums of every plan fit the no-allocation entry's fixed array
-// (kNoAllocScratchBytes) and stay below the stated bound of 4 x CUs tiles of
+// (kNoAllocScratchBytes less its arrival counters), the tiles' counters fit
+// theirs (kNoAllocCounterBytes), and the partials stay below the stated bound of 4 x CUs tiles of
 // 64 x 64 floats, over the GEMM sweep, the MLP and ResNet weight-gradient
 // shapes, the shapes that reach the bound, and a dense grid of small M / N.
 // Exit status 0 = all checks passed.
@@ -18,10 +19,11 @@ static void check(int M, int N, int K, int batch, long long cus) {
     const omhip::GemmPlan p = omhip::planGemmFor(M, N, K, batch, wsOk, cus);
     if (p.splits <= 1) return;
     const int pieces = omhip::splitPieces(K, p.splits);
-    const long long bytes = (long long)pieces * batch * M * N * 4;
     const long long tiles = (long long)((M + 63) / 64) * ((N + 63) / 64) * batch;
+    const long long bytes = (long long)pieces * tiles * 64 * 64 * 4;   // partials in whole 64 x 64 tiles
     if (g_maxBytes < bytes && cus == 256) g_maxBytes = bytes;
-    if (p.cfg != 2 || bytes > (long long)omhip::kNoAllocScratchBytes || tiles * p.splits >= 4 * cus ||
+    if (p.cfg != 2 || bytes > (long long)(omhip::kNoAllocScratchBytes - omhip::kNoAllocCounterBytes) ||
+        tiles * 4 > (long long)omhip::kNoAllocCounterBytes || tiles * p.splits >= 4 * cus ||
         bytes > 4 * cus * 64LL * 64 * 4) {
         std::printf("FAIL M=%d N=%d K=%d batch=%d cus=%lld: cfg %d splits %d (%d pieces) %lld bytes\n", M, N, K, batch,
                     cus, p.cfg, p.splits, pieces, bytes);
