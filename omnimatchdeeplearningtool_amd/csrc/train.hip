@@ -18,9 +18,11 @@
 //
 // Weight gradient: an implicit GEMM over every output pixel of the batch
 // (conv_wgrad.hip), no column matrix. Bias gradient and the BatchNorm
-// reductions are per-channel sums over N x H x W: each (channel, part)
-// workgroup sums a contiguous range of images in a fixed order, a second
-// kernel adds the parts in order — deterministic.
+// reductions are per-channel reductions over N x H x W: each (channel, part)
+// workgroup reduces a contiguous range of the channel's elements in a fixed
+// order (the batch statistics as each part's mean and sum of squared
+// deviations, read once), a second kernel combines the parts in order —
+// deterministic.
 #include "omhip_internal.hpp"
 #include "buffer_io.hpp"
 #include "conv.hpp"
@@ -153,31 +155,23 @@ __device__ __forceinline__ float partSum(const float* __restrict__ part, int c, 
     return a;
 }
 
-// MODE 0: sum x.  MODE 1: sum (x - mean)^2, mean = (sum of prev's parts) / cnt
-// (bit-identical to the reference's sum / count).  MODE 2: sum dy*xhat and
-// sum dy, xhat = (x - mean) * invStd, dy gated by mask > 0 when mask is given
-// (the reference's reluBackward folded in). part[(c*P + p)*2 + k].
+// Per-channel sum of x (a bias gradient), part p of channel c:
+// part[(c*P + p)*2] = sum, part[(c*P + p)*2 + 1] = 0.
 //
 // The part's images n0..n1-1 are one sequence of (image, element) pairs —
 // elements in groups of V (V = 4: 16-byte loads, when HW % 4 == 0 and the
-// buffers are 16-byte aligned) — walked 256 groups per trip, so small planes
+// buffer is 16-byte aligned) — walked 256 groups per trip, so small planes
 // keep every lane busy. U trips are loaded before any is added, so U loads of
 // each lane are in flight at once; a lane adds its elements in sequence order
 // (a fixed order: the result does not depend on timing).
-template <int MODE, int V>
-__global__ __launch_bounds__(256) void chan_partial_kernel(const float* __restrict__ x, const float* __restrict__ dy,
-                                                           const float* __restrict__ mask,
-                                                           const float* __restrict__ mean,
-                                                           const float* __restrict__ invStd,
-                                                           const float* __restrict__ prev, float* __restrict__ part,
-                                                           int N, int C, int HW, int P, float cnt) {
+template <int V>
+__global__ __launch_bounds__(256) void chan_sum_kernel(const float* __restrict__ x, float* __restrict__ part, int N,
+                                                       int C, int HW, int P) {
     typedef float fv __attribute__((ext_vector_type(V)));
     constexpr int U = 4;
     __shared__ float red[2 * 256];
     const int c = blockIdx.x, p = blockIdx.y;
     const int n0 = (int)((long long)p * N / P), n1 = (int)((long long)(p + 1) * N / P);
-    const float m = MODE == 1 ? partSum(prev, c, P, 0) / cnt : (MODE == 2 ? mean[c] : 0.f);
-    const float is = MODE == 2 ? invStd[c] : 0.f;
     const int HWV = HW / V;   // groups per plane
     float v[2] = {0.f, 0.f};
     const int dn = 256 / HWV, ds = 256 % HWV;
@@ -191,21 +185,14 @@ __global__ __launch_bounds__(256) void chan_partial_kernel(const float* __restri
         }
     };
     while (n < n1) {
-        fv xv[U], gv[U], mv[U];
+        fv xv[U];
         bool ok[U];
         {
             int nn = n, ss = sg;
 #pragma unroll
             for (int u = 0; u < U; ++u) {
                 ok[u] = nn < n1;
-                const long long e = ((long long)nn * C + c) * HW + (long long)ss * V;
-                if (ok[u]) {
-                    xv[u] = *reinterpret_cast<const fv*>(x + e);
-                    if constexpr (MODE == 2) {
-                        gv[u] = *reinterpret_cast<const fv*>(dy + e);
-                        if (mask) mv[u] = *reinterpret_cast<const fv*>(mask + e);
-                    }
-                }
+                if (ok[u]) xv[u] = *reinterpret_cast<const fv*>(x + ((long long)nn * C + c) * HW + (long long)ss * V);
                 advance(nn, ss);
             }
             n = nn;
@@ -215,21 +202,7 @@ __global__ __launch_bounds__(256) void chan_partial_kernel(const float* __restri
         for (int u = 0; u < U; ++u) {
             if (!ok[u]) continue;
 #pragma unroll
-            for (int k = 0; k < V; ++k) {
-                const float xe = V == 1 ? xv[u][0] : xv[u][k];
-                if constexpr (MODE == 0) {
-                    v[0] += xe;
-                } else if constexpr (MODE == 1) {
-                    const float d = xe - m;
-                    v[0] = __builtin_fmaf(d, d, v[0]);
-                } else {
-                    const float ge = V == 1 ? gv[u][0] : gv[u][k];
-                    const float g = (mask && !((V == 1 ? mv[u][0] : mv[u][k]) > 0.f)) ? 0.f : ge;
-                    const float xh = (xe - m) * is;
-                    v[0] = __builtin_fmaf(g, xh, v[0]);
-                    v[1] += g;
-                }
-            }
+            for (int k = 0; k < V; ++k) v[0] += V == 1 ? xv[u][0] : xv[u][k];
         }
     }
     blockSum<2>(v, red);
@@ -251,22 +224,98 @@ __global__ void chan_finish_kernel(const float* __restrict__ part, float* out0, 
     if (out1) out1[c] = accumulate ? out1[c] + b / divisor : b / divisor;
 }
 
-// BatchNorm training forward, statistics (cpu_backend.ixx:796-822): batch
-// mean = sum(x)/cnt and biased variance = sum((x-mean)^2)/cnt from the two
-// passes' parts (summed in part order), invStd = 1/sqrt(var+eps); stat[c] =
-// (mean, invStd); also the saved statistics and the running averages
-// fma(1-m, run, m*batch). One wave per channel: its lanes load the parts
-// together (partSum), lane 0 writes.
-__global__ __launch_bounds__(256) void bn_stats_kernel(const float* __restrict__ part0, const float* __restrict__ part1,
-                                                       int P, float cnt, float eps, float momentum, float* savedMean,
-                                                       float* savedInvStd, float* runMean, float* runVar,
-                                                       float* __restrict__ stat, int C) {
+// ---- BatchNorm statistics in one pass ------------------------------------------------
+// A channel's N*HW elements, taken as one sequence (image by image), split into
+// parts of kStatPart elements (the last may be shorter); a part is one
+// workgroup of 256 threads, each holding kStatElems of its elements in
+// registers, so every load is issued before any arithmetic and the part is read
+// from memory once. The part's mean and its sum of squared deviations from that
+// mean (an exact two-pass over the registers, fixed-order tree sums) are
+// combined across parts in part order by the pairwise update of Chan, Golub and
+// LeVeque (1979): n = na + nb, d = mb - ma, mean = ma + d nb / n,
+// M2 = M2a + M2b + d^2 na nb / n. The parts depend on the shape only, so the
+// result is deterministic.
+constexpr int kStatElems = 32;
+constexpr int kStatPart = 256 * kStatElems;
+
+static int statParts(long long L) { return (int)((L + kStatPart - 1) / kStatPart); }
+
+// part[(c*P + p)*2] = (mean, M2) of part p of channel c.
+template <int V>
+__global__ __launch_bounds__(256) void bn_stats_part_kernel(const float* __restrict__ x, float* __restrict__ part, int C,
+                                                            int HW, FastDiv dHW, long long L, int P) {
+    typedef float fv __attribute__((ext_vector_type(V)));
+    constexpr int G = kStatElems / V;   // loads per thread
+    __shared__ float red[256];
+    const int c = blockIdx.x, p = blockIdx.y;
+    const long long beg = (long long)p * kStatPart;
+    const int cntP = (int)min((long long)kStatPart, L - beg);
+    fv xv[G];
+#pragma unroll
+    for (int j = 0; j < G; ++j) {
+        const int i = (int)threadIdx.x * V + j * 256 * V;   // element of the part
+        if (i < cntP) {
+            const uint32_t gi = (uint32_t)(beg + i);
+            const uint32_t n = dHW.div(gi);
+            xv[j] = *reinterpret_cast<const fv*>(x + ((long long)n * C + c) * HW + (gi - n * (uint32_t)HW));
+        } else {
+#pragma unroll
+            for (int k = 0; k < V; ++k) xv[j][k] = 0.f;   // adds nothing; excluded from M2 below
+        }
+    }
+    float v[1] = {0.f};
+#pragma unroll
+    for (int j = 0; j < G; ++j)
+#pragma unroll
+        for (int k = 0; k < V; ++k) v[0] += xv[j][k];
+    blockSum<1>(v, red);
+    const float mean = v[0] / (float)cntP;
+    __syncthreads();   // red is reused
+    float m2[1] = {0.f};
+#pragma unroll
+    for (int j = 0; j < G; ++j) {
+        if ((int)threadIdx.x * V + j * 256 * V < cntP) {
+#pragma unroll
+            for (int k = 0; k < V; ++k) {
+                const float d = xv[j][k] - mean;
+                m2[0] = __builtin_fmaf(d, d, m2[0]);
+            }
+        }
+    }
+    blockSum<1>(m2, red);
+    if (threadIdx.x == 0) {
+        part[((long long)c * P + p) * 2] = mean;
+        part[((long long)c * P + p) * 2 + 1] = m2[0];
+    }
+}
+
+// Per channel (one thread): the parts merged in part order; mean, biased
+// variance M2 / cnt, invStd = 1/sqrt(var + eps); stat[c] = (mean, invStd),
+// the saved statistics and the running averages fma(1-m, run, m*batch).
+__global__ __launch_bounds__(256) void bn_stats_merge_kernel(const float* __restrict__ part, int P, long long L,
+                                                             float eps, float momentum, float* savedMean,
+                                                             float* savedInvStd, float* runMean, float* runVar,
+                                                             float* __restrict__ stat, int C) {
 #pragma clang fp contract(off)
-    const int c = blockIdx.x * 4 + (threadIdx.x >> 6);   // wave-uniform
+    const int c = blockIdx.x * 256 + threadIdx.x;
     if (c >= C) return;
-    const float mu = partSum(part0, c, P, 0) / cnt;
-    const float var = partSum(part1, c, P, 0) / cnt;
-    if ((threadIdx.x & 63) != 0) return;
+    float n = 0.f, mu = 0.f, m2 = 0.f;
+    for (int p = 0; p < P; ++p) {
+        const float nb = (float)min((long long)kStatPart, L - (long long)p * kStatPart);
+        const float mb = part[((long long)c * P + p) * 2], m2b = part[((long long)c * P + p) * 2 + 1];
+        if (p == 0) {
+            n = nb;
+            mu = mb;
+            m2 = m2b;
+        } else {
+            const double nn = (double)n + (double)nb;
+            const float d = mb - mu;
+            mu = mu + d * (float)((double)nb / nn);
+            m2 = m2 + m2b + d * d * (float)((double)n * (double)nb / nn);
+            n = (float)nn;
+        }
+    }
+    const float var = m2 / (float)L;
     const float inv = 1.0f / sqrtf(var + eps);
     stat[2 * c] = mu;
     stat[2 * c + 1] = inv;
@@ -274,6 +323,59 @@ __global__ __launch_bounds__(256) void bn_stats_kernel(const float* __restrict__
     if (savedInvStd) savedInvStd[c] = inv;
     runMean[c] = __builtin_fmaf(1.0f - momentum, runMean[c], momentum * mu);
     runVar[c] = __builtin_fmaf(1.0f - momentum, runVar[c], momentum * var);
+}
+
+// BatchNorm backward sums of one part (the parts of bn_stats_part_kernel, 16
+// elements per thread: dy, x and the mask are all in flight at once):
+// part[(c*P + p)*2] = (sum dy*xhat, sum dy), xhat = (x - mean) * invStd, dy
+// gated by mask > 0 when a mask is given (the reference's reluBackward folded
+// in). Summed in a fixed order (per thread, then a fixed tree).
+constexpr int kBwdElems = 16;
+constexpr int kBwdPart = 256 * kBwdElems;
+
+template <int V>
+__global__ __launch_bounds__(256) void bn_bwd_part_kernel(const float* __restrict__ x, const float* __restrict__ dy,
+                                                          const float* __restrict__ mask,
+                                                          const float* __restrict__ mean,
+                                                          const float* __restrict__ invStd, float* __restrict__ part,
+                                                          int C, int HW, FastDiv dHW, long long L, int P) {
+    typedef float fv __attribute__((ext_vector_type(V)));
+    constexpr int G = kBwdElems / V;
+    __shared__ float red[2 * 256];
+    const int c = blockIdx.x, p = blockIdx.y;
+    const long long beg = (long long)p * kBwdPart;
+    const int cntP = (int)min((long long)kBwdPart, L - beg);
+    const float m = mean[c], is = invStd[c];
+    fv xv[G], gv[G], mv[G];
+#pragma unroll
+    for (int j = 0; j < G; ++j) {
+        const int i = (int)threadIdx.x * V + j * 256 * V;
+#pragma unroll
+        for (int k = 0; k < V; ++k) { xv[j][k] = 0.f; gv[j][k] = 0.f; mv[j][k] = 1.f; }
+        if (i < cntP) {
+            const uint32_t gi = (uint32_t)(beg + i);
+            const uint32_t n = dHW.div(gi);
+            const long long e = ((long long)n * C + c) * HW + (gi - n * (uint32_t)HW);
+            xv[j] = *reinterpret_cast<const fv*>(x + e);
+            gv[j] = *reinterpret_cast<const fv*>(dy + e);
+            if (mask) mv[j] = *reinterpret_cast<const fv*>(mask + e);
+        }
+    }
+    float v[2] = {0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < G; ++j)
+#pragma unroll
+        for (int k = 0; k < V; ++k) {
+            const float g = mv[j][k] > 0.f ? gv[j][k] : 0.f;
+            const float xh = (xv[j][k] - m) * is;
+            v[0] = __builtin_fmaf(g, xh, v[0]);
+            v[1] += g;
+        }
+    blockSum<2>(v, red);
+    if (threadIdx.x == 0) {
+        part[((long long)c * P + p) * 2] = v[0];
+        part[((long long)c * P + p) * 2 + 1] = v[1];
+    }
 }
 
 // BatchNorm backward, statistics: stat[c] = (sum(dy*xhat), sum(dy)) from the
@@ -306,7 +408,8 @@ struct BnFlat {
 };
 
 // y = act(gamma*((x-mean)*invStd) + beta [+ res]) (the reference's
-// batchNorm2d, add and relu, each rounded as there).
+// batchNorm2d, add and relu, each rounded as there). Each thread takes U
+// groups a grid stride apart and issues all their loads before any store.
 template <int V>
 __global__ __launch_bounds__(256) void bn_train_apply_kernel(const float* __restrict__ x, float* __restrict__ y,
                                                              const float* __restrict__ gamma,
@@ -315,29 +418,42 @@ __global__ __launch_bounds__(256) void bn_train_apply_kernel(const float* __rest
                                                              const float* __restrict__ res, int act, BnFlat f) {
 #pragma clang fp contract(off)
     typedef float fv __attribute__((ext_vector_type(V)));
+    constexpr int U = 4;
     const long long groups = f.total / V;
-    for (long long i = blockIdx.x * 256LL + threadIdx.x; i < groups; i += (long long)gridDim.x * 256) {
-        const uint32_t e = (uint32_t)(i * V);
-        const int c = f.channel(e);
-        const fv xv = *reinterpret_cast<const fv*>(x + e);
-        fv rv{};
-        if (res) rv = *reinterpret_cast<const fv*>(res + e);
-        const float mu = stat[2 * c], inv = stat[2 * c + 1], g = gamma[c], b = beta[c];
-        fv out;
+    const long long stride = (long long)gridDim.x * 256;
+    for (long long i0 = blockIdx.x * 256LL + threadIdx.x; i0 < groups; i0 += stride * U) {
+        fv xv[U], rv[U];
 #pragma unroll
-        for (int k = 0; k < V; ++k) {
-            float v = __builtin_fmaf(g, (xv[k] - mu) * inv, b);
-            if (res) v = v + rv[k];
-            if (act == 1) v = v > 0.f ? v : 0.f;
-            out[k] = v;
+        for (int u = 0; u < U; ++u) {
+            const long long i = i0 + u * stride;
+            if (i < groups) {
+                xv[u] = *reinterpret_cast<const fv*>(x + i * V);
+                if (res) rv[u] = *reinterpret_cast<const fv*>(res + i * V);
+            }
         }
-        *reinterpret_cast<fv*>(y + e) = out;
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const long long i = i0 + u * stride;
+            if (i >= groups) break;
+            const uint32_t e = (uint32_t)(i * V);
+            const int c = f.channel(e);
+            const float mu = stat[2 * c], inv = stat[2 * c + 1], g = gamma[c], b = beta[c];
+            fv out;
+#pragma unroll
+            for (int k = 0; k < V; ++k) {
+                float v = __builtin_fmaf(g, (xv[u][k] - mu) * inv, b);
+                if (res) v = v + rv[u][k];
+                if (act == 1) v = v > 0.f ? v : 0.f;
+                out[k] = v;
+            }
+            *reinterpret_cast<fv*>(y + e) = out;
+        }
     }
 }
 
 // dx = gamma*invStd*(1/cnt) * (cnt*dy - sum(dy) - xhat*sum(dy*xhat)) (cpu_backend.ixx:883-886),
 // with the multiply-adds fused as the reference compiled by clang fuses them;
-// dy gated by mask > 0 when mask is given.
+// dy gated by mask > 0 when mask is given. U groups per thread, loads first.
 template <int V>
 __global__ __launch_bounds__(256) void bn_backward_apply_kernel(const float* __restrict__ dy,
                                                                 const float* __restrict__ mask,
@@ -348,24 +464,37 @@ __global__ __launch_bounds__(256) void bn_backward_apply_kernel(const float* __r
                                                                 const float* __restrict__ stat, float* __restrict__ dx,
                                                                 float cnt, float invCnt, BnFlat f) {
     typedef float fv __attribute__((ext_vector_type(V)));
+    constexpr int U = 4;
     const long long groups = f.total / V;
-    for (long long i = blockIdx.x * 256LL + threadIdx.x; i < groups; i += (long long)gridDim.x * 256) {
-        const uint32_t e = (uint32_t)(i * V);
-        const int c = f.channel(e);
-        const fv dv = *reinterpret_cast<const fv*>(dy + e);
-        const fv xv = *reinterpret_cast<const fv*>(x + e);
-        fv mv{};
-        if (mask) mv = *reinterpret_cast<const fv*>(mask + e);
-        const float m = mean[c], is = invStd[c], sg = stat[2 * c], sb = stat[2 * c + 1];
-        const float k = gamma[c] * is * invCnt;
-        fv out;
+    const long long stride = (long long)gridDim.x * 256;
+    for (long long i0 = blockIdx.x * 256LL + threadIdx.x; i0 < groups; i0 += stride * U) {
+        fv dv[U], xv[U], mv[U];
 #pragma unroll
-        for (int j = 0; j < V; ++j) {
-            const float d = (mask && !(mv[j] > 0.f)) ? 0.f : dv[j];
-            const float xh = (xv[j] - m) * is;
-            out[j] = k * __builtin_fmaf(-xh, sg, __builtin_fmaf(cnt, d, -sb));
+        for (int u = 0; u < U; ++u) {
+            const long long i = i0 + u * stride;
+            if (i < groups) {
+                dv[u] = *reinterpret_cast<const fv*>(dy + i * V);
+                xv[u] = *reinterpret_cast<const fv*>(x + i * V);
+                if (mask) mv[u] = *reinterpret_cast<const fv*>(mask + i * V);
+            }
         }
-        *reinterpret_cast<fv*>(dx + e) = out;
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const long long i = i0 + u * stride;
+            if (i >= groups) break;
+            const uint32_t e = (uint32_t)(i * V);
+            const int c = f.channel(e);
+            const float m = mean[c], is = invStd[c], sg = stat[2 * c], sb = stat[2 * c + 1];
+            const float k = gamma[c] * is * invCnt;
+            fv out;
+#pragma unroll
+            for (int j = 0; j < V; ++j) {
+                const float d = (mask && !(mv[u][j] > 0.f)) ? 0.f : dv[u][j];
+                const float xh = (xv[u][j] - m) * is;
+                out[j] = k * __builtin_fmaf(-xh, sg, __builtin_fmaf(cnt, d, -sb));
+            }
+            *reinterpret_cast<fv*>(dx + e) = out;
+        }
     }
 }
 
@@ -393,31 +522,18 @@ static int forElements(int planes, int HW, int C, bool vec4, F launch) {
 
 static bool aligned16(const void* q) { return (reinterpret_cast<uintptr_t>(q) & 15u) == 0; }
 
-// Per-channel sums into out0/out1 (divided by divisor): MODE as chan_partial_kernel.
-// Partial sums of every channel over P parts (MODE as chan_partial_kernel).
-template <int MODE>
-static int launchPartial(const float* x, const float* dy, const float* mask, const float* mean, const float* invStd,
-                         const float* prev, float* part, int N, int C, int HW, int P, float cnt) {
-    const bool vec = HW % 4 == 0 && aligned16(x) && (MODE != 2 || (aligned16(dy) && (!mask || aligned16(mask))));
-    if (vec)
-        hipLaunchKernelGGL((chan_partial_kernel<MODE, 4>), dim3(C, P), dim3(256), 0, stream(), x, dy, mask, mean, invStd,
-                           prev, part, N, C, HW, P, cnt);
-    else
-        hipLaunchKernelGGL((chan_partial_kernel<MODE, 1>), dim3(C, P), dim3(256), 0, stream(), x, dy, mask, mean, invStd,
-                           prev, part, N, C, HW, P, cnt);
-    OMHIP_CHECK_LAUNCH();
-    return 0;
-}
-
-// Per-channel sums into out0/out1 (divided by divisor): MODE as chan_partial_kernel.
-template <int MODE>
-static int channelSums(const float* x, const float* dy, const float* mean, const float* invStd, float* out0,
-                       float* out1, int N, int C, int HW, float divisor, bool accumulate) {
+// Per-channel sums of x over N x HW into out0 (divided by divisor, or added
+// to it when accumulating): parts in a fixed order, then the parts in order.
+static int channelSums(const float* x, float* out0, int N, int C, int HW, float divisor, bool accumulate) {
     const int P = channelParts(N, C);
     float* part = static_cast<float*>(workspace((size_t)C * P * 2 * sizeof(float)));
     if (!part) return -1;   // workspace() recorded the cause
-    if (launchPartial<MODE>(x, dy, nullptr, mean, invStd, nullptr, part, N, C, HW, P, 1.0f)) return -1;
-    hipLaunchKernelGGL(chan_finish_kernel, dim3((C + 255) / 256), dim3(256), 0, stream(), part, out0, out1, C, P,
+    if (HW % 4 == 0 && aligned16(x))
+        hipLaunchKernelGGL(chan_sum_kernel<4>, dim3(C, P), dim3(256), 0, stream(), x, part, N, C, HW, P);
+    else
+        hipLaunchKernelGGL(chan_sum_kernel<1>, dim3(C, P), dim3(256), 0, stream(), x, part, N, C, HW, P);
+    OMHIP_CHECK_LAUNCH();
+    hipLaunchKernelGGL(chan_finish_kernel, dim3((C + 255) / 256), dim3(256), 0, stream(), part, out0, nullptr, C, P,
                        divisor, accumulate ? 1 : 0);
     OMHIP_CHECK_LAUNCH();
     return 0;
@@ -427,18 +543,22 @@ int batchNorm2dTrainAct(const float* x, float* y, const float* gamma, const floa
                         float* runVar, float* savedMean, float* savedInvStd, int N, int C, int H, int W, float eps,
                         float momentum, const float* res, int act) {
     const int HW = H * W;
-    const float cnt = (float)((long long)N * HW);
-    const int P = channelParts(N, C);
-    float* part = static_cast<float*>(workspace((size_t)C * P * 4 * sizeof(float) + (size_t)C * 2 * sizeof(float)));
+    const long long L = (long long)N * HW;   // elements per channel
+    if (L >= (1LL << 32)) return fail("batchNorm2d: %lld elements per channel exceed 2^32", L);
+    const int P = statParts(L);
+    float* part = static_cast<float*>(workspace((size_t)C * P * 2 * sizeof(float) + (size_t)C * 2 * sizeof(float)));
     if (!part) return -1;
-    float* part0 = part;
-    float* part1 = part + (size_t)C * P * 2;
-    float* stat = part + (size_t)C * P * 4;
-    // two passes, as the reference: sum(x), then sum((x-mean)^2) with the first pass's mean
-    if (launchPartial<0>(x, nullptr, nullptr, nullptr, nullptr, nullptr, part0, N, C, HW, P, cnt)) return -1;
-    if (launchPartial<1>(x, nullptr, nullptr, nullptr, nullptr, part0, part1, N, C, HW, P, cnt)) return -1;
-    hipLaunchKernelGGL(bn_stats_kernel, dim3((C + 3) / 4), dim3(256), 0, stream(), part0, part1, P, cnt, eps,
-                       momentum, savedMean, savedInvStd, runMean, runVar, stat, C);
+    float* stat = part + (size_t)C * P * 2;
+    // one read of x: each part's mean and M2 (two passes over registers), merged in part order
+    const bool vx = HW % 4 == 0 && aligned16(x);
+    const FastDiv dHW = FastDiv::make((uint32_t)HW);
+    if (vx)
+        hipLaunchKernelGGL(bn_stats_part_kernel<4>, dim3(C, P), dim3(256), 0, stream(), x, part, C, HW, dHW, L, P);
+    else
+        hipLaunchKernelGGL(bn_stats_part_kernel<1>, dim3(C, P), dim3(256), 0, stream(), x, part, C, HW, dHW, L, P);
+    OMHIP_CHECK_LAUNCH();
+    hipLaunchKernelGGL(bn_stats_merge_kernel, dim3((C + 255) / 256), dim3(256), 0, stream(), part, P, L, eps, momentum,
+                       savedMean, savedInvStd, runMean, runVar, stat, C);
     OMHIP_CHECK_LAUNCH();
     const bool vec = HW % 4 == 0 && aligned16(x) && aligned16(y) && (!res || aligned16(res));
     return forElements(N * C, HW, C, vec, [&](dim3 g, bool v4, long long off, const BnFlat& f) {
@@ -464,11 +584,21 @@ static int batchNorm2dBackwardMasked(const char* name, const float* gO, const fl
     if (N <= 0 || C <= 0 || H <= 0 || W <= 0) return 0;
     if (!gO || !x || !mean || !invStd || !gamma || !gI) return fail("%s: null pointer", name);
     const int HW = H * W;
-    const int P = channelParts(N, C);
+    const long long L = (long long)N * HW;
+    if (L >= (1LL << 32)) return fail("%s: %lld elements per channel exceed 2^32", name, L);
+    const int P = (int)((L + kBwdPart - 1) / kBwdPart);
     float* part = static_cast<float*>(workspace((size_t)C * P * 2 * sizeof(float) + (size_t)C * 2 * sizeof(float)));
     if (!part) return -1;
     float* stat = part + (size_t)C * P * 2;
-    if (launchPartial<2>(x, gO, mask, mean, invStd, nullptr, part, N, C, HW, P, 1.0f)) return -1;
+    const bool vp = HW % 4 == 0 && aligned16(x) && aligned16(gO) && (!mask || aligned16(mask));
+    const FastDiv dHW = FastDiv::make((uint32_t)HW);
+    if (vp)
+        hipLaunchKernelGGL(bn_bwd_part_kernel<4>, dim3(C, P), dim3(256), 0, stream(), x, gO, mask, mean, invStd, part,
+                           C, HW, dHW, L, P);
+    else
+        hipLaunchKernelGGL(bn_bwd_part_kernel<1>, dim3(C, P), dim3(256), 0, stream(), x, gO, mask, mean, invStd, part,
+                           C, HW, dHW, L, P);
+    OMHIP_CHECK_LAUNCH();
     hipLaunchKernelGGL(bn_bwd_stats_kernel, dim3((C + 3) / 4), dim3(256), 0, stream(), part, P, gGamma, gBeta, stat,
                        C);
     OMHIP_CHECK_LAUNCH();
@@ -573,8 +703,7 @@ int omHipConv2dBackwardWeight(const float* pInput, const float* pGradOutput, flo
                          nPad))
         return -1;
     const long long HWo = (long long)Ho * Wo;
-    if (pGradBias) return channelSums<0>(pGradOutput, nullptr, nullptr, nullptr, pGradBias, nullptr, nBatch, nCout,
-                                         (int)HWo, 1.0f, false);
+    if (pGradBias) return channelSums(pGradOutput, pGradBias, nBatch, nCout, (int)HWo, 1.0f, false);
     return 0;
 }
 
