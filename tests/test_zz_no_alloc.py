@@ -18,10 +18,11 @@ from conftest import empty_dev, to_dev
 
 pytestmark = pytest.mark.gpu
 
-# (transA, transB, batch, M, N, K): pairs of calls in a row, the second smaller. On a
-# 256-CU device 128x4096x4096 splits K 4 ways (8 MiB of partials), 64x1024x2048 8 ways
-# (2 MiB), and 448x4672x2048 (511 tiles of 64x64) 2 ways: 16.5 MB, the largest plan any
-# shape reaches there (the bound a CPU test checks over a grid of shapes).
+# (transA, transB, batch, M, N, K): pairs of calls in a row, the second smaller. Partials
+# are whole 64x64 tiles (16 KiB each per split). On a 256-CU device 128x4096x4096 splits K
+# 4 ways (128 tiles: 8 MiB of partials), 64x1024x2048 8 ways (16 tiles: 2 MiB), and
+# 448x4672x2048 (511 tiles) 2 ways: 16.7 MB, the largest plan any shape reaches there (the
+# bound a CPU test checks over a grid of shapes).
 PAIRS = [
     ((0, 0, 1, 448, 4672, 2048), (0, 0, 1, 128, 4096, 4096)),
     ((0, 0, 1, 128, 4096, 4096), (0, 0, 1, 64, 1024, 2048)),
