@@ -822,6 +822,10 @@ static int convChunk(ConvParams p, int n0, int nb) {
     p.out = p.out + (long long)n0 * p.Cout * p.oH * p.oW;
     if (p.res) p.res = p.res + (long long)n0 * p.Cout * p.oH * p.oW;
     p.N = nb;
+    if (p.oStride == 1 && p.oOffH == 0 && p.oOffW == 0 && p.oH == p.Ho && p.oW == p.Wo &&
+        stemGeometry(p.Cin, p.W, p.KH, p.KW, p.stride, p.padH, p.padW))
+        return convStem(p.x, p.w, p.bias, p.gamma, p.beta, p.mean, p.var, p.eps, p.res, p.act, p.out, nb, p.H, p.W,
+                        p.Cout, p.Ho, p.Wo);
     p.Nq = nb * p.Ho * p.Wo;
     p.padOff = std::max(p.padH, 0) * p.W + std::max(p.padW, 0);
     p.xBytes = (uint32_t)(((long long)nb * p.Cin * p.H * p.W + p.padOff) * 4);

@@ -27,6 +27,17 @@ int conv2dToGrid(const char* name, const float* x, const float* w, float* out, i
                  int KH, int KW, int padH, int padW, int Ho, int Wo, int oH, int oW, int oStride, int oOffH,
                  int oOffW);
 
+// The RGB stem geometry (3 input channels, 7x7, stride 2, pad 3, W a multiple
+// of 4 up to 224) has a kernel of its own (conv_stem.hip); conv2dFused sends
+// each batch chunk of that geometry there.
+bool stemGeometry(int Cin, int W, int KH, int KW, int stride, int padH, int padW);
+
+// out = act(BN(conv(x, w) + bias) + res) for the stem geometry, one chunk whose
+// x, w and out views are at most 2^30 bytes. 0 or -1.
+int convStem(const float* x, const float* w, const float* bias, const float* gamma, const float* beta,
+             const float* mean, const float* var, float eps, const float* res, int act, float* out, int N, int H,
+             int W, int Cout, int Ho, int Wo);
+
 // gW[co][(ci*KH+kh)*KW+kw] = sum over images and output pixels of
 // gradOutput[n][co][oh][ow] * x[n][ci][oh*stride-pad+kh][ow*stride-pad+kw]
 // (overwrites gW). `name` prefixes error messages. 0 or -1.

@@ -207,6 +207,57 @@ def test_odd_geometry(hip, geom, variant):
     _check(out, x, wt, bias, bn, act, s, p)
 
 
+# The RGB stem geometry (3 channels, 7x7, stride 2, pad 3, W % 4 == 0, W <= 224) runs on its own kernel:
+# up to 7 consecutive output rows of one image per block, 64 channels per block (ragged Cout 40 and 100
+# leave partial channel blocks), rows above / below the image and both side pads zero, Wo < 112 leaves
+# partial pixel subtiles. On 256 CUs 8 x 101 output rows run 4 rows per block with a 1-row last block
+# per image (the batch-32 ResNet stem, 7 rows per block, is in the b32 layer tests). W = 228 and
+# W = 30 fall back to the general kernel.
+STEM = [(2, 3, 224, 224, 64), (3, 3, 33, 64, 40), (1, 3, 17, 220, 100), (2, 3, 224, 4, 130), (1, 3, 7, 8, 64),
+        (8, 3, 202, 96, 64), (1, 3, 20, 228, 64), (1, 3, 15, 30, 16)]
+
+
+@pytest.mark.parametrize("geom", STEM, ids=lambda g: "N{}C{}H{}W{}o{}".format(*g))
+@pytest.mark.parametrize("variant", ["plain", "bias", "bias_bn", "bn_relu", "bias_bn_relu"])
+def test_stem_geometry(hip, geom, variant):
+    N, cin, h, w, cout = geom
+    seed = 300 + sum(geom)
+    x = O.randn((N, cin, h, w), seed)
+    wt = _kaiming_uniform((cout, cin, 7, 7), seed + 1)
+    bias = O.randn((cout,), seed + 2) if "bias" in variant else None
+    bn = _params(cout, seed + 3) if "bn" in variant else None
+    act = 1 if "relu" in variant else 0
+    print(f"case stem {geom} {variant}", flush=True)
+    if variant in ("plain", "bias"):
+        out = _run_conv(hip, x, wt, bias, None, 0, 2, 3, entry="omHipConv2d")
+    else:
+        out = _run_conv(hip, x, wt, bias, bn, act, 2, 3)
+    _check(out, x, wt, bias, bn, act, 2, 3)
+
+
+@pytest.mark.parametrize("geom", STEM[:3], ids=lambda g: "N{}C{}H{}W{}o{}".format(*g))
+def test_stem_residual(hip, geom):
+    """The stem kernel's residual epilogue: relu(BN(conv) + res) against float64 and the reference chain."""
+    N, cin, h, w, cout = geom
+    Ho, Wo = out_hw(h, 7, 2, 3), out_hw(w, 7, 2, 3)
+    x = O.randn((N, cin, h, w), 41 + h)
+    wt = _kaiming_uniform((cout, cin, 7, 7), 42)
+    gam, bet, mu, var = _params(cout, 43)
+    res = O.randn((N, cout, Ho, Wo), 44)
+    dout = empty_dev(hip, (N, cout, Ho, Wo))
+    print(f"case stem residual {geom}", flush=True)
+    hip.HIPBackend.conv2dBiasBnAddAct(to_dev(hip, x), to_dev(hip, wt), None, to_dev(hip, gam), to_dev(hip, bet),
+                                      to_dev(hip, mu), to_dev(hip, var), 1e-5, to_dev(hip, res), 1, dout, N, cin, h,
+                                      w, cout, 7, 7, 2, 3)
+    y64, bound = O.conv_f64(x, wt, None, 2, 3, gam, bet, mu, var, 1e-5, act=0)
+    y64 = np.maximum(y64 + res, 0.0)
+    bound = bound + np.abs(res)
+    got = dout.numpy()
+    assert O.normalized_error(got, y64, bound) <= TOL
+    chain = O.relu(O.add(O.conv_bn_act(x, wt, None, gam, bet, mu, var, 1e-5, act=0, stride=2, pad=3), res))
+    assert O.normalized_error(got, chain, bound) <= TOL
+
+
 @pytest.mark.parametrize("geom", [(2, 3, 9, 9, 4, 3, 2, 1), (2, 64, 56, 56, 64, 3, 1, 1), (2, 3, 224, 224, 64, 7, 2, 3),
                                   (2, 256, 14, 14, 512, 1, 2, 0)])
 def test_im2col_path(hip, geom):
