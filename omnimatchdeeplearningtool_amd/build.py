@@ -27,7 +27,7 @@ HIPCC = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
 DEVICE_FLAGS = ["-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
 COMMON = ["-O3", "-std=c++20", "-fPIC", "-Wall", "-Wno-unused-function", "-Wno-unused-variable"]
 
-SOURCES = ["runtime.cpp", "eltwise.hip", "gemm_f32.hip", "conv.hip", "conv_stem.hip", "conv_wgrad.hip", "gemm_half.hip", "train.hip",
+SOURCES = ["runtime.cpp", "eltwise.hip", "gemm_f32.hip", "conv.hip", "conv_stem.hip", "conv_wgrad.hip", "gemm_half.hip", "gemm_half_heads.hip", "train.hip",
            "pool.hip", "attention.hip", "infer.hip", "loss.hip", "mha.hip", "heads.hip"]
 # conv tiles keep at most 128 accumulators per lane: forcing the VGPR form of
 # the MFMA operands stops the register allocator from copying every

@@ -1151,6 +1151,10 @@ static int dispatchH(bool ta, bool tb, const GemmHalfParams& prm, int batch, boo
 }
 
 int zeroOutput(float* C, int batch, int M, int N, long long ldc, long long sC);
+int headScoresHalf(bool bf16, int batch, int M, int N, int K, const uint16_t* A, long long lda, long long sA,
+                   const uint16_t* B, long long ldb, long long sB, float* C, long long ldc, long long sC);
+int headContextHalf(bool bf16, int batch, int M, int N, int K, const uint16_t* A, long long lda, long long sA,
+                    const uint16_t* B, long long ldb, long long sB, float* C, long long ldc, long long sC);
 
 // C = act(op(A) op(B) + bias), fp32 or (outHalf) the input half type.
 static int gemmHalf(const char* name, int dtype, bool ta, bool tb, int batch, int M, int N, int K,
@@ -1173,6 +1177,16 @@ static int gemmHalf(const char* name, int dtype, bool ta, bool tb, int batch, in
     if (empty) {   // the generic kernel's loads are all masked off when K is 0
         return dtype == 1 ? launchGenericC<true, false, false>(prm, batch, false, false)
                           : launchGenericC<false, false, false>(prm, batch, false, false);
+    }
+    if (!ta && tb && !outHalf && !bias && act == 0) {   // many small A . B^T: the attention scores
+        const int rc = headScoresHalf(dtype == 1, batch, M, N, K, A, lda, sA, B, ldb, sB, static_cast<float*>(C), ldc,
+                                      sC);
+        if (rc <= 0) return rc;
+    }
+    if (!ta && !tb && !outHalf && !bias && act == 0) {   // many small A . B with 64 columns: the attention context
+        const int rc = headContextHalf(dtype == 1, batch, M, N, K, A, lda, sA, B, ldb, sB, static_cast<float*>(C), ldc,
+                                       sC);
+        if (rc <= 0) return rc;
     }
     auto al = [](const void* q) { return (reinterpret_cast<uintptr_t>(q) & 15u) == 0; };
     const bool va = al(A) && lda % 8 == 0 && sA % 8 == 0 && (ta ? M % 8 == 0 : K % 8 == 0);

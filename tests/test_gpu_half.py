@@ -135,6 +135,76 @@ def test_half_compact_store(hip, bf16, batch, M, N, K, transB, gap):
     assert not np.any(np.isnan(runs[:, :M * N])), "every element of every batch is written"
 
 
+# Many small A . B^T with K = 64 (the attention scores: one workgroup per batch entry, B in LDS,
+# 16-row blocks of A): a partial last column tile (N = 250, 7), whole tiles only (N = 256), M past
+# the 16-row blocks (1000, 17), ldc wider than N and batch strides with gaps (left untouched).
+HEAD_SCORE_SHAPES = [(300, 100, 250, 256, 40), (256, 1000, 7, 9, 5), (512, 17, 256, 256, 0)]
+
+
+@pytest.mark.parametrize("bf16", [False, True], ids=["f16", "bf16"])
+@pytest.mark.parametrize("batch,M,N,ldc,gap", HEAD_SCORE_SHAPES)
+def test_half_head_scores(hip, bf16, batch, M, N, ldc, gap):
+    K = 64
+    seed = batch + M + N
+    A = O.randn((batch, M, K), seed)
+    B = O.randn((batch, N, K), seed + 1)
+    dA, dB = to_dev(hip, _bits(A, bf16)), to_dev(hip, _bits(B, bf16))
+    sC = M * ldc + gap
+    C0 = np.full(batch * sC + 33, np.nan, np.float32)
+    dC = to_dev(hip, C0)
+    print(f"case head scores {batch}x{M}x{N} ldc {ldc}", flush=True)
+    hip.HIPBackend.gemmStridedBatchedHalf(1 if bf16 else 0, 0, 1, batch, M, N, K, dA, K, M * K, dB, K, N * K, dC, ldc,
+                                          sC)
+    C = dC.numpy()
+    Ar, Br = _round(A, bf16), _round(B, bf16)
+    for b in sorted({0, 1, batch // 2, batch - 1}):
+        C64, bound = O.gemm_f64(Ar[b], Br[b], transB=True)
+        got = C[b * sC:b * sC + M * ldc].reshape(M, ldc)
+        assert O.normalized_error(got[:, :N], C64, bound) <= 1e-4, f"batch {b}"
+    runs = C[:batch * sC].reshape(batch, sC)
+    assert not np.any(np.isnan(runs[:, :M * ldc].reshape(batch, M, ldc)[:, :, :N])), "every element is written"
+    assert np.all(np.isnan(runs[:, :M * ldc].reshape(batch, M, ldc)[:, :, N:])), "columns past N stay untouched"
+    assert np.all(np.isnan(runs[:, M * ldc:])), "batch gaps stay untouched"
+    assert np.all(np.isnan(C[batch * sC:])), "nothing past the last batch is written"
+
+
+# Many small A . B with 64 output columns (the attention context P . V: one workgroup per batch
+# entry, V in LDS read through transposing reads, P rows at any half offset): K = 197 (the ViT
+# keys), 250 and 256 (full steps), 33 and 1; odd lda and sub-view offsets make the P rows ragged;
+# A's padding halves past K hold Inf (they must be zeroed, not multiplied by V's zero rows);
+# ldc wider than 64 leaves columns untouched.
+HEAD_CONTEXT_SHAPES = [(256, 197, 197, 197, 64, 0), (300, 100, 250, 251, 68, 1), (256, 1000, 33, 40, 64, 0),
+                       (512, 17, 256, 256, 64, 3), (256, 5, 1, 2, 64, 1)]
+
+
+@pytest.mark.parametrize("bf16", [False, True], ids=["f16", "bf16"])
+@pytest.mark.parametrize("batch,M,K,lda,ldc,offA", HEAD_CONTEXT_SHAPES)
+def test_half_head_context(hip, bf16, batch, M, K, lda, ldc, offA):
+    N = 64
+    seed = batch + M + K + lda
+    A = O.randn((batch, M, lda), seed)
+    B = O.randn((batch, K, N), seed + 1)
+    Ab = _bits(A, bf16)
+    Ab[:, :, K:] = 0x7c00 if not bf16 else 0x7f80   # +Inf in the row padding
+    flat = np.concatenate([np.zeros(offA, np.uint16), Ab.reshape(-1), np.zeros(8, np.uint16)])
+    dAall, dB = to_dev(hip, flat), to_dev(hip, _bits(B, bf16))
+    sC = M * ldc + 4
+    dC = to_dev(hip, np.full(batch * sC + 20, np.nan, np.float32))
+    print(f"case head context {batch}x{M}x{K} lda {lda} off {offA}", flush=True)
+    hip.call("omHipGemmStridedBatchedHalf", 1 if bf16 else 0, 0, 0, batch, M, N, K, dAall.ptr + 2 * offA, lda,
+             M * lda, dB.ptr, N, K * N, dC.ptr, ldc, sC)
+    C = dC.numpy()
+    Ar, Br = _round(A[:, :, :K], bf16), _round(B, bf16)
+    for b in sorted({0, 1, batch // 2, batch - 1}):
+        C64, bound = O.gemm_f64(Ar[b], Br[b])
+        got = C[b * sC:b * sC + M * ldc].reshape(M, ldc)
+        assert O.normalized_error(got[:, :N], C64, bound) <= 1e-4, f"batch {b}"
+    runs = C[:batch * sC].reshape(batch, sC)[:, :M * ldc].reshape(batch, M, ldc)
+    assert np.all(np.isfinite(runs[:, :, :N])), "every element is written, and finite"
+    assert np.all(np.isnan(runs[:, :, N:])), "columns past N stay untouched"
+    assert np.all(np.isnan(C.reshape(-1)[batch * sC:])), "nothing past the last batch is written"
+
+
 def test_half_strided_views(hip):
     """Leading dimensions wider than the rows and batch strides with gaps (sub-matrix views)."""
     batch, M, N, K = 3, 72, 80, 96
