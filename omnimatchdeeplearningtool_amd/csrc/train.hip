@@ -289,40 +289,42 @@ __global__ __launch_bounds__(256) void bn_stats_part_kernel(const float* __restr
     }
 }
 
-// Per channel (one thread): the parts merged in part order; mean, biased
-// variance M2 / cnt, invStd = 1/sqrt(var + eps); stat[c] = (mean, invStd),
-// the saved statistics and the running averages fma(1-m, run, m*batch).
-__global__ __launch_bounds__(256) void bn_stats_merge_kernel(const float* __restrict__ part, int P, long long L,
-                                                             float eps, float momentum, float* savedMean,
-                                                             float* savedInvStd, float* runMean, float* runVar,
-                                                             float* __restrict__ stat, int C) {
+// Channel c's statistics from its P parts, merged in part order by the
+// pairwise update (the first part as is, then each next part into the running
+// result), by the 64 lanes of one wave: lane l loads part l (all loads in
+// flight at once) and every lane folds the lanes' values in from registers —
+// the rounding of a sequential loop, without its chain of dependent loads.
+// Returns mean and the biased variance M2 / L.
+__device__ __forceinline__ void mergeStats(const float* __restrict__ part, int c, int P, long long L, float& mean,
+                                           float& var) {
 #pragma clang fp contract(off)
-    const int c = blockIdx.x * 256 + threadIdx.x;
-    if (c >= C) return;
+    const int lane = threadIdx.x & 63;
     float n = 0.f, mu = 0.f, m2 = 0.f;
-    for (int p = 0; p < P; ++p) {
-        const float nb = (float)min((long long)kStatPart, L - (long long)p * kStatPart);
-        const float mb = part[((long long)c * P + p) * 2], m2b = part[((long long)c * P + p) * 2 + 1];
-        if (p == 0) {
-            n = nb;
-            mu = mb;
-            m2 = m2b;
-        } else {
-            const double nn = (double)n + (double)nb;
-            const float d = mb - mu;
-            mu = mu + d * (float)((double)nb / nn);
-            m2 = m2 + m2b + d * d * (float)((double)n * (double)nb / nn);
-            n = (float)nn;
+    for (int p0 = 0; p0 < P; p0 += 64) {
+        const int pl = p0 + lane;
+        const float mv = pl < P ? part[((long long)c * P + pl) * 2] : 0.f;
+        const float m2v = pl < P ? part[((long long)c * P + pl) * 2 + 1] : 0.f;
+        const int cnt = min(64, P - p0);
+        for (int j = 0; j < cnt; ++j) {
+            const int pp = p0 + j;
+            const float nb = (float)min((long long)kStatPart, L - (long long)pp * kStatPart);
+            const float mb = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, mv), j));
+            const float m2b = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, m2v), j));
+            if (pp == 0) {
+                n = nb;
+                mu = mb;
+                m2 = m2b;
+            } else {
+                const double nn = (double)n + (double)nb;
+                const float d = mb - mu;
+                mu = mu + d * (float)((double)nb / nn);
+                m2 = m2 + m2b + d * d * (float)((double)n * (double)nb / nn);
+                n = (float)nn;
+            }
         }
     }
-    const float var = m2 / (float)L;
-    const float inv = 1.0f / sqrtf(var + eps);
-    stat[2 * c] = mu;
-    stat[2 * c + 1] = inv;
-    if (savedMean) savedMean[c] = mu;
-    if (savedInvStd) savedInvStd[c] = inv;
-    runMean[c] = __builtin_fmaf(1.0f - momentum, runMean[c], momentum * mu);
-    runVar[c] = __builtin_fmaf(1.0f - momentum, runVar[c], momentum * var);
+    mean = mu;
+    var = m2 / (float)L;
 }
 
 // BatchNorm backward sums of one part (the parts of bn_stats_part_kernel, 16
@@ -378,82 +380,93 @@ __global__ __launch_bounds__(256) void bn_bwd_part_kernel(const float* __restric
     }
 }
 
-// BatchNorm backward, statistics: stat[c] = (sum(dy*xhat), sum(dy)) from the
-// parts in part order; also gradGamma and gradBeta. One wave per channel.
-__global__ __launch_bounds__(256) void bn_bwd_stats_kernel(const float* __restrict__ part, int P, float* gradGamma,
-                                                           float* gradBeta, float* __restrict__ stat, int C) {
-    const int c = blockIdx.x * 4 + (threadIdx.x >> 6);   // wave-uniform
-    if (c >= C) return;
-    const float sg = partSum(part, c, P, 0), sb = partSum(part, c, P, 1);
-    if ((threadIdx.x & 63) != 0) return;
-    stat[2 * c] = sg;
-    stat[2 * c + 1] = sb;
-    if (gradGamma) gradGamma[c] = sg;
-    if (gradBeta) gradBeta[c] = sb;
-}
+// Element-wise BatchNorm passes, one workgroup per (channel, chunk of
+// kApplyChunk<V> of the channel's N*HW elements): element i of channel c is
+// x[(i / HW) * C + c][i % HW] (groups of V = 4 never straddle two planes:
+// HW % 4 == 0). Wave 0 first forms the channel's statistics from the parts
+// (the merge of the statistics kernel's parts), while every thread's loads
+// are already in flight; workgroup (c, 0) also writes the channel's saved /
+// running statistics or parameter gradients. Each thread takes U groups of V.
+template <int V>
+constexpr int kApplyChunk = 256 * V * 4;
 
-// Element-wise BatchNorm passes over planes plane0 .. of an [N*C][HW] tensor
-// (x etc. point at plane plane0; fewer than 2^30 elements per launch), V
-// elements per thread and trip (V = 4: 16-byte accesses when HW % 4 == 0 and
-// every buffer is 16-byte aligned). Element e's channel is
-// (c0 + e / HW) mod C, both divisions by launch-time magic numbers.
-struct BnFlat {
-    long long total;   // elements in this launch
-    FastDiv dHW, dC;
-    int C, c0;         // channel of the launch's first plane
-    __device__ __forceinline__ int channel(uint32_t e) const {
-        const uint32_t pl = dHW.div(e) + (uint32_t)c0;
-        return (int)(pl - dC.div(pl) * (uint32_t)C);
+struct BnChan {
+    int C, HW, Q;   // Q: workgroups per channel
+    long long L;    // elements per channel
+    FastDiv dHW;
+    __device__ __forceinline__ long long offset(int c, long long i) const {
+        const uint32_t n = dHW.div((uint32_t)i);
+        return ((long long)n * C + c) * HW + (long long)((uint32_t)i - n * (uint32_t)HW);
     }
 };
 
 // y = act(gamma*((x-mean)*invStd) + beta [+ res]) (the reference's
-// batchNorm2d, add and relu, each rounded as there). Each thread takes U
-// groups a grid stride apart and issues all their loads before any store.
+// batchNorm2d, add and relu, each rounded as there), with the batch
+// statistics merged from the parts: mean, var = M2 / L, invStd =
+// 1/sqrt(var + eps); saved statistics and running averages fma(1-m, run,
+// m*batch) written once per channel.
 template <int V>
 __global__ __launch_bounds__(256) void bn_train_apply_kernel(const float* __restrict__ x, float* __restrict__ y,
                                                              const float* __restrict__ gamma,
                                                              const float* __restrict__ beta,
-                                                             const float* __restrict__ stat,
-                                                             const float* __restrict__ res, int act, BnFlat f) {
+                                                             const float* __restrict__ part, int P, float eps,
+                                                             float momentum, float* savedMean, float* savedInvStd,
+                                                             float* runMean, float* runVar,
+                                                             const float* __restrict__ res, int act, BnChan f) {
 #pragma clang fp contract(off)
     typedef float fv __attribute__((ext_vector_type(V)));
     constexpr int U = 4;
-    const long long groups = f.total / V;
-    const long long stride = (long long)gridDim.x * 256;
-    for (long long i0 = blockIdx.x * 256LL + threadIdx.x; i0 < groups; i0 += stride * U) {
-        fv xv[U], rv[U];
+    __shared__ float st[2];
+    const int c = blockIdx.x / f.Q, q = blockIdx.x - c * f.Q;
+    const long long i0 = (long long)q * kApplyChunk<V> + (long long)threadIdx.x * V;
+    fv xv[U], rv[U];
+    long long off[U];
 #pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const long long i = i0 + u * stride;
-            if (i < groups) {
-                xv[u] = *reinterpret_cast<const fv*>(x + i * V);
-                if (res) rv[u] = *reinterpret_cast<const fv*>(res + i * V);
+    for (int u = 0; u < U; ++u) {
+        const long long i = i0 + (long long)u * 256 * V;
+        off[u] = i < f.L ? f.offset(c, i) : -1;
+        if (off[u] >= 0) {
+            xv[u] = *reinterpret_cast<const fv*>(x + off[u]);
+            if (res) rv[u] = *reinterpret_cast<const fv*>(res + off[u]);
+        }
+    }
+    if (threadIdx.x < 64) {
+        float mu, var;
+        mergeStats(part, c, P, f.L, mu, var);
+        const float inv = 1.0f / sqrtf(var + eps);
+        if (threadIdx.x == 0) {
+            st[0] = mu;
+            st[1] = inv;
+            if (q == 0) {
+                if (savedMean) savedMean[c] = mu;
+                if (savedInvStd) savedInvStd[c] = inv;
+                runMean[c] = __builtin_fmaf(1.0f - momentum, runMean[c], momentum * mu);
+                runVar[c] = __builtin_fmaf(1.0f - momentum, runVar[c], momentum * var);
             }
         }
+    }
+    __syncthreads();
+    const float mu = st[0], inv = st[1], g = gamma[c], b = beta[c];
 #pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const long long i = i0 + u * stride;
-            if (i >= groups) break;
-            const uint32_t e = (uint32_t)(i * V);
-            const int c = f.channel(e);
-            const float mu = stat[2 * c], inv = stat[2 * c + 1], g = gamma[c], b = beta[c];
-            fv out;
+    for (int u = 0; u < U; ++u) {
+        if (off[u] < 0) break;
+        fv out;
 #pragma unroll
-            for (int k = 0; k < V; ++k) {
-                float v = __builtin_fmaf(g, (xv[u][k] - mu) * inv, b);
-                if (res) v = v + rv[u][k];
-                if (act == 1) v = v > 0.f ? v : 0.f;
-                out[k] = v;
-            }
-            *reinterpret_cast<fv*>(y + e) = out;
+        for (int k = 0; k < V; ++k) {
+            float v = __builtin_fmaf(g, (xv[u][k] - mu) * inv, b);
+            if (res) v = v + rv[u][k];
+            if (act == 1) v = v > 0.f ? v : 0.f;
+            out[k] = v;
         }
+        *reinterpret_cast<fv*>(y + off[u]) = out;
     }
 }
 
 // dx = gamma*invStd*(1/cnt) * (cnt*dy - sum(dy) - xhat*sum(dy*xhat)) (cpu_backend.ixx:883-886),
 // with the multiply-adds fused as the reference compiled by clang fuses them;
-// dy gated by mask > 0 when mask is given. U groups per thread, loads first.
+// dy gated by mask > 0 when mask is given. sum(dy*xhat) and sum(dy) are the
+// parts summed in part order (also gradGamma and gradBeta, written once per
+// channel).
 template <int V>
 __global__ __launch_bounds__(256) void bn_backward_apply_kernel(const float* __restrict__ dy,
                                                                 const float* __restrict__ mask,
@@ -461,63 +474,63 @@ __global__ __launch_bounds__(256) void bn_backward_apply_kernel(const float* __r
                                                                 const float* __restrict__ mean,
                                                                 const float* __restrict__ invStd,
                                                                 const float* __restrict__ gamma,
-                                                                const float* __restrict__ stat, float* __restrict__ dx,
-                                                                float cnt, float invCnt, BnFlat f) {
+                                                                const float* __restrict__ part, int P,
+                                                                float* gradGamma, float* gradBeta,
+                                                                float* __restrict__ dx, float cnt, float invCnt,
+                                                                BnChan f) {
     typedef float fv __attribute__((ext_vector_type(V)));
     constexpr int U = 4;
-    const long long groups = f.total / V;
-    const long long stride = (long long)gridDim.x * 256;
-    for (long long i0 = blockIdx.x * 256LL + threadIdx.x; i0 < groups; i0 += stride * U) {
-        fv dv[U], xv[U], mv[U];
+    __shared__ float st[2];
+    const int c = blockIdx.x / f.Q, q = blockIdx.x - c * f.Q;
+    const long long i0 = (long long)q * kApplyChunk<V> + (long long)threadIdx.x * V;
+    fv dv[U], xv[U], mv[U];
+    long long off[U];
 #pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const long long i = i0 + u * stride;
-            if (i < groups) {
-                dv[u] = *reinterpret_cast<const fv*>(dy + i * V);
-                xv[u] = *reinterpret_cast<const fv*>(x + i * V);
-                if (mask) mv[u] = *reinterpret_cast<const fv*>(mask + i * V);
+    for (int u = 0; u < U; ++u) {
+        const long long i = i0 + (long long)u * 256 * V;
+        off[u] = i < f.L ? f.offset(c, i) : -1;
+        if (off[u] >= 0) {
+            dv[u] = *reinterpret_cast<const fv*>(dy + off[u]);
+            xv[u] = *reinterpret_cast<const fv*>(x + off[u]);
+            if (mask) mv[u] = *reinterpret_cast<const fv*>(mask + off[u]);
+        }
+    }
+    if (threadIdx.x < 64) {
+        const float sg = partSum(part, c, P, 0), sb = partSum(part, c, P, 1);
+        if (threadIdx.x == 0) {
+            st[0] = sg;
+            st[1] = sb;
+            if (q == 0) {
+                if (gradGamma) gradGamma[c] = sg;
+                if (gradBeta) gradBeta[c] = sb;
             }
         }
+    }
+    __syncthreads();
+    const float m = mean[c], is = invStd[c], sg = st[0], sb = st[1];
+    const float k = gamma[c] * is * invCnt;
 #pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const long long i = i0 + u * stride;
-            if (i >= groups) break;
-            const uint32_t e = (uint32_t)(i * V);
-            const int c = f.channel(e);
-            const float m = mean[c], is = invStd[c], sg = stat[2 * c], sb = stat[2 * c + 1];
-            const float k = gamma[c] * is * invCnt;
-            fv out;
+    for (int u = 0; u < U; ++u) {
+        if (off[u] < 0) break;
+        fv out;
 #pragma unroll
-            for (int j = 0; j < V; ++j) {
-                const float d = (mask && !(mv[u][j] > 0.f)) ? 0.f : dv[u][j];
-                const float xh = (xv[u][j] - m) * is;
-                out[j] = k * __builtin_fmaf(-xh, sg, __builtin_fmaf(cnt, d, -sb));
-            }
-            *reinterpret_cast<fv*>(dx + e) = out;
+        for (int j = 0; j < V; ++j) {
+            const float d = (mask && !(mv[u][j] > 0.f)) ? 0.f : dv[u][j];
+            const float xh = (xv[u][j] - m) * is;
+            out[j] = k * __builtin_fmaf(-xh, sg, __builtin_fmaf(cnt, d, -sb));
         }
+        *reinterpret_cast<fv*>(dx + off[u]) = out;
     }
 }
 
-// Runs an element-wise BatchNorm pass over the N*C planes of HW elements in
-// launches of whole planes with fewer than 2^30 elements each. launch(grid,
-// vec4, elementOffset, BnFlat).
-template <class F>
-static int forElements(int planes, int HW, int C, bool vec4, F launch) {
-    const long long perLaunch = std::max<long long>(1, ((1LL << 30) - 1) / HW);
-    for (long long p0 = 0; p0 < planes; p0 += perLaunch) {
-        const long long np = std::min<long long>(perLaunch, planes - p0);
-        BnFlat f{};
-        f.total = np * HW;
-        f.dHW = FastDiv::make((uint32_t)HW);
-        f.dC = FastDiv::make((uint32_t)C);
-        f.C = C;
-        f.c0 = (int)(p0 % C);
-        const long long groups = f.total / (vec4 ? 4 : 1);
-        const int grid = (int)std::max<long long>(1, std::min<long long>((groups + 255) / 256, (long long)cuCount() * 32));
-        launch(dim3(grid), vec4, p0 * HW, f);
-        OMHIP_CHECK_LAUNCH();
-    }
-    return 0;
+static BnChan bnChan(int N, int C, int HW, int V) {
+    BnChan f{};
+    f.C = C;
+    f.HW = HW;
+    f.L = (long long)N * HW;
+    f.Q = (int)((f.L + (256LL * V * 4) - 1) / (256LL * V * 4));
+    f.dHW = FastDiv::make((uint32_t)HW);
+    return f;
 }
 
 static bool aligned16(const void* q) { return (reinterpret_cast<uintptr_t>(q) & 15u) == 0; }
@@ -546,9 +559,8 @@ int batchNorm2dTrainAct(const float* x, float* y, const float* gamma, const floa
     const long long L = (long long)N * HW;   // elements per channel
     if (L >= (1LL << 32)) return fail("batchNorm2d: %lld elements per channel exceed 2^32", L);
     const int P = statParts(L);
-    float* part = static_cast<float*>(workspace((size_t)C * P * 2 * sizeof(float) + (size_t)C * 2 * sizeof(float)));
+    float* part = static_cast<float*>(workspace((size_t)C * P * 2 * sizeof(float)));
     if (!part) return -1;
-    float* stat = part + (size_t)C * P * 2;
     // one read of x: each part's mean and M2 (two passes over registers), merged in part order
     const bool vx = HW % 4 == 0 && aligned16(x);
     const FastDiv dHW = FastDiv::make((uint32_t)HW);
@@ -557,18 +569,17 @@ int batchNorm2dTrainAct(const float* x, float* y, const float* gamma, const floa
     else
         hipLaunchKernelGGL(bn_stats_part_kernel<1>, dim3(C, P), dim3(256), 0, stream(), x, part, C, HW, dHW, L, P);
     OMHIP_CHECK_LAUNCH();
-    hipLaunchKernelGGL(bn_stats_merge_kernel, dim3((C + 255) / 256), dim3(256), 0, stream(), part, P, L, eps, momentum,
-                       savedMean, savedInvStd, runMean, runVar, stat, C);
-    OMHIP_CHECK_LAUNCH();
     const bool vec = HW % 4 == 0 && aligned16(x) && aligned16(y) && (!res || aligned16(res));
-    return forElements(N * C, HW, C, vec, [&](dim3 g, bool v4, long long off, const BnFlat& f) {
-        if (v4)
-            hipLaunchKernelGGL(bn_train_apply_kernel<4>, g, dim3(256), 0, stream(), x + off, y + off, gamma, beta, stat,
-                               res ? res + off : nullptr, act, f);
-        else
-            hipLaunchKernelGGL(bn_train_apply_kernel<1>, g, dim3(256), 0, stream(), x + off, y + off, gamma, beta, stat,
-                               res ? res + off : nullptr, act, f);
-    });
+    const BnChan f = bnChan(N, C, HW, vec ? 4 : 1);
+    if ((long long)C * f.Q >= (1LL << 31)) return fail("batchNorm2d: tensor too large");
+    if (vec)
+        hipLaunchKernelGGL(bn_train_apply_kernel<4>, dim3(C * f.Q), dim3(256), 0, stream(), x, y, gamma, beta, part, P,
+                           eps, momentum, savedMean, savedInvStd, runMean, runVar, res, act, f);
+    else
+        hipLaunchKernelGGL(bn_train_apply_kernel<1>, dim3(C * f.Q), dim3(256), 0, stream(), x, y, gamma, beta, part, P,
+                           eps, momentum, savedMean, savedInvStd, runMean, runVar, res, act, f);
+    OMHIP_CHECK_LAUNCH();
+    return 0;
 }
 
 int batchNorm2dTrain(const float* x, float* y, const float* gamma, const float* beta, float* runMean, float* runVar,
@@ -587,9 +598,8 @@ static int batchNorm2dBackwardMasked(const char* name, const float* gO, const fl
     const long long L = (long long)N * HW;
     if (L >= (1LL << 32)) return fail("%s: %lld elements per channel exceed 2^32", name, L);
     const int P = (int)((L + kBwdPart - 1) / kBwdPart);
-    float* part = static_cast<float*>(workspace((size_t)C * P * 2 * sizeof(float) + (size_t)C * 2 * sizeof(float)));
+    float* part = static_cast<float*>(workspace((size_t)C * P * 2 * sizeof(float)));
     if (!part) return -1;
-    float* stat = part + (size_t)C * P * 2;
     const bool vp = HW % 4 == 0 && aligned16(x) && aligned16(gO) && (!mask || aligned16(mask));
     const FastDiv dHW = FastDiv::make((uint32_t)HW);
     if (vp)
@@ -599,21 +609,20 @@ static int batchNorm2dBackwardMasked(const char* name, const float* gO, const fl
         hipLaunchKernelGGL(bn_bwd_part_kernel<1>, dim3(C, P), dim3(256), 0, stream(), x, gO, mask, mean, invStd, part,
                            C, HW, dHW, L, P);
     OMHIP_CHECK_LAUNCH();
-    hipLaunchKernelGGL(bn_bwd_stats_kernel, dim3((C + 3) / 4), dim3(256), 0, stream(), part, P, gGamma, gBeta, stat,
-                       C);
-    OMHIP_CHECK_LAUNCH();
     const long long cntL = (long long)N * HW;
     const float fcnt = (float)cntL;
     const float invCnt = 1.0f / fcnt;
     const bool vec = HW % 4 == 0 && aligned16(gO) && aligned16(x) && aligned16(gI) && (!mask || aligned16(mask));
-    return forElements(N * C, HW, C, vec, [&](dim3 g, bool v4, long long off, const BnFlat& f) {
-        if (v4)
-            hipLaunchKernelGGL(bn_backward_apply_kernel<4>, g, dim3(256), 0, stream(), gO + off,
-                               mask ? mask + off : nullptr, x + off, mean, invStd, gamma, stat, gI + off, fcnt, invCnt, f);
-        else
-            hipLaunchKernelGGL(bn_backward_apply_kernel<1>, g, dim3(256), 0, stream(), gO + off,
-                               mask ? mask + off : nullptr, x + off, mean, invStd, gamma, stat, gI + off, fcnt, invCnt, f);
-    });
+    const BnChan f = bnChan(N, C, HW, vec ? 4 : 1);
+    if ((long long)C * f.Q >= (1LL << 31)) return fail("%s: tensor too large", name);
+    if (vec)
+        hipLaunchKernelGGL(bn_backward_apply_kernel<4>, dim3(C * f.Q), dim3(256), 0, stream(), gO, mask, x, mean,
+                           invStd, gamma, part, P, gGamma, gBeta, gI, fcnt, invCnt, f);
+    else
+        hipLaunchKernelGGL(bn_backward_apply_kernel<1>, dim3(C * f.Q), dim3(256), 0, stream(), gO, mask, x, mean,
+                           invStd, gamma, part, P, gGamma, gBeta, gI, fcnt, invCnt, f);
+    OMHIP_CHECK_LAUNCH();
+    return 0;
 }
 
 static int validateConvGrad(const char* name, int N, int Cin, int H, int W, int Cout, int KH, int KW, int stride,
