@@ -568,11 +568,12 @@ def bench_vit_half(om, steps: int, warmup: int, bf16: bool, proj_nt: bool = Fals
 
 def bench_mlp(om, steps: int, warmup: int, batch: int = 128):
     """MLP 784-256-128-10 (ReLU) training step, fp32, batch 128, labels uniform in 0..9:
-    each Linear (+ ReLU) is one fused launch; softmax, cross-entropy and its gradient one
-    launch (tensorSoftmaxCrossEntropy + SoftmaxCrossEntropyBackward); each layer's backward
-    one launch (omHipLinearBackward: the reference's TN / NT products for dW and dA, the bias
-    gradient of AddBiasBackward and the ReLU gate of the layer below, each element equal to
-    the separate entries'). No optimizer update."""
+    each hidden Linear (+ ReLU) is one fused launch; the classifier head — its Linear,
+    softmax, cross-entropy and their backward (dW, db, dA gated by the ReLU below) — one
+    launch (omHipLinearSoftmaxCrossEntropyStep); each hidden layer's backward one launch
+    (omHipLinearBackward: the reference's TN / NT products for dW and dA, the bias gradient
+    of AddBiasBackward and the ReLU gate of the layer below, each element equal to the
+    separate entries'). Five launches. No optimizer update."""
     from omnimatchdeeplearningtool_amd.hiptime import StreamTimer
     H = om.HIPBackend
     dims = [784, 256, 128, 10]
@@ -591,14 +592,16 @@ def bench_mlp(om, steps: int, warmup: int, batch: int = 128):
     loss = om.DeviceBuffer.empty((1,))
 
     def step():
-        # forward: one fused launch per layer, act(x W + b); the hidden layers
-        # keep only the activation, whose sign is the ReLU gate of the backward
-        for j in range(3):
+        # forward of the hidden layers: one fused launch per layer, act(x W + b), keeping
+        # only the activation, whose sign is the ReLU gate of the backward
+        for j in range(2):
             i, o = dims[j], dims[j + 1]
-            H.linearBiasAct(a[j], Ws[j], bs[j], a[j + 1] if j < 2 else z[j], batch, i, o, 1 if j < 2 else 0)
-        # loss and its gradient (p - t) / batch, one launch
-        H.softmaxCrossEntropy(z[2], T, None, loss, g[2], batch, 10)
-        for j in reversed(range(3)):
+            H.linearBiasAct(a[j], Ws[j], bs[j], a[j + 1], batch, i, o, 1)
+        # the classifier head in one launch: logits, softmax + cross-entropy, (p - t) / batch,
+        # the head's dW, db and dA gated by the ReLU output below it
+        H.linearSoftmaxCrossEntropyStep(a[2], Ws[2], bs[2], T, a[2], z[2], loss, g[2], gW[2], gb[2], g[1], batch,
+                                        dims[2], dims[3])
+        for j in reversed(range(2)):
             i, o = dims[j], dims[j + 1]
             # dW = A^T G, db = column sums of G, dA = G W^T (as the reference, every layer);
             # above the first layer dA goes through the ReLU gate below it (a > 0 exactly

@@ -238,6 +238,27 @@ int omHipLinearBiasAct(const float* pA, const float* pW, const float* pBias, flo
  * one pass, in the same order). */
 int omHipLinearBackward(const float* pInput, const float* pGradOut, const float* pWeight, const float* pGate,
                         float* pGradWeight, float* pGradBias, float* pGradInput, int nBatch, int nIn, int nOut);
+/* NEW: the classifier head of a training step in one launch — Linear (tensorMatmul + addBias,
+ * linear.ixx:50-58) -> tensorSoftmaxCrossEntropy (tensor_ops.ixx:583-633) -> their backward
+ * (SoftmaxCrossEntropyBackward autograd.ixx:440-488, AddBiasBackward :399-433, MatMulBackward
+ * :261-286) and, when pGate is given, the ReLU backward of the layer below. From X [nBatch, nIn],
+ * W [nIn, nClasses], b [nClasses] (nullable) and one-hot targets T [nBatch, nClasses]:
+ *   logits = X W + b, p = softmax(logits), loss = mean -log(max(p_target, 1e-7)),
+ *   g = (p - T) / nBatch, gW = X^T g, gb = column sums of g, gX = g W^T (kept where pGate > 0).
+ * pLogits, pLoss, pGradLogits, pGradBias, pGradInput and pGate may be NULL. Heads of at most
+ * 64 classes run one kernel: the whole batch in one workgroup when its padded operands fit
+ * 128 KB of LDS (the 784-256-128-10 MLP's 128 x 128 x 10 head), otherwise a workgroup per block
+ * of 64, 32 or 16 rows whose weight-gradient parts the last one to finish adds in block order
+ * (nBatch * (nClasses + 1) floats within 128 KB). The products' summation order differs from
+ * omHipLinearBiasAct / omHipLinearBackward (within the fp32 bar); the softmax adds a row's
+ * exponentials in class order as the reference's loops (omHipSoftmaxCrossEntropy reduces a row
+ * across a wave: p agrees within a few ulp); gb and the loss add the rows in order from 0.
+ * Larger heads run those three entries. Calls on one stream run in order; this entry shares
+ * the library's workspace and arrival counters with the other entries. */
+int omHipLinearSoftmaxCrossEntropyStep(const float* pInput, const float* pWeight, const float* pBias,
+                                       const float* pTarget, const float* pGate, float* pLogits, float* pLoss,
+                                       float* pGradLogits, float* pGradWeight, float* pGradBias, float* pGradInput,
+                                       int nBatch, int nIn, int nClasses);
 /* replaces omCudaBatchedMatmul (cuh:112): C[b] = A[b] * B[b], strides M*K, K*N, M*N
  * (CPUBackend::batchedMatmul cpu_backend.ixx:1520-1532) */
 int omHipBatchedMatmul(const float* pA, const float* pB, float* pC, int nBatch, int nM, int nK, int nN);

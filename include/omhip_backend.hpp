@@ -299,6 +299,16 @@ public:
                                   nOut),
               "linearBackward");
     }
+    // The classifier head of a training step in one launch: logits = X W + b, softmax
+    // cross-entropy, g = (p - T) / nBatch, gW = X^T g, gb, gX = g W^T (gated by pGate > 0).
+    static void linearSoftmaxCrossEntropyStep(const float* pInput, const float* pWeight, const float* pBias,
+                                              const float* pTarget, const float* pGate, float* pLogits, float* pLoss,
+                                              float* pGradLogits, float* pGradWeight, float* pGradBias,
+                                              float* pGradInput, int nBatch, int nIn, int nClasses) {
+        check(omHipLinearSoftmaxCrossEntropyStep(pInput, pWeight, pBias, pTarget, pGate, pLogits, pLoss, pGradLogits,
+                                                 pGradWeight, pGradBias, pGradInput, nBatch, nIn, nClasses),
+              "linearSoftmaxCrossEntropyStep");
+    }
     static void batchedMatmulTransB(const float* pA, const float* pB, float* pC, int nBatch, int nM, int nK, int nN) {
         check(omHipBatchedMatmulTransB(pA, pB, pC, nBatch, nM, nK, nN), "batchedMatmulTransB");
     }

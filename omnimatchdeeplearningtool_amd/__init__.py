@@ -100,6 +100,7 @@ _SIGS = {
     "omHipMatmulTransA": [_vp, _vp, _vp, _i, _i, _i],
     "omHipLinearBiasAct": [_vp, _vp, _vp, _vp, _i, _i, _i, _i],
     "omHipLinearBackward": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i],
+    "omHipLinearSoftmaxCrossEntropyStep": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i],
     "omHipBatchedMatmul": [_vp, _vp, _vp, _i, _i, _i, _i],
     "omHipBatchedMatmulTransB": [_vp, _vp, _vp, _i, _i, _i, _i],
     "omHipGemmStridedBatched": [_i, _i, _i, _i, _i, _i, _vp, _ll, _ll, _vp, _ll, _ll, _vp, _ll, _ll],
@@ -591,6 +592,17 @@ class HIPBackend:
         G, dX = G W^T (kept where pGate > 0)."""
         call("omHipLinearBackward", _ptr(pInput), _ptr(pGradOut), _ptr(pWeight), _ptr(pGate), _ptr(pGradWeight),
              _ptr(pGradBias), _ptr(pGradInput), nBatch, nIn, nOut)
+
+    @staticmethod
+    def linearSoftmaxCrossEntropyStep(pInput, pWeight, pBias, pTarget, pGate, pLogits, pLoss, pGradLogits,
+                                      pGradWeight, pGradBias, pGradInput, nBatch: int, nIn: int,
+                                      nClasses: int) -> None:
+        """The classifier head of a training step in one launch: logits = X W + b, softmax cross-entropy
+        (loss and g = (p - T) / nBatch), gW = X^T g, gb = column sums of g, gX = g W^T kept where
+        pGate > 0 (linear.ixx:50-58, tensor_ops.ixx:583-633, autograd.ixx:261-286, :399-488)."""
+        call("omHipLinearSoftmaxCrossEntropyStep", _ptr(pInput), _ptr(pWeight), _ptr(pBias), _ptr(pTarget),
+             _ptr(pGate), _ptr(pLogits), _ptr(pLoss), _ptr(pGradLogits), _ptr(pGradWeight), _ptr(pGradBias),
+             _ptr(pGradInput), nBatch, nIn, nClasses)
 
     @staticmethod
     def batchedMatmulTransB(pA, pB, pC, nBatch: int, nM: int, nK: int, nN: int) -> None:

@@ -201,3 +201,82 @@ def test_linear_backward_degenerate(hip):
     xs = to_dev(hip, np.abs(O.randn((3, 8), 4)))
     H.linearBackward(xs, g, w, xs, None, None, gX, 3, 8, 0)
     assert not gX.numpy().any()
+
+
+# (batch, in, classes): the MLP's 128 x 128 x 10 head and ragged sizes in one workgroup;
+# 512 and 1000 rows (a last block of 40), 300 x 70 (K % 4 != 0) and 64 x 200 x 64 (LDS
+# for 32 rows only) in blocks of rows; and two heads the fused kernel does not take
+# (100 classes; 4000 rows, whose gradient and terms exceed the last workgroup's LDS):
+# the separate entries run those.
+HEAD_STEP_SHAPES = [(128, 128, 10), (100, 70, 13), (33, 16, 1), (256, 128, 10), (512, 128, 10), (1000, 64, 10),
+                    (300, 70, 13), (64, 200, 64), (512, 256, 10), (64, 32, 100), (4000, 16, 10)]
+
+
+def _head_mode(nb, ni, nc):
+    """Which kernel omHipLinearSoftmaxCrossEntropyStep runs for these sizes: "single" (the
+    whole batch in one workgroup: at most 256 rows padded to 16), "rows" (a workgroup per
+    block of 64, 32 or 16 rows, the whole batch's gradient and terms in the last one's LDS)
+    or None (the separate entries). LDS budget 128 KiB, row strides 17 mod 64."""
+    pad = lambda v: -(-v // 16) * 16
+    s17 = lambda v: v + (17 - v % 64) % 64
+    if nc > 64:
+        return None
+    kp, np_ = pad(ni), pad(nc)
+    block = lambda r: 4 * (r * s17(kp) + kp * s17(np_) + r * s17(np_) + r * nc + r)
+    if pad(nb) <= 256 and block(pad(nb)) <= 128 * 1024:
+        return "single"
+    if 4 * (nb * nc + nb) <= 128 * 1024 and any(block(r) <= 128 * 1024 for r in (64, 32, 16)):
+        return "rows"
+    return None
+
+
+@pytest.mark.parametrize("nb,ni,nc", HEAD_STEP_SHAPES, ids=lambda v: str(v))
+@pytest.mark.parametrize("gated", [False, True], ids=["plain", "relu_gate"])
+def test_linear_softmax_ce_step(hip, nb, ni, nc, gated):
+    """omHipLinearSoftmaxCrossEntropyStep: logits and the three products against float64 (K-scaled
+    bound); the logit gradient against the oracle's softmax of the step's own logits within the
+    softmax bar above (times 1/batch, plus the roundings of p - t and of the product by
+    1/batch); the loss against the oracle's
+    cross-entropy of those probabilities within 1e-5 relative; the bias gradient bit for bit
+    (rows added in order from 0). Heads the fused kernel does not take run the separate entries:
+    there the loss and the logit gradient are also bit-identical to omHipSoftmaxCrossEntropy's.
+    The second call (only the weight gradient asked for) reproduces the first's bit for bit,
+    which also shows the first left its arrival counter at zero."""
+    H = hip.HIPBackend
+    x = O.randn((nb, ni), nb + ni)
+    x[x < 0] *= 0.0   # a ReLU output: the gate of the layer below
+    w = _kaiming_uniform(ni, nc, ni + nc)
+    b = O.randn((nc,), nc, 0.1)
+    T = np.eye(nc, dtype=np.float32)[O.rng(nb).integers(0, nc, nb)]
+    dx_, dw, db, dT = to_dev(hip, x), to_dev(hip, w), to_dev(hip, b), to_dev(hip, T)
+    z, loss, g = empty_dev(hip, (nb, nc)), empty_dev(hip, (1,)), empty_dev(hip, (nb, nc))
+    gW, gb, gX = empty_dev(hip, (ni, nc)), empty_dev(hip, (nc,)), empty_dev(hip, (nb, ni))
+    print(f"case head step {nb}x{ni}x{nc} gated {gated} mode {_head_mode(nb, ni, nc)}", flush=True)
+    H.linearSoftmaxCrossEntropyStep(dx_, dw, db, dT, dx_ if gated else None, z, loss, g, gW, gb, gX, nb, ni, nc)
+    zg, gg = z.numpy(), g.numpy()
+    z64, bz = O.gemm_f64(x, w)
+    assert O.normalized_error(zg, z64 + b, bz + np.abs(b)) <= TOL
+    p_ref = O.softmax(zg)
+    g_ref = O.cross_entropy_softmax_backward(p_ref, T)
+    # the roundings of p - t and of the product by fl(1/batch) (inexact when batch is not a
+    # power of two), on both sides: 3 * 2^-24 |p - t| / batch
+    bar = (softmax_budget(zg) * p_ref + 3 * 2.0 ** -24 * np.abs(p_ref - T) + 2.0 ** -126) / nb * 1.0001
+    assert np.all(np.abs(gg - g_ref) <= bar)
+    lv = float(loss.numpy()[0])
+    assert abs(lv - O.cross_entropy(p_ref, T)) <= 1e-5 * abs(lv)
+    if _head_mode(nb, ni, nc) is None:   # the separate entries ran
+        loss2, g2 = empty_dev(hip, (1,)), empty_dev(hip, (nb, nc))
+        H.softmaxCrossEntropy(z, dT, None, loss2, g2, nb, nc)
+        assert np.array_equal(loss.numpy().view(np.uint32), loss2.numpy().view(np.uint32))
+        assert np.array_equal(gg.view(np.uint32), g2.numpy().view(np.uint32))
+    refW, bW = O.gemm_f64(x, gg, transA=True)
+    assert O.normalized_error(gW.numpy(), refW, bW) <= TOL
+    assert np.array_equal(gb.numpy(), O.add_bias_backward(gg, nb, nc))
+    refX, bX = O.gemm_f64(gg, w, transB=True)
+    if gated:
+        refX = np.where(x > 0, refX, 0.0)
+    assert O.normalized_error(gX.numpy(), refX, bX) <= TOL
+    # optional outputs: only the weight gradient asked for
+    gW2 = empty_dev(hip, (ni, nc))
+    H.linearSoftmaxCrossEntropyStep(dx_, dw, db, dT, None, None, None, None, gW2, None, None, nb, ni, nc)
+    assert np.array_equal(gW2.numpy(), gW.numpy())
