@@ -455,9 +455,54 @@ __global__ void __launch_bounds__(kHeadMaxThreads) linear_ce_rows_kernel(
         }
     }
     __syncthreads();
-    // softmax, g and the loss terms: a lane per (row, class), G lanes per row, a row's
-    // lanes in one wave (padded rows and classes: g = 0)
-    {
+    // softmax, g and the loss terms. Up to 16 classes: a thread per row with the row in
+    // registers (the scans are sequential either way; one thread per row issues each
+    // exponential, divide and logarithm once).
+    if (d.Np == 16) {
+        for (int r = tid; r < d.R; r += nT) {
+            float* zr = sG + r * d.NS;
+            if (r >= rows) {   // padded rows: g = 0
+#pragma unroll
+                for (int i = 0; i < 16; ++i) zr[i] = 0.f;
+                continue;
+            }
+            // whole rows of 16 are read: a row of z has 17 slots, the targets' rows are
+            // followed by more LDS; the values past N are not used
+            float v[16], t[16];
+#pragma unroll
+            for (int i = 0; i < 16; ++i) v[i] = zr[i];
+#pragma unroll
+            for (int i = 0; i < 16; ++i) t[i] = sT[r * d.N + i];
+            float mx = v[0];   // the reference's scan: a NaN first element stays
+#pragma unroll
+            for (int i = 1; i < 16; ++i) mx = (i < d.N && v[i] > mx) ? v[i] : mx;
+            float sum = 0.f;
+#pragma unroll
+            for (int i = 0; i < 16; ++i)
+                if (i < d.N) {
+                    v[i] = expf(v[i] - mx);
+                    sum += v[i];
+                }
+            float term = 0.f;
+            const long long o = (long long)(r0 + r) * d.N;
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                float g = 0.f;
+                if (i < d.N) {
+                    const float p = v[i] / sum;
+                    if (t[i] > 0.5f) term -= logf(p < 1e-7f ? 1e-7f : p);
+                    g = (p - t[i]) * scale;
+                    if (!single) bufStore1Agent(rws, d.gOff + (uint32_t)(o + i) * 4u, 0, g);
+                    if (grad) grad[o + i] = g;
+                }
+                zr[i] = g;
+            }
+            if (single) sL[r] = term;
+            else bufStore1Agent(rws, d.termOff + (uint32_t)(r0 + r) * 4u, 0, term);
+        }
+    } else {
+        // 17 to 64 classes: a lane per (row, class), G lanes per row, a row's
+        // lanes in one wave (padded rows and classes: g = 0)
         const int per = 64 / d.G;   // rows per wave and pass
         const int j = lane % d.G;
         for (int rb = wave * per; rb < d.R; rb += nW * per) {
