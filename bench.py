@@ -974,7 +974,8 @@ def workload_probe(name: str):
     resnet18_train — three ResNet-18 b32 training steps; vit_attention — ten fused
     attentions (ViT-B/16 b64, fp16) after the ten Q.K^T / P.V batched products they replace;
     vit_gemms — each ViT-B/16 b64 GEMM (fp16, fp32 output) three times;
-    half_power — the fp16 GEMM on constant and on random operands (same kernel and shape)."""
+    half_power — the fp16 GEMM on constant and on random operands (same kernel and shape);
+    mlp — thirty MLP 784-256-128-10 b128 training steps after five untimed ones."""
     import omnimatchdeeplearningtool_amd as om
     om.init(0)
     H = om.HIPBackend
@@ -1056,6 +1057,9 @@ def workload_probe(name: str):
             t.stop()
             ms = t.ms() / 10
             log(f"half_power {tag}: {ms * 1e3:.1f} us per launch, {2.0 * n ** 3 / ms / 1e9:.0f} TFLOP/s")
+    elif name == "mlp":
+        ms = bench_mlp(om, 30, 5)[0]
+        log(f"mlp step {ms * 1e3:.1f} us")
     else:
         raise SystemExit(f"unknown probe {name}")
     om.synchronize()
@@ -1068,7 +1072,7 @@ def main():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--probe", choices=["resnet18_train", "vit_attention", "half_power", "vit_gemms"],
+    ap.add_argument("--probe", choices=["resnet18_train", "vit_attention", "half_power", "vit_gemms", "mlp"],
                     help="run only a short dispatch sequence for kernel-trace profiling (no JSON line)")
     ap.add_argument("--traffic-probe", action="store_true",
                     help="run only the dispatch sequence profiled for HBM traffic (no JSON line)")
