@@ -345,6 +345,10 @@ __device__ __forceinline__ f32x4l tileProduct(const float* px, int xi, int xk, c
     py += lg * yk + li * yj;
     float xa[4], ya[4], xb[4], yb[4];
     readChunk(xa, ya, px, xk, py, yk, 0);
+    if (kLen == 16) {   // one chunk
+        mfmaChunk(a0, a1, xa, ya);
+        return a0 + a1;
+    }
     const int lastK = kLen - 16;
     for (int k0 = 0;; k0 += 32) {
         readChunk(xb, yb, px, xk, py, yk, min(k0 + 16, lastK));
@@ -599,31 +603,49 @@ __global__ void __launch_bounds__(kHeadMaxThreads) linear_ce_rows_kernel(
         }
     }
     // gA = g W^T for the workgroup's rows ([R][Kp], reduction over Np), kept where the
-    // gate is positive (read from LDS when the gate is the input itself, as for a ReLU
-    // output feeding the head)
+    // gate is positive. Each tile is computed transposed (W g^T), so that a lane holds
+    // four consecutive columns of one row: with K % 4 == 0 and 16-byte aligned rows, the
+    // gate is one 16-byte load and the output one 16-byte store.
     if (gA) {
-        const bool gateIsA = gate == A;
         const int tk = d.Kp / 16, tiles = (d.R / 16) * tk;
-        for (int t = wave; t < tiles; t += nW) {
-            const int m0 = (t / tk) * 16, k0 = (t % tk) * 16;
-            const int k = k0 + li;
-            float gv[4] = {1.f, 1.f, 1.f, 1.f};
-            if (gateIsA) {   // LDS (rows and columns past the real ones are not stored)
+        const bool vec4 = d.K % 4 == 0 && (reinterpret_cast<uintptr_t>(gA) & 15) == 0 &&
+                          (reinterpret_cast<uintptr_t>(gate) & 15) == 0;
+        const auto gateAt = [&](int t) {   // the lane's four gate values of tile t (1 where none)
+            f32x4 v = {1.f, 1.f, 1.f, 1.f};
+            const int m = (t / tk) * 16 + li, kq = (t % tk) * 16 + 4 * lg;
+            if (gate && vec4 && t < tiles && m < rows && kq < d.K)
+                v = *reinterpret_cast<const f32x4*>(gate + (long long)(r0 + m) * d.K + kq);
+            return v;
+        };
+        // a wave's tiles four at a time: the four gates are loaded before the first product
+        for (int t0 = wave; t0 < tiles; t0 += 4 * nW) {
+            f32x4 gq[4];
 #pragma unroll
-                for (int r = 0; r < 4; ++r) gv[r] = sA[(m0 + 4 * lg + r) * d.KA + k];
-            } else if (gate) {
+            for (int q = 0; q < 4; ++q) gq[q] = gateAt(t0 + q * nW);
 #pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    const int m = m0 + 4 * lg + r;
-                    if (m < rows && k < d.K) gv[r] = gate[(long long)(r0 + m) * d.K + k];
+            for (int q = 0; q < 4; ++q) {
+                const int t = t0 + q * nW;
+                if (t >= tiles) break;
+                const int m0 = (t / tk) * 16, k0 = (t % tk) * 16;
+                const int m = m0 + li, kq = k0 + 4 * lg;
+                const f32x4l acc = tileProduct(sW + k0 * d.NS, d.NS, 1, sG + m0 * d.NS, 1, d.NS, d.Np, li, lg);
+                if (m >= rows) continue;
+                float* out = gA + (long long)(r0 + m) * d.K + kq;
+                if (vec4) {
+                    if (kq < d.K) {
+                        f32x4 o;
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) o[r] = (gate && !(gq[q][r] > 0.f)) ? 0.f : acc[r];
+                        *reinterpret_cast<f32x4*>(out) = o;
+                    }
+                } else {
+#pragma unroll
+                    for (int r = 0; r < 4; ++r)
+                        if (kq + r < d.K) {
+                            const bool keep = !gate || gate[(long long)(r0 + m) * d.K + kq + r] > 0.f;
+                            out[r] = keep ? acc[r] : 0.f;
+                        }
                 }
-            }
-            const f32x4l acc = tileProduct(sG + m0 * d.NS, d.NS, 1, sW + k0 * d.NS, 1, d.NS, d.Np, li, lg);
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int m = m0 + 4 * lg + r;
-                if (m < rows && k < d.K)
-                    gA[(long long)(r0 + m) * d.K + k] = (gate && !(gv[r] > 0.f)) ? 0.f : acc[r];
             }
         }
     }
