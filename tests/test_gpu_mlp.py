@@ -280,3 +280,38 @@ def test_linear_softmax_ce_step(hip, nb, ni, nc, gated):
     gW2 = empty_dev(hip, (ni, nc))
     H.linearSoftmaxCrossEntropyStep(dx_, dw, db, dT, None, None, None, None, gW2, None, None, nb, ni, nc)
     assert np.array_equal(gW2.numpy(), gW.numpy())
+
+
+@pytest.mark.parametrize("nb,ni,nc", [(128, 128, 10), (300, 128, 13)], ids=lambda v: str(v))
+def test_linear_softmax_ce_step_unaligned(hip, nb, ni, nc):
+    """The head's scalar paths: the input, a separate gate (the ReLU output below, equal to
+    the input) and the input gradient 4 bytes past 16-byte alignment take the element-wise
+    copy, gate and store paths of the fused kernel (one workgroup at 128 rows, row blocks at
+    300). Every output equals the aligned call's (the input as its own gate) bit for bit."""
+    H = hip.HIPBackend
+    x = O.randn((nb, ni), 77 + nb)
+    x[x < 0] *= 0.0
+    w = _kaiming_uniform(ni, nc, 5 + nc)
+    b = O.randn((nc,), nc + 1, 0.1)
+    T = np.eye(nc, dtype=np.float32)[O.rng(nb + 1).integers(0, nc, nb)]
+    dx, dw, db, dT = to_dev(hip, x), to_dev(hip, w), to_dev(hip, b), to_dev(hip, T)
+    outs = lambda: (empty_dev(hip, (nb, nc)), empty_dev(hip, (1,)), empty_dev(hip, (nb, nc)),
+                    empty_dev(hip, (ni, nc)), empty_dev(hip, (nc,)))
+    z1, l1, g1, w1, b1 = outs()
+    gx1 = empty_dev(hip, (nb, ni))
+    print(f"case head step aligned {nb}x{ni}x{nc}", flush=True)
+    H.linearSoftmaxCrossEntropyStep(dx, dw, db, dT, dx, z1, l1, g1, w1, b1, gx1, nb, ni, nc)
+    # the same operands one float into buffers one float longer
+    pad = np.zeros((1,), np.float32)
+    xs = to_dev(hip, np.concatenate([pad, x.ravel()]))
+    gs = to_dev(hip, np.concatenate([pad, x.ravel()]))
+    gxs = to_dev(hip, np.full((nb * ni + 1,), 7.0, np.float32))
+    z2, l2, g2, w2, b2 = outs()
+    print(f"case head step unaligned {nb}x{ni}x{nc}", flush=True)
+    H.linearSoftmaxCrossEntropyStep(xs.ptr + 4, dw, db, dT, gs.ptr + 4, z2, l2, g2, w2, b2, gxs.ptr + 4, nb, ni, nc)
+    same = lambda a, c: np.array_equal(a.view(np.uint32), c.view(np.uint32))
+    for a, c in ((z1, z2), (l1, l2), (g1, g2), (w1, w2), (b1, b2)):
+        assert same(a.numpy(), c.numpy())
+    gxu = gxs.numpy()
+    assert gxu[0] == 7.0   # nothing written before the view
+    assert same(gx1.numpy().ravel(), gxu[1:])
