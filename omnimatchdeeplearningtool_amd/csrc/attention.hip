@@ -228,7 +228,13 @@ __device__ __forceinline__ void attnBlock(const uint16_t* sK, uint32_t sVa, cons
     // ks's MFMAs; LDS reads return in order, so "at most 8 outstanding" means
     // step ks's 8 have landed. The reads are inline assembly and waited for
     // here: through the builtin the compiler would also wait for any LDS DMA
-    // in flight, i.e. for every global load still outstanding.
+    // in flight, i.e. for every global load still outstanding. The wait does
+    // not depend on what else the compiler places around the reads: other LDS
+    // operations complete in order with them and scalar loads only add to the
+    // count, so "at most 8 outstanding" can only be reached once every
+    // operation older than step ks + 1's 8 reads has completed (the 8 volatile
+    // reads keep their order, and the waits' "memory" clobber keeps the
+    // compiler's own LDS accesses on their side of the wait).
     u32x2a lo[2][4], up[2][4];
 #pragma unroll
     for (int dt = 0; dt < 4; ++dt) {
