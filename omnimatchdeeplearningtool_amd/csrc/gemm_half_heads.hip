@@ -32,9 +32,12 @@
 //    ds_read_b64_tr_b16 (lane i of a 16-lane group receives element
 //    E[4j + i/4][i%4] of what the group addressed: addressing rows 8g4 + i/4
 //    and 8g4 + 4 + i/4 at columns 16dt + 4(i%4) gives lane i the column
-//    16dt + i of 8 consecutive keys). V row r keeps its 16-byte chunk c in
-//    slot c ^ 2((r >> 3) & 3): the 32 pieces a wave reads per instruction
-//    then spread two to each 16-byte bank group.
+//    16dt + i of 8 consecutive keys). V row r (128 bytes) keeps its 16-byte
+//    chunk c in slot c ^ 2((r >> 3) & 3) ^ 4((r >> 1) & 1): within a half-wave
+//    the two 16-lane groups (8 rows apart) and the row pairs of one group
+//    (2 rows apart) take different slots, so its 32 8-byte pieces cover every
+//    bank evenly (the two-term form left the row pairs on the same slots:
+//    half of the LDS cycles were bank conflicts).
 //  * the P fragment (8 consecutive keys of one row per lane) is fetched as the
 //    16 bytes from the dword boundary below it plus the next dword and
 //    funnel-shifted into place; halves past K are zeroed on the last step
@@ -186,7 +189,7 @@ struct HeadContextArgs {
 constexpr int kCtxN = 64;        // output columns (the head dimension)
 constexpr int kCtxMaxK = 256;    // keys
 
-__device__ __forceinline__ int vSlotS(int r, int c) { return c ^ (2 * ((r >> 3) & 3)); }
+__device__ __forceinline__ int vSlotS(int r, int c) { return c ^ (2 * ((r >> 3) & 3)) ^ (4 * ((r >> 1) & 1)); }
 
 template <bool BF16>
 __global__ __launch_bounds__(kHeadNT) void head_context_kernel(HeadContextArgs p) {
