@@ -1069,7 +1069,9 @@ static int launchFast(HalfFastParams prm, int batch) {
 // where the model picks the fastest tile or one within 4 % of it: e.g.
 // 12608 x 2304 x 768 and 4096^3 take 256x256, 2048 x 4096 x 4096 128x128,
 // 768 x (197 x 64 x 197), 2048^3 and 1024^3 64x64.
-static int pickFastTile(int M, int N, int K, int batch, bool transA) {
+// cost: the model's time per CU of the chosen tile, in elements of C per unit rate
+// (a 256x256 tile on a CU of its own = 65536).
+static int pickFastTile(int M, int N, int K, int batch, bool transA, double* cost = nullptr) {
     const long long cus = cuCount();
     struct T { int bm, bn, slots; double rate; };
     const T cand[4] = {{256, 256, 1, 1.0}, {128, 128, 2, 0.75}, {64, 64, 4, 0.5}, {192, 256, 1, OMHIP_HALF_R_RATE}};
@@ -1084,10 +1086,33 @@ static int pickFastTile(int M, int N, int K, int batch, bool transA) {
         const long long tiles = (long long)((M + cand[c].bm - 1) / cand[c].bm) * ((N + cand[c].bn - 1) / cand[c].bn) * batch;
         const long long n = (tiles + cus - 1) / cus;
         const double fill = (double)std::min<long long>(n, cand[c].slots) / cand[c].slots;
-        const double cost = (double)n * cand[c].bm * cand[c].bn / (cand[c].rate * std::pow(fill, 0.6));
-        if (c == 0 || cost < bestCost) { best = c; bestCost = cost; }
+        const double cst = (double)n * cand[c].bm * cand[c].bn / (cand[c].rate * std::pow(fill, 0.6));
+        if (c == 0 || cst < bestCost) { best = c; bestCost = cst; }
     }
+    if (cost) *cost = bestCost;
     return best;
+}
+
+// Row split of one large product on 256x256 tiles whose last round is short
+// (12608 x 3072 x 768: 600 tiles, 2.34 rounds): the rows of the whole rounds
+// run as one launch and the rest as a second launch on the tile the model
+// picks for them (128x128, two workgroups per CU), when that model's time for
+// the tail plus a launch's worth (0.15 of a tile) beats the partial round of
+// 256x256 tiles. Each element is still one tile's whole-K sum. Returns the
+// first launch's row count, or 0.
+static int planRowSplit(int M, int N, int K, int batch, bool transA) {
+    if (batch != 1 || pickFastTile(M, N, K, 1, transA) != 0) return 0;
+    const long long U = cuCount();
+    const int tm = (M + 255) / 256, tn = (N + 255) / 256;
+    const long long rounds = ((long long)tm * tn + U - 1) / U;
+    if (rounds < 2) return 0;
+    const int headRows = (int)((rounds - 1) * U / tn);
+    if (headRows <= 0 || headRows >= tm) return 0;
+    const int M1 = headRows * 256;
+    double tail = 0;
+    pickFastTile(M - M1, N, K, 1, transA, &tail);
+    const double head = (double)(((long long)headRows * tn + U - 1) / U);
+    return head + tail / 65536.0 + 0.15 < (double)rounds ? M1 : 0;
 }
 
 template <bool BF16, bool TA, bool TB, bool SWAP, bool RAG>
@@ -1187,6 +1212,14 @@ static int gemmHalf(const char* name, int dtype, bool ta, bool tb, int batch, in
         const int rc = headContextHalf(dtype == 1, batch, M, N, K, A, lda, sA, B, ldb, sB, static_cast<float*>(C), ldc,
                                        sC);
         if (rc <= 0) return rc;
+    }
+    if (const int M1 = planRowSplit(M, N, K, batch, ta)) {
+        const size_t es = outHalf ? 2 : 4;
+        if (gemmHalf(name, dtype, ta, tb, 1, M1, N, K, A, lda, sA, B, ldb, sB, C, ldc, sC, bias, act, outHalf))
+            return -1;
+        return gemmHalf(name, dtype, ta, tb, 1, M - M1, N, K, A + (ta ? (long long)M1 : (long long)M1 * lda), lda, sA,
+                        B, ldb, sB, static_cast<char*>(C) + (size_t)M1 * (size_t)ldc * es, ldc, sC, bias, act,
+                        outHalf);
     }
     auto al = [](const void* q) { return (reinterpret_cast<uintptr_t>(q) & 15u) == 0; };
     const bool va = al(A) && lda % 8 == 0 && sA % 8 == 0 && (ta ? M % 8 == 0 : K % 8 == 0);

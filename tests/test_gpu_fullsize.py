@@ -73,12 +73,17 @@ def test_vit_projection_full(hip, proj, transB, bf16):
     print(f"[{name}] worst K-scaled error {err:.2e}")
 
 
+@pytest.mark.parametrize("N", [2304, 3072], ids=["qkv", "fc1"])
 @pytest.mark.parametrize("bf16", [False, True], ids=["f16", "bf16"])
-def test_vit_qkv_linear_full(hip, bf16):
-    """The fused Linear (bias in the epilogue, half output) at the QKV size, as the ViT layer
-    runs it: every element against the unfused chain gemm -> addBias -> convert."""
+def test_vit_qkv_linear_full(hip, bf16, N):
+    """The fused Linear (bias in the epilogue, half output) at the QKV and fc1 sizes, as the ViT
+    layer runs it: every element against the unfused chain gemm -> addBias -> convert. fc1
+    (600 tiles of 256 x 256) runs as two launches split by rows (the rows of two whole rounds,
+    then the rest on 128 x 128 tiles), so the half-output and bias offsets of the second launch
+    are checked here too."""
     H = hip.HIPBackend
-    M, N, K = TOKENS, 2304, 768
+    M, K = TOKENS, 768
+    print(f"case linear {M}x{N}x{K} bf16={bf16}", flush=True)
     A = O.randn((M, K), 31)
     W = O.randn((K, N), 32, 0.02)
     bias = O.randn((N,), 33, 0.1)
