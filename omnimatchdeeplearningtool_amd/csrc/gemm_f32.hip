@@ -225,12 +225,18 @@ __device__ __forceinline__ void gemmF32Tile(const GemmF32Params& p, float* smem,
     // region of an LDS stage as [BK][BN + 4].
     const bool doSum = BSUM && p.colSum && tm == 0 && tid < Cfg::BN && n0 + tid < p.N;
     float colAcc = 0.f;
+    // The slice's BK values are read first (all inside the LDS stage) and then added in
+    // row order; rows past the K range add -0.0f, which leaves every sum unchanged (a
+    // guarded read per row made each read wait alone: the first tile row's mainloop ran
+    // ~3x longer than the others').
     auto colSum = [&](const float* sB, int k0) {
         if constexpr (BSUM) {
             if (doSum) {
+                float v[Cfg::BK];
 #pragma unroll
-                for (int k = 0; k < Cfg::BK; ++k)
-                    if (k0 + k < kEnd) colAcc += sB[k * SB::LD + tid];
+                for (int k = 0; k < Cfg::BK; ++k) v[k] = sB[k * SB::LD + tid];
+#pragma unroll
+                for (int k = 0; k < Cfg::BK; ++k) colAcc += k0 + k < kEnd ? v[k] : -0.0f;
             }
         }
     };
