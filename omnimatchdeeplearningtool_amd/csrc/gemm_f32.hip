@@ -254,6 +254,35 @@ __device__ __forceinline__ void gemmF32Tile(const GemmF32Params& p, float* smem,
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
+    // Small tiles (short main loops) load the epilogue's bias and gate values before the
+    // first slice, so that their latency passes under the main loop instead of in front
+    // of the C stores; the large tiles' registers are spoken for, and their main loops
+    // are long, so they load the bias in the epilogue.
+    constexpr bool PRE = Cfg::BM * Cfg::BN <= 128 * 128;
+    float biasv[Cfg::FN];
+    if constexpr (PRE) {
+#pragma unroll
+        for (int fn = 0; fn < Cfg::FN; ++fn) {
+            const int col = n0 + wn * Cfg::WN + fn * 32 + (lane & 31);
+            biasv[fn] = (p.bias && col < p.N) ? p.bias[col] : 0.f;
+        }
+    }
+    static_assert(!GATE || PRE, "gated tiles prefetch their gate");
+    float gatev[GATE ? Cfg::FM : 1][GATE ? Cfg::FN : 1][GATE ? 16 : 1];
+    if constexpr (GATE) {
+#pragma unroll
+        for (int fm = 0; fm < Cfg::FM; ++fm)
+#pragma unroll
+            for (int fn = 0; fn < Cfg::FN; ++fn) {
+                const int col = n0 + wn * Cfg::WN + fn * 32 + (lane & 31);
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int row = m0 + wm * Cfg::WM + fm * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+                    gatev[fm][fn][r] = (row < p.M && col < p.N) ? p.gate[(long long)row * p.ldg + col] : 0.f;
+                }
+            }
+    }
+
     const int nk = (kEnd - kBeg + Cfg::BK - 1) / Cfg::BK;
     la.template load<false>(kBeg, kEnd, tid);
     lb.template load<false>(kBeg, kEnd, tid);
@@ -338,7 +367,9 @@ __device__ __forceinline__ void gemmF32Tile(const GemmF32Params& p, float* smem,
         for (int fn = 0; fn < Cfg::FN; ++fn) {
             const int col = n0 + wn * Cfg::WN + fn * 32 + li;
             if (col >= p.N) continue;
-            const float b = bias ? p.bias[col] : 0.f;
+            float b = 0.f;
+            if constexpr (PRE) b = biasv[fn];
+            else b = bias ? p.bias[col] : 0.f;
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const int row = m0 + wm * Cfg::WM + fm * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
@@ -346,7 +377,7 @@ __device__ __forceinline__ void gemmF32Tile(const GemmF32Params& p, float* smem,
                 if (bias) v += b;
                 if (relu) v = v > 0.f ? v : 0.f;
                 if (row < p.M) {
-                    if constexpr (GATE) v = p.gate[(long long)row * p.ldg + col] > 0.f ? v : 0.f;
+                    if constexpr (GATE) v = gatev[fm][fn][r] > 0.f ? v : 0.f;
                     C[(long long)row * ldc + col] = v;
                 }
             }
