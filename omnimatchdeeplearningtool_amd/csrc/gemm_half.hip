@@ -798,10 +798,24 @@ __device__ __forceinline__ void waveLdsOrder() {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
+template <class Cfg>
+__device__ __forceinline__ void stagedBias(const HalfFastParams& p, int n0, int wn, int lane, float (&bz)[4]) {
+    constexpr int LPR = Cfg::WN / 4;
+    const int n = n0 + wn * Cfg::WN + 4 * (lane % LPR);   // as storeStaged's columns
+#pragma unroll
+    for (int j = 0; j < 4; ++j) bz[j] = 0.f;
+    if (p.bias && n < p.N) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) bz[j] = p.bias[n + j];
+    }
+}
+
+// bz: the lane's four bias values (stagedBias, loaded before the main loop so that
+// their latency is hidden by it).
 template <class Cfg, bool BF16>
 __device__ __forceinline__ void storeStaged(const HalfFastParams& p, const f32x16h (&acc)[Cfg::FM][Cfg::FN],
                                             uint16_t* hsm, long long cb, int m0, int n0, int wm, int wn, int li,
-                                            int h, int lane, int wave) {
+                                            int h, int lane, int wave, const float (&bz)[4]) {
     typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
     constexpr int PF = StagedStore<Cfg>::PF;
     constexpr int LPR = Cfg::WN / 4;        // lanes per row
@@ -809,11 +823,6 @@ __device__ __forceinline__ void storeStaged(const HalfFastParams& p, const f32x1
     float* st = reinterpret_cast<float*>(hsm) + wave * 32 * PF;
     const int lr = lane / LPR, lc = 4 * (lane % LPR);
     const int n = n0 + wn * Cfg::WN + lc;   // the lane's four columns n .. n+3 (N % 4 == 0: all in or all out)
-    float bz[4] = {0.f, 0.f, 0.f, 0.f};
-    if (p.bias && n < p.N) {
-#pragma unroll
-        for (int j = 0; j < 4; ++j) bz[j] = p.bias[n + j];
-    }
 #pragma unroll
     for (int fm = 0; fm < Cfg::FM; ++fm) {
         // lane (li, h) holds row li, columns fn*32 + 8g + 4h .. +3 of block (fm, fn)
@@ -875,6 +884,10 @@ __global__ __launch_bounds__(Cfg::NT) void gemm_half_fast(HalfFastParams p) {
     const int m0 = tm * Cfg::BM, n0 = tn * Cfg::BN;
     const uint16_t* Ab = p.A + batch * p.sA;
     const uint16_t* Bb = p.B + batch * p.sB;
+    float bzPre[4] = {0.f, 0.f, 0.f, 0.f};   // the staged store's bias, loaded ahead of the main loop
+    if constexpr (SWAP && StagedStore<Cfg>::USED) {
+        if (p.staged) stagedBias<Cfg>(p, n0, wn, lane, bzPre);
+    }
 
     // A's rows are m: K-major unless transposed. B's rows are n: K-major when transposed.
     using Ops = HalfOps<Cfg, TA, TB, RAG>;
@@ -975,7 +988,7 @@ __global__ __launch_bounds__(Cfg::NT) void gemm_half_fast(HalfFastParams p) {
         if constexpr (StagedStore<Cfg>::USED) {
             if (p.staged) {
                 __syncthreads();   // every wave is done reading the stages
-                storeStaged<Cfg, BF16>(p, acc, hsm, cb, m0, n0, wm, wn, li, h, lane, wave);
+                storeStaged<Cfg, BF16>(p, acc, hsm, cb, m0, n0, wm, wn, li, h, lane, wave, bzPre);
                 return;
             }
         }
