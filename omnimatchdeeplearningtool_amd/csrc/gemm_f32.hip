@@ -288,63 +288,128 @@ __device__ __forceinline__ void gemmF32Tile(const GemmF32Params& p, float* smem,
     lb.template load<false>(kBeg, kEnd, tid);
     la.store(smem, tid);
     lb.store(smem + SA::SIZE, tid);
-    __syncthreads();
-    // Two slices per trip so both LDS stage addresses are compile-time
-    // offsets. The main loop runs while both slices it fetches (t+1, t+2) lie
-    // wholly inside the K range, so its loads test nothing; the last slices
-    // run in the checked loop below (slice t is always in stage t & 1). The
-    // schedule barriers keep each half in the order global loads, MFMAs, LDS
-    // stores, block barrier.
     const int nFull = (kEnd - kBeg) / Cfg::BK;
     int t = 0;
-    for (; t + 2 < nFull; t += 2) {
-        la.template load<true>(kBeg + (t + 1) * Cfg::BK, kEnd, tid);
-        lb.template load<true>(kBeg + (t + 1) * Cfg::BK, kEnd, tid);
-        __builtin_amdgcn_sched_barrier(0);
-        colSum(smem + SA::SIZE, kBeg + t * Cfg::BK);
-        mma_slice_split<Cfg, A_KMAJOR, B_KMAJOR>(smem, smem + SA::SIZE, acc, wm, wn, lane, [&] {
-            la.store(smem + STAGE, tid);
-            lb.store(smem + STAGE + SA::SIZE, tid);
-        });
+    if constexpr (PRE) {
+        // Two slices in flight: while slice t is multiplied from LDS, slice t+1 (loaded
+        // one slice earlier) is stored to the other stage and slice t+2 is loaded into a
+        // second register set (la2 / lb2), so a load has two slices of MFMA work to land
+        // instead of one. The small tiles run one workgroup per CU with short main loops,
+        // where a single slice did not cover the load latency.
+        GemmLoader<A_KMAJOR, LA, Cfg::BM, Cfg::BK, Cfg::NT> la2;
+        la2.init(p.A + batch * p.sA, p.lda, p.M, m0, tid);
+        GemmLoader<B_KMAJOR, LB, Cfg::BN, Cfg::BK, Cfg::NT> lb2;
+        lb2.init(p.B + batch * p.sB, p.ldb, p.N, n0, tid);
+        if (nk > 1) {
+            la.template load<false>(kBeg + Cfg::BK, kEnd, tid);
+            lb.template load<false>(kBeg + Cfg::BK, kEnd, tid);
+        }
         __syncthreads();
-        la.template load<true>(kBeg + (t + 2) * Cfg::BK, kEnd, tid);
-        lb.template load<true>(kBeg + (t + 2) * Cfg::BK, kEnd, tid);
-        __builtin_amdgcn_sched_barrier(0);
-        colSum(smem + STAGE + SA::SIZE, kBeg + (t + 1) * Cfg::BK);
-        mma_slice_split<Cfg, A_KMAJOR, B_KMAJOR>(smem + STAGE, smem + STAGE + SA::SIZE, acc, wm, wn, lane, [&] {
-            la.store(smem, tid);
-            lb.store(smem + SA::SIZE, tid);
-        });
-        __syncthreads();
-    }
-    for (; t < nk; t += 2) {
-        {
-            const bool more = (t + 1) < nk;
-            if (more) {
-                la.template load<false>(kBeg + (t + 1) * Cfg::BK, kEnd, tid);
-                lb.template load<false>(kBeg + (t + 1) * Cfg::BK, kEnd, tid);
+        // Slice t is in stage t & 1; on entry to a trip la / lb hold slice t+1. The
+        // unchecked loop runs while the slices it fetches (t+2, t+3) are whole.
+        for (; t + 3 < nFull; t += 2) {
+            la2.template load<true>(kBeg + (t + 2) * Cfg::BK, kEnd, tid);
+            lb2.template load<true>(kBeg + (t + 2) * Cfg::BK, kEnd, tid);
+            __builtin_amdgcn_sched_barrier(0);
+            colSum(smem + SA::SIZE, kBeg + t * Cfg::BK);
+            mma_slice_split<Cfg, A_KMAJOR, B_KMAJOR>(smem, smem + SA::SIZE, acc, wm, wn, lane, [&] {
+                la.store(smem + STAGE, tid);
+                lb.store(smem + STAGE + SA::SIZE, tid);
+            });
+            __syncthreads();
+            la.template load<true>(kBeg + (t + 3) * Cfg::BK, kEnd, tid);
+            lb.template load<true>(kBeg + (t + 3) * Cfg::BK, kEnd, tid);
+            __builtin_amdgcn_sched_barrier(0);
+            colSum(smem + STAGE + SA::SIZE, kBeg + (t + 1) * Cfg::BK);
+            mma_slice_split<Cfg, A_KMAJOR, B_KMAJOR>(smem + STAGE, smem + STAGE + SA::SIZE, acc, wm, wn, lane, [&] {
+                la2.store(smem, tid);
+                lb2.store(smem + SA::SIZE, tid);
+            });
+            __syncthreads();
+        }
+        for (; t < nk; t += 2) {
+            if (t + 2 < nk) {
+                la2.template load<false>(kBeg + (t + 2) * Cfg::BK, kEnd, tid);
+                lb2.template load<false>(kBeg + (t + 2) * Cfg::BK, kEnd, tid);
             }
             colSum(smem + SA::SIZE, kBeg + t * Cfg::BK);
             mma_slice<Cfg, A_KMAJOR, B_KMAJOR>(smem, smem + SA::SIZE, acc, wm, wn, lane);
-            if (more) {
+            if (t + 1 < nk) {
                 la.store(smem + STAGE, tid);
                 lb.store(smem + STAGE + SA::SIZE, tid);
             }
             __syncthreads();
-        }
-        if (t + 1 < nk) {
-            const bool more = (t + 2) < nk;
-            if (more) {
-                la.template load<false>(kBeg + (t + 2) * Cfg::BK, kEnd, tid);
-                lb.template load<false>(kBeg + (t + 2) * Cfg::BK, kEnd, tid);
+            if (t + 1 < nk) {
+                if (t + 3 < nk) {
+                    la.template load<false>(kBeg + (t + 3) * Cfg::BK, kEnd, tid);
+                    lb.template load<false>(kBeg + (t + 3) * Cfg::BK, kEnd, tid);
+                }
+                colSum(smem + STAGE + SA::SIZE, kBeg + (t + 1) * Cfg::BK);
+                mma_slice<Cfg, A_KMAJOR, B_KMAJOR>(smem + STAGE, smem + STAGE + SA::SIZE, acc, wm, wn, lane);
+                if (t + 2 < nk) {
+                    la2.store(smem, tid);
+                    lb2.store(smem + SA::SIZE, tid);
+                }
+                __syncthreads();
             }
+        }
+    } else {
+        __syncthreads();
+        // Two slices per trip so both LDS stage addresses are compile-time
+        // offsets. The main loop runs while both slices it fetches (t+1, t+2) lie
+        // wholly inside the K range, so its loads test nothing; the last slices
+        // run in the checked loop below (slice t is always in stage t & 1). The
+        // schedule barriers keep each half in the order global loads, MFMAs, LDS
+        // stores, block barrier.
+        for (; t + 2 < nFull; t += 2) {
+            la.template load<true>(kBeg + (t + 1) * Cfg::BK, kEnd, tid);
+            lb.template load<true>(kBeg + (t + 1) * Cfg::BK, kEnd, tid);
+            __builtin_amdgcn_sched_barrier(0);
+            colSum(smem + SA::SIZE, kBeg + t * Cfg::BK);
+            mma_slice_split<Cfg, A_KMAJOR, B_KMAJOR>(smem, smem + SA::SIZE, acc, wm, wn, lane, [&] {
+                la.store(smem + STAGE, tid);
+                lb.store(smem + STAGE + SA::SIZE, tid);
+            });
+            __syncthreads();
+            la.template load<true>(kBeg + (t + 2) * Cfg::BK, kEnd, tid);
+            lb.template load<true>(kBeg + (t + 2) * Cfg::BK, kEnd, tid);
+            __builtin_amdgcn_sched_barrier(0);
             colSum(smem + STAGE + SA::SIZE, kBeg + (t + 1) * Cfg::BK);
-            mma_slice<Cfg, A_KMAJOR, B_KMAJOR>(smem + STAGE, smem + STAGE + SA::SIZE, acc, wm, wn, lane);
-            if (more) {
+            mma_slice_split<Cfg, A_KMAJOR, B_KMAJOR>(smem + STAGE, smem + STAGE + SA::SIZE, acc, wm, wn, lane, [&] {
                 la.store(smem, tid);
                 lb.store(smem + SA::SIZE, tid);
-            }
+            });
             __syncthreads();
+        }
+        for (; t < nk; t += 2) {
+            {
+                const bool more = (t + 1) < nk;
+                if (more) {
+                    la.template load<false>(kBeg + (t + 1) * Cfg::BK, kEnd, tid);
+                    lb.template load<false>(kBeg + (t + 1) * Cfg::BK, kEnd, tid);
+                }
+                colSum(smem + SA::SIZE, kBeg + t * Cfg::BK);
+                mma_slice<Cfg, A_KMAJOR, B_KMAJOR>(smem, smem + SA::SIZE, acc, wm, wn, lane);
+                if (more) {
+                    la.store(smem + STAGE, tid);
+                    lb.store(smem + STAGE + SA::SIZE, tid);
+                }
+                __syncthreads();
+            }
+            if (t + 1 < nk) {
+                const bool more = (t + 2) < nk;
+                if (more) {
+                    la.template load<false>(kBeg + (t + 2) * Cfg::BK, kEnd, tid);
+                    lb.template load<false>(kBeg + (t + 2) * Cfg::BK, kEnd, tid);
+                }
+                colSum(smem + STAGE + SA::SIZE, kBeg + (t + 1) * Cfg::BK);
+                mma_slice<Cfg, A_KMAJOR, B_KMAJOR>(smem + STAGE, smem + STAGE + SA::SIZE, acc, wm, wn, lane);
+                if (more) {
+                    la.store(smem, tid);
+                    lb.store(smem + SA::SIZE, tid);
+                }
+                __syncthreads();
+            }
         }
     }
 
