@@ -294,32 +294,41 @@ __global__ __launch_bounds__(256) void bn_stats_part_kernel(const float* __restr
 // result), by the 64 lanes of one wave: lane l loads part l (all loads in
 // flight at once) and every lane folds the lanes' values in from registers —
 // the rounding of a sequential loop, without its chain of dependent loads.
+// The update's two weights, nb / (n + nb) and n nb / (n + nb) (in double,
+// rounded to float), depend only on the part's index: every part before the
+// last is full, so n = p * kStatPart exactly (a multiple of 2^13 below 2^32, a
+// float that holds it exactly). Lane l computes part l's weights, so the
+// serial fold has no division in it (each step of it had two in double).
 // Returns mean and the biased variance M2 / L.
 __device__ __forceinline__ void mergeStats(const float* __restrict__ part, int c, int P, long long L, float& mean,
                                            float& var) {
 #pragma clang fp contract(off)
     const int lane = threadIdx.x & 63;
-    float n = 0.f, mu = 0.f, m2 = 0.f;
+    float mu = 0.f, m2 = 0.f;
     for (int p0 = 0; p0 < P; p0 += 64) {
         const int pl = p0 + lane;
-        const float mv = pl < P ? part[((long long)c * P + pl) * 2] : 0.f;
-        const float m2v = pl < P ? part[((long long)c * P + pl) * 2 + 1] : 0.f;
+        const bool have = pl < P;
+        const float mv = have ? part[((long long)c * P + pl) * 2] : 0.f;
+        const float m2v = have ? part[((long long)c * P + pl) * 2 + 1] : 0.f;
+        const long long before = (long long)pl * kStatPart;
+        const double na = (double)before;
+        const double nb = have ? (double)min((long long)kStatPart, L - before) : 1.0;
+        const double nn = na + nb;
+        const float wMean = (float)(nb / nn);
+        const float wM2 = (float)(na * nb / nn);
         const int cnt = min(64, P - p0);
         for (int j = 0; j < cnt; ++j) {
-            const int pp = p0 + j;
-            const float nb = (float)min((long long)kStatPart, L - (long long)pp * kStatPart);
             const float mb = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, mv), j));
             const float m2b = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, m2v), j));
-            if (pp == 0) {
-                n = nb;
+            if (p0 + j == 0) {
                 mu = mb;
                 m2 = m2b;
             } else {
-                const double nn = (double)n + (double)nb;
+                const float wa = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wMean), j));
+                const float wb = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wM2), j));
                 const float d = mb - mu;
-                mu = mu + d * (float)((double)nb / nn);
-                m2 = m2 + m2b + d * d * (float)((double)n * (double)nb / nn);
-                n = (float)nn;
+                mu = mu + d * wa;
+                m2 = m2 + m2b + d * d * wb;
             }
         }
     }
