@@ -207,6 +207,25 @@ def test_odd_geometry(hip, geom, variant):
     _check(out, x, wt, bias, bn, act, s, p)
 
 
+# The implicit-GEMM loop keeps two K slices in flight; these reductions cover 1 to 5 whole
+# slices of 16 (1x1 kernels over 16 ... 80 channels, the unmasked gather) and 2 to 5 slices
+# with a partial last one (3x3 over 2 ... 8 channels).
+SLICES = [(2, c, 12, 10, 24, 1, 1, 0) for c in (16, 32, 48, 64, 80)] + \
+         [(2, c, 12, 10, 24, 3, 1, 1) for c in (2, 4, 6, 8)]
+
+
+@pytest.mark.parametrize("geom", SLICES, ids=lambda g: "C{}k{}".format(g[1], g[5]))
+def test_slice_counts(hip, geom):
+    N, cin, h, w, cout, k, s, p = geom
+    seed = 300 + cin + k
+    x = O.randn((N, cin, h, w), seed)
+    wt = O.randn((cout, cin, k, k), seed + 1, 0.3)
+    bias = O.randn((cout,), seed + 2)
+    bn = _params(cout, seed + 3)
+    out = _run_conv(hip, x, wt, bias, bn, 1, s, p)
+    _check(out, x, wt, bias, bn, 1, s, p)
+
+
 # The RGB stem geometry (3 channels, 7x7, stride 2, pad 3, W % 4 == 0, W <= 224) runs on its own kernel:
 # up to 7 consecutive output rows of one image per block, 64 channels per block (ragged Cout 40 and 100
 # leave partial channel blocks), rows above / below the image and both side pads zero, Wo < 112 leaves

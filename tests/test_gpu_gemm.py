@@ -71,6 +71,24 @@ def test_matmul_nt(hip, M, K, N):
     assert O.normalized_error(C, C64, bound) <= TOL
 
 
+# Tiles of at most 128 x 128 keep two K slices in flight, and their loop takes different
+# paths for 1 to 7 slices, a partial last slice and split-K pieces of a few slices: 70 x 70
+# runs on 64 x 64 tiles, 2048 x 2048 on 128 x 128 tiles, and 64 x 528 x 64 splits K into
+# pieces of 144 / 144 / 144 / 96.
+@pytest.mark.parametrize("M,K,N", [(70, 16, 70), (70, 32, 70), (70, 48, 70), (70, 80, 70), (70, 96, 70),
+                                   (70, 111, 70), (2048, 48, 2048), (2048, 80, 2048), (64, 528, 64)])
+@pytest.mark.parametrize("nt", [False, True])
+def test_matmul_slice_counts(hip, M, K, N, nt):
+    A = O.randn((M, K), 5000 + K)
+    B = O.randn((N, K) if nt else (K, N), 6000 + K)
+    print(f"case slices nt={nt} M={M} K={K} N={N}", flush=True)
+    C = _run(hip, "omHipMatmulTransB" if nt else "omHipMatmul", A, B, M, K, N)
+    ref = O.matmul_transB(A, B) if nt else O.matmul(A, B)
+    C64, bound = O.gemm_f64(A, B, transB=nt)
+    assert O.normalized_error(C, ref, bound) <= TOL
+    assert O.normalized_error(C, C64, bound) <= TOL
+
+
 @pytest.mark.parametrize("M,K,N", [(3, 5, 7), (784, 128, 256), (256, 128, 128), (128, 128, 10), (1024, 512, 768)])
 def test_matmul_tn(hip, M, K, N):
     Akm = O.randn((K, M), 5000 + M)
