@@ -612,8 +612,9 @@ __global__ __launch_bounds__(Cfg::NT) void conv_igemm_kernel(ConvParams p) {
 // ---- tile configuration -------------------------------------------------------
 // 64 x 64 output tile, 4 waves of 32 x 32, 16-deep K slices. Measured on MI355X
 // across the ResNet conv shapes this tile beats 64x128 ... 256x128 tiles on
-// every layer: it keeps 8 waves per SIMD resident, which hides the gather
-// latency, and (with the buffer-load loaders) costs about two VALU per MFMA.
+// every layer: it keeps 7 blocks per CU resident (7 waves per SIMD, 68 VGPRs and
+// ~22 KB of LDS each), which hides the gather latency, and (with the buffer-load
+// loaders) costs about two VALU per MFMA.
 #ifndef OMHIP_CONV_BK
 #define OMHIP_CONV_BK 16
 #endif
