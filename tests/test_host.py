@@ -43,6 +43,42 @@ def test_python_signatures_cover_header():
     assert set(declared_functions()) == sigs
 
 
+def header_parameter_kinds():
+    """name -> parameter kinds ('ptr', 'i', 'll', 'sz', 'f') of every declaration in omhip.h."""
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    text = re.sub(r"//[^\n]*", "", text)
+    out = {}
+    for name, params in re.findall(r"\b(omHip\w+)\s*\(([^)]*)\)\s*;", text):
+        kinds = []
+        for p in params.split(","):
+            p = " ".join(p.split())
+            if not p or p == "void":
+                continue
+            t = re.sub(r"\b\w+$", "", p).strip()   # drop the parameter name
+            kinds.append("ptr" if "*" in t else "ll" if t == "long long" else "sz" if t == "size_t"
+                         else "f" if t == "float" else "i" if t == "int" else t)
+        out[name] = kinds
+    return out
+
+
+def test_python_argtypes_match_header():
+    """Every ctypes signature the package binds has the header's parameter count and kinds, so a
+    call never passes an int where the C function reads a pointer, a float or a 64-bit size."""
+    import omnimatchdeeplearningtool_amd as om
+
+    def kind(t):
+        if t in (ctypes.c_void_p, ctypes.c_char_p) or issubclass(t, ctypes._Pointer):
+            return "ptr"
+        return {ctypes.c_int: "i", ctypes.c_longlong: "ll", ctypes.c_size_t: "sz", ctypes.c_float: "f"}[t]
+
+    decl = header_parameter_kinds()
+    assert len(decl) >= 90
+    wrong = {n: ([kind(t) for t in args], decl[n]) for n, args in om._SIGS.items()
+             if [kind(t) for t in args] != decl[n]}
+    assert not wrong, wrong
+
+
 def test_headers_compile_as_c_and_cpp23(tmp_path):
     c_src = tmp_path / "c.c"
     c_src.write_text('#include "omhip.h"\nint main(void){ int (*f)(int) = omHipInit; (void)f; return 0; }\n')
