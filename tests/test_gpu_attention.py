@@ -51,6 +51,18 @@ def test_attention(hip, bf16, out_half, B, S, H, D):
     assert O.normalized_error(got, ref, bound) <= tol
 
 
+# Grids of several rounds (two 8-wave workgroups per CU, 512 per round on 256 CUs): 770 pairs end
+# in a partial round, S = 16 is one query block per head, S = 100 seven, S = 197 / 208 thirteen
+# (the 13 key tiles of a full last tile at 208).
+MANY = [(385, 16, 2, 64), (256, 100, 3, 64), (130, 197, 6, 64), (64, 208, 12, 64)]
+
+
+@pytest.mark.parametrize("bf16,out_half", [(False, False), (True, True)], ids=["f16-out32", "bf16-outhalf"])
+@pytest.mark.parametrize("B,S,H,D", MANY, ids=lambda v: str(v))
+def test_attention_many_heads(hip, bf16, out_half, B, S, H, D):
+    test_attention(hip, bf16, out_half, B, S, H, D)
+
+
 def test_attention_rejects_unsupported(hip):
     d = to_dev(hip, np.zeros(3 * 32 * 4, np.uint16))
     o = empty_dev(hip, (4 * 32,))
